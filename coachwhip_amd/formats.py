@@ -1,0 +1,45 @@
+"""GGUF block formats on the expert path: type ids, weights per block, bytes per block.
+
+Type ids are GGUF's (vendor/candle-core/src/quantized/mod.rs:314-339), plus 21 (IQ3_S) and
+22 (IQ2_S), which the reference's Metal shaders implement (quantized.metal:232-257) but its
+type enum does not. Sizes: k_quants.rs:125-200, 631-635; quantized.metal:217-257.
+"""
+F32, F16 = 0, 1
+Q8_0 = 8
+Q4_K = 12
+Q8_K = 15
+IQ2_XXS = 16
+IQ3_S = 21
+IQ2_S = 22
+MXFP4 = 39
+
+NAMES = {F32: "f32", F16: "f16", Q8_0: "q8_0", Q4_K: "q4_K", Q8_K: "q8_K", IQ2_XXS: "iq2_xxs",
+         IQ3_S: "iq3_s", IQ2_S: "iq2_s", MXFP4: "mxfp4"}
+BY_NAME = {v: k for k, v in NAMES.items()}
+
+_BLOCK = {F32: 1, F16: 1, Q8_0: 32, Q4_K: 256, Q8_K: 256, IQ2_XXS: 256, IQ3_S: 256, IQ2_S: 256,
+          MXFP4: 32}
+_SIZE = {F32: 4, F16: 2, Q8_0: 34, Q4_K: 144, Q8_K: 292, IQ2_XXS: 66, IQ3_S: 110, IQ2_S: 82,
+         MXFP4: 17}
+
+# the weight formats the kernels take (Q8_K is an activation format only)
+WEIGHT_TYPES = (Q8_0, Q4_K, IQ2_XXS, IQ2_S, IQ3_S, MXFP4)
+
+
+def block_size(dtype):
+    return _BLOCK[dtype]
+
+
+def type_size(dtype):
+    return _SIZE[dtype]
+
+
+def row_bytes(dtype, k):
+    bs = _BLOCK[dtype]
+    if k % bs:
+        raise ValueError("%s rows need a multiple of %d weights, got %d" % (NAMES[dtype], bs, k))
+    return k // bs * _SIZE[dtype]
+
+
+def matrix_bytes(dtype, n, k):
+    return n * row_bytes(dtype, k)

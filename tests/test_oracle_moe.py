@@ -1,0 +1,219 @@
+"""Pins the CPU oracle's router, activations, combine, slot resolve and MoE layer composition
+(TEST INFRASTRUCTURE). Router and rank cases are the reference's own known answers
+(crates/engine/tests/router.rs, crates/engine/tests/lookahead.rs)."""
+import math
+
+import numpy as np
+import pytest
+
+from coachwhip_amd import formats as F
+from coachwhip_amd import synth
+from oracle import oracle as O
+
+
+def _softmax64(row):
+    row = np.asarray(row, dtype=np.float64)
+    e = np.exp(row - row.max())
+    return e / e.sum()
+
+
+# ---------------------------------------------------------------- router.rs
+
+def test_picks_the_top_k_best_first():                       # router.rs:20-24
+    ids, _ = O.route(np.array([[0.1, 3.0, 2.0, -1.0, 1.0]]), 3, True)
+    assert ids.tolist() == [[1, 2, 4]]
+
+
+def test_each_word_is_routed_on_its_own():                   # router.rs:27-30
+    ids, _ = O.route(np.array([[5.0, 0.0, 1.0, 2.0], [0.0, 1.0, 9.0, 3.0]]), 2, True)
+    assert ids.tolist() == [[0, 3], [2, 3]]
+
+
+def test_renormalised_weights_sum_to_one_and_keep_their_ratios():   # router.rs:33-43
+    row = [0.5, 2.0, 1.0, -0.5, 1.5]
+    _, w = O.route(np.array([row]), 3, True)
+    w = w[0]
+    assert abs(w.sum() - 1.0) < 1e-5
+    p = _softmax64(row)
+    kept = p[1] + p[4] + p[2]
+    for got, i in zip(w, [1, 4, 2]):
+        assert abs(got - p[i] / kept) < 1e-5
+
+
+def test_without_renormalising_the_weights_are_the_router_probabilities():  # router.rs:46-53
+    row = [1.0, 0.0, 3.0, 2.0]
+    _, w = O.route(np.array([row]), 2, False)
+    p = _softmax64(row)
+    assert abs(w[0][0] - p[2]) < 1e-5 and abs(w[0][1] - p[3]) < 1e-5
+    assert w[0].sum() < 1.0
+
+
+def test_weights_follow_the_order_of_the_picks():            # router.rs:56-60
+    _, w = O.route(np.array([[0.0, 4.0, 1.0, 2.0, 3.0]]), 4, True)
+    assert all(a >= b for a, b in zip(w[0], w[0][1:]))
+
+
+def test_ties_go_to_the_lowest_index():                       # sort.rs:40-53, fuse_kernel.rs:54-60
+    ids, w = O.route(np.array([[1.0, 2.0, 2.0, 0.0, 2.0]]), 3, False)
+    assert ids.tolist() == [[1, 2, 4]] and w[0][0] == w[0][1] == w[0][2]
+
+
+def test_route_is_a_stable_descending_argsort_of_the_probabilities():
+    rng = np.random.default_rng(5)
+    logits = rng.standard_normal((64, 256)).astype(np.float32)
+    ids, w = O.route(logits, 8, False)
+    p = O.softmax(logits)
+    want = np.argsort(-p, axis=1, kind="stable")[:, :8]
+    assert np.array_equal(ids, want)
+    assert np.array_equal(w, np.take_along_axis(p, want, axis=1))
+    # the f32 softmax is within a few ulps of the f64 one
+    assert np.allclose(p, np.apply_along_axis(_softmax64, 1, logits), rtol=1e-6, atol=1e-9)
+
+
+# ---------------------------------------------------------------- lookahead.rs (rank)
+
+def test_rank_puts_the_best_scores_first():                  # lookahead.rs:6-9
+    assert O.rank([0.1, 3.0, 2.0, -1.0, 1.0]).tolist() == [1, 2, 4, 0, 3]
+
+
+def test_rank_breaks_ties_by_expert_id():                    # lookahead.rs:11-17
+    assert O.rank([1.0, 1.0, 2.0, 1.0]).tolist() == [2, 0, 1, 3]
+    assert O.rank([0.5] * 6).tolist() == [0, 1, 2, 3, 4, 5]
+
+
+def test_rank_covers_every_expert_once():                    # lookahead.rs:19-27
+    scores = np.array([((i * 7919) % 97) * 0.01 for i in range(512)], dtype=np.float32)
+    ids = O.rank(scores)
+    assert len(ids) == 512
+    assert all(scores[a] >= scores[b] for a, b in zip(ids, ids[1:]))
+    assert sorted(ids.tolist()) == list(range(512))
+
+
+def test_rank_does_not_fail_on_nan():                        # lookahead.rs:29-33
+    assert len(O.rank([1.0, float("nan"), 2.0])) == 3
+
+
+# ---------------------------------------------------------------- activations, combine, resolve
+
+def test_silu_mul_closed_forms():
+    g = np.array([0.0, 1.0, -1.0, 20.0, -20.0, 3.5], dtype=np.float32)
+    u = np.array([5.0, 2.0, 2.0, 1.0, 1.0, -1.0], dtype=np.float32)
+    h = O.silu_mul(g, u)
+    want = [0.0, 2 / (1 + math.exp(-1)), -2 / (1 + math.e), 20 / (1 + math.exp(-20)),
+            -20 / (1 + math.exp(20)), -3.5 / (1 + math.exp(-3.5))]
+    assert np.allclose(h, want, rtol=2e-7, atol=0)
+
+
+def test_clamped_swiglu_limits_bias_and_padding():
+    # gate capped at +limit only; up clamped to +-limit; hidden = (up + 1) * gate * sigmoid(alpha gate)
+    g = np.array([[10.0, -10.0, 0.5]], dtype=np.float32)
+    u = np.array([[10.0, -10.0, 0.25]], dtype=np.float32)
+    gb = np.array([[0.0, 0.0, 0.5], [9.0, 9.0, 9.0]], dtype=np.float32)
+    ub = np.array([[0.0, 0.0, 0.25], [9.0, 9.0, 9.0]], dtype=np.float32)
+    h = O.clamped_swiglu(g, u, gb, ub, [0], pad=5)
+    sig = lambda v: 1 / (1 + math.exp(-1.702 * v))
+    want = [8 * 7 * sig(7), -6 * -10 * sig(-10), 1.5 * 1.0 * sig(1.0), 0.0, 0.0]
+    assert np.allclose(h[0], want, rtol=1e-6, atol=1e-12)
+
+
+def test_weighted_sum_is_the_pick_weighted_combination():
+    down = np.arange(2 * 3 * 4, dtype=np.float32).reshape(2, 3, 4)
+    w = np.array([[1.0, 0.0, 0.5], [0.25, 0.25, 0.5]], dtype=np.float32)
+    out = O.weighted_sum(down, w)
+    assert out.tolist() == [[4.0, 5.5, 7.0, 8.5], [17.0, 18.0, 19.0, 20.0]]
+
+
+def test_resolve_maps_ids_through_the_table_and_counts_misses():   # gpu_sync.rs:49-66
+    table = np.array([3, 0xFFFFFFFF, 1, 0xFFFFFFFF, 2], dtype=np.uint32)
+    slots, missing = O.resolve([0, 1, 2, 3, 4, 0], table)
+    assert slots.tolist() == [3, 0, 1, 0, 2, 3] and missing == 2
+
+
+# ---------------------------------------------------------------- matvec_id and the layer
+
+@pytest.mark.parametrize("rows_per_expert", [False, True])
+def test_matvec_id_reads_each_picks_slot_and_row(rows_per_expert):
+    rng = np.random.default_rng(3)
+    n, k, slots, T, K = 16, 256, 5, 3, 2
+    w = synth.random_blocks(F.IQ2_XXS, slots * n * k, rng)
+    stride = n * F.row_bytes(F.IQ2_XXS, k)
+    ids = rng.integers(0, slots, size=(T, K), dtype=np.uint32)
+    x = rng.standard_normal((T * K if rows_per_expert else T, k)).astype(np.float32)
+    out = O.matvec_id(F.IQ2_XXS, n, k, w, stride, x, ids, rows_per_expert)
+    for t in range(T):
+        for j in range(K):
+            s = int(ids[t, j])
+            xr = x[t * K + j] if rows_per_expert else x[t]
+            want = O.qmatmul_f64(F.IQ2_XXS, w[s * stride:(s + 1) * stride], n, k, xr)[0]
+            assert np.allclose(out[t, j], want, rtol=1e-13, atol=1e-12)
+
+
+def _compose(layer, x, logits, table=None):
+    """The layer as its separately pinned pieces (route, matvec_id, activation, combine)."""
+    ids, w = O.route(logits, layer.top_k, layer.norm)
+    slots = ids if table is None else O.resolve(ids, table)[0].reshape(ids.shape)
+    g = O.matvec_id(layer.dtypes[0], layer.inter, layer.hidden, layer.host[0], layer.slot_stride[0], x, slots, False)
+    u = O.matvec_id(layer.dtypes[1], layer.inter, layer.hidden, layer.host[1], layer.slot_stride[1], x, slots, False)
+    if layer.act == 0:
+        h = g / (1 + np.exp(-g)) * u
+    else:
+        gb = layer.bias[0][ids]
+        ub = layer.bias[1][ids]
+        gg = np.minimum(g + gb, layer.limit)
+        uu = np.clip(u + ub, -layer.limit, layer.limit)
+        h = (uu + 1) * gg / (1 + np.exp(-layer.alpha * gg))
+    width = max(layer.pad, layer.inter)
+    hp = np.zeros(h.shape[:2] + (width,))
+    hp[..., :layer.inter] = h
+    down = O.matvec_id(layer.dtypes[2], layer.hidden, width, layer.host[2], layer.slot_stride[2],
+                       hp.reshape(-1, width).astype(np.float32), slots, True)
+    if layer.act == 1:
+        down = down + layer.bias[2][ids]
+    return np.einsum("tk,tkh->th", w.astype(np.float64), down), ids, w
+
+
+@pytest.mark.parametrize("act", [0, 1])
+def test_moe_layer_equals_the_composition_of_its_pieces(act):
+    rng = np.random.default_rng(21 + act)
+    dts = (F.IQ2_XXS, F.IQ2_XXS, F.IQ2_S) if act == 0 else (F.MXFP4, F.MXFP4, F.MXFP4)
+    layer = synth.moe_weights(16, 4, 256, 256 if act == 0 else 96, dts, rng, act=act,
+                              pad=0 if act == 0 else 128)
+    x = rng.standard_normal((5, 256)).astype(np.float32)
+    logits = rng.standard_normal((5, 16)).astype(np.float32)
+    out, ids, w, missing = O.moe_layer(layer, x, logits)
+    want, wids, ww = _compose(layer, x, logits)
+    assert missing == 0 and np.array_equal(ids, wids) and np.array_equal(w, ww)
+    # the pieces see h rounded to f32 on its way into down; the layer keeps f64 throughout
+    assert O.rel_l2(out, want) < 1e-6
+
+
+def test_moe_layer_through_a_slot_table():
+    rng = np.random.default_rng(9)
+    E, slots = 16, 6
+    layer = synth.moe_weights(E, 2, 256, 256, (F.Q4_K, F.Q4_K, F.IQ3_S), rng, n_slots=slots)
+    table = np.full(E, 0xFFFFFFFF, dtype=np.uint32)
+    resident = rng.choice(E, size=slots, replace=False)
+    table[resident] = np.arange(slots, dtype=np.uint32)
+    x = rng.standard_normal((3, 256)).astype(np.float32)
+    logits = rng.standard_normal((3, E)).astype(np.float32)
+    mask = np.full(E, -1e30, dtype=np.float32)
+    mask[resident] = 0.0                                # experts.rs:2355-2360 (restrict)
+    out, ids, _, missing = O.moe_layer(layer, x, logits + mask, slot_table=table, n_slots=slots)
+    assert missing == 0 and set(ids.reshape(-1).tolist()) <= set(resident.tolist())
+    want, _, _ = _compose(layer, x, logits + mask, table=table)
+    assert O.rel_l2(out, want) < 1e-6
+    # unmasked routing can pick experts with no slot: they are counted and read from slot 0
+    _, _, _, missing = O.moe_layer(layer, x, logits, slot_table=table, n_slots=slots)
+    _, m2 = O.resolve(O.route(logits, 2, True)[0], table)
+    assert missing == m2
+
+
+@pytest.mark.parametrize("dtype", [F.Q8_0, F.Q4_K, F.MXFP4])
+def test_candle_cpu_path_deviation_is_activation_quantization_sized(dtype):
+    # reported, not gated, by the benchmarks: candle quantizes x to Q8 before the dot
+    rng = np.random.default_rng(4)
+    n, k = 64, 1024
+    w = synth.random_blocks(dtype, n * k, rng)
+    x = rng.standard_normal((2, k)).astype(np.float32)
+    err = O.rel_l2(O.candle_matmul(dtype, w, n, k, x), O.qmatmul_f64(dtype, w, n, k, x))
+    assert 1e-4 < err < 3e-2
