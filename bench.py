@@ -1,0 +1,196 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized MoE expert path on one MI355X.
+
+Workload (decode b=1): MoE layers of 256 experts, top-8, hidden 2048,
+expert FFN 512, gate/up IQ2_XXS and down IQ2_S, router logits ~ N(0,1), SwiGLU, every expert
+resident. A step is one token through a chain of --layers such layers (40 by default, the layer
+count of the model config 3 copies); each layer reads its own 224 MB bank, so the 256 MB
+Infinity Cache cannot serve a step's 280 MB of picked expert weights from a previous step, and
+every step routes with fresh logits. Weights are seeded synthetic blocks built on the device.
+
+Prints one JSON line: the headline value is the achieved HBM throughput on the algorithmic bytes
+of a decode layer (the picked experts' GGUF blocks plus activations in and out), beside µs per
+layer, the roofline fraction, a prefill measurement at 1,500 tokens, the parity of layer 0
+against the CPU oracle, and the oracle timed on the host as the CPU baseline.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+METRIC = "MoE layer µs + achieved HBM GB/s (decode b=1); prefill tokens/s; MFMA util"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--layers", type=int, default=40)
+    ap.add_argument("--prefill-tokens", type=int, default=1500)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--seed", type=int, default=3)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (experts would shard across GPUs "
+              "by expert id with one all-reduce per decode layer; not built). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    root = os.path.dirname(os.path.abspath(__file__))
+    sys.path.insert(0, root)
+    import coachwhip_amd as cw
+    from coachwhip_amd import formats as F
+    from coachwhip_amd import ops, synth
+
+    cw.lib()  # fails loudly when the HIP library is not built
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    E, K, H, I = 256, 8, 2048, 512
+    dts = (F.IQ2_XXS, F.IQ2_XXS, F.IQ2_S)
+    L = args.layers
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+
+    log("building %d layers of %d experts on the device" % (L, E))
+    shapes = [(I, H), (I, H), (H, I)]
+    layers = []
+    for l in range(L):
+        banks = []
+        for m in range(3):
+            n, k = shapes[m]
+            raw = synth.device_blocks(dts[m], E * n * k, gen, dev)
+            banks.append(ops.ExpertBank(raw, dts[m], n, k, E, F.matrix_bytes(dts[m], n, k)))
+        layers.append(ops.MoeLayer(*banks, n_experts=E, top_k=K, norm_topk_prob=True))
+    expert_bytes = sum(F.matrix_bytes(dts[m], *shapes[m]) for m in range(3))
+    total_steps = args.warmup + args.steps
+    x_all = torch.randn((total_steps, 1, H), generator=gen, device=dev)
+    logits_all = torch.randn((total_steps, L, 1, E), generator=gen, device=dev)
+    torch.cuda.synchronize()
+
+    # parity of layer 0, step 0 against the CPU oracle (picked experts only travel to the host)
+    log("parity check against the CPU oracle")
+    sys.path.insert(0, os.path.join(root, "oracle"))
+    from oracle import oracle as O
+    out0, ids0, w0 = layers[0].forward(x_all[0], logits_all[0, 0])
+    torch.cuda.synchronize()
+    host_layer = synth.MoeWeights(E, K, H, I, dts, [b.data.cpu().numpy() for b in layers[0].banks],
+                                  [b.slot_stride for b in layers[0].banks], E)
+    x0 = x_all[0].cpu().numpy()
+    lg0 = logits_all[0, 0].cpu().numpy()
+    want, wids, ww, _ = O.moe_layer(host_layer, x0, lg0)
+    parity = {"rel_l2": O.rel_l2(out0.cpu().numpy(), want),
+              "ids_equal": bool(np.array_equal(ids0.cpu().numpy().view(np.uint32), wids)),
+              "max_weight_err": float(np.max(np.abs(w0.cpu().numpy() - ww)))}
+    log("parity", parity)
+
+    # one graph per phase: warmup steps, then the timed steps; each step is L layer calls
+    def capture(step_lo, step_hi):
+        g = torch.cuda.CUDAGraph()
+        outs = []
+        with torch.cuda.graph(g):
+            for s in range(step_lo, step_hi):
+                for l in range(L):
+                    outs.append(layers[l].forward(x_all[s], logits_all[s, l])[0])
+        return g, outs
+
+    for l in range(L):  # workspaces exist before capture
+        layers[l].forward(x_all[0], logits_all[0, l])
+    torch.cuda.synchronize()
+    log("capturing graphs")
+    g_warm, _ = capture(0, args.warmup)
+    g_run, _ = capture(args.warmup, total_steps)
+    torch.cuda.synchronize()
+    g_warm.replay()
+    torch.cuda.synchronize()
+
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    log("timing %d steps x %d layers" % (args.steps, L))
+    t0 = time.perf_counter()
+    torch.cuda.synchronize()
+    start.record()
+    g_run.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = start.elapsed_time(stop)
+    us_per_layer = ms * 1e3 / (args.steps * L)
+
+    # algorithmic bytes of one decode layer: the K distinct picked experts' blocks + x, logits, out
+    layer_bytes = K * expert_bytes + H * 4 + E * 4 + H * 4
+    gbs = layer_bytes / (us_per_layer * 1e-6) / 1e9
+    log("decode: %.2f us/layer, %.1f GB/s (wall %.3f s)" % (us_per_layer, gbs, wall))
+
+    # prefill: one layer, T tokens (the reference reads prompts in pieces; this is one piece)
+    T = args.prefill_tokens
+    xp = torch.randn((T, H), generator=gen, device=dev)
+    lp = torch.randn((T, E), generator=gen, device=dev)
+    layers[1].forward(xp, lp)
+    torch.cuda.synchronize()
+    reps = 3
+    start.record()
+    for _ in range(reps):
+        layers[1].forward(xp, lp)
+    stop.record()
+    torch.cuda.synchronize()
+    pre_us = start.elapsed_time(stop) * 1e3 / reps
+    pre_flops = 2.0 * T * K * 3 * H * I
+    prefill = {"tokens": T, "us_per_layer": pre_us, "tokens_per_s": T / (pre_us * 1e-6),
+               "tflops": pre_flops / (pre_us * 1e-6) / 1e12, "path": "f32 matvec per token (no MFMA yet)"}
+    log("prefill", prefill)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        log("cpu baseline: oracle MoE layer, %d threads, ~%.0f s" % (threads, args.cpu_seconds))
+        rng = np.random.default_rng(args.seed)
+        n, t_cpu = 0, 0.0
+        while t_cpu < args.cpu_seconds and n < 1000:
+            lg = rng.standard_normal((1, E)).astype(np.float32)
+            t1 = time.perf_counter()
+            O.moe_layer(host_layer, x0, lg)
+            t_cpu += time.perf_counter() - t1
+            n += 1
+        cpu = {"value": t_cpu / n * 1e6, "unit": "us/layer", "cores": threads, "kind": "port",
+               "sample": "%d decode calls (T=1) of the C oracle MoE layer (dequantize the picked experts, f64 dots) "
+                         "on layer 0 of the same bank; IQ formats have no candle CPU path" % n}
+        log("cpu", cpu)
+
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms / args.steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded GGUF blocks and N(0,1) activations/logits, generated on the device)",
+        "config": {"workload": "config 3 decode: MoE layer chain, b=1", "experts": E, "top_k": K, "hidden": H,
+                   "expert_ffn": I, "gate_up": "iq2_xxs", "down": "iq2_s", "layers": L, "tokens": 1},
+        "us_per_layer": round(us_per_layer, 3),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "MoE decode layer (route + fused gate/up+SwiGLU + fused down+combine)",
+                     "bytes_per_launch": layer_bytes},
+        "prefill": prefill,
+        "parity": parity,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

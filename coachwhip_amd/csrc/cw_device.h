@@ -1,0 +1,319 @@
+// Device-side readers of the GGUF block formats on the expert path (gfx950).
+//
+// The unit every kernel works in is a 32-weight sub-block: one Q8_0 or MXFP4 block, or one
+// eighth of a Q4_K / IQ super-block. For each format, Fmt::load() reads the bytes one
+// sub-block needs straight from the raw row (gfx950 runs with unaligned access enabled, so the
+// odd GGUF block strides of 17, 34, 66, 82 and 110 bytes cost no extra instructions),
+// Fmt::dequant() writes its 32 exact f32 values and Fmt::dot() returns their dot product with
+// 32 f32 activations. Dequantization is an exact product of an f16 (or power-of-two) scale and
+// small integers in every format here, so dequant() is bit-identical to the CPU dequantizers;
+// dot() factors the scales out of the sum and differs from dequantize-then-dot only by f32
+// rounding of the sum.
+//
+// Layout and arithmetic follow vendor/candle-core/src/quantized/k_quants.rs (Q8_0 766-782,
+// Q4_K 1821-1849 with get_scale_min_k4 in quantized/utils.rs:50-60, MXFP4 638-691) and the
+// Metal dequantizers in vendor/candle-metal-kernels/src/metal_src/quantized.metal
+// (IQ2_XXS 6820-6843, IQ2_S 6918-6935, IQ3_S 6893-6916).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "cw_grids.h"
+
+namespace cw {
+
+// Lattice tables, copied to LDS by the kernels that read IQ formats.
+static __constant__ uint64_t c_iq2xxs_grid[256] = {CW_IQ2XXS_GRID_VALUES};
+static __constant__ uint64_t c_iq2s_grid[1024] = {CW_IQ2S_GRID_VALUES};
+static __constant__ uint32_t c_iq3s_grid[512] = {CW_IQ3S_GRID_VALUES};
+
+__device__ __forceinline__ uint32_t ld_u32(const uint8_t *p) { uint32_t v; __builtin_memcpy(&v, p, 4); return v; }
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t *p) { uint16_t v; __builtin_memcpy(&v, p, 2); return v; }
+__device__ __forceinline__ uint2 ld_u64(const uint8_t *p) { uint2 v; __builtin_memcpy(&v, p, 8); return v; }
+__device__ __forceinline__ uint4 ld_u128(const uint8_t *p) { uint4 v; __builtin_memcpy(&v, p, 16); return v; }
+
+__device__ __forceinline__ float h2f(uint32_t h) { return __half2float(__ushort_as_half((unsigned short)h)); }
+__device__ __forceinline__ float ubyte(uint32_t w, int i) { return (float)((w >> (8 * i)) & 0xFFu); }
+// x with its sign flipped when bit `bit` of `mask` is set
+__device__ __forceinline__ float flip(float x, uint32_t mask, int bit) {
+    return __uint_as_float(__float_as_uint(x) ^ (((mask >> bit) & 1u) << 31));
+}
+// ksigns_iq2xs[i] (quantized.metal:305): 7 sign bits plus a parity bit that makes the count even
+__device__ __forceinline__ uint32_t ksign(uint32_t i7) { return i7 | ((__popc(i7) & 1u) << 7); }
+
+// 2^(e-128), with the f32 subnormals for e < 2 (k_quants.rs:642-649)
+__device__ __forceinline__ float e8m0_half(uint32_t e) {
+    return __uint_as_float(e < 2 ? (0x00200000u << e) : ((e - 1) << 23));
+}
+// doubled E2M1 value of a 4-bit code (k_quants.rs:639): magnitudes {0,1,2,3,4,6,8,12}
+__device__ __forceinline__ float kv_mxfp4(uint32_t c) {
+    uint32_t m = c & 7u;
+    int mag = (int)(m < 4 ? m : ((2u | (m & 1u)) << ((m >> 1) - 1)));  // 4, 6, 8, 12 for 4..7
+    // the reference table is i8, so code 8 is +0, not -0
+    return (float)((c & 8u) ? -mag : mag);
+}
+
+// ---------------------------------------------------------------------------------- Q8_0
+struct FQ8_0 {
+    static constexpr int BS = 32, TS = 34, LDS_BYTES = 0;
+    struct Raw { uint32_t d; uint4 q0, q1; };
+    static __device__ __forceinline__ void fill_lds(void *, int, int) {}
+    static __device__ __forceinline__ Raw load(const uint8_t *row, int sb) {
+        const uint8_t *b = row + TS * sb;
+        Raw r;
+        r.d = ld_u16(b);
+        r.q0 = ld_u128(b + 2);
+        r.q1 = ld_u128(b + 18);
+        return r;
+    }
+    static __device__ __forceinline__ int8_t q(const Raw &r, int j) {
+        uint32_t w = j < 16 ? (&r.q0.x)[j >> 2] : (&r.q1.x)[(j - 16) >> 2];
+        return (int8_t)(w >> (8 * (j & 3)));
+    }
+    static __device__ __forceinline__ void dequant(const Raw &r, const void *, float *y) {
+        float d = h2f(r.d);
+#pragma unroll
+        for (int j = 0; j < 32; j++) y[j] = (float)q(r, j) * d;
+    }
+    static __device__ __forceinline__ float dot(const Raw &r, const void *, const float *x) {
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < 32; j++) s = fmaf((float)q(r, j), x[j], s);
+        return s * h2f(r.d);
+    }
+};
+
+// ---------------------------------------------------------------------------------- Q4_K
+struct FQ4_K {
+    static constexpr int BS = 256, TS = 144, LDS_BYTES = 0;
+    struct Raw { uint32_t dd; uint32_t sc; uint32_t mn; uint4 q0, q1; int hi; };
+    static __device__ __forceinline__ void fill_lds(void *, int, int) {}
+    static __device__ __forceinline__ Raw load(const uint8_t *row, int sb) {
+        const uint8_t *b = row + TS * (sb >> 3);
+        const int j = sb & 7;
+        Raw r;
+        r.dd = ld_u32(b);
+        // get_scale_min_k4 (quantized/utils.rs:50-60) for sub-block j
+        const uint8_t *q = b + 4;
+        if (j < 4) {
+            r.sc = q[j] & 63;
+            r.mn = q[j + 4] & 63;
+        } else {
+            r.sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+            r.mn = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+        }
+        // sub-blocks 2c and 2c+1 share the 32 bytes qs[32c..32c+32): low and high nibbles
+        const uint8_t *qs = b + 16 + 32 * (j >> 1);
+        r.q0 = ld_u128(qs);
+        r.q1 = ld_u128(qs + 16);
+        r.hi = j & 1;
+        return r;
+    }
+    static __device__ __forceinline__ uint32_t nib(const Raw &r, int l) {
+        uint32_t w = l < 16 ? (&r.q0.x)[l >> 2] : (&r.q1.x)[(l - 16) >> 2];
+        return (w >> (8 * (l & 3) + 4 * r.hi)) & 0xFu;
+    }
+    static __device__ __forceinline__ void dequant(const Raw &r, const void *, float *y) {
+        // y = (d*sc)*q - dmin*m: both products exact, one rounding (k_quants.rs:1834-1843)
+        float d1 = h2f(r.dd & 0xFFFF) * (float)r.sc, m1 = h2f(r.dd >> 16) * (float)r.mn;
+#pragma unroll
+        for (int l = 0; l < 32; l++) y[l] = d1 * (float)nib(r, l) - m1;
+    }
+    static __device__ __forceinline__ float dot(const Raw &r, const void *, const float *x) {
+        float s = 0.f, xs = 0.f;
+#pragma unroll
+        for (int l = 0; l < 32; l++) {
+            s = fmaf((float)nib(r, l), x[l], s);
+            xs += x[l];
+        }
+        return h2f(r.dd & 0xFFFF) * (float)r.sc * s - h2f(r.dd >> 16) * (float)r.mn * xs;
+    }
+};
+
+// ---------------------------------------------------------------------------------- MXFP4
+struct FMXFP4 {
+    static constexpr int BS = 32, TS = 17, LDS_BYTES = 0;
+    struct Raw { uint32_t e; uint4 q; };
+    static __device__ __forceinline__ void fill_lds(void *, int, int) {}
+    static __device__ __forceinline__ Raw load(const uint8_t *row, int sb) {
+        const uint8_t *b = row + TS * sb;
+        Raw r;
+        r.e = b[0];
+        r.q = ld_u128(b + 1);
+        return r;
+    }
+    static __device__ __forceinline__ uint32_t byte(const Raw &r, int j) { return ((&r.q.x)[j >> 2] >> (8 * (j & 3))) & 0xFFu; }
+    static __device__ __forceinline__ void dequant(const Raw &r, const void *, float *y) {
+        float d = e8m0_half(r.e);
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            y[j] = kv_mxfp4(byte(r, j) & 0xF) * d;
+            y[j + 16] = kv_mxfp4(byte(r, j) >> 4) * d;
+        }
+    }
+    static __device__ __forceinline__ float dot(const Raw &r, const void *, const float *x) {
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            s = fmaf(kv_mxfp4(byte(r, j) & 0xF), x[j], s);
+            s = fmaf(kv_mxfp4(byte(r, j) >> 4), x[j + 16], s);
+        }
+        return s * e8m0_half(r.e);
+    }
+};
+
+// ---------------------------------------------------------------------------------- IQ2_XXS
+struct FIQ2_XXS {
+    static constexpr int BS = 256, TS = 66, LDS_BYTES = 256 * 8;
+    struct Raw { uint32_t d; uint32_t g; uint32_t s; };
+    static __device__ __forceinline__ void fill_lds(void *lds, int tid, int nt) {
+        uint64_t *t = (uint64_t *)lds;
+        for (int i = tid; i < 256; i += nt) t[i] = c_iq2xxs_grid[i];
+    }
+    static __device__ __forceinline__ Raw load(const uint8_t *row, int sb) {
+        const uint8_t *b = row + TS * (sb >> 3);
+        Raw r;
+        r.d = ld_u16(b);
+        uint2 v = ld_u64(b + 2 + 8 * (sb & 7));
+        r.g = v.x;  // four grid indices (bytes)
+        r.s = v.y;  // four 7-bit sign indices and the 4-bit scale in the top nibble
+        return r;
+    }
+    static __device__ __forceinline__ void dequant(const Raw &r, const void *lds, float *y) {
+        const uint64_t *grid = (const uint64_t *)lds;
+        float dl = h2f(r.d) * (0.5f + (float)(r.s >> 28)) * 0.25f;
+#pragma unroll
+        for (int l = 0; l < 4; l++) {
+            uint64_t g = grid[(r.g >> (8 * l)) & 0xFF];
+            uint32_t sg = ksign((r.s >> (7 * l)) & 127);
+            uint32_t lo = (uint32_t)g, hi = (uint32_t)(g >> 32);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                float gv = i < 4 ? ubyte(lo, i) : ubyte(hi, i - 4);
+                y[8 * l + i] = dl * gv * ((sg >> i) & 1 ? -1.f : 1.f);
+            }
+        }
+    }
+    static __device__ __forceinline__ float dot(const Raw &r, const void *lds, const float *x) {
+        const uint64_t *grid = (const uint64_t *)lds;
+        float s = 0.f;
+#pragma unroll
+        for (int l = 0; l < 4; l++) {
+            uint64_t g = grid[(r.g >> (8 * l)) & 0xFF];
+            uint32_t sg = ksign((r.s >> (7 * l)) & 127);
+            uint32_t lo = (uint32_t)g, hi = (uint32_t)(g >> 32);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                float gv = i < 4 ? ubyte(lo, i) : ubyte(hi, i - 4);
+                s = fmaf(gv, flip(x[8 * l + i], sg, i), s);
+            }
+        }
+        return s * (h2f(r.d) * (0.5f + (float)(r.s >> 28)) * 0.25f);
+    }
+};
+
+// ---------------------------------------------------------------------------------- IQ2_S
+struct FIQ2_S {
+    static constexpr int BS = 256, TS = 82, LDS_BYTES = 1024 * 8;
+    struct Raw { uint32_t d; uint32_t qs; uint32_t sg; uint32_t qh; uint32_t sc; };
+    static __device__ __forceinline__ void fill_lds(void *lds, int tid, int nt) {
+        uint64_t *t = (uint64_t *)lds;
+        for (int i = tid; i < 1024; i += nt) t[i] = c_iq2s_grid[i];
+    }
+    static __device__ __forceinline__ Raw load(const uint8_t *row, int sb) {
+        const uint8_t *b = row + TS * (sb >> 3);
+        const int ib = sb & 7;
+        Raw r;
+        r.d = ld_u16(b);
+        r.qs = ld_u32(b + 2 + 4 * ib);        // low 8 bits of the four grid indices
+        r.sg = ld_u32(b + 2 + 32 + 4 * ib);   // one sign byte per 8 weights
+        r.qh = b[66 + ib];                    // 2 high index bits per group
+        r.sc = b[74 + ib];                    // two 4-bit scales, one per 16 weights
+        return r;
+    }
+    static __device__ __forceinline__ void dequant(const Raw &r, const void *lds, float *y) {
+        const uint64_t *grid = (const uint64_t *)lds;
+        float d = h2f(r.d);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            float dl = d * (0.5f + (float)((r.sc >> (4 * (t >> 1))) & 0xF)) * 0.25f;
+            uint64_t g = grid[((r.qs >> (8 * t)) & 0xFF) | (((r.qh >> (2 * t)) & 3) << 8)];
+            uint32_t sg = (r.sg >> (8 * t)) & 0xFF;
+            uint32_t lo = (uint32_t)g, hi = (uint32_t)(g >> 32);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                float gv = i < 4 ? ubyte(lo, i) : ubyte(hi, i - 4);
+                y[8 * t + i] = dl * gv * ((sg >> i) & 1 ? -1.f : 1.f);
+            }
+        }
+    }
+    static __device__ __forceinline__ float dot(const Raw &r, const void *lds, const float *x) {
+        const uint64_t *grid = (const uint64_t *)lds;
+        float s[2] = {0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            uint64_t g = grid[((r.qs >> (8 * t)) & 0xFF) | (((r.qh >> (2 * t)) & 3) << 8)];
+            uint32_t sg = r.sg >> (8 * t);
+            uint32_t lo = (uint32_t)g, hi = (uint32_t)(g >> 32);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                float gv = i < 4 ? ubyte(lo, i) : ubyte(hi, i - 4);
+                s[t >> 1] = fmaf(gv, flip(x[8 * t + i], sg, i), s[t >> 1]);
+            }
+        }
+        float d = h2f(r.d) * 0.25f;
+        return d * ((0.5f + (float)(r.sc & 0xF)) * s[0] + (0.5f + (float)(r.sc >> 4)) * s[1]);
+    }
+};
+
+// ---------------------------------------------------------------------------------- IQ3_S
+struct FIQ3_S {
+    static constexpr int BS = 256, TS = 110, LDS_BYTES = 512 * 4;
+    struct Raw { uint32_t d; uint2 qs; uint32_t qh; uint32_t sg; uint32_t sc; };
+    static __device__ __forceinline__ void fill_lds(void *lds, int tid, int nt) {
+        uint32_t *t = (uint32_t *)lds;
+        for (int i = tid; i < 512; i += nt) t[i] = c_iq3s_grid[i];
+    }
+    static __device__ __forceinline__ Raw load(const uint8_t *row, int sb) {
+        const uint8_t *b = row + TS * (sb >> 3);
+        const int ib = sb & 7;
+        Raw r;
+        r.d = ld_u16(b);
+        r.qs = ld_u64(b + 2 + 8 * ib);            // low 8 bits of eight grid indices
+        r.qh = b[66 + ib];                        // their 9th bits
+        r.sg = ld_u32(b + 74 + 4 * ib);           // one sign bit per weight
+        r.sc = (b[106 + (ib >> 1)] >> (4 * (ib & 1))) & 0xF;
+        return r;
+    }
+    static __device__ __forceinline__ uint32_t gidx(const Raw &r, int g) {
+        uint32_t w = g < 4 ? r.qs.x : r.qs.y;
+        return ((w >> (8 * (g & 3))) & 0xFF) | (((r.qh >> g) & 1) << 8);
+    }
+    static __device__ __forceinline__ void dequant(const Raw &r, const void *lds, float *y) {
+        const uint32_t *grid = (const uint32_t *)lds;
+        float dl = h2f(r.d) * (float)(1 + 2 * (int)r.sc);
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            uint32_t gw = grid[gidx(r, g)];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                int v = 4 * g + i;
+                y[v] = dl * ubyte(gw, i) * ((r.sg >> v) & 1 ? -1.f : 1.f);
+            }
+        }
+    }
+    static __device__ __forceinline__ float dot(const Raw &r, const void *lds, const float *x) {
+        const uint32_t *grid = (const uint32_t *)lds;
+        float s = 0.f;
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            uint32_t gw = grid[gidx(r, g)];
+#pragma unroll
+            for (int i = 0; i < 4; i++) s = fmaf(ubyte(gw, i), flip(x[4 * g + i], r.sg, 4 * g + i), s);
+        }
+        return s * (h2f(r.d) * (float)(1 + 2 * (int)r.sc));
+    }
+};
+
+}  // namespace cw

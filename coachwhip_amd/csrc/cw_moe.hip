@@ -1,0 +1,381 @@
+// Router top-k, activations, weighted combine, slot resolve and the MoE layer (gfx950).
+#include <math.h>
+
+#include "cw_common.h"
+#include "cw_gemv.h"
+
+namespace cw {
+
+// ------------------------------------------------------------------------------ reductions
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+// (value, index) maximum; ties go to the lower index, exhausted candidates carry index ~0u
+__device__ __forceinline__ bool better(float va, uint32_t ia, float vb, uint32_t ib) {
+    if (ia == 0xFFFFFFFFu) return false;
+    if (ib == 0xFFFFFFFFu) return true;
+    return va > vb || (va == vb && ia < ib);
+}
+__device__ __forceinline__ void wave_argmax(float &v, uint32_t &i) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        float ov = __shfl_xor(v, off);
+        uint32_t oi = __shfl_xor(i, off);
+        if (better(ov, oi, v, i)) { v = ov; i = oi; }
+    }
+}
+
+// ------------------------------------------------------------------------------ router
+
+// One block of 256 threads per token; PER logits per thread (E <= 256 * PER).
+// Softmax as candle-nn's softmax_last_dim: max, exp of the differences, sum, divide. The K picks
+// are taken best first by logit (softmax is monotone, and comparing logits is exact), the lowest
+// index winning ties, which is the order of the stable descending argsort route() uses
+// (crates/engine/src/experts.rs:2364-2372, vendor/candle-core/src/sort.rs:40-53).
+template <int PER>
+__global__ __launch_bounds__(256) void k_route(const float *logits, int E, int K, int norm, uint32_t *ids, float *w) {
+    __shared__ float red_v[4];
+    __shared__ uint32_t red_i[4];
+    __shared__ float pick_v[32];
+    __shared__ uint32_t pick_i[32];
+    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const float *x = logits + (int64_t)t * E;
+    float v[PER];
+    bool live[PER];
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        int e = tid + 256 * i;
+        live[i] = e < E;
+        v[i] = live[i] ? x[e] : -INFINITY;
+    }
+    float m = v[0];
+#pragma unroll
+    for (int i = 1; i < PER; i++) m = fmaxf(m, v[i]);
+    m = wave_max(m);
+    if (lane == 0) red_v[wv] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red_v[0], red_v[1]), fmaxf(red_v[2], red_v[3]));
+    __syncthreads();
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < PER; i++) s += live[i] ? expf(v[i] - m) : 0.f;
+    s = wave_sum(s);
+    if (lane == 0) red_v[wv] = s;
+    __syncthreads();
+    s = (red_v[0] + red_v[1]) + (red_v[2] + red_v[3]);
+    __syncthreads();
+    for (int j = 0; j < K; j++) {
+        float bv = -INFINITY;
+        uint32_t bi = 0xFFFFFFFFu;
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            uint32_t e = (uint32_t)(tid + 256 * i);
+            if (live[i] && better(v[i], e, bv, bi)) { bv = v[i]; bi = e; }
+        }
+        wave_argmax(bv, bi);
+        if (lane == 0) { red_v[wv] = bv; red_i[wv] = bi; }
+        __syncthreads();
+        if (tid == 0) {
+            float b = red_v[0];
+            uint32_t ix = red_i[0];
+            for (int q = 1; q < 4; q++)
+                if (better(red_v[q], red_i[q], b, ix)) { b = red_v[q]; ix = red_i[q]; }
+            pick_v[j] = b;
+            pick_i[j] = ix;
+        }
+        __syncthreads();
+        const uint32_t won = pick_i[j];
+#pragma unroll
+        for (int i = 0; i < PER; i++)
+            if ((uint32_t)(tid + 256 * i) == won) live[i] = false;
+    }
+    if (tid == 0) {
+        float tot = 0.f;
+        for (int j = 0; j < K; j++) {
+            pick_v[j] = expf(pick_v[j] - m) / s;
+            tot += pick_v[j];
+        }
+        for (int j = 0; j < K; j++) {
+            ids[(int64_t)t * K + j] = pick_i[j];
+            w[(int64_t)t * K + j] = norm ? pick_v[j] / tot : pick_v[j];
+        }
+    }
+}
+
+__global__ void k_swiglu(const float *g, const float *u, float *h, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        float v = g[i];
+        h[i] = v / (1.0f + expf(-v)) * u[i];
+    }
+}
+
+__global__ void k_clamped_swiglu(const float *g, const float *u, const float *gb, const float *ub, const uint32_t *ids,
+                                 int64_t rows, int width, int out_w, float alpha, float limit, float *h) {
+    const int64_t n = rows * out_w;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / out_w;
+        const int c = (int)(i % out_w);
+        if (c >= width) { h[i] = 0.f; continue; }
+        const uint32_t e = ids[r];
+        float gv = g[r * width + c] + (gb ? gb[(int64_t)e * width + c] : 0.f);
+        float uv = u[r * width + c] + (ub ? ub[(int64_t)e * width + c] : 0.f);
+        gv = fminf(gv, limit);
+        uv = fminf(fmaxf(uv, -limit), limit);
+        h[i] = (uv + 1.0f) * (gv * (1.0f / (1.0f + expf(-(gv * alpha)))));
+    }
+}
+
+__global__ void k_weighted_sum(const float *down, const float *w, const float *bd, const uint32_t *ids, int T, int K, int H,
+                               float *out) {
+    const int64_t n = (int64_t)T * H;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t t = i / H;
+        const int j = (int)(i % H);
+        float acc = 0.f;
+        for (int e = 0; e < K; e++) {
+            float d = down[(t * K + e) * H + j];
+            if (bd) d += bd[(int64_t)ids[t * K + e] * H + j];
+            acc += d * w[t * K + e];
+        }
+        out[i] = acc;
+    }
+}
+
+__global__ void k_resolve(const uint32_t *ids, const uint32_t *table, int n, uint32_t *slots, uint32_t *missing) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        uint32_t s = table[ids[i]];
+        if (s == CW_NO_SLOT) {
+            if (missing) atomicAdd(missing, 1u);
+            s = 0;
+        }
+        slots[i] = s;
+    }
+}
+
+static dim3 flat_grid(int64_t n) {
+    int64_t b = (n + 255) / 256;
+    return dim3((unsigned)(b < 8192 ? (b > 0 ? b : 1) : 8192));
+}
+
+static int route(const float *logits, int T, int E, int K, int norm, uint32_t *ids, float *w, hipStream_t s) {
+    if (T == 0) return CW_OK;
+    if (E <= 256) hipLaunchKernelGGL(k_route<1>, dim3(T), dim3(256), 0, s, logits, E, K, norm, ids, w);
+    else if (E <= 512) hipLaunchKernelGGL(k_route<2>, dim3(T), dim3(256), 0, s, logits, E, K, norm, ids, w);
+    else hipLaunchKernelGGL(k_route<4>, dim3(T), dim3(256), 0, s, logits, E, K, norm, ids, w);
+    return check_launch("k_route");
+}
+
+// ------------------------------------------------------------------------------ MoE layer
+
+struct MoeLayout {
+    size_t ids, w, slots, g, u, h, total;
+};
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static int check_desc(const cw_moe_desc *d, int T) {
+    CW_REQUIRE(d != nullptr, "moe: null descriptor");
+    CW_REQUIRE(T >= 0, "moe: negative token count %d", T);
+    CW_REQUIRE(d->n_experts > 0 && d->n_experts <= 1024, "moe: %d experts (1..1024 supported)", d->n_experts);
+    CW_REQUIRE(d->top_k > 0 && d->top_k <= 32 && d->top_k <= d->n_experts, "moe: top_k %d for %d experts", d->top_k, d->n_experts);
+    CW_REQUIRE(d->hidden > 0 && d->inter > 0, "moe: hidden %d, inter %d", d->hidden, d->inter);
+    CW_REQUIRE(d->act == CW_ACT_SILU || d->act == CW_ACT_CLAMPED_SWIGLU, "moe: unknown activation %d", d->act);
+    CW_REQUIRE(d->pad == 0 || d->pad >= d->inter, "moe: pad %d below inter %d", d->pad, d->inter);
+    const int P = d->pad > d->inter ? d->pad : d->inter;
+    const int ks[3] = {d->hidden, d->hidden, P};
+    const int ns[3] = {d->inter, d->inter, d->hidden};
+    const int n_slots = d->slot_table ? d->n_slots : d->n_experts;
+    CW_REQUIRE(n_slots > 0, "moe: %d slots", n_slots);
+    for (int m = 0; m < 3; m++) {
+        if (!is_weight_type(d->dtype[m])) return set_error(CW_ENOTSUP, "moe: matrix %d has unsupported dtype %d", m, d->dtype[m]);
+        const int bs = cw_block_size(d->dtype[m]);
+        CW_REQUIRE(ks[m] % bs == 0, "moe: matrix %d rows of %d weights are not whole %d-weight blocks", m, ks[m], bs);
+        if (ks[m] > max_gemv_k()) return set_error(CW_ENOTSUP, "moe: rows of %d weights exceed %d", ks[m], max_gemv_k());
+        const int64_t need = (int64_t)ns[m] * (ks[m] / bs) * cw_type_size(d->dtype[m]);
+        CW_REQUIRE(d->slot_stride[m] >= need, "moe: matrix %d slot stride %lld below its %lld bytes", m,
+                   (long long)d->slot_stride[m], (long long)need);
+        CW_REQUIRE(d->w[m] != nullptr, "moe: matrix %d is null", m);
+    }
+    CW_REQUIRE(d->act == CW_ACT_CLAMPED_SWIGLU || (!d->bias[0] && !d->bias[1] && !d->bias[2]),
+               "moe: biases need the clamped SwiGLU activation");
+    return CW_OK;
+}
+
+static MoeLayout layout(const cw_moe_desc *d, int T) {
+    const size_t TK = (size_t)T * d->top_k;
+    const int P = d->pad > d->inter ? d->pad : d->inter;
+    MoeLayout L;
+    size_t off = 0;
+    L.ids = off; off = align256(off + TK * 4);
+    L.w = off; off = align256(off + TK * 4);
+    L.slots = off; off = align256(off + TK * 4);
+    const bool split = d->dtype[0] != d->dtype[1];
+    L.g = off; off = align256(off + (split ? TK * d->inter * 4 : 0));
+    L.u = off; off = align256(off + (split ? TK * d->inter * 4 : 0));
+    L.h = off; off = align256(off + TK * (size_t)P * 4);
+    L.total = off;
+    return L;
+}
+
+static int moe_layer(const cw_moe_desc *d, const float *x, const float *logits, int T, float *out, uint32_t *ids_out,
+                     float *w_out, uint32_t *missing, void *ws, size_t ws_bytes, hipStream_t s) {
+    int rc = check_desc(d, T);
+    if (rc) return rc;
+    if (T == 0) return CW_OK;
+    CW_REQUIRE(x && logits && out, "moe: null x, logits or out");
+    const MoeLayout L = layout(d, T);
+    CW_REQUIRE(ws && ws_bytes >= L.total, "moe: workspace of %zu bytes, %zu needed", ws_bytes, L.total);
+    uint8_t *base = (uint8_t *)ws;
+    const int K = d->top_k, P = d->pad > d->inter ? d->pad : d->inter;
+    uint32_t *ids = ids_out ? ids_out : (uint32_t *)(base + L.ids);
+    float *w = w_out ? w_out : (float *)(base + L.w);
+    if ((rc = route(logits, T, d->n_experts, K, d->norm, ids, w, s))) return rc;
+    const uint32_t *slots = ids;
+    const int n_slots = d->slot_table ? d->n_slots : d->n_experts;
+    if (d->slot_table) {
+        uint32_t *sl = (uint32_t *)(base + L.slots);
+        hipLaunchKernelGGL(k_resolve, flat_grid((int64_t)T * K), dim3(256), 0, s, ids, d->slot_table, T * K, sl, missing);
+        if ((rc = check_launch("k_resolve"))) return rc;
+        slots = sl;
+    }
+    float *h = (float *)(base + L.h);
+
+    GemvArgs a = {};
+    a.n = d->inter;
+    a.k = d->hidden;
+    a.nsb = d->hidden / 32;
+    a.n_slots = n_slots;
+    a.x = x;
+    a.x_per_pick = 0;
+    a.ids = slots;
+    a.experts = ids;
+    a.K = K;
+    if (d->dtype[0] == d->dtype[1]) {
+        a.w0 = (const uint8_t *)d->w[0];
+        a.w1 = (const uint8_t *)d->w[1];
+        a.slot_stride0 = d->slot_stride[0];
+        a.slot_stride1 = d->slot_stride[1];
+        a.row_bytes = (int64_t)(d->hidden / cw_block_size(d->dtype[0])) * cw_type_size(d->dtype[0]);
+        a.out = h;
+        a.out_width = P;
+        a.act = d->act;
+        a.alpha = d->alpha;
+        a.limit = d->limit;
+        a.b0 = d->bias[0];
+        a.b1 = d->bias[1];
+        if ((rc = gemv_gateup(d->dtype[0], a, T * K, s))) return rc;
+    } else {
+        float *g = (float *)(base + L.g), *u = (float *)(base + L.u);
+        for (int m = 0; m < 2; m++) {
+            GemvArgs b = a;
+            b.w0 = (const uint8_t *)d->w[m];
+            b.slot_stride0 = d->slot_stride[m];
+            b.row_bytes = (int64_t)(d->hidden / cw_block_size(d->dtype[m])) * cw_type_size(d->dtype[m]);
+            b.out = m == 0 ? g : u;
+            b.out_width = d->inter;
+            if ((rc = gemv_plain(d->dtype[m], b, T * K, s))) return rc;
+        }
+        const int64_t rows = (int64_t)T * K;
+        if (d->act == CW_ACT_SILU && P == d->inter) {
+            hipLaunchKernelGGL(k_swiglu, flat_grid(rows * d->inter), dim3(256), 0, s, g, u, h, rows * d->inter);
+        } else {
+            const float alpha = d->act == CW_ACT_SILU ? 1.0f : d->alpha;
+            hipLaunchKernelGGL(k_clamped_swiglu, flat_grid(rows * P), dim3(256), 0, s, g, u, d->bias[0], d->bias[1], ids, rows,
+                               d->inter, P, alpha, d->act == CW_ACT_SILU ? INFINITY : d->limit, h);
+        }
+        if ((rc = check_launch("k_swiglu"))) return rc;
+    }
+    GemvArgs b = {};
+    b.w0 = (const uint8_t *)d->w[2];
+    b.slot_stride0 = d->slot_stride[2];
+    b.row_bytes = (int64_t)(P / cw_block_size(d->dtype[2])) * cw_type_size(d->dtype[2]);
+    b.n = d->hidden;
+    b.k = P;
+    b.nsb = P / 32;
+    b.n_slots = n_slots;
+    b.x = h;
+    b.x_per_pick = 1;
+    b.ids = slots;
+    b.experts = ids;
+    b.K = K;
+    b.out = out;
+    b.out_width = d->hidden;
+    b.wts = w;
+    b.bd = d->bias[2];
+    return gemv_down(d->dtype[2], b, T, s);
+}
+
+}  // namespace cw
+
+using namespace cw;
+
+extern "C" {
+
+int cw_route_topk(const float *logits, int T, int E, int K, int norm, uint32_t *ids, float *w, cw_stream_t stream) {
+    CW_REQUIRE(T >= 0, "route: negative token count %d", T);
+    CW_REQUIRE(E > 0 && E <= 1024, "route: %d experts (1..1024 supported)", E);
+    CW_REQUIRE(K > 0 && K <= 32 && K <= E, "route: top-%d of %d experts", K, E);
+    CW_REQUIRE(T == 0 || (logits && ids && w), "route: null pointer");
+    return route(logits, T, E, K, norm, ids, w, (hipStream_t)stream);
+}
+
+int cw_swiglu(const float *g, const float *u, float *h, int64_t n, cw_stream_t stream) {
+    CW_REQUIRE(n >= 0, "swiglu: negative size");
+    if (n == 0) return CW_OK;
+    CW_REQUIRE(g && u && h, "swiglu: null pointer");
+    hipLaunchKernelGGL(k_swiglu, flat_grid(n), dim3(256), 0, (hipStream_t)stream, g, u, h, n);
+    return check_launch("k_swiglu");
+}
+
+int cw_clamped_swiglu(const float *g, const float *u, const float *gate_b, const float *up_b, const uint32_t *ids,
+                      int64_t rows, int width, int pad, float alpha, float limit, float *h, cw_stream_t stream) {
+    CW_REQUIRE(rows >= 0 && width > 0, "clamped_swiglu: %lld rows of %d", (long long)rows, width);
+    CW_REQUIRE(pad == 0 || pad >= width, "clamped_swiglu: pad %d below width %d", pad, width);
+    if (rows == 0) return CW_OK;
+    CW_REQUIRE(g && u && h, "clamped_swiglu: null pointer");
+    CW_REQUIRE(ids || (!gate_b && !up_b), "clamped_swiglu: biases need ids");
+    const int out_w = pad > width ? pad : width;
+    hipLaunchKernelGGL(k_clamped_swiglu, flat_grid(rows * out_w), dim3(256), 0, (hipStream_t)stream, g, u, gate_b, up_b, ids,
+                       rows, width, out_w, alpha, limit, h);
+    return check_launch("k_clamped_swiglu");
+}
+
+int cw_weighted_sum(const float *down, const float *w, const float *down_b, const uint32_t *ids, int T, int K, int H,
+                    float *out, cw_stream_t stream) {
+    CW_REQUIRE(T >= 0 && K > 0 && H > 0, "weighted_sum: T %d, K %d, H %d", T, K, H);
+    CW_REQUIRE(!down_b || ids, "weighted_sum: a down bias needs ids");
+    if (T == 0) return CW_OK;
+    CW_REQUIRE(down && w && out, "weighted_sum: null pointer");
+    hipLaunchKernelGGL(k_weighted_sum, flat_grid((int64_t)T * H), dim3(256), 0, (hipStream_t)stream, down, w, down_b, ids, T,
+                       K, H, out);
+    return check_launch("k_weighted_sum");
+}
+
+int cw_slots_resolve(const uint32_t *ids, const uint32_t *table, int n, uint32_t *slots, uint32_t *missing,
+                     cw_stream_t stream) {
+    CW_REQUIRE(n >= 0, "resolve: negative count");
+    if (n == 0) return CW_OK;
+    CW_REQUIRE(ids && table && slots, "resolve: null pointer");
+    hipLaunchKernelGGL(k_resolve, flat_grid(n), dim3(256), 0, (hipStream_t)stream, ids, table, n, slots, missing);
+    return check_launch("k_resolve");
+}
+
+size_t cw_moe_workspace_size(const cw_moe_desc *desc, int T) {
+    if (check_desc(desc, T)) return 0;
+    return layout(desc, T).total;
+}
+
+int cw_moe_layer(const cw_moe_desc *desc, const float *x, const float *logits, int T, float *out, uint32_t *ids_out,
+                 float *w_out, uint32_t *missing, void *ws, size_t ws_bytes, cw_stream_t stream) {
+    return moe_layer(desc, x, logits, T, out, ids_out, w_out, missing, ws, ws_bytes, (hipStream_t)stream);
+}
+
+}  // extern "C"

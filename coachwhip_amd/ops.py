@@ -1,0 +1,263 @@
+"""Python mirror of the reference engine's quantized-expert interfaces, running on the HIP C ABI.
+
+Names and argument meanings follow the reference so tests read like its own:
+
+- ``QTensor`` / ``QMatMul``: vendor/candle-core/src/quantized/mod.rs:846-1345 (weights as raw
+  GGUF blocks, ``forward`` maps ``[..., k]`` to ``[..., n]``).
+- ``route``: crates/engine/src/experts.rs:2364-2372 (softmax, top-k best first, renormalised
+  weights when ``norm``).
+- ``ExpertAct``: experts.rs:2376-2423 (``Silu`` and ``ClampedSwiglu``).
+- ``MoeMatvec``: experts.rs:2183-2309 (``forward(x, ids)`` -> ``(tokens, nei0, n)``).
+- ``MoeLayer``: the resident branch of ``StreamedMoe::forward`` (experts.rs:2562-2614), and with
+  a slot table the bank branch (3003-3015).
+
+Torch provides device memory and the current stream only; all arithmetic runs in libcwmoe.so.
+Shape and dtype errors raise ``CwError`` (the reference bails with the same conditions).
+"""
+import ctypes
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+import torch
+
+from . import formats as F
+from ._lib import CwError, MoeDesc, check, lib, CW_EINVAL
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _p(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _need(t, dtype, what):
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise CwError(CW_EINVAL, "%s must be a device tensor" % what)
+    if t.dtype != dtype:
+        raise CwError(CW_EINVAL, "%s must be %s, got %s" % (what, dtype, t.dtype))
+    if not t.is_contiguous():
+        raise CwError(CW_EINVAL, "%s must be contiguous" % what)
+
+
+def to_device(a, device="cuda"):
+    """A host numpy array as a device tensor (u32 arrays travel as int32 bits)."""
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint32:
+        a = a.view(np.int32)
+    return torch.from_numpy(a).to(device)
+
+
+class QTensor:
+    """Raw GGUF blocks of an (n, k) matrix on the device."""
+
+    def __init__(self, data: torch.Tensor, dtype: int, shape):
+        n, k = shape
+        _need(data, torch.uint8, "QTensor data")
+        if data.numel() != F.matrix_bytes(dtype, n, k):
+            raise CwError(CW_EINVAL, "QTensor: %d bytes for a %dx%d %s matrix" % (data.numel(), n, k, F.NAMES[dtype]))
+        self.data, self.dtype, self.shape = data, dtype, (n, k)
+
+    @classmethod
+    def from_blocks(cls, raw, dtype, shape, device="cuda"):
+        return cls(to_device(np.asarray(raw, dtype=np.uint8), device), dtype, shape)
+
+    def dequantize(self) -> torch.Tensor:
+        n, k = self.shape
+        out = torch.empty((n, k), dtype=torch.float32, device=self.data.device)
+        check(lib().cw_dequantize(self.dtype, _p(self.data), n * k, _p(out), _stream()))
+        return out
+
+
+def dequantize(dtype, blocks: torch.Tensor, n_elems) -> torch.Tensor:
+    """Flat dequantization of n_elems weights of raw blocks."""
+    _need(blocks, torch.uint8, "blocks")
+    out = torch.empty(n_elems, dtype=torch.float32, device=blocks.device)
+    check(lib().cw_dequantize(dtype, _p(blocks), n_elems, _p(out), _stream()))
+    return out
+
+
+class QMatMul:
+    def __init__(self, qtensor: QTensor):
+        self.w = qtensor
+
+    @classmethod
+    def from_qtensor(cls, qtensor):
+        return cls(qtensor)
+
+    def forward(self, xs: torch.Tensor) -> torch.Tensor:
+        n, k = self.w.shape
+        _need(xs, torch.float32, "xs")
+        if xs.dim() < 2:
+            raise CwError(CW_EINVAL, "input tensor has only one dimension")
+        if xs.shape[-1] != k:
+            raise CwError(CW_EINVAL, "input tensor %s incompatible with (%d, %d)" % (tuple(xs.shape), n, k))
+        m = xs.numel() // k
+        y = torch.empty(xs.shape[:-1] + (n,), dtype=torch.float32, device=xs.device)
+        ws_bytes = lib().cw_qmatmul_workspace_size(self.w.dtype, n, k, m)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=xs.device) if ws_bytes else None
+        check(lib().cw_qmatmul(self.w.dtype, _p(self.w.data), n, k, _p(xs), m, _p(y), _p(ws), ws_bytes, _stream()))
+        return y
+
+    __call__ = forward
+
+
+def route(logits: torch.Tensor, top_k: int, norm: bool):
+    """(ids (T, K) u32 as int32 bits, weights (T, K) f32)."""
+    _need(logits, torch.float32, "logits")
+    t, e = logits.shape
+    ids = torch.empty((t, top_k), dtype=torch.int32, device=logits.device)
+    w = torch.empty((t, top_k), dtype=torch.float32, device=logits.device)
+    check(lib().cw_route_topk(_p(logits), t, e, top_k, int(norm), _p(ids), _p(w), _stream()))
+    return ids, w
+
+
+def swiglu(g, u):
+    _need(g, torch.float32, "gate")
+    _need(u, torch.float32, "up")
+    h = torch.empty_like(g)
+    check(lib().cw_swiglu(_p(g), _p(u), _p(h), g.numel(), _stream()))
+    return h
+
+
+def clamped_swiglu(g, u, gate_b, up_b, ids, pad=0, alpha=1.702, limit=7.0):
+    _need(g, torch.float32, "gate")
+    rows, width = g.shape
+    out_w = max(pad, width)
+    h = torch.empty((rows, out_w), dtype=torch.float32, device=g.device)
+    check(lib().cw_clamped_swiglu(_p(g), _p(u), _p(gate_b), _p(up_b), _p(ids), rows, width, pad, alpha, limit, _p(h),
+                                  _stream()))
+    return h
+
+
+def weighted_sum(down, w, down_b=None, ids=None):
+    _need(down, torch.float32, "down")
+    t, k, h = down.shape
+    out = torch.empty((t, h), dtype=torch.float32, device=down.device)
+    check(lib().cw_weighted_sum(_p(down), _p(w), _p(down_b), _p(ids), t, k, h, _p(out), _stream()))
+    return out
+
+
+def slots_resolve(ids, table):
+    """(slots, missing) with slots the same shape as ids."""
+    _need(ids, torch.int32, "ids")
+    slots = torch.empty_like(ids)
+    missing = torch.zeros(1, dtype=torch.int32, device=ids.device)
+    check(lib().cw_slots_resolve(_p(ids), _p(table), ids.numel(), _p(slots), _p(missing), _stream()))
+    return slots, missing
+
+
+@dataclass
+class ExpertBank:
+    """One matrix of a layer's bank: ``n_slots`` (n, k) matrices ``slot_stride`` bytes apart."""
+    data: torch.Tensor
+    dtype: int
+    n: int
+    k: int
+    n_slots: int
+    slot_stride: int
+
+    @classmethod
+    def from_blocks(cls, raw, dtype, n, k, n_slots, device="cuda"):
+        stride = F.matrix_bytes(dtype, n, k)
+        raw = np.asarray(raw, dtype=np.uint8)
+        if raw.size != stride * n_slots:
+            raise CwError(CW_EINVAL, "bank: %d bytes for %d slots of %d" % (raw.size, n_slots, stride))
+        return cls(to_device(raw, device), dtype, n, k, n_slots, stride)
+
+
+class MoeMatvec:
+    """out[t][j] = W[ids[t][j]] . x_row, x_row = x[t] or x[t*nei0 + j] (rows_per_expert)."""
+
+    def __init__(self, bank: ExpertBank, nei0: int, rows_per_expert: bool):
+        self.bank, self.nei0, self.rows_per_expert = bank, nei0, rows_per_expert
+
+    def forward(self, x: torch.Tensor, ids: torch.Tensor) -> torch.Tensor:
+        _need(x, torch.float32, "x")
+        _need(ids, torch.int32, "ids")
+        tokens, nei0 = ids.shape
+        if nei0 != self.nei0:
+            raise CwError(CW_EINVAL, "%d ids per token, expected %d" % (nei0, self.nei0))
+        rows, k = x.shape
+        want = tokens * nei0 if self.rows_per_expert else tokens
+        if k != self.bank.k or rows != want:
+            raise CwError(CW_EINVAL, "x is %dx%d, expected k=%d for %d tokens" % (rows, k, self.bank.k, tokens))
+        b = self.bank
+        out = torch.empty((tokens, nei0, b.n), dtype=torch.float32, device=x.device)
+        check(lib().cw_matvec_id(b.dtype, b.n, b.k, b.n_slots, b.slot_stride, _p(b.data), _p(x), int(self.rows_per_expert),
+                                 _p(ids), nei0, tokens, _p(out), _stream()))
+        return out
+
+
+@dataclass
+class ExpertAct:
+    """Silu (alpha/limit unused) or ClampedSwiglu with per-expert biases and padding."""
+    kind: int = 0
+    alpha: float = 1.702
+    limit: float = 7.0
+    gate_b: Optional[torch.Tensor] = None
+    up_b: Optional[torch.Tensor] = None
+    down_b: Optional[torch.Tensor] = None
+    pad: int = 0
+
+    @classmethod
+    def silu(cls):
+        return cls(0)
+
+    @classmethod
+    def clamped_swiglu(cls, alpha, limit, gate_b, up_b, down_b, pad=0):
+        return cls(1, alpha, limit, gate_b, up_b, down_b, pad)
+
+
+class MoeLayer:
+    """A MoE layer whose experts are resident in device banks (gate, up, down).
+
+    ``slot_table`` (device u32 expert -> slot, NO_SLOT when absent) switches to the bank
+    variant: picks resolve through the table and picks without a slot are counted."""
+
+    def __init__(self, gate: ExpertBank, up: ExpertBank, down: ExpertBank, n_experts: int, top_k: int,
+                 norm_topk_prob: bool = True, act: ExpertAct = None, slot_table: torch.Tensor = None):
+        self.banks = (gate, up, down)
+        self.n_experts, self.top_k, self.norm = n_experts, top_k, norm_topk_prob
+        self.act = act or ExpertAct.silu()
+        self.slot_table = slot_table
+        self.hidden, self.inter = gate.k, gate.n
+        d = MoeDesc()
+        d.n_experts, d.top_k, d.hidden, d.inter = n_experts, top_k, self.hidden, self.inter
+        d.norm, d.act = int(norm_topk_prob), self.act.kind
+        d.alpha, d.limit, d.pad = self.act.alpha, self.act.limit, self.act.pad
+        for m, b in enumerate(self.banks):
+            d.dtype[m] = b.dtype
+            d.w[m] = b.data.data_ptr()
+            d.slot_stride[m] = b.slot_stride
+        for m, b in enumerate((self.act.gate_b, self.act.up_b, self.act.down_b)):
+            d.bias[m] = None if b is None else b.data_ptr()
+        d.slot_table = None if slot_table is None else slot_table.data_ptr()
+        d.n_slots = gate.n_slots
+        self.desc = d
+        self._ws = None
+
+    def workspace(self, tokens, device):
+        need = lib().cw_moe_workspace_size(ctypes.byref(self.desc), tokens)
+        if need == 0 and tokens > 0:
+            raise CwError(CW_EINVAL, lib().cw_last_error().decode(errors="replace"))
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(need, dtype=torch.uint8, device=device)
+        return self._ws, need
+
+    def forward(self, xs: torch.Tensor, logits: torch.Tensor, missing: torch.Tensor = None):
+        """xs (T, hidden) f32, logits (T, E) f32 -> (out (T, hidden), ids (T, K), w (T, K))."""
+        _need(xs, torch.float32, "xs")
+        _need(logits, torch.float32, "logits")
+        t = xs.shape[0]
+        if xs.shape[1] != self.hidden or logits.shape != (t, self.n_experts):
+            raise CwError(CW_EINVAL, "xs %s / logits %s do not fit the layer" % (tuple(xs.shape), tuple(logits.shape)))
+        out = torch.empty((t, self.hidden), dtype=torch.float32, device=xs.device)
+        ids = torch.empty((t, self.top_k), dtype=torch.int32, device=xs.device)
+        w = torch.empty((t, self.top_k), dtype=torch.float32, device=xs.device)
+        ws, need = self.workspace(t, xs.device)
+        check(lib().cw_moe_layer(ctypes.byref(self.desc), _p(xs), _p(logits), t, _p(out), _p(ids), _p(w), _p(missing),
+                                 _p(ws), need, _stream()))
+        return out, ids, w

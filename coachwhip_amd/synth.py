@@ -106,3 +106,31 @@ def near_ties_within_top_k(logits, k, eps=1e-5):
     s = -np.sort(-np.asarray(logits, dtype=np.float64), axis=1)[:, :k + 1]
     gaps = s[:, :-1] - s[:, 1:]
     return bool(np.any(gaps <= eps * np.maximum(1.0, np.abs(s[:, :-1]))))
+
+
+def device_blocks(dtype, n_weights, gen, device="cuda"):
+    """random_blocks' distribution generated on the device with a seeded torch.Generator (for
+    benchmark banks of several GB that would be slow to build on the host)."""
+    import torch
+    bs, ts = F.block_size(dtype), F.type_size(dtype)
+    assert n_weights % bs == 0
+    nb = n_weights // bs
+    raw = torch.randint(0, 256, (nb, ts), dtype=torch.uint8, device=device, generator=gen)
+
+    def f16_scales():
+        v = torch.rand(nb, device=device, generator=gen) * (0.02 - 0.001) + 0.001
+        return v.to(torch.float16).view(torch.uint8).view(nb, 2)
+
+    if dtype == F.Q8_0:
+        raw[:, 0:2] = f16_scales()
+        raw[:, 2:34] = torch.randint(-127, 128, (nb, 32), dtype=torch.int8, device=device, generator=gen).view(torch.uint8)
+    elif dtype == F.Q4_K:
+        raw[:, 0:2] = f16_scales()
+        raw[:, 2:4] = f16_scales()
+    elif dtype in (F.IQ2_XXS, F.IQ2_S, F.IQ3_S):
+        raw[:, 0:2] = f16_scales()
+    elif dtype == F.MXFP4:
+        raw[:, 0] = torch.randint(119, 124, (nb,), dtype=torch.uint8, device=device, generator=gen)
+    else:
+        raise ValueError("no generator for dtype %d" % dtype)
+    return raw.view(-1)

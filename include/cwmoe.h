@@ -1,0 +1,206 @@
+/*
+ * cwmoe.h — C ABI of the MI355X (gfx950) quantized mixture-of-experts expert path.
+ *
+ * This is the drop-in boundary for the reference engine's quantized matmul and MoE-layer
+ * custom ops. Each entry point below names the reference interface it replaces (paths are
+ * relative to the reference checkout: vendor/candle-* are the vendored candle crates,
+ * crates/engine is the coachwhip engine crate).
+ *
+ * Conventions, kept from the reference (vendor/candle-core/src/custom_op.rs:8-95 and the
+ * Metal launchers in vendor/candle-metal-kernels/src/kernels/quantized.rs):
+ *  - Weights are raw GGUF blocks exactly as stored in the file (no repacking); `dtype` is the
+ *    GGUF type id (vendor/candle-core/src/quantized/mod.rs:314-339, plus 21 = IQ3_S and
+ *    22 = IQ2_S, which the reference's shaders implement).
+ *  - A weight matrix is `n` rows of `k` weights, rows along the output dimension, blocks along
+ *    k (GGUF order). Expert banks hold `n_slots` such matrices `slot_stride` bytes apart.
+ *  - Activations and outputs are contiguous f32; routing ids are u32. Strides are in bytes.
+ *  - All pointers are device pointers unless stated. Every call is asynchronous on `stream`
+ *    (a hipStream_t; NULL = the default stream) and never synchronizes the device.
+ *  - No entry point allocates device memory: scratch comes from a caller-owned workspace
+ *    whose size the matching *_workspace_size query returns (the role of
+ *    crates/engine/src/arena.rs:15-33).
+ *  - Errors are returned, never thrown: CW_OK, CW_ENOTSUP (a capability probe said no; the
+ *    caller may fall back, as mv_id.rs:156-179 does with Ok(false)), CW_EINVAL (shape, stride
+ *    or argument error, as candle::bail! in crates/engine/src/experts.rs:2204-2217), CW_EHIP
+ *    (the HIP runtime failed). cw_last_error() describes the last failure on this thread.
+ *  - Calls on distinct streams may run concurrently; the library keeps no mutable global
+ *    state apart from one-time initialisation, which is thread-safe.
+ */
+#ifndef CWMOE_H
+#define CWMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *cw_stream_t; /* hipStream_t */
+
+enum cw_status { CW_OK = 0, CW_ENOTSUP = 1, CW_EINVAL = 2, CW_EHIP = 3 };
+
+/* GGUF type ids of the weight formats this library reads. */
+enum cw_dtype {
+    CW_F32 = 0,
+    CW_F16 = 1,
+    CW_Q8_0 = 8,     /* {f16 d; i8 qs[32]}: 34 B per 32 weights */
+    CW_Q4_K = 12,    /* {f16 d, dmin; u8 scales[12]; u8 qs[128]}: 144 B per 256 */
+    CW_IQ2_XXS = 16, /* {f16 d; u16 qs[32]}: 66 B per 256 */
+    CW_IQ3_S = 21,   /* {f16 d; u8 qs[64], qh[8], signs[32], scales[4]}: 110 B per 256 */
+    CW_IQ2_S = 22,   /* {f16 d; u8 qs[64], qh[8], scales[8]}: 82 B per 256 */
+    CW_MXFP4 = 39    /* {u8 e8m0; u8 qs[16]}: 17 B per 32 */
+};
+
+enum cw_act { CW_ACT_SILU = 0, CW_ACT_CLAMPED_SWIGLU = 1 };
+
+#define CW_NO_SLOT 0xFFFFFFFFu /* crates/engine/src/gpu_sync.rs:20 */
+
+/* ---- library ---------------------------------------------------------------------------- */
+
+/* Version string and the last error message of the calling thread. */
+const char *cw_version(void);
+const char *cw_last_error(void);
+
+/* Weights per block and bytes per block of a dtype; 0 when the dtype is not supported.
+ * Replaces GgmlDType::block_size / type_size (vendor/candle-core/src/quantized/mod.rs:420-460). */
+int cw_block_size(int dtype);
+int cw_type_size(int dtype);
+
+/* ---- formats ---------------------------------------------------------------------------- */
+
+/* out[i] = the f32 value of weight i, for n_elems weights (a multiple of the block size).
+ * Bit-exact with the CPU dequantizers (every in-scope dequantization is an exact product).
+ * Replaces QTensor::dequantize / QMetalStorage::dequantize
+ * (vendor/candle-core/src/quantized/metal.rs:40-139) and the Metal dequantize_* functions
+ * (vendor/candle-metal-kernels/src/metal_src/quantized.metal:6691-7017). */
+int cw_dequantize(int dtype, const void *blocks, int64_t n_elems, float *out, cw_stream_t stream);
+
+/* ---- dense quantized matmul ------------------------------------------------------------- */
+
+/* y[m][n] = x[m][k] . W[n][k]^T for a quantized W; the QMatMul::forward contract
+ * (vendor/candle-core/src/quantized/mod.rs:1206-1345 with the Metal dispatch of
+ * quantized/metal.rs:359-470, call_quantized_matmul_mv_t / _mm_t in
+ * vendor/candle-metal-kernels/src/kernels/quantized.rs:32-43, 198-213).
+ * ws may be NULL when cw_qmatmul_workspace_size returns 0. */
+size_t cw_qmatmul_workspace_size(int dtype, int64_t n, int64_t k, int64_t m);
+int cw_qmatmul(int dtype, const void *w, int64_t n, int64_t k, const float *x, int64_t m,
+               float *y, void *ws, size_t ws_bytes, cw_stream_t stream);
+
+/* ---- routing ---------------------------------------------------------------------------- */
+
+/* Softmax over E logits per token, the K likeliest experts best first (ties to the lowest
+ * index), their probabilities renormalised over the K when norm != 0.
+ * ids[T][K] u32, w[T][K] f32. E <= 1024, K <= 32.
+ * Replaces experts::route (crates/engine/src/experts.rs:2364-2372) and the fused cw_route
+ * (crates/engine/src/fuse_kernel.rs:20-75, 347-352), whose limits were E <= 256, K <= 16. */
+int cw_route_topk(const float *logits, int T, int E, int K, int norm, uint32_t *ids, float *w,
+                  cw_stream_t stream);
+
+/* ---- expert matvec ---------------------------------------------------------------------- */
+
+/* For each token t < T and pick j < K: out[t][j][0..n) = W[s] . x_row, with s = ids[t][j] a
+ * slot index, W[s] the n x k matrix at bank + s * slot_stride bytes, and x_row = x[t]
+ * (x_rows_per_expert == 0) or x[t*K + j] (!= 0). Ids >= n_slots are rejected on the device
+ * (the output row is set to NaN and the call still completes).
+ * Replaces MoeMatvec (crates/engine/src/experts.rs:2183-2309) and its launchers
+ * mv_id::matvec_id / matvec_id_new (crates/engine/src/mv_id.rs:17-31, 158-171). */
+int cw_matvec_id(int dtype, int64_t n, int64_t k, int64_t n_slots, int64_t slot_stride,
+                 const void *bank, const float *x, int x_rows_per_expert, const uint32_t *ids,
+                 int K, int T, float *out, cw_stream_t stream);
+
+/* ---- activations and combine ------------------------------------------------------------ */
+
+/* h = silu(g) * u elementwise (cw_silu_mul, crates/engine/src/fuse_kernel.rs:77-85). */
+int cw_swiglu(const float *g, const float *u, float *h, int64_t n, cw_stream_t stream);
+
+/* gpt-oss clamped SwiGLU on rows of `width` (ExpertAct::ClampedSwiglu::hidden,
+ * crates/engine/src/experts.rs:2384-2404): g += gate_b[ids[r]], u += up_b[ids[r]],
+ * g = min(g, limit), u = clamp(u, -limit, limit), h = (u + 1) * g * sigmoid(alpha * g); output
+ * rows are max(pad, width) wide with zeros past width. Biases are (E x width) or NULL. */
+int cw_clamped_swiglu(const float *g, const float *u, const float *gate_b, const float *up_b,
+                      const uint32_t *ids, int64_t rows, int width, int pad, float alpha,
+                      float limit, float *h, cw_stream_t stream);
+
+/* out[t][:] = sum_j w[t][j] * (down[t][j][:] + (down_b ? down_b[ids[t][j]][:] : 0)), summed in
+ * pick order. Replaces cw_weighted_sum (crates/engine/src/fuse_kernel.rs:277-291, 377-398) and
+ * ExpertAct::finish (crates/engine/src/experts.rs:2412-2415); ids may be NULL without down_b. */
+int cw_weighted_sum(const float *down, const float *w, const float *down_b, const uint32_t *ids,
+                    int T, int K, int H, float *out, cw_stream_t stream);
+
+/* ---- bank slot table -------------------------------------------------------------------- */
+
+/* slots[i] = table[ids[i]]; a CW_NO_SLOT entry resolves to slot 0 and adds 1 to *missing
+ * (device u32; the caller zeroes it). Replaces coachwhip_resolve
+ * (crates/engine/src/gpu_sync.rs:49-66, op 262-293). */
+int cw_slots_resolve(const uint32_t *ids, const uint32_t *table, int n, uint32_t *slots,
+                     uint32_t *missing, cw_stream_t stream);
+
+/* ---- the MoE layer ---------------------------------------------------------------------- */
+
+/* One MoE layer's experts. Matrices are slot-major as GGUF stores ffn_{gate,up,down}_exps:
+ * gate and up are [slots][inter][hidden], down is [slots][hidden][max(pad, inter)]. */
+typedef struct cw_moe_desc {
+    int n_experts;           /* E: router width */
+    int top_k;               /* K */
+    int hidden;              /* h */
+    int inter;               /* I: expert FFN width */
+    int norm;                /* renormalise the K weights */
+    int act;                 /* enum cw_act */
+    float alpha, limit;      /* clamped SwiGLU constants (1.702, 7; model_gptoss.rs:16-17) */
+    int pad;                 /* width down reads, >= inter; 0 = inter */
+    int dtype[3];            /* gate, up, down */
+    const void *w[3];        /* device bank of each matrix */
+    int64_t slot_stride[3];  /* bytes per slot */
+    const float *bias[3];    /* gate_b, up_b (E x inter), down_b (E x hidden), or NULL */
+    const uint32_t *slot_table; /* device expert -> slot map (CW_NO_SLOT = absent), or NULL
+                                   when slot == expert (all experts resident) */
+    int n_slots;             /* slots per bank (= n_experts when slot_table is NULL) */
+} cw_moe_desc;
+
+/* out[T][hidden] = the resident MoE layer for T tokens: route the logits, gate and up
+ * matvecs over the picked experts' slots, the activation, down, the weighted combine.
+ * Replaces StreamedMoe::forward's resident branch (crates/engine/src/experts.rs:2562-2614)
+ * and its bank branch with a slot map (3003-3015, with coachwhip_resolve). When slot_table is
+ * set, picks whose expert has no slot read slot 0 and are counted in *missing (device u32,
+ * may be NULL). ids_out / w_out (T x K, device, may be NULL) receive the routing. */
+size_t cw_moe_workspace_size(const cw_moe_desc *desc, int T);
+int cw_moe_layer(const cw_moe_desc *desc, const float *x, const float *logits, int T, float *out,
+                 uint32_t *ids_out, float *w_out, uint32_t *missing, void *ws, size_t ws_bytes,
+                 cw_stream_t stream);
+
+/* ---- host bank bookkeeping (no GPU) ----------------------------------------------------- */
+
+/* The expert bank's slot bookkeeping without its memory: Slots in
+ * crates/engine/src/experts.rs:84-286 (new 222-224, assign 227-248, release 251-258,
+ * pop 261-269, reserve 273-285). A handle is owned by one thread at a time.
+ * `ready` is a host array of n_slots flags (NULL = every slot ready). */
+typedef struct cw_slots cw_slots;
+cw_slots *cw_slots_new(int n_slots);
+void cw_slots_free(cw_slots *s);
+/* Returns 1 and fills hit/miss lists ((expert, slot) pairs, host arrays sized n_needed) and
+ * *prefetch_hits on success; 0 and no change when too few slots are free (the caller then reads
+ * the experts fresh); -1 on a bad argument. */
+int cw_slots_assign(cw_slots *s, const uint32_t *needed, int n_needed, const uint8_t *ready,
+                    uint32_t *hits, int *n_hits, uint32_t *misses, int *n_misses,
+                    uint64_t *prefetch_hits);
+void cw_slots_release(cw_slots *s, uint32_t expert);
+void cw_slots_pop(cw_slots *s, const uint32_t *used, int n);
+/* Reserves slots for predicted experts not yet held; returns how many (expert, slot) pairs
+ * were written to out (sized n_predicted). */
+int cw_slots_reserve(cw_slots *s, const uint32_t *predicted, int n_predicted,
+                     const uint8_t *ready, uint32_t *out);
+/* Introspection for tests: holder of a slot (CW_NO_SLOT if empty), slot of an expert
+ * (-1 if absent), the LRU order (least recent first, n_slots entries), prefetched flag. */
+uint32_t cw_slots_holder(const cw_slots *s, int slot);
+int cw_slots_slot_of(const cw_slots *s, uint32_t expert);
+void cw_slots_lru(const cw_slots *s, int *order);
+int cw_slots_is_prefetched(const cw_slots *s, uint32_t expert);
+/* Writes the expert -> slot table for experts [0, n_experts) (CW_NO_SLOT when absent), the
+ * host image of Bank::sync_table (crates/engine/src/experts.rs:73-81). */
+void cw_slots_table(const cw_slots *s, uint32_t *table, int n_experts);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -13,7 +13,8 @@ REF_METAL = "/root/reference/vendor/candle-metal-kernels/src/metal_src/quantized
 def _parse_header():
     text = open(HEADER).read()
     out = {}
-    for ctype, name, size, body in re.findall(r"static const (\w+) cw_(\w+)\[(\d+)\] = \{(.*?)\};", text, re.S):
+    for ctype, name, size, macro in re.findall(r"static const (\w+) cw_(\w+)\[(\d+)\] = \{(\w+)\};", text):
+        body = re.search(r"#define %s \\(.*?)\n\n" % macro, text, re.S).group(1)
         vals = [int(v.rstrip("ul"), 16) for v in re.findall(r"0x[0-9a-f]+u?l*", body)]
         assert len(vals) == int(size)
         out[name] = np.array(vals, dtype=np.uint64 if ctype == "uint64_t" else np.uint32)

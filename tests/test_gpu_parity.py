@@ -1,0 +1,254 @@
+"""HIP path vs the CPU oracle on the same seeded inputs, through the C ABI.
+
+Gates (tolerances stated per test): dequantized weights bit-exact; routing ids identical and
+weights within 1e-5; matmul / matvec / MoE outputs within 1e-3 relative L2 of the f64 oracle
+(the f32 kernels land near 1e-6, which the tighter f32 checks below also hold them to)."""
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+import coachwhip_amd as cw
+from coachwhip_amd import formats as F
+from coachwhip_amd import ops, synth
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+REL_L2_GATE = 1e-3      # north-star tolerance for matmul / MoE outputs
+REL_L2_F32 = 2e-5       # what an f32-activation path must reach
+
+
+def dev(a):
+    return ops.to_device(a)
+
+
+def host(t):
+    return t.detach().cpu().numpy()
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+# ------------------------------------------------------------------------------ dequantize
+
+@pytest.mark.parametrize("dtype", F.WEIGHT_TYPES)
+def test_dequantize_is_bit_exact(dtype):
+    say("dequantize", F.NAMES[dtype])
+    rng = np.random.default_rng(1000 + dtype)
+    n = 256 * 1024
+    raw = synth.random_blocks(dtype, n, rng)
+    # scale edge cases: negative and subnormal f16 scales, every e8m0 exponent
+    if dtype == F.MXFP4:
+        nb = n // 32
+        raw.reshape(nb, 17)[:256, 0] = np.arange(256, dtype=np.uint8)
+    else:
+        ts = F.type_size(dtype)
+        nb = n // F.block_size(dtype)
+        edge = np.array([0x8001, 0x0001, 0x03FF, 0xBC00, 0x7BFF, 0x0000], dtype=np.uint16).view(np.uint8).reshape(-1, 2)
+        raw.reshape(nb, ts)[:len(edge), 0:2] = edge
+    got = host(ops.dequantize(dtype, dev(raw), n))
+    want = O.dequantize(dtype, raw, n)
+    if dtype == F.MXFP4:
+        # e = 255 overflows to inf in both; compare the bit patterns of everything
+        pass
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+# ------------------------------------------------------------------------------ dense matvec
+
+QMM_CASES = [
+    (F.Q8_0, 2048, 2048, 1),      # config 1
+    (F.Q4_K, 4096, 4096, 1),      # config 2, M = 1
+    (F.Q4_K, 4096, 4096, 16),     # config 2, M = 16
+    (F.MXFP4, 512, 2880, 2),      # gpt-oss rows (90 blocks: two sub-blocks on some lanes)
+    (F.IQ2_XXS, 512, 2048, 3),
+    (F.IQ2_S, 2048, 512, 3),
+    (F.IQ3_S, 512, 2048, 2),
+    (F.Q8_0, 96, 64, 5),          # short rows: 2 blocks, 8 lanes per row
+    (F.Q4_K, 33, 256, 1),         # one super-block per row, ragged row count
+]
+
+
+@pytest.mark.parametrize("dtype,n,k,m", QMM_CASES)
+def test_qmatmul_matches_the_oracle(dtype, n, k, m):
+    say("qmatmul", F.NAMES[dtype], n, k, m)
+    rng = np.random.default_rng(n * 7 + k + m)
+    raw = synth.random_blocks(dtype, n * k, rng)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    y = host(ops.QMatMul(ops.QTensor.from_blocks(raw, dtype, (n, k))).forward(dev(x)))
+    want = O.qmatmul_f64(dtype, raw, n, k, x)
+    err = O.rel_l2(y, want)
+    say("  rel_l2", err)
+    assert err <= REL_L2_GATE and err <= REL_L2_F32
+
+
+def test_qmatmul_rejects_bad_shapes():
+    qt = ops.QTensor.from_blocks(np.zeros(34 * 2, np.uint8), F.Q8_0, (1, 64))
+    with pytest.raises(cw.CwError):
+        ops.QMatMul(qt).forward(torch.zeros((2, 32), device="cuda"))
+
+
+# ------------------------------------------------------------------------------ expert matvec
+
+@pytest.mark.parametrize("dtype,n,k", [(F.IQ2_XXS, 512, 2048), (F.IQ2_S, 2048, 512), (F.Q4_K, 512, 2048),
+                                       (F.IQ3_S, 512, 2048), (F.MXFP4, 256, 2880), (F.Q8_0, 128, 1024)])
+@pytest.mark.parametrize("rows_per_expert", [False, True])
+def test_matvec_id_matches_the_oracle(dtype, n, k, rows_per_expert):
+    say("matvec_id", F.NAMES[dtype], n, k, rows_per_expert)
+    rng = np.random.default_rng(dtype * 31 + n)
+    slots, T, K = 12, 3, 4
+    raw = synth.random_blocks(dtype, slots * n * k, rng)
+    bank = ops.ExpertBank.from_blocks(raw, dtype, n, k, slots)
+    ids = rng.integers(0, slots, size=(T, K), dtype=np.uint32)
+    x = rng.standard_normal((T * K if rows_per_expert else T, k)).astype(np.float32)
+    out = host(ops.MoeMatvec(bank, K, rows_per_expert).forward(dev(x), dev(ids)))
+    want = O.matvec_id(dtype, n, k, raw, bank.slot_stride, x, ids, rows_per_expert)
+    err = O.rel_l2(out, want)
+    say("  rel_l2", err)
+    assert err <= REL_L2_F32
+
+
+def test_matvec_id_marks_out_of_range_slots():
+    rng = np.random.default_rng(2)
+    raw = synth.random_blocks(F.Q8_0, 2 * 8 * 64, rng)
+    bank = ops.ExpertBank.from_blocks(raw, F.Q8_0, 8, 64, 2)
+    ids = np.array([[0, 5]], dtype=np.uint32)
+    out = host(ops.MoeMatvec(bank, 2, False).forward(dev(rng.standard_normal((1, 64)).astype(np.float32)), dev(ids)))
+    assert np.all(np.isfinite(out[0, 0])) and np.all(np.isnan(out[0, 1]))
+
+
+# ------------------------------------------------------------------------------ routing
+
+def test_route_reference_known_answers():
+    # crates/engine/tests/router.rs:20-30, 56-60
+    ids, _ = ops.route(dev(np.array([[0.1, 3.0, 2.0, -1.0, 1.0]], np.float32)), 3, True)
+    assert host(ids).tolist() == [[1, 2, 4]]
+    ids, _ = ops.route(dev(np.array([[5.0, 0.0, 1.0, 2.0], [0.0, 1.0, 9.0, 3.0]], np.float32)), 2, True)
+    assert host(ids).tolist() == [[0, 3], [2, 3]]
+    _, w = ops.route(dev(np.array([[0.0, 4.0, 1.0, 2.0, 3.0]], np.float32)), 4, True)
+    w = host(w)[0]
+    assert all(a >= b for a, b in zip(w, w[1:]))
+    ids, _ = ops.route(dev(np.array([[1.0, 2.0, 2.0, 0.0, 2.0]], np.float32)), 3, False)
+    assert host(ids).tolist() == [[1, 2, 4]]
+
+
+@pytest.mark.parametrize("E,K,norm", [(256, 8, True), (128, 4, True), (512, 10, True), (1024, 32, False), (20, 20, True)])
+def test_route_matches_the_oracle(E, K, norm):
+    rng = np.random.default_rng(E + K)
+    T = 200
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    assert not synth.near_ties_within_top_k(logits, K)
+    ids, w = ops.route(dev(logits), K, norm)
+    wids, ww = O.route(logits, K, norm)
+    assert np.array_equal(host(ids).view(np.uint32), wids)
+    assert np.max(np.abs(host(w) - ww)) < 1e-5
+
+
+# ------------------------------------------------------------------------------ elementwise
+
+def test_activations_combine_and_resolve_match_the_oracle():
+    rng = np.random.default_rng(8)
+    g = (rng.standard_normal((64, 96)) * 6).astype(np.float32)
+    u = (rng.standard_normal((64, 96)) * 6).astype(np.float32)
+    h = host(ops.swiglu(dev(g), dev(u)))
+    assert np.allclose(h, O.silu_mul(g, u), rtol=2e-6, atol=1e-6)
+    ids = rng.integers(0, 5, size=64, dtype=np.uint32)
+    gb = rng.normal(0, 0.5, (5, 96)).astype(np.float32)
+    ub = rng.normal(0, 0.5, (5, 96)).astype(np.float32)
+    hc = host(ops.clamped_swiglu(dev(g), dev(u), dev(gb), dev(ub), dev(ids), pad=128))
+    assert np.allclose(hc, O.clamped_swiglu(g, u, gb, ub, ids, pad=128), rtol=2e-6, atol=1e-6)
+    down = rng.standard_normal((6, 4, 80)).astype(np.float32)
+    wts = rng.random((6, 4)).astype(np.float32)
+    assert np.allclose(host(ops.weighted_sum(dev(down), dev(wts))), O.weighted_sum(down, wts), rtol=1e-6, atol=1e-6)
+    table = np.array([3, 0xFFFFFFFF, 1, 0xFFFFFFFF, 2], dtype=np.uint32)
+    pick = np.array([[0, 1], [2, 3], [4, 0]], dtype=np.uint32)
+    slots, missing = ops.slots_resolve(dev(pick), dev(table))
+    ws, wm = O.resolve(pick, table)
+    assert host(slots).view(np.uint32).reshape(-1).tolist() == ws.tolist() and int(host(missing)[0]) == wm
+
+
+# ------------------------------------------------------------------------------ MoE layer
+
+def upload_layer(layer, slot_table=None):
+    banks = []
+    shapes = [(layer.inter, layer.hidden), (layer.inter, layer.hidden), (layer.hidden, max(layer.pad, layer.inter))]
+    for m in range(3):
+        n, k = shapes[m]
+        banks.append(ops.ExpertBank.from_blocks(layer.host[m], layer.dtypes[m], n, k, layer.n_slots))
+    act = ops.ExpertAct.silu()
+    if layer.act == 1:
+        act = ops.ExpertAct.clamped_swiglu(layer.alpha, layer.limit, *[dev(b) for b in layer.bias], pad=layer.pad)
+    table = None if slot_table is None else dev(slot_table)
+    return ops.MoeLayer(*banks, n_experts=layer.n_experts, top_k=layer.top_k, norm_topk_prob=layer.norm, act=act,
+                        slot_table=table)
+
+
+MOE_CASES = [
+    # name, E, K, h, I, dtypes, act, pad, T
+    ("c3_decode", 256, 8, 2048, 512, (F.IQ2_XXS, F.IQ2_XXS, F.IQ2_S), 0, 0, 1),
+    ("c3_tokens", 256, 8, 2048, 512, (F.IQ2_XXS, F.IQ2_XXS, F.IQ2_S), 0, 0, 24),
+    ("c3_mixed_gate_up", 64, 8, 2048, 512, (F.IQ2_XXS, F.IQ2_S, F.IQ2_S), 0, 0, 3),
+    ("c4_decode_shape", 16, 4, 2880, 2880, (F.MXFP4, F.MXFP4, F.MXFP4), 1, 0, 1),
+    ("c4_padded", 16, 4, 1024, 720, (F.MXFP4, F.MXFP4, F.Q4_K), 1, 768, 5),
+]
+
+
+@pytest.mark.parametrize("name,E,K,h,I,dts,act,pad,T", MOE_CASES, ids=[c[0] for c in MOE_CASES])
+def test_moe_layer_matches_the_oracle(name, E, K, h, I, dts, act, pad, T):
+    say("moe", name)
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    layer = synth.moe_weights(E, K, h, I, dts, rng, act=act, pad=pad)
+    x = rng.standard_normal((T, h)).astype(np.float32)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    assert not synth.near_ties_within_top_k(logits, K)
+    moe = upload_layer(layer)
+    out, ids, w = moe.forward(dev(x), dev(logits))
+    want, wids, ww, _ = O.moe_layer(layer, x, logits)
+    assert np.array_equal(host(ids).view(np.uint32), wids)
+    assert np.max(np.abs(host(w) - ww)) < 1e-5
+    err = O.rel_l2(host(out), want)
+    say("  rel_l2", err)
+    assert err <= REL_L2_GATE and err <= REL_L2_F32
+
+
+def test_moe_layer_through_a_slot_table():
+    # config 5's shape on one layer: 512 experts, top-10, 56 resident slots, IQ3_S / Q4_K mix
+    say("moe bank")
+    rng = np.random.default_rng(55)
+    E, K, slots = 512, 10, 56
+    layer = synth.moe_weights(E, K, 2048, 512, (F.IQ3_S, F.IQ3_S, F.Q4_K), rng, n_slots=slots)
+    table = np.full(E, 0xFFFFFFFF, dtype=np.uint32)
+    resident = rng.choice(E, size=slots, replace=False)
+    table[resident] = rng.permutation(slots).astype(np.uint32)
+    mask = np.full(E, -1e30, dtype=np.float32)
+    mask[resident] = 0.0
+    x = rng.standard_normal((2, 2048)).astype(np.float32)
+    logits = rng.standard_normal((2, E)).astype(np.float32) + mask
+    moe = upload_layer(layer, slot_table=table)
+    missing = torch.zeros(1, dtype=torch.int32, device="cuda")
+    out, ids, w = moe.forward(dev(x), dev(logits), missing=missing)
+    want, wids, ww, wmiss = O.moe_layer(layer, x, logits, slot_table=table, n_slots=slots)
+    assert wmiss == 0 and int(host(missing)[0]) == 0
+    assert np.array_equal(host(ids).view(np.uint32), wids)
+    assert O.rel_l2(host(out), want) <= REL_L2_F32
+    # unmasked logits pick absent experts: they read slot 0 and are counted, as the oracle does
+    logits2 = rng.standard_normal((2, E)).astype(np.float32)
+    missing.zero_()
+    out2, _, _ = moe.forward(dev(x), dev(logits2), missing=missing)
+    want2, _, _, wmiss2 = O.moe_layer(layer, x, logits2, slot_table=table, n_slots=slots)
+    assert int(host(missing)[0]) == wmiss2 > 0
+    assert O.rel_l2(host(out2), want2) <= REL_L2_F32
+
+
+def test_moe_layer_output_is_deterministic():
+    rng = np.random.default_rng(77)
+    layer = synth.moe_weights(64, 8, 2048, 512, (F.IQ2_XXS, F.IQ2_XXS, F.IQ2_S), rng)
+    moe = upload_layer(layer)
+    x = dev(rng.standard_normal((4, 2048)).astype(np.float32))
+    lg = dev(rng.standard_normal((4, 64)).astype(np.float32))
+    a = host(moe.forward(x, lg)[0])
+    b = host(moe.forward(x, lg)[0])
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
