@@ -79,7 +79,6 @@ def main():
 
     # parity of layer 0, step 0 against the CPU oracle (picked experts only travel to the host)
     log("parity check against the CPU oracle")
-    sys.path.insert(0, os.path.join(root, "oracle"))
     from oracle import oracle as O
     out0, ids0, w0 = layers[0].forward(x_all[0], logits_all[0, 0])
     torch.cuda.synchronize()

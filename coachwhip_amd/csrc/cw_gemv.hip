@@ -1,8 +1,8 @@
 // Dequantize and matrix-vector kernels over raw GGUF blocks (gfx950, wave64).
 //
-// One kernel template, k_gemv, serves the dense quantized matvec (QMatMul at small M), the
-// expert matvec over a bank of slots (MoeMatvec), the fused gate/up matvec with its activation,
-// and the fused down matvec with the weighted combine of the picks:
+// One kernel template, k_gemv, serves the dense quantized matvec (QMatMul at small M) and the
+// expert matvec over a bank of slots (MoeMatvec); the fused MoE-layer kernels live in
+// cw_moe_fused.hip:
 //
 //  - A row of k weights is nsb = k/32 sub-blocks. LPR lanes of a wavefront share one row
 //    (LPR = 8, 16, 32 or 64, the smallest power of two >= nsb, capped at 64) and lane l always
@@ -16,8 +16,6 @@
 #include "cw_gemv.h"
 
 namespace cw {
-
-enum { MODE_PLAIN = 0, MODE_GATEUP = 1, MODE_DOWN = 2 };
 
 template <int NX>
 __device__ __forceinline__ void load_x(float (&xr)[NX][32], const float *xrow, int sub, int lpr, int nsb) {
@@ -45,8 +43,6 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
-__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
-
 template <class Fmt, int LPR, int NX>
 __device__ __forceinline__ float row_dot(const uint8_t *row, const void *lds, const float (&xr)[NX][32], int sub, int nsb) {
     float acc = 0.f;
@@ -58,93 +54,28 @@ __device__ __forceinline__ float row_dot(const uint8_t *row, const void *lds, co
     return acc;
 }
 
-// PLAIN / GATEUP: blockIdx.y = pick p; the block's waves stride over the n rows.
-// DOWN: blockIdx.y = token t; the block owns a tile of rows and every pick of the token; waves
-// split the picks, each pick's partial dots land in LDS and are combined in pick order.
-template <class Fmt, int LPR, int NX, int MODE>
+// blockIdx.y = pick p (a token of a dense matmul, or a (token, expert pick) of an expert
+// matvec); the block's waves stride over the n rows of that pick's matrix.
+template <class Fmt, int LPR, int NX>
 __global__ __launch_bounds__(256) void k_gemv(const GemvArgs a) {
     __shared__ __align__(16) uint8_t lds[Fmt::LDS_BYTES > 0 ? Fmt::LDS_BYTES : 16];
-    Fmt::fill_lds(lds, threadIdx.x, blockDim.x);
-    if (Fmt::LDS_BYTES > 0) __syncthreads();
-
     constexpr int RPW = 64 / LPR;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
     const int sub = lane % LPR, rsub = lane / LPR;
     const int p = blockIdx.y;
+    const uint32_t slot = a.ids ? a.ids[p] : 0u;
+    const bool bad = slot >= (uint32_t)a.n_slots;
     float xr[NX][32];
-
-    if constexpr (MODE != MODE_DOWN) {
-        const uint32_t slot = a.ids ? a.ids[p] : 0u;
-        const bool bad = slot >= (uint32_t)a.n_slots;
-        const float *xrow = a.x + (int64_t)(a.x_per_pick ? p : p / a.K) * a.k;
-        load_x<NX>(xr, xrow, sub, LPR, a.nsb);
-        const uint8_t *base0 = a.w0 + (int64_t)(bad ? 0 : slot) * a.slot_stride0;
-        const uint8_t *base1 = a.w1 + (int64_t)(bad ? 0 : slot) * a.slot_stride1;
-        const uint32_t expert = a.experts ? a.experts[p] : 0u;
-        for (int r0 = (blockIdx.x * nwaves + wave) * RPW; r0 < a.n; r0 += gridDim.x * nwaves * RPW) {
-            const int r = r0 + rsub;
-            const bool rv = r < a.n;
-            float g = 0.f, u = 0.f;
-            if (rv) {
-                g = row_dot<Fmt, LPR, NX>(base0 + (int64_t)r * a.row_bytes, lds, xr, sub, a.nsb);
-                if constexpr (MODE == MODE_GATEUP) u = row_dot<Fmt, LPR, NX>(base1 + (int64_t)r * a.row_bytes, lds, xr, sub, a.nsb);
-            }
-            g = group_sum<LPR>(g);
-            if constexpr (MODE == MODE_GATEUP) u = group_sum<LPR>(u);
-            if (sub == 0 && rv) {
-                float o;
-                if constexpr (MODE == MODE_GATEUP) {
-                    if (a.act == CW_ACT_SILU) {
-                        o = silu(g) * u;
-                    } else {
-                        if (a.b0) g += a.b0[(int64_t)expert * a.n + r];
-                        if (a.b1) u += a.b1[(int64_t)expert * a.n + r];
-                        g = fminf(g, a.limit);
-                        u = fminf(fmaxf(u, -a.limit), a.limit);
-                        o = (u + 1.0f) * (g * (1.0f / (1.0f + expf(-(g * a.alpha)))));
-                    }
-                } else {
-                    o = g;
-                }
-                a.out[(int64_t)p * a.out_width + r] = bad ? __int_as_float(0x7fc00000) : o;
-            }
-        }
-        if constexpr (MODE == MODE_GATEUP) {
-            // zero padding of the hidden row up to the width down reads
-            for (int c = a.n + blockIdx.x * blockDim.x + threadIdx.x; c < a.out_width; c += gridDim.x * blockDim.x)
-                a.out[(int64_t)p * a.out_width + c] = 0.f;
-        }
-    } else {
-        // a.tile rows per block, K picks; part[j][r] in LDS
-        extern __shared__ float part[];
-        const int t = p;
-        const int r_begin = blockIdx.x * a.tile;
-        const int r_end = min(r_begin + a.tile, a.n);
-        for (int j = wave; j < a.K; j += nwaves) {
-            const int pick = t * a.K + j;
-            const uint32_t slot = a.ids[pick];
-            const bool bad = slot >= (uint32_t)a.n_slots;
-            load_x<NX>(xr, a.x + (int64_t)pick * a.k, sub, LPR, a.nsb);
-            const uint8_t *base = a.w0 + (int64_t)(bad ? 0 : slot) * a.slot_stride0;
-            for (int r0 = r_begin; r0 < r_end; r0 += RPW) {
-                const int r = r0 + rsub;
-                float d = 0.f;
-                if (r < r_end) d = row_dot<Fmt, LPR, NX>(base + (int64_t)r * a.row_bytes, lds, xr, sub, a.nsb);
-                d = group_sum<LPR>(d);
-                if (sub == 0 && r < r_end) part[j * a.tile + (r - r_begin)] = bad ? __int_as_float(0x7fc00000) : d;
-            }
-        }
-        __syncthreads();
-        for (int r = r_begin + threadIdx.x; r < r_end; r += blockDim.x) {
-            float acc = 0.f;
-            for (int j = 0; j < a.K; j++) {
-                const int pick = t * a.K + j;
-                float d = part[j * a.tile + (r - r_begin)];
-                if (a.bd) d += a.bd[(int64_t)a.experts[pick] * a.n + r];
-                acc += a.wts[pick] * d;
-            }
-            a.out[(int64_t)t * a.n + r] = acc;
-        }
+    load_x<NX>(xr, a.x + (int64_t)(a.x_per_pick ? p : p / a.K) * a.k, sub, LPR, a.nsb);
+    Fmt::fill_lds(lds, threadIdx.x, blockDim.x);
+    if (Fmt::LDS_BYTES > 0) __syncthreads();
+    const uint8_t *base = a.w0 + (int64_t)(bad ? 0 : slot) * a.slot_stride0;
+    for (int r0 = (blockIdx.x * nwaves + wave) * RPW; r0 < a.n; r0 += gridDim.x * nwaves * RPW) {
+        const int r = r0 + rsub;
+        float g = 0.f;
+        if (r < a.n) g = row_dot<Fmt, LPR, NX>(base + (int64_t)r * a.row_bytes, lds, xr, sub, a.nsb);
+        g = group_sum<LPR>(g);
+        if (sub == 0 && r < a.n) a.out[(int64_t)p * a.out_width + r] = bad ? __int_as_float(0x7fc00000) : g;
     }
 }
 
@@ -173,27 +104,26 @@ static int pick_lpr(int nsb) {
     return l;
 }
 
-template <class Fmt, int MODE>
+template <class Fmt>
 static int launch_lpr(const GemvArgs &a, dim3 grid, int threads, size_t shmem, hipStream_t s) {
     const int lpr = pick_lpr(a.nsb);
     const int nx = (a.nsb + lpr - 1) / lpr;
 #define CW_GEMV_CASE(L, X) \
-    if (lpr == L && nx == X) { hipLaunchKernelGGL((k_gemv<Fmt, L, X, MODE>), grid, dim3(threads), shmem, s, a); return check_launch("k_gemv"); }
+    if (lpr == L && nx == X) { hipLaunchKernelGGL((k_gemv<Fmt, L, X>), grid, dim3(threads), shmem, s, a); return check_launch("k_gemv"); }
     CW_GEMV_CASE(8, 1) CW_GEMV_CASE(16, 1) CW_GEMV_CASE(32, 1) CW_GEMV_CASE(64, 1)
     CW_GEMV_CASE(64, 2) CW_GEMV_CASE(64, 3) CW_GEMV_CASE(64, 4)
 #undef CW_GEMV_CASE
     return set_error(CW_ENOTSUP, "gemv: rows of %d weights exceed the %d-weight limit", a.k, 64 * 4 * 32);
 }
 
-template <int MODE>
 static int launch_fmt(int dtype, const GemvArgs &a, dim3 grid, int threads, size_t shmem, hipStream_t s) {
     switch (dtype) {
-    case CW_Q8_0: return launch_lpr<FQ8_0, MODE>(a, grid, threads, shmem, s);
-    case CW_Q4_K: return launch_lpr<FQ4_K, MODE>(a, grid, threads, shmem, s);
-    case CW_MXFP4: return launch_lpr<FMXFP4, MODE>(a, grid, threads, shmem, s);
-    case CW_IQ2_XXS: return launch_lpr<FIQ2_XXS, MODE>(a, grid, threads, shmem, s);
-    case CW_IQ2_S: return launch_lpr<FIQ2_S, MODE>(a, grid, threads, shmem, s);
-    case CW_IQ3_S: return launch_lpr<FIQ3_S, MODE>(a, grid, threads, shmem, s);
+    case CW_Q8_0: return launch_lpr<FQ8_0>(a, grid, threads, shmem, s);
+    case CW_Q4_K: return launch_lpr<FQ4_K>(a, grid, threads, shmem, s);
+    case CW_MXFP4: return launch_lpr<FMXFP4>(a, grid, threads, shmem, s);
+    case CW_IQ2_XXS: return launch_lpr<FIQ2_XXS>(a, grid, threads, shmem, s);
+    case CW_IQ2_S: return launch_lpr<FIQ2_S>(a, grid, threads, shmem, s);
+    case CW_IQ3_S: return launch_lpr<FIQ3_S>(a, grid, threads, shmem, s);
     default: return set_error(CW_ENOTSUP, "gemv: dtype %d is not supported", dtype);
     }
 }
@@ -209,25 +139,7 @@ static dim3 rows_grid(const GemvArgs &a, int picks) {
 
 int gemv_plain(int dtype, const GemvArgs &a, int picks, hipStream_t s) {
     if (picks == 0 || a.n == 0) return CW_OK;
-    return launch_fmt<MODE_PLAIN>(dtype, a, rows_grid(a, picks), 256, 0, s);
-}
-
-int gemv_gateup(int dtype, const GemvArgs &a, int picks, hipStream_t s) {
-    if (picks == 0) return CW_OK;
-    return launch_fmt<MODE_GATEUP>(dtype, a, rows_grid(a, picks), 256, 0, s);
-}
-
-int gemv_down(int dtype, GemvArgs a, int tokens, hipStream_t s) {
-    if (tokens == 0 || a.n == 0) return CW_OK;
-    const int lpr = pick_lpr(a.nsb);
-    // a tile of rows per block, sized so a decode step still spreads over the chip
-    int tile = 4 * (64 / lpr);
-    while (tile < 64 && (int64_t)((a.n + 2 * tile - 1) / (2 * tile)) * tokens >= 1024) tile *= 2;
-    a.tile = tile;
-    const size_t shmem = (size_t)a.K * tile * sizeof(float);
-    if (shmem > 64 * 1024) return set_error(CW_ENOTSUP, "gemv_down: %d picks x %d rows exceed LDS", a.K, tile);
-    dim3 grid((a.n + tile - 1) / tile, tokens);
-    return launch_fmt<MODE_DOWN>(dtype, a, grid, 256, shmem, s);
+    return launch_fmt(dtype, a, rows_grid(a, picks), 256, 0, s);
 }
 
 int dequantize(int dtype, const void *blocks, int64_t n_elems, float *out, hipStream_t s) {

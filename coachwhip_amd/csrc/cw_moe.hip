@@ -3,110 +3,23 @@
 
 #include "cw_common.h"
 #include "cw_gemv.h"
+#include "cw_moe_fused.h"
+#include "cw_wave.h"
 
 namespace cw {
 
-// ------------------------------------------------------------------------------ reductions
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-    return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    return v;
-}
-// (value, index) maximum; ties go to the lower index, exhausted candidates carry index ~0u
-__device__ __forceinline__ bool better(float va, uint32_t ia, float vb, uint32_t ib) {
-    if (ia == 0xFFFFFFFFu) return false;
-    if (ib == 0xFFFFFFFFu) return true;
-    return va > vb || (va == vb && ia < ib);
-}
-__device__ __forceinline__ void wave_argmax(float &v, uint32_t &i) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        float ov = __shfl_xor(v, off);
-        uint32_t oi = __shfl_xor(i, off);
-        if (better(ov, oi, v, i)) { v = ov; i = oi; }
-    }
-}
-
 // ------------------------------------------------------------------------------ router
 
-// One block of 256 threads per token; PER logits per thread (E <= 256 * PER).
-// Softmax as candle-nn's softmax_last_dim: max, exp of the differences, sum, divide. The K picks
-// are taken best first by logit (softmax is monotone, and comparing logits is exact), the lowest
-// index winning ties, which is the order of the stable descending argsort route() uses
-// (crates/engine/src/experts.rs:2364-2372, vendor/candle-core/src/sort.rs:40-53).
+// One wavefront per token (cw_wave.h: softmax, top-k on the logits, ties to the lower index).
 template <int PER>
-__global__ __launch_bounds__(256) void k_route(const float *logits, int E, int K, int norm, uint32_t *ids, float *w) {
-    __shared__ float red_v[4];
-    __shared__ uint32_t red_i[4];
-    __shared__ float pick_v[32];
-    __shared__ uint32_t pick_i[32];
-    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const float *x = logits + (int64_t)t * E;
-    float v[PER];
-    bool live[PER];
-#pragma unroll
-    for (int i = 0; i < PER; i++) {
-        int e = tid + 256 * i;
-        live[i] = e < E;
-        v[i] = live[i] ? x[e] : -INFINITY;
-    }
-    float m = v[0];
-#pragma unroll
-    for (int i = 1; i < PER; i++) m = fmaxf(m, v[i]);
-    m = wave_max(m);
-    if (lane == 0) red_v[wv] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(red_v[0], red_v[1]), fmaxf(red_v[2], red_v[3]));
-    __syncthreads();
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < PER; i++) s += live[i] ? expf(v[i] - m) : 0.f;
-    s = wave_sum(s);
-    if (lane == 0) red_v[wv] = s;
-    __syncthreads();
-    s = (red_v[0] + red_v[1]) + (red_v[2] + red_v[3]);
-    __syncthreads();
-    for (int j = 0; j < K; j++) {
-        float bv = -INFINITY;
-        uint32_t bi = 0xFFFFFFFFu;
-#pragma unroll
-        for (int i = 0; i < PER; i++) {
-            uint32_t e = (uint32_t)(tid + 256 * i);
-            if (live[i] && better(v[i], e, bv, bi)) { bv = v[i]; bi = e; }
-        }
-        wave_argmax(bv, bi);
-        if (lane == 0) { red_v[wv] = bv; red_i[wv] = bi; }
-        __syncthreads();
-        if (tid == 0) {
-            float b = red_v[0];
-            uint32_t ix = red_i[0];
-            for (int q = 1; q < 4; q++)
-                if (better(red_v[q], red_i[q], b, ix)) { b = red_v[q]; ix = red_i[q]; }
-            pick_v[j] = b;
-            pick_i[j] = ix;
-        }
-        __syncthreads();
-        const uint32_t won = pick_i[j];
-#pragma unroll
-        for (int i = 0; i < PER; i++)
-            if ((uint32_t)(tid + 256 * i) == won) live[i] = false;
-    }
-    if (tid == 0) {
-        float tot = 0.f;
-        for (int j = 0; j < K; j++) {
-            pick_v[j] = expf(pick_v[j] - m) / s;
-            tot += pick_v[j];
-        }
-        for (int j = 0; j < K; j++) {
-            ids[(int64_t)t * K + j] = pick_i[j];
-            w[(int64_t)t * K + j] = norm ? pick_v[j] / tot : pick_v[j];
-        }
+__global__ __launch_bounds__(64) void k_route(const float *logits, int E, int K, int norm, uint32_t *ids, float *w) {
+    const int t = blockIdx.x, lane = threadIdx.x;
+    uint32_t id;
+    float wt;
+    wave_route<PER>(logits + (int64_t)t * E, E, K, norm, &id, &wt);
+    if (lane < K) {
+        ids[(int64_t)t * K + lane] = id;
+        w[(int64_t)t * K + lane] = wt;
     }
 }
 
@@ -117,13 +30,19 @@ __global__ void k_swiglu(const float *g, const float *u, float *h, int64_t n) {
     }
 }
 
+// silu != 0: plain h = silu(g) * u with zero padding (the fallback of mixed gate/up formats)
 __global__ void k_clamped_swiglu(const float *g, const float *u, const float *gb, const float *ub, const uint32_t *ids,
-                                 int64_t rows, int width, int out_w, float alpha, float limit, float *h) {
+                                 int64_t rows, int width, int out_w, float alpha, float limit, float *h, int silu) {
     const int64_t n = rows * out_w;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
         const int64_t r = i / out_w;
         const int c = (int)(i % out_w);
         if (c >= width) { h[i] = 0.f; continue; }
+        if (silu) {
+            const float v = g[r * width + c];
+            h[i] = v / (1.0f + expf(-v)) * u[r * width + c];
+            continue;
+        }
         const uint32_t e = ids[r];
         float gv = g[r * width + c] + (gb ? gb[(int64_t)e * width + c] : 0.f);
         float uv = u[r * width + c] + (ub ? ub[(int64_t)e * width + c] : 0.f);
@@ -167,9 +86,8 @@ static dim3 flat_grid(int64_t n) {
 
 static int route(const float *logits, int T, int E, int K, int norm, uint32_t *ids, float *w, hipStream_t s) {
     if (T == 0) return CW_OK;
-    if (E <= 256) hipLaunchKernelGGL(k_route<1>, dim3(T), dim3(256), 0, s, logits, E, K, norm, ids, w);
-    else if (E <= 512) hipLaunchKernelGGL(k_route<2>, dim3(T), dim3(256), 0, s, logits, E, K, norm, ids, w);
-    else hipLaunchKernelGGL(k_route<4>, dim3(T), dim3(256), 0, s, logits, E, K, norm, ids, w);
+    if (E <= 256) hipLaunchKernelGGL(k_route<4>, dim3(T), dim3(64), 0, s, logits, E, K, norm, ids, w);
+    else hipLaunchKernelGGL(k_route<16>, dim3(T), dim3(64), 0, s, logits, E, K, norm, ids, w);
     return check_launch("k_route");
 }
 
@@ -235,82 +153,77 @@ static int moe_layer(const cw_moe_desc *d, const float *x, const float *logits, 
     CW_REQUIRE(ws && ws_bytes >= L.total, "moe: workspace of %zu bytes, %zu needed", ws_bytes, L.total);
     uint8_t *base = (uint8_t *)ws;
     const int K = d->top_k, P = d->pad > d->inter ? d->pad : d->inter;
-    uint32_t *ids = ids_out ? ids_out : (uint32_t *)(base + L.ids);
-    float *w = w_out ? w_out : (float *)(base + L.w);
-    if ((rc = route(logits, T, d->n_experts, K, d->norm, ids, w, s))) return rc;
-    const uint32_t *slots = ids;
-    const int n_slots = d->slot_table ? d->n_slots : d->n_experts;
-    if (d->slot_table) {
-        uint32_t *sl = (uint32_t *)(base + L.slots);
-        hipLaunchKernelGGL(k_resolve, flat_grid((int64_t)T * K), dim3(256), 0, s, ids, d->slot_table, T * K, sl, missing);
-        if ((rc = check_launch("k_resolve"))) return rc;
-        slots = sl;
-    }
-    float *h = (float *)(base + L.h);
 
-    GemvArgs a = {};
-    a.n = d->inter;
-    a.k = d->hidden;
-    a.nsb = d->hidden / 32;
-    a.n_slots = n_slots;
-    a.x = x;
-    a.x_per_pick = 0;
-    a.ids = slots;
-    a.experts = ids;
+    MoeArgs a = {};
+    a.wg = (const uint8_t *)d->w[0];
+    a.wu = (const uint8_t *)d->w[1];
+    a.wd = (const uint8_t *)d->w[2];
+    a.sg = d->slot_stride[0];
+    a.su = d->slot_stride[1];
+    a.sd = d->slot_stride[2];
+    a.rbg = (int64_t)(d->hidden / cw_block_size(d->dtype[0])) * cw_type_size(d->dtype[0]);
+    a.rbd = (int64_t)(P / cw_block_size(d->dtype[2])) * cw_type_size(d->dtype[2]);
+    a.E = d->n_experts;
     a.K = K;
+    a.H = d->hidden;
+    a.I = d->inter;
+    a.P = P;
+    a.n_slots = d->slot_table ? d->n_slots : d->n_experts;
+    a.norm = d->norm;
+    a.act = d->act;
+    a.alpha = d->alpha;
+    a.limit = d->limit;
+    a.bg = d->bias[0];
+    a.bu = d->bias[1];
+    a.bd = d->bias[2];
+    a.table = d->slot_table;
+    a.missing = missing;
+    a.x = x;
+    a.logits = logits;
+    a.ids = ids_out ? ids_out : (uint32_t *)(base + L.ids);
+    a.w = w_out ? w_out : (float *)(base + L.w);
+    a.slots = (uint32_t *)(base + L.slots);
+    a.h = (float *)(base + L.h);
+    a.out = out;
+
     if (d->dtype[0] == d->dtype[1]) {
-        a.w0 = (const uint8_t *)d->w[0];
-        a.w1 = (const uint8_t *)d->w[1];
-        a.slot_stride0 = d->slot_stride[0];
-        a.slot_stride1 = d->slot_stride[1];
-        a.row_bytes = (int64_t)(d->hidden / cw_block_size(d->dtype[0])) * cw_type_size(d->dtype[0]);
-        a.out = h;
-        a.out_width = P;
-        a.act = d->act;
-        a.alpha = d->alpha;
-        a.limit = d->limit;
-        a.b0 = d->bias[0];
-        a.b1 = d->bias[1];
-        if ((rc = gemv_gateup(d->dtype[0], a, T * K, s))) return rc;
+        if ((rc = moe_gateup(d->dtype[0], a, T, s))) return rc;
     } else {
+        // gate and up in different formats: route, resolve, two matvecs, the activation
+        if ((rc = route(logits, T, a.E, K, d->norm, a.ids, a.w, s))) return rc;
+        if (d->slot_table) {
+            hipLaunchKernelGGL(k_resolve, flat_grid((int64_t)T * K), dim3(256), 0, s, a.ids, d->slot_table, T * K, a.slots,
+                               missing);
+            if ((rc = check_launch("k_resolve"))) return rc;
+        } else {
+            a.slots = a.ids;
+        }
         float *g = (float *)(base + L.g), *u = (float *)(base + L.u);
         for (int m = 0; m < 2; m++) {
-            GemvArgs b = a;
+            GemvArgs b = {};
             b.w0 = (const uint8_t *)d->w[m];
             b.slot_stride0 = d->slot_stride[m];
             b.row_bytes = (int64_t)(d->hidden / cw_block_size(d->dtype[m])) * cw_type_size(d->dtype[m]);
+            b.n = d->inter;
+            b.k = d->hidden;
+            b.nsb = d->hidden / 32;
+            b.n_slots = a.n_slots;
+            b.x = x;
+            b.x_per_pick = 0;
+            b.ids = a.slots;
+            b.K = K;
             b.out = m == 0 ? g : u;
             b.out_width = d->inter;
             if ((rc = gemv_plain(d->dtype[m], b, T * K, s))) return rc;
         }
         const int64_t rows = (int64_t)T * K;
-        if (d->act == CW_ACT_SILU && P == d->inter) {
-            hipLaunchKernelGGL(k_swiglu, flat_grid(rows * d->inter), dim3(256), 0, s, g, u, h, rows * d->inter);
-        } else {
-            const float alpha = d->act == CW_ACT_SILU ? 1.0f : d->alpha;
-            hipLaunchKernelGGL(k_clamped_swiglu, flat_grid(rows * P), dim3(256), 0, s, g, u, d->bias[0], d->bias[1], ids, rows,
-                               d->inter, P, alpha, d->act == CW_ACT_SILU ? INFINITY : d->limit, h);
-        }
-        if ((rc = check_launch("k_swiglu"))) return rc;
+        const bool silu = d->act == CW_ACT_SILU;
+        hipLaunchKernelGGL(k_clamped_swiglu, flat_grid(rows * P), dim3(256), 0, s, g, u, silu ? nullptr : d->bias[0],
+                           silu ? nullptr : d->bias[1], a.ids, rows, d->inter, P, silu ? 1.0f : d->alpha,
+                           silu ? INFINITY : d->limit, a.h, silu ? 1 : 0);
+        if ((rc = check_launch("k_clamped_swiglu"))) return rc;
     }
-    GemvArgs b = {};
-    b.w0 = (const uint8_t *)d->w[2];
-    b.slot_stride0 = d->slot_stride[2];
-    b.row_bytes = (int64_t)(P / cw_block_size(d->dtype[2])) * cw_type_size(d->dtype[2]);
-    b.n = d->hidden;
-    b.k = P;
-    b.nsb = P / 32;
-    b.n_slots = n_slots;
-    b.x = h;
-    b.x_per_pick = 1;
-    b.ids = slots;
-    b.experts = ids;
-    b.K = K;
-    b.out = out;
-    b.out_width = d->hidden;
-    b.wts = w;
-    b.bd = d->bias[2];
-    return gemv_down(d->dtype[2], b, T, s);
+    return moe_down(d->dtype[2], a, T, s);
 }
 
 }  // namespace cw
@@ -344,7 +257,7 @@ int cw_clamped_swiglu(const float *g, const float *u, const float *gate_b, const
     CW_REQUIRE(ids || (!gate_b && !up_b), "clamped_swiglu: biases need ids");
     const int out_w = pad > width ? pad : width;
     hipLaunchKernelGGL(k_clamped_swiglu, flat_grid(rows * out_w), dim3(256), 0, (hipStream_t)stream, g, u, gate_b, up_b, ids,
-                       rows, width, out_w, alpha, limit, h);
+                       rows, width, out_w, alpha, limit, h, 0);
     return check_launch("k_clamped_swiglu");
 }
 

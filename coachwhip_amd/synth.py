@@ -100,12 +100,16 @@ def top_k_margin(logits, k):
     return float(np.min(s[:, k - 1] - s[:, k]))
 
 
-def near_ties_within_top_k(logits, k, eps=1e-5):
-    """True when two of a row's top k+1 logits are within eps (relative): their softmax
-    probabilities could round to the same f32 value and the order becomes index-dependent."""
+def near_ties_within_top_k(logits, k, eps=1e-6):
+    """True when two distinct logits among a row's top k+1 are within eps of each other.
+
+    The CPU route ranks f32 softmax probabilities (ties to the lower index) and the GPU ranks
+    the logits themselves; the orders can only differ when two distinct logits give the same f32
+    probability, which needs a gap of about one ulp of exp (~1e-7). Exact ties are ranked by
+    index on both sides and do not count."""
     s = -np.sort(-np.asarray(logits, dtype=np.float64), axis=1)[:, :k + 1]
     gaps = s[:, :-1] - s[:, 1:]
-    return bool(np.any(gaps <= eps * np.maximum(1.0, np.abs(s[:, :-1]))))
+    return bool(np.any((gaps > 0) & (gaps <= eps * np.maximum(1.0, np.abs(s[:, :-1])))))
 
 
 def device_blocks(dtype, n_weights, gen, device="cuda"):
