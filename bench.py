@@ -21,6 +21,7 @@ import time
 
 METRIC = "MoE layer µs + achieved HBM GB/s (decode b=1); prefill tokens/s; MFMA util"
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_F16_TFLOPS = 2500.0  # dense fp16
 
 
 def log(*a):
@@ -143,8 +144,11 @@ def main():
     torch.cuda.synchronize()
     pre_us = start.elapsed_time(stop) * 1e3 / reps
     pre_flops = 2.0 * T * K * 3 * H * I
-    prefill = {"tokens": T, "us_per_layer": pre_us, "tokens_per_s": T / (pre_us * 1e-6),
-               "tflops": pre_flops / (pre_us * 1e-6) / 1e12, "path": "f32 matvec per token (no MFMA yet)"}
+    tflops = pre_flops / (pre_us * 1e-6) / 1e12
+    prefill = {"tokens": T, "us_per_layer": round(pre_us, 2), "tokens_per_s": round(T / (pre_us * 1e-6)),
+               "tflops": round(tflops, 2), "mfma_util": round(tflops / MFMA_PEAK_F16_TFLOPS, 4),
+               "mfma_peak_tflops": MFMA_PEAK_F16_TFLOPS,
+               "path": "grouped MFMA GEMMs (fp16 integer weight codes, fp16 activations, f32 accumulate)"}
     log("prefill", prefill)
 
     cpu = None

@@ -14,6 +14,7 @@
 #include "cw_common.h"
 #include "cw_device.h"
 #include "cw_gemv.h"
+#include "cw_wave.h"
 
 namespace cw {
 
@@ -34,13 +35,6 @@ __device__ __forceinline__ void load_x(float (&xr)[NX][32], const float *xrow, i
             for (int v = 0; v < 32; v++) xr[i][v] = 0.f;
         }
     }
-}
-
-template <int LPR>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    return v;
 }
 
 template <class Fmt, int LPR, int NX>

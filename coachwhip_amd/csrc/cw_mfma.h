@@ -1,0 +1,54 @@
+// Internal interface of the MFMA grouped-GEMM path (cw_mfma.hip): prefill of the MoE layer.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cw {
+
+constexpr int MF_MT = 64;   // activation rows per tile (4 MFMA blocks of 16)
+constexpr int MF_NT = 64;   // weight rows per tile (4 waves x 16)
+
+struct MfTile {
+    int slot, pos0, m, pad;
+};
+
+struct MfArgs {
+    // weights: one matrix (or a gate/up pair) per slot
+    const uint8_t *w0, *w1;
+    int64_t s0, s1;            // slot strides
+    int64_t row_bytes;
+    int n, k;                  // weight rows, weights per row
+    // activations: fp16 rows of k (lda halves) with a power-of-two scale per row
+    const uint16_t *a16;
+    const float *ascale;
+    int lda;
+    const int *rows;           // activation row of each pile position, or NULL (position itself)
+    // piles
+    const MfTile *tiles;
+    const int *n_tiles;
+    const int *pile_pick;      // pick index (t*K + j) of each pile position
+    int K;
+    // epilogues
+    int act;
+    float alpha, limit;
+    const float *bias0, *bias1;   // gate/up bias (E x n)
+    const uint32_t *ids;          // expert of each pick (bias lookup)
+    float *h;                     // gate/up: hidden rows in pile order (ldh floats)
+    int ldh;
+    const float *w;               // down: routing weight of each pick
+    const float *bias_d;          // down: bias (E x n)
+    float *out;                   // down: (T x n), accumulated atomically
+};
+
+bool mfma_supported(int dtype);
+// one block: expert piles of the (slot) picks, and the tile list
+int mfma_piles(const uint32_t *slots, int TK, int K, int n_slots, int *pile_pick, int *pile_tok, MfTile *tiles,
+               int *n_tiles, hipStream_t s);
+int max_tiles(int TK, int n_slots);
+// rows x k f32 -> fp16 rows (ld = k) with per-row power-of-two scales
+int pack_rows_f16(const float *x, int rows, int k, int ldx, uint16_t *a16, float *ascale, hipStream_t s);
+int fill_zero(float *p, int64_t n, hipStream_t s);
+int mfma_gateup(int dtype, const MfArgs &a, int tiles_max, hipStream_t s);
+int mfma_down(int dtype, const MfArgs &a, int tiles_max, hipStream_t s);
+
+}  // namespace cw

@@ -1,8 +1,10 @@
 // Router top-k, activations, weighted combine, slot resolve and the MoE layer (gfx950).
 #include <math.h>
+#include <stdlib.h>
 
 #include "cw_common.h"
 #include "cw_gemv.h"
+#include "cw_mfma.h"
 #include "cw_moe_fused.h"
 #include "cw_wave.h"
 
@@ -95,7 +97,23 @@ static int route(const float *logits, int T, int E, int K, int norm, uint32_t *i
 
 struct MoeLayout {
     size_t ids, w, slots, g, u, h, total;
+    // grouped (MFMA) path
+    bool grouped;
+    size_t pile_pick, pile_tok, tiles, n_tiles, x16, xscale, h16, hscale;
 };
+
+// Token count from which the layer runs as grouped MFMA GEMMs instead of per-pick matvecs
+// (CWMOE_PREFILL_MIN_TOKENS overrides; the reference switches to grouped kernels above 8 tokens,
+// crates/engine/src/experts.rs:2225).
+static int prefill_min_tokens() {
+    const char *e = getenv("CWMOE_PREFILL_MIN_TOKENS");
+    return e ? atoi(e) : 16;
+}
+
+static bool grouped_path(const cw_moe_desc *d, int T) {
+    return T >= prefill_min_tokens() && d->dtype[0] == d->dtype[1] && mfma_supported(d->dtype[0]) &&
+           mfma_supported(d->dtype[2]) && (d->slot_table ? d->n_slots : d->n_experts) <= 1024;
+}
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -139,8 +157,89 @@ static MoeLayout layout(const cw_moe_desc *d, int T) {
     L.g = off; off = align256(off + (split ? TK * d->inter * 4 : 0));
     L.u = off; off = align256(off + (split ? TK * d->inter * 4 : 0));
     L.h = off; off = align256(off + TK * (size_t)P * 4);
+    L.grouped = grouped_path(d, T);
+    if (L.grouped) {
+        const int n_slots = d->slot_table ? d->n_slots : d->n_experts;
+        L.pile_pick = off; off = align256(off + TK * 4);
+        L.pile_tok = off; off = align256(off + TK * 4);
+        L.tiles = off; off = align256(off + (size_t)max_tiles((int)TK, n_slots) * sizeof(MfTile));
+        L.n_tiles = off; off = align256(off + 4);
+        L.x16 = off; off = align256(off + (size_t)T * d->hidden * 2);
+        L.xscale = off; off = align256(off + (size_t)T * 4);
+        L.h16 = off; off = align256(off + TK * (size_t)P * 2);
+        L.hscale = off; off = align256(off + TK * 4);
+    }
     L.total = off;
     return L;
+}
+
+// Prefill: route, group the picks by slot, gate/up and down as grouped MFMA GEMMs.
+static int moe_grouped(const cw_moe_desc *d, const MoeArgs &a, const MoeLayout &L, uint8_t *base, int T, hipStream_t s) {
+    int rc;
+    const int K = a.K, TK = T * K, P = a.P;
+    if ((rc = route(a.logits, T, a.E, K, d->norm, a.ids, a.w, s))) return rc;
+    const uint32_t *slots = a.ids;
+    if (d->slot_table) {
+        hipLaunchKernelGGL(k_resolve, flat_grid(TK), dim3(256), 0, s, a.ids, d->slot_table, TK, a.slots, a.missing);
+        if ((rc = check_launch("k_resolve"))) return rc;
+        slots = a.slots;
+    }
+    int *pile_pick = (int *)(base + L.pile_pick), *pile_tok = (int *)(base + L.pile_tok), *n_tiles = (int *)(base + L.n_tiles);
+    MfTile *tiles = (MfTile *)(base + L.tiles);
+    if ((rc = mfma_piles(slots, TK, K, a.n_slots, pile_pick, pile_tok, tiles, n_tiles, s))) return rc;
+    uint16_t *x16 = (uint16_t *)(base + L.x16), *h16 = (uint16_t *)(base + L.h16);
+    float *xscale = (float *)(base + L.xscale), *hscale = (float *)(base + L.hscale);
+    if ((rc = pack_rows_f16(a.x, T, a.H, a.H, x16, xscale, s))) return rc;
+    if (P > a.I && (rc = fill_zero(a.h, (int64_t)TK * P, s))) return rc;
+    const int tmax = max_tiles(TK, a.n_slots);
+
+    MfArgs g = {};
+    g.w0 = a.wg;
+    g.w1 = a.wu;
+    g.s0 = a.sg;
+    g.s1 = a.su;
+    g.row_bytes = a.rbg;
+    g.n = a.I;
+    g.k = a.H;
+    g.a16 = x16;
+    g.ascale = xscale;
+    g.lda = a.H;
+    g.rows = pile_tok;
+    g.tiles = tiles;
+    g.n_tiles = n_tiles;
+    g.pile_pick = pile_pick;
+    g.K = K;
+    g.act = a.act;
+    g.alpha = a.alpha;
+    g.limit = a.limit;
+    g.bias0 = a.bg;
+    g.bias1 = a.bu;
+    g.ids = a.ids;
+    g.h = a.h;
+    g.ldh = P;
+    if ((rc = mfma_gateup(d->dtype[0], g, tmax, s))) return rc;
+    if ((rc = pack_rows_f16(a.h, TK, P, P, h16, hscale, s))) return rc;
+    if ((rc = fill_zero(a.out, (int64_t)T * a.H, s))) return rc;
+
+    MfArgs dn = {};
+    dn.w0 = a.wd;
+    dn.s0 = a.sd;
+    dn.row_bytes = a.rbd;
+    dn.n = a.H;
+    dn.k = P;
+    dn.a16 = h16;
+    dn.ascale = hscale;
+    dn.lda = P;
+    dn.rows = nullptr;
+    dn.tiles = tiles;
+    dn.n_tiles = n_tiles;
+    dn.pile_pick = pile_pick;
+    dn.K = K;
+    dn.ids = a.ids;
+    dn.w = a.w;
+    dn.bias_d = a.bd;
+    dn.out = a.out;
+    return mfma_down(d->dtype[2], dn, tmax, s);
 }
 
 static int moe_layer(const cw_moe_desc *d, const float *x, const float *logits, int T, float *out, uint32_t *ids_out,
@@ -186,6 +285,7 @@ static int moe_layer(const cw_moe_desc *d, const float *x, const float *logits, 
     a.h = (float *)(base + L.h);
     a.out = out;
 
+    if (L.grouped) return moe_grouped(d, a, L, base, T, s);
     if (d->dtype[0] == d->dtype[1]) {
         if ((rc = moe_gateup(d->dtype[0], a, T, s))) return rc;
     } else {

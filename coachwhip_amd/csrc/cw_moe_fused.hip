@@ -17,13 +17,6 @@
 
 namespace cw {
 
-template <int LPR>
-__device__ __forceinline__ float lane_group_sum(float v) {
-#pragma unroll
-    for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    return v;
-}
-
 template <int NX>
 __device__ __forceinline__ void load_xs(float (&xr)[NX][32], const float *xrow, int sub, int lpr, int nsb) {
 #pragma unroll
@@ -105,8 +98,8 @@ __global__ __launch_bounds__(256) void k_moe_gateup(const MoeArgs a) {
                 u += Fmt::dot(ru[q][i], lds, xr[i]);
             }
         }
-        g = lane_group_sum<LPR>(g);
-        u = lane_group_sum<LPR>(u);
+        g = group_sum<LPR>(g);
+        u = group_sum<LPR>(u);
         if (sub == 0 && r < a.I) {
             float o;
             if (a.act == CW_ACT_SILU) {
@@ -172,7 +165,7 @@ __global__ __launch_bounds__(256) void k_moe_down(const MoeArgs a) {
             const int sb = sub + i * LPR;
             if (r < a.H && sb < nsb) d += Fmt::dot(raw[q][i], lds, xr[q][i]);
         }
-        d = lane_group_sum<LPR>(d);
+        d = group_sum<LPR>(d);
         if (sub == 0) part[j * RPW + rsub] = bad[q] ? __int_as_float(0x7fc00000) : d;
     }
     __syncthreads();

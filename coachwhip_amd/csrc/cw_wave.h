@@ -1,4 +1,4 @@
-// Wavefront-level helpers (wave64): reductions and the router's top-k, shared by the kernels.
+// Wavefront-level helpers (wave64): cross-lane reductions and the router's top-k.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -6,16 +6,42 @@
 
 namespace cw {
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+// Cross-lane steps without LDS traffic: DPP moves within 16-lane rows, readlane across rows.
+// DPP controls (GCN3+ encoding): quad_perm [1,0,3,2] = 0xB1 and [2,3,0,1] = 0x4E swap lanes
+// 1 and 2 apart; row_half_mirror (0x141) pairs quads of an 8-lane half-row, row_mirror (0x140)
+// pairs the two halves of a row. After the four steps every lane holds its row's reduction.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, true);
+}
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// sum over groups of G consecutive lanes (G = 8, 16, 32 or 64), the result in every lane
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    if constexpr (G >= 16) v += dpp_f<0x140>(v);
+    if constexpr (G == 32) v += __shfl_xor(v, 16);
+    if constexpr (G == 64) v = (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
     return v;
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    return v;
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
 }
 
 // (value, index) order of the router: larger value first, the lower index among equals;
@@ -26,13 +52,29 @@ __device__ __forceinline__ bool route_better(float va, uint32_t ia, float vb, ui
     return va > vb || (va == vb && ia < ib);
 }
 
+template <int CTRL>
+__device__ __forceinline__ void argmax_step(float &v, uint32_t &i) {
+    const float ov = dpp_f<CTRL>(v);
+    const uint32_t oi = dpp_u<CTRL>(i);
+    if (route_better(ov, oi, v, i)) { v = ov; i = oi; }
+}
+
+// the best (value, index) of the wave, in every lane
 __device__ __forceinline__ void wave_argmax(float &v, uint32_t &i) {
+    argmax_step<0xB1>(v, i);
+    argmax_step<0x4E>(v, i);
+    argmax_step<0x141>(v, i);
+    argmax_step<0x140>(v, i);
+    float bv = readlane_f(v, 0);
+    uint32_t bi = (uint32_t)__builtin_amdgcn_readlane((int)i, 0);
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        float ov = __shfl_xor(v, off);
-        uint32_t oi = __shfl_xor(i, off);
-        if (route_better(ov, oi, v, i)) { v = ov; i = oi; }
+    for (int row = 16; row < 64; row += 16) {
+        const float rv = readlane_f(v, row);
+        const uint32_t ri = (uint32_t)__builtin_amdgcn_readlane((int)i, row);
+        if (route_better(rv, ri, bv, bi)) { bv = rv; bi = ri; }
     }
+    v = bv;
+    i = bi;
 }
 
 // One wavefront routes one token: softmax over E = 64*PER (or fewer) logits as candle-nn's
