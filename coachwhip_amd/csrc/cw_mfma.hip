@@ -36,14 +36,77 @@ __device__ __forceinline__ uint4 scale4(uint4 v, uint32_t sc2) {
     return make_uint4(pk_mul_u(v.x, sc2), pk_mul_u(v.y, sc2), pk_mul_u(v.z, sc2), pk_mul_u(v.w, sc2));
 }
 __device__ __forceinline__ uint4 xor4(uint4 a, uint4 b) { return make_uint4(a.x ^ b.x, a.y ^ b.y, a.z ^ b.z, a.w ^ b.w); }
-__device__ __forceinline__ uint32_t f16_of(uint32_t byte) { return __builtin_bit_cast(uint16_t, (_Float16)(float)byte); }
 
-// sign masks of 8 fp16 lanes for an 8-bit sign pattern
-__device__ __forceinline__ uint4 sign_mask8(uint32_t s) {
-    uint32_t w[4];
-#pragma unroll
+// ------------------------------------------------------------------------------ code tables
+// Lattice entries as fp16 integers and sign masks as fp16 sign bits, built at compile time; a
+// kernel copies the ones its format needs into LDS.
+struct U4 { uint32_t x, y, z, w; };
+template <int N> struct Tab { U4 v[N]; };
+
+constexpr uint32_t f16_int(uint32_t v) {  // fp16 bits of a small non-negative integer (< 2048)
+    if (v == 0) return 0;
+    int e = 0;
+    for (uint32_t t = v; t >= 2; t >>= 1) e++;
+    return (uint32_t)((e + 15) << 10) | ((v << (10 - e)) & 0x3FFu);
+}
+constexpr U4 pack8(uint64_t bytes) {
+    uint32_t h[8] = {};
+    for (int b = 0; b < 8; b++) h[b] = f16_int((uint32_t)(bytes >> (8 * b)) & 0xFF);
+    return U4{h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16};
+}
+constexpr U4 signs8(uint32_t s) {
+    uint32_t w[4] = {};
     for (int i = 0; i < 4; i++) w[i] = (((s >> (2 * i)) & 1u) << 15) | (((s >> (2 * i + 1)) & 1u) << 31);
-    return make_uint4(w[0], w[1], w[2], w[3]);
+    return U4{w[0], w[1], w[2], w[3]};
+}
+constexpr uint32_t parity_signs(uint32_t i7) {  // ksigns_iq2xs: 7 bits plus an even-parity bit
+    uint32_t p = i7 ^ (i7 >> 4);
+    p ^= p >> 2;
+    p ^= p >> 1;
+    return i7 | ((p & 1u) << 7);
+}
+constexpr Tab<256> make_iq2xxs_f16() {
+    constexpr uint64_t g[256] = {CW_IQ2XXS_GRID_VALUES};
+    Tab<256> t{};
+    for (int i = 0; i < 256; i++) t.v[i] = pack8(g[i]);
+    return t;
+}
+constexpr Tab<1024> make_iq2s_f16() {
+    constexpr uint64_t g[1024] = {CW_IQ2S_GRID_VALUES};
+    Tab<1024> t{};
+    for (int i = 0; i < 1024; i++) t.v[i] = pack8(g[i]);
+    return t;
+}
+constexpr Tab<256> make_iq3s_f16() {  // two 4-value entries per U4: entry 2i in x,y and 2i+1 in z,w
+    constexpr uint32_t g[512] = {CW_IQ3S_GRID_VALUES};
+    Tab<256> t{};
+    for (int i = 0; i < 256; i++) {
+        const U4 a = pack8((uint64_t)g[2 * i] | ((uint64_t)g[2 * i + 1] << 32));
+        t.v[i] = a;
+    }
+    return t;
+}
+constexpr Tab<128> make_parity_signs() {
+    Tab<128> t{};
+    for (int i = 0; i < 128; i++) t.v[i] = signs8(parity_signs((uint32_t)i));
+    return t;
+}
+constexpr Tab<256> make_signs() {
+    Tab<256> t{};
+    for (int i = 0; i < 256; i++) t.v[i] = signs8((uint32_t)i);
+    return t;
+}
+static __constant__ Tab<256> c_iq2xxs_f16 = make_iq2xxs_f16();
+static __constant__ Tab<1024> c_iq2s_f16 = make_iq2s_f16();
+static __constant__ Tab<256> c_iq3s_f16 = make_iq3s_f16();
+static __constant__ Tab<128> c_psigns = make_parity_signs();
+static __constant__ Tab<256> c_signs = make_signs();
+
+template <int N>
+__device__ __forceinline__ void copy_tab(uint8_t *lds, const Tab<N> &t, int tid, int nt) {
+    uint4 *d = (uint4 *)lds;
+    const uint4 *src = (const uint4 *)&t;
+    for (int i = tid; i < N; i += nt) d[i] = src[i];
 }
 
 // ------------------------------------------------------------------------------ formats
@@ -55,14 +118,8 @@ struct MIQ2_XXS {
     static constexpr int TS = 66, SBK = 256, LDS = 256 * 16 + 128 * 16;
     struct Raw { uint32_t d; uint2 q[8]; };
     static __device__ void fill(uint8_t *lds, int tid, int nt) {
-        uint4 *g = (uint4 *)lds, *sg = (uint4 *)(lds + 256 * 16);
-        for (int i = tid; i < 256; i += nt) {
-            const uint64_t e = c_iq2xxs_grid[i];
-            uint32_t h[8];
-            for (int b = 0; b < 8; b++) h[b] = f16_of((uint32_t)(e >> (8 * b)) & 0xFF);
-            g[i] = make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16);
-        }
-        for (int i = tid; i < 128; i += nt) sg[i] = sign_mask8(ksign((uint32_t)i));
+        copy_tab(lds, c_iq2xxs_f16, tid, nt);
+        copy_tab(lds + 256 * 16, c_psigns, tid, nt);
     }
     static __device__ __forceinline__ void load(Raw &r, const uint8_t *row, int u) {
         const uint8_t *b = row + (int64_t)TS * u;
@@ -84,14 +141,8 @@ struct MIQ2_S {
     static constexpr int TS = 82, SBK = 256, LDS = 1024 * 16 + 256 * 16;
     struct Raw { uint32_t d; uint32_t qs[8]; uint32_t sg[8]; uint2 qh; uint2 sc; };
     static __device__ void fill(uint8_t *lds, int tid, int nt) {
-        uint4 *g = (uint4 *)lds, *sg = (uint4 *)(lds + 1024 * 16);
-        for (int i = tid; i < 1024; i += nt) {
-            const uint64_t e = c_iq2s_grid[i];
-            uint32_t h[8];
-            for (int b = 0; b < 8; b++) h[b] = f16_of((uint32_t)(e >> (8 * b)) & 0xFF);
-            g[i] = make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16);
-        }
-        for (int i = tid; i < 256; i += nt) sg[i] = sign_mask8((uint32_t)i);
+        copy_tab(lds, c_iq2s_f16, tid, nt);
+        copy_tab(lds + 1024 * 16, c_signs, tid, nt);
     }
     static __device__ __forceinline__ void load(Raw &r, const uint8_t *row, int u) {
         const uint8_t *b = row + (int64_t)TS * u;
@@ -120,15 +171,8 @@ struct MIQ3_S {
     static constexpr int TS = 110, SBK = 256, LDS = 512 * 8 + 256 * 16;
     struct Raw { uint32_t d; uint32_t qs[8]; uint2 qh; uint32_t sg[8]; uint32_t sc; };
     static __device__ void fill(uint8_t *lds, int tid, int nt) {
-        uint2 *g = (uint2 *)lds;
-        uint4 *sg = (uint4 *)(lds + 512 * 8);
-        for (int i = tid; i < 512; i += nt) {
-            const uint32_t e = c_iq3s_grid[i];
-            uint32_t h[4];
-            for (int b = 0; b < 4; b++) h[b] = f16_of((e >> (8 * b)) & 0xFF);
-            g[i] = make_uint2(h[0] | h[1] << 16, h[2] | h[3] << 16);
-        }
-        for (int i = tid; i < 256; i += nt) sg[i] = sign_mask8((uint32_t)i);
+        copy_tab(lds, c_iq3s_f16, tid, nt);   // entry i as 4 halves at byte 8*i
+        copy_tab(lds + 512 * 8, c_signs, tid, nt);
     }
     static __device__ __forceinline__ void load(Raw &r, const uint8_t *row, int u) {
         const uint8_t *b = row + (int64_t)TS * u;
@@ -202,116 +246,123 @@ __device__ __forceinline__ f16x8 as_f16x8(uint4 v) { return __builtin_bit_cast(f
 
 // MODE 0: gate and up (two matrices) with the activation, hidden rows written in pile order.
 // MODE 1: down, the pick's routing weight (and bias) applied, accumulated into out[token].
-template <class MF, int MODE>
+// A block owns one M-tile (up to 64 picks of a slot) and NTB consecutive N-tiles of 64 weight
+// rows; k streams through LDS in chunks of 256 (8 K-steps). Latency is hidden by occupancy
+// (several blocks per CU).
+template <class MF, int MODE, int NTB>
 __global__ __launch_bounds__(256) void k_mfma(const MfArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     uint8_t *tab = smem;
     _Float16 *As = (_Float16 *)(smem + ((MF::LDS + 15) & ~15));
+    constexpr int UPC = 256 / MF::SBK;   // scale units per chunk
+    constexpr int KPU = MF::SBK / 32;    // K-steps per scale unit
     const int n_nt = (a.n + MF_NT - 1) / MF_NT;
-    const int mt = blockIdx.x / n_nt, nt = blockIdx.x - mt * n_nt;
+    const int groups = (n_nt + NTB - 1) / NTB;
+    // blocks go to XCDs round-robin; block b of each run of 8*groups takes M-tile 8*run + b%8
+    // and N-group b/8, so an M-tile's N-groups share an XCD and every XCD gets valid tiles
+    const int run = blockIdx.x / (8 * groups), b = blockIdx.x - run * 8 * groups;
+    const int mt = run * 8 + (b & 7);
     if (mt >= *a.n_tiles) return;  // whole block exits before any barrier
+    const int nt_begin = (b >> 3) * NTB, nt_end = min(nt_begin + NTB, n_nt);
     const MfTile tile = a.tiles[mt];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = lane >> 4, l16 = lane & 15;
     MF::fill(tab, tid, 256);
-
-    const int n = nt * MF_NT + wave * 16 + l16;   // this lane's weight row
-    const bool nv = n < a.n;
-    const uint8_t *r0 = a.w0 + (int64_t)tile.slot * a.s0 + (int64_t)(nv ? n : 0) * a.row_bytes;
-    const uint8_t *r1 = MODE == 0 ? a.w1 + (int64_t)tile.slot * a.s1 + (int64_t)(nv ? n : 0) * a.row_bytes : r0;
-    f32x4 acc0[4], acc1[4];
-#pragma unroll
-    for (int mb = 0; mb < 4; mb++) { acc0[mb] = f32x4{0, 0, 0, 0}; acc1[mb] = f32x4{0, 0, 0, 0}; }
-
     const int n_ks = a.k / 32;
-    constexpr int UPC = 256 / MF::SBK;           // scale units per 256-wide chunk
-    constexpr int KPU = MF::SBK / 32;            // K-steps per scale unit
-    for (int c0 = 0; c0 < n_ks; c0 += 8) {
-        const int nks = min(8, n_ks - c0);
-        __syncthreads();  // previous chunk's readers are done
-        // stage the chunk's activations: 64 rows x nks*32 halves
-        for (int idx = tid; idx < MF_MT * 32; idx += 256) {
-            const int r = idx >> 5, c = idx & 31;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (r < tile.m && c < nks * 4) {
-                const int pos = tile.pos0 + r;
-                const int src = a.rows ? a.rows[pos] : pos;
-                v = *(const uint4 *)(a.a16 + (int64_t)src * a.lda + (int64_t)c0 * 32 + c * 8);
-            }
-            *(uint4 *)(As + r * A_LD + c * 8) = v;
-        }
-        // this lane's weight units for the chunk
-        typename MF::Raw raw0[UPC], raw1[UPC];
+
+    for (int nt = nt_begin; nt < nt_end; nt++) {
+        const int n = nt * MF_NT + wave * 16 + l16;   // this lane's weight row
+        const bool nv = n < a.n;
+        const uint8_t *r0 = a.w0 + (int64_t)tile.slot * a.s0 + (int64_t)(nv ? n : 0) * a.row_bytes;
+        const uint8_t *r1 = MODE == 0 ? a.w1 + (int64_t)tile.slot * a.s1 + (int64_t)(nv ? n : 0) * a.row_bytes : r0;
+        f32x4 acc0[4], acc1[4];
 #pragma unroll
-        for (int u = 0; u < UPC; u++) {
-            const int unit = c0 / KPU + u;
-            if (u * KPU < nks) {
-                MF::load(raw0[u], r0, unit);
-                if constexpr (has_grp_load<MF>::value) MF::load_grp(raw0[u], r0, unit, grp);
-                if constexpr (MODE == 0) {
-                    MF::load(raw1[u], r1, unit);
-                    if constexpr (has_grp_load<MF>::value) MF::load_grp(raw1[u], r1, unit, grp);
+        for (int mb = 0; mb < 4; mb++) { acc0[mb] = f32x4{0, 0, 0, 0}; acc1[mb] = f32x4{0, 0, 0, 0}; }
+        for (int c0 = 0; c0 < n_ks; c0 += 8) {
+            const int nks = min(8, n_ks - c0);
+            __syncthreads();  // previous chunk's readers are done
+            for (int idx = tid; idx < MF_MT * 32; idx += 256) {
+                const int r = idx >> 5, c = idx & 31;
+                uint4 v = make_uint4(0, 0, 0, 0);
+                if (r < tile.m && c < nks * 4) {
+                    const int pos = tile.pos0 + r;
+                    const int src = a.rows ? a.rows[pos] : pos;
+                    v = *(const uint4 *)(a.a16 + (int64_t)src * a.lda + (int64_t)c0 * 32 + c * 8);
+                }
+                *(uint4 *)(As + r * A_LD + c * 8) = v;
+            }
+            typename MF::Raw raw0[UPC], raw1[UPC];
+#pragma unroll
+            for (int u = 0; u < UPC; u++) {
+                const int unit = c0 / KPU + u;
+                if (u * KPU < nks) {
+                    MF::load(raw0[u], r0, unit);
+                    if constexpr (has_grp_load<MF>::value) MF::load_grp(raw0[u], r0, unit, grp);
+                    if constexpr (MODE == 0) {
+                        MF::load(raw1[u], r1, unit);
+                        if constexpr (has_grp_load<MF>::value) MF::load_grp(raw1[u], r1, unit, grp);
+                    }
                 }
             }
-        }
-        __syncthreads();
+            __syncthreads();
 #pragma unroll
-        for (int u = 0; u < UPC; u++) {
-            if (u * KPU >= nks) break;
-            f32x4 p0[4], p1[4];
+            for (int u = 0; u < UPC; u++) {
+                if (u * KPU >= nks) break;
+                f32x4 p0[4], p1[4];
 #pragma unroll
-            for (int mb = 0; mb < 4; mb++) { p0[mb] = f32x4{0, 0, 0, 0}; p1[mb] = f32x4{0, 0, 0, 0}; }
+                for (int mb = 0; mb < 4; mb++) { p0[mb] = f32x4{0, 0, 0, 0}; p1[mb] = f32x4{0, 0, 0, 0}; }
 #pragma unroll
-            for (int ks = 0; ks < KPU; ks++) {
-                const int kk = u * KPU + ks;  // K-step within the chunk
-                const f16x8 b0 = as_f16x8(MF::frag(raw0[u], ks, grp, tab));
-                f16x8 b1;
-                if constexpr (MODE == 0) b1 = as_f16x8(MF::frag(raw1[u], ks, grp, tab));
+                for (int ks = 0; ks < KPU; ks++) {
+                    const int kk = u * KPU + ks;
+                    const f16x8 b0 = as_f16x8(MF::frag(raw0[u], ks, grp, tab));
+                    f16x8 b1;
+                    if constexpr (MODE == 0) b1 = as_f16x8(MF::frag(raw1[u], ks, grp, tab));
+#pragma unroll
+                    for (int mb = 0; mb < 4; mb++) {
+                        const f16x8 av = as_f16x8(*(const uint4 *)(As + (16 * mb + l16) * A_LD + kk * 32 + 8 * grp));
+                        p0[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b0, p0[mb], 0, 0, 0);
+                        if constexpr (MODE == 0) p1[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b1, p1[mb], 0, 0, 0);
+                    }
+                }
+                const float s0 = MF::scale(raw0[u]);
+                const float s1 = MODE == 0 ? MF::scale(raw1[u]) : 0.f;
 #pragma unroll
                 for (int mb = 0; mb < 4; mb++) {
-                    const f16x8 av = as_f16x8(*(const uint4 *)(As + (16 * mb + l16) * A_LD + kk * 32 + 8 * grp));
-                    p0[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b0, p0[mb], 0, 0, 0);
-                    if constexpr (MODE == 0) p1[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b1, p1[mb], 0, 0, 0);
+                    acc0[mb] += s0 * p0[mb];
+                    if constexpr (MODE == 0) acc1[mb] += s1 * p1[mb];
                 }
-            }
-            const float s0 = MF::scale(raw0[u]);
-            const float s1 = MODE == 0 ? MF::scale(raw1[u]) : 0.f;
-#pragma unroll
-            for (int mb = 0; mb < 4; mb++) {
-                acc0[mb] += s0 * p0[mb];
-                if constexpr (MODE == 0) acc1[mb] += s1 * p1[mb];
             }
         }
-    }
 
-    // epilogue: lane holds rows 16*mb + 4*grp + i (i < 4) of weight row n
-    if (!nv) return;
+        // epilogue: lane holds rows 16*mb + 4*grp + i (i < 4) of weight row n
+        if (!nv) continue;
 #pragma unroll
-    for (int mb = 0; mb < 4; mb++) {
+        for (int mb = 0; mb < 4; mb++) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int r = 16 * mb + 4 * grp + i;
-            if (r >= tile.m) continue;
-            const int pos = tile.pos0 + r;
-            const int src = a.rows ? a.rows[pos] : pos;
-            const float sa = a.ascale[src];
-            const int pick = a.pile_pick[pos];
-            if constexpr (MODE == 0) {
-                float g = acc0[mb][i] * sa, u = acc1[mb][i] * sa, o;
-                if (a.act == CW_ACT_SILU) {
-                    o = g / (1.0f + expf(-g)) * u;
+            for (int i = 0; i < 4; i++) {
+                const int r = 16 * mb + 4 * grp + i;
+                if (r >= tile.m) continue;
+                const int pos = tile.pos0 + r;
+                const int src = a.rows ? a.rows[pos] : pos;
+                const float sa = a.ascale[src];
+                const int pick = a.pile_pick[pos];
+                if constexpr (MODE == 0) {
+                    float g = acc0[mb][i] * sa, u = acc1[mb][i] * sa, o;
+                    if (a.act == CW_ACT_SILU) {
+                        o = g / (1.0f + expf(-g)) * u;
+                    } else {
+                        const uint32_t e = a.ids[pick];
+                        if (a.bias0) g += a.bias0[(int64_t)e * a.n + n];
+                        if (a.bias1) u += a.bias1[(int64_t)e * a.n + n];
+                        g = fminf(g, a.limit);
+                        u = fminf(fmaxf(u, -a.limit), a.limit);
+                        o = (u + 1.0f) * (g * (1.0f / (1.0f + expf(-(g * a.alpha)))));
+                    }
+                    a.h[(int64_t)pos * a.ldh + n] = o;
                 } else {
-                    const uint32_t e = a.ids[pick];
-                    if (a.bias0) g += a.bias0[(int64_t)e * a.n + n];
-                    if (a.bias1) u += a.bias1[(int64_t)e * a.n + n];
-                    g = fminf(g, a.limit);
-                    u = fminf(fmaxf(u, -a.limit), a.limit);
-                    o = (u + 1.0f) * (g * (1.0f / (1.0f + expf(-(g * a.alpha)))));
+                    float v = acc0[mb][i] * sa;
+                    if (a.bias_d) v += a.bias_d[(int64_t)a.ids[pick] * a.n + n];
+                    atomicAdd(a.out + (int64_t)(pick / a.K) * a.n + n, a.w[pick] * v);
                 }
-                a.h[(int64_t)pos * a.ldh + n] = o;
-            } else {
-                float v = acc0[mb][i] * sa;
-                if (a.bias_d) v += a.bias_d[(int64_t)a.ids[pick] * a.n + n];
-                atomicAdd(a.out + (int64_t)(pick / a.K) * a.n + n, a.w[pick] * v);
             }
         }
     }
@@ -408,13 +459,21 @@ int fill_zero(float *p, int64_t n, hipStream_t s) {
     return check_launch("k_fill_zero");
 }
 
-template <class MF, int MODE>
-static int launch(const MfArgs &a, int tiles_max, hipStream_t s) {
+template <class MF, int MODE, int NTB>
+static int launch_v(const MfArgs &a, int tiles_max, hipStream_t s) {
     const size_t shmem = ((MF::LDS + 15) & ~15) + (size_t)MF_MT * A_LD * 2;
     const int n_nt = (a.n + MF_NT - 1) / MF_NT;
-    if (a.k % 32) return set_error(CW_ENOTSUP, "mfma: k %d is not a multiple of 32", a.k);
-    hipLaunchKernelGGL((k_mfma<MF, MODE>), dim3(tiles_max * n_nt), dim3(256), shmem, s, a);
+    const int64_t blocks = (int64_t)((tiles_max + 7) / 8) * 8 * ((n_nt + NTB - 1) / NTB);
+    hipLaunchKernelGGL((k_mfma<MF, MODE, NTB>), dim3((unsigned)blocks), dim3(256), shmem, s, a);
     return check_launch("k_mfma");
+}
+
+template <class MF, int MODE>
+static int launch(const MfArgs &a, int tiles_max, hipStream_t s) {
+    if (a.k % 32) return set_error(CW_ENOTSUP, "mfma: k %d is not a multiple of 32", a.k);
+    // short rows (down's k = expert FFN) do little work per N-tile: a block takes four
+    if (a.k <= 1024) return launch_v<MF, MODE, 4>(a, tiles_max, s);
+    return launch_v<MF, MODE, 1>(a, tiles_max, s);
 }
 
 template <int MODE>
