@@ -54,6 +54,7 @@ SIGNATURES = {
     "cw_slots_resolve": ([_P, _P, _I, _P, _P, _P], _I),
     "cw_moe_workspace_size": ([ctypes.POINTER(MoeDesc), _I], ctypes.c_size_t),
     "cw_moe_layer": ([ctypes.POINTER(MoeDesc), _P, _P, _I, _P, _P, _P, _P, _P, ctypes.c_size_t, _P], _I),
+    "cw_device_errors": ([], ctypes.c_uint32),
     "cw_slots_new": ([_I], _P),
     "cw_slots_free": ([_P], None),
     "cw_slots_assign": ([_P, _P, _I, _P, _P, ctypes.POINTER(_I), _P, ctypes.POINTER(_I),

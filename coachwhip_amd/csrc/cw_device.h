@@ -23,6 +23,9 @@
 
 namespace cw {
 
+template <class F>
+struct TableRegs;
+
 // Lattice tables, copied to LDS by the kernels that read IQ formats.
 static __constant__ uint64_t c_iq2xxs_grid[256] = {CW_IQ2XXS_GRID_VALUES};
 static __constant__ uint64_t c_iq2s_grid[1024] = {CW_IQ2S_GRID_VALUES};
@@ -57,6 +60,7 @@ __device__ __forceinline__ float kv_mxfp4(uint32_t c) {
 // ---------------------------------------------------------------------------------- Q8_0
 struct FQ8_0 {
     static constexpr int BS = 32, TS = 34, LDS_BYTES = 0;
+    static __device__ __forceinline__ uint64_t table_word(int) { return 0; }
     struct Raw { uint32_t d; uint4 q0, q1; };
     static __device__ __forceinline__ void fill_lds(void *, int, int) {}
     static __device__ __forceinline__ Raw load(const uint8_t *row, int sb) {
@@ -87,6 +91,7 @@ struct FQ8_0 {
 // ---------------------------------------------------------------------------------- Q4_K
 struct FQ4_K {
     static constexpr int BS = 256, TS = 144, LDS_BYTES = 0;
+    static __device__ __forceinline__ uint64_t table_word(int) { return 0; }
     struct Raw { uint32_t dd; uint32_t sc; uint32_t mn; uint4 q0, q1; int hi; };
     static __device__ __forceinline__ void fill_lds(void *, int, int) {}
     static __device__ __forceinline__ Raw load(const uint8_t *row, int sb) {
@@ -134,6 +139,7 @@ struct FQ4_K {
 // ---------------------------------------------------------------------------------- MXFP4
 struct FMXFP4 {
     static constexpr int BS = 32, TS = 17, LDS_BYTES = 0;
+    static __device__ __forceinline__ uint64_t table_word(int) { return 0; }
     struct Raw { uint32_t e; uint4 q; };
     static __device__ __forceinline__ void fill_lds(void *, int, int) {}
     static __device__ __forceinline__ Raw load(const uint8_t *row, int sb) {
@@ -166,6 +172,7 @@ struct FMXFP4 {
 // ---------------------------------------------------------------------------------- IQ2_XXS
 struct FIQ2_XXS {
     static constexpr int BS = 256, TS = 66, LDS_BYTES = 256 * 8;
+    static __device__ __forceinline__ uint64_t table_word(int i) { return c_iq2xxs_grid[i]; }
     struct Raw { uint32_t d; uint32_t g; uint32_t s; };
     static __device__ __forceinline__ void fill_lds(void *lds, int tid, int nt) {
         uint64_t *t = (uint64_t *)lds;
@@ -216,6 +223,7 @@ struct FIQ2_XXS {
 // ---------------------------------------------------------------------------------- IQ2_S
 struct FIQ2_S {
     static constexpr int BS = 256, TS = 82, LDS_BYTES = 1024 * 8;
+    static __device__ __forceinline__ uint64_t table_word(int i) { return c_iq2s_grid[i]; }
     struct Raw { uint32_t d; uint32_t qs; uint32_t sg; uint32_t qh; uint32_t sc; };
     static __device__ __forceinline__ void fill_lds(void *lds, int tid, int nt) {
         uint64_t *t = (uint64_t *)lds;
@@ -270,6 +278,9 @@ struct FIQ2_S {
 // ---------------------------------------------------------------------------------- IQ3_S
 struct FIQ3_S {
     static constexpr int BS = 256, TS = 110, LDS_BYTES = 512 * 4;
+    static __device__ __forceinline__ uint64_t table_word(int i) {
+        return (uint64_t)c_iq3s_grid[2 * i] | ((uint64_t)c_iq3s_grid[2 * i + 1] << 32);
+    }
     struct Raw { uint32_t d; uint2 qs; uint32_t qh; uint32_t sg; uint32_t sc; };
     static __device__ __forceinline__ void fill_lds(void *lds, int tid, int nt) {
         uint32_t *t = (uint32_t *)lds;
@@ -313,6 +324,29 @@ struct FIQ3_S {
             for (int i = 0; i < 4; i++) s = fmaf(ubyte(gw, i), flip(x[4 * g + i], r.sg, 4 * g + i), s);
         }
         return s * (h2f(r.d) * (float)(1 + 2 * (int)r.sc));
+    }
+};
+
+// A block's share of a format's LDS table, held in registers between the global loads and the
+// LDS stores, so the loads can be issued early and waited for late.
+template <class F>
+struct TableRegs {
+    static constexpr int WORDS = F::LDS_BYTES / 8;
+    static constexpr int PER = WORDS > 0 ? (WORDS + 255) / 256 : 1;
+    uint64_t r[PER];
+    __device__ __forceinline__ void load(int tid) {
+#pragma unroll
+        for (int q = 0; q < PER; q++) {
+            const int i = tid + 256 * q;
+            if (i < WORDS) r[q] = F::table_word(i);
+        }
+    }
+    __device__ __forceinline__ void store(void *lds, int tid) const {
+#pragma unroll
+        for (int q = 0; q < PER; q++) {
+            const int i = tid + 256 * q;
+            if (i < WORDS) ((uint64_t *)lds)[i] = r[q];
+        }
     }
 };
 

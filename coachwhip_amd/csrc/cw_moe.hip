@@ -110,6 +110,13 @@ static int prefill_min_tokens() {
     return e ? atoi(e) : 16;
 }
 
+// One-token layers run as one persistent launch unless CWMOE_DECODE_KERNELS=2 asks for the
+// two-kernel form (gate/up, then down).
+static bool decode_single_launch() {
+    const char *e = getenv("CWMOE_DECODE_KERNELS");
+    return !(e && atoi(e) == 2);
+}
+
 static bool grouped_path(const cw_moe_desc *d, int T) {
     return T >= prefill_min_tokens() && d->dtype[0] == d->dtype[1] && mfma_supported(d->dtype[0]) &&
            mfma_supported(d->dtype[2]) && (d->slot_table ? d->n_slots : d->n_experts) <= 1024;
@@ -286,6 +293,10 @@ static int moe_layer(const cw_moe_desc *d, const float *x, const float *logits, 
     a.out = out;
 
     if (L.grouped) return moe_grouped(d, a, L, base, T, s);
+    if (T == 1 && d->dtype[0] == d->dtype[1] && decode_single_launch()) {
+        rc = moe_decode(d->dtype[0], d->dtype[2], a, s);
+        if (rc != CW_ENOTSUP) return rc;
+    }
     if (d->dtype[0] == d->dtype[1]) {
         if ((rc = moe_gateup(d->dtype[0], a, T, s))) return rc;
     } else {
@@ -379,6 +390,11 @@ int cw_slots_resolve(const uint32_t *ids, const uint32_t *table, int n, uint32_t
     CW_REQUIRE(ids && table && slots, "resolve: null pointer");
     hipLaunchKernelGGL(k_resolve, flat_grid(n), dim3(256), 0, (hipStream_t)stream, ids, table, n, slots, missing);
     return check_launch("k_resolve");
+}
+
+uint32_t cw_device_errors(void) {
+    (void)hipDeviceSynchronize();
+    return decode_barrier_errors();
 }
 
 size_t cw_moe_workspace_size(const cw_moe_desc *desc, int T) {

@@ -26,6 +26,9 @@ struct MoeArgs {
 };
 
 int moe_gateup(int dtype, const MoeArgs &a, int T, hipStream_t s);
+// the whole layer for one token in one launch (CW_ENOTSUP for shapes it does not cover)
+int moe_decode(int dtype_gate_up, int dtype_down, const MoeArgs &a, hipStream_t s);
+uint32_t decode_barrier_errors();
 int moe_down(int dtype, const MoeArgs &a, int T, hipStream_t s);
 
 }  // namespace cw

@@ -184,6 +184,293 @@ __global__ __launch_bounds__(256) void k_moe_down(const MoeArgs a) {
     }
 }
 
+// ------------------------------------------------------------------------------ one-kernel decode
+
+// Device-wide barrier of the persistent decode kernel. The state lives in the library (zero
+// at load) and resets itself. Blocks first arrive on a counter of their XCD (blocks go to the
+// 8 XCDs round-robin, blockIdx % 8); the last of each XCD arrives on a top counter, and the
+// last of those clears it and bumps the generation every block waits on. Splitting the
+// arrivals over 9 counters, 128 bytes apart, keeps them from serializing on one address (one
+// counter for 512 blocks measured ~15 us, this ~2.3 us). Everything the blocks exchange
+// through memory inside the kernel is written and read with agent-scope atomics, which go to
+// the coherence point, so the counters need no fences: an agent-scope release / acquire pair
+// here (L2 write-back and invalidate in every block) measured 3x slower, and so did polling
+// all 8 XCD counters from every block. A wait gives up after a bounded number of polls and
+// counts an error instead of hanging. One persistent decode call runs at a time per device.
+struct DecodeBarrier {
+    uint32_t sub[8][32];
+    uint32_t top[32];
+    uint32_t gen[32];
+    uint32_t errors;
+};
+static __device__ DecodeBarrier g_decode_barrier;
+
+#define CW_AGENT __HIP_MEMORY_SCOPE_AGENT
+__device__ bool grid_barrier(uint32_t nblocks) {
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's coherent stores have landed
+    __syncthreads();
+    __shared__ int ok;
+    if (threadIdx.x == 0) {
+        DecodeBarrier *b = &g_decode_barrier;
+        const uint32_t gen = __hip_atomic_load(&b->gen[0], __ATOMIC_RELAXED, CW_AGENT);
+        const uint32_t x = blockIdx.x & 7;
+        const uint32_t nsub = (nblocks - x + 7) / 8, nx = nblocks < 8 ? nblocks : 8;
+        bool last = false;
+        if (__hip_atomic_fetch_add(&b->sub[x][0], 1u, __ATOMIC_RELAXED, CW_AGENT) == nsub - 1) {
+            // the reset only has to land before the next call, which the kernel's end ensures
+            __hip_atomic_store(&b->sub[x][0], 0u, __ATOMIC_RELAXED, CW_AGENT);
+            last = __hip_atomic_fetch_add(&b->top[0], 1u, __ATOMIC_RELAXED, CW_AGENT) == nx - 1;
+            if (last) __hip_atomic_store(&b->top[0], 0u, __ATOMIC_RELAXED, CW_AGENT);
+        }
+        int good = 1;
+        if (last) {
+            __hip_atomic_fetch_add(&b->gen[0], 1u, __ATOMIC_RELAXED, CW_AGENT);
+        } else {
+            uint32_t polls = 0;
+            while (__hip_atomic_load(&b->gen[0], __ATOMIC_RELAXED, CW_AGENT) == gen) {
+                __builtin_amdgcn_s_sleep(1);
+                if (++polls > (1u << 17)) {
+                    good = 0;
+                    __hip_atomic_fetch_add(&b->errors, 1u, __ATOMIC_RELAXED, CW_AGENT);
+                    break;
+                }
+            }
+        }
+        ok = good;
+    }
+    __syncthreads();
+    return ok != 0;
+}
+
+__device__ __forceinline__ void store_coherent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The whole decode layer (one token) in one launch of a grid that fits on the device at once.
+// Loads are issued as early as their addresses are known, since every wait on them counts in
+// issue order:
+//   1. every wave loads the logits, then the LDS tables and its x slice, and routes the token;
+//   2. each wave issues the loads of its first gate/up item (pick, 2 rows) and of its block's
+//      first down rows (all its picks), stores the tables to LDS, then computes its gate/up
+//      items: dots, activation, hidden rows stored at the coherence point;
+//   3. device-wide barrier;
+//   4. each block copies all K hidden rows into LDS (one read per block, not per wave) and
+//      computes down row groups of 64/LD rows: per-pick dots, combined in pick order.
+template <class FG, int LG, int XG, class FD, int LD, int XD, int PER, int PPW>
+__global__ __launch_bounds__(256) void k_moe_decode(const MoeArgs a) {
+    __shared__ __align__(16) uint8_t ldsg[FG::LDS_BYTES > 0 ? FG::LDS_BYTES : 16];
+    __shared__ __align__(16) uint8_t ldsd[FD::LDS_BYTES > 0 ? FD::LDS_BYTES : 16];
+    constexpr int RPG = 64 / LG, RPD = 64 / LD;
+    __shared__ float part[32 * RPD];
+    __shared__ float pick_w[32];
+    __shared__ uint32_t pick_e[32];
+    extern __shared__ __align__(16) float hs[];  // hidden rows, sub-blocks of 32 floats 36 apart
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int K = a.K;
+    // the logits first (waits on loads count in issue order), then the loads that need nothing
+    // from the routing: LDS tables and this lane's x slice
+    float lv[PER];
+    route_load<PER>(a.logits, a.E, lv);
+    TableRegs<FG> tg;
+    TableRegs<FD> td;
+    tg.load(threadIdx.x);
+    td.load(threadIdx.x);
+    const int subg = lane % LG, rsg = lane / LG, nsbg = a.H / 32;
+    float xr[XG][32];
+    load_xs<XG>(xr, a.x, subg, LG, nsbg);
+
+    uint32_t rid;
+    float rw;
+    wave_route<PER>(lv, a.E, K, a.norm, &rid, &rw);
+    uint32_t my_slot = 0xFFFFFFFFu;  // lane j < K: slot of pick j
+    bool absent = false;
+    if (lane < K) {
+        my_slot = a.table ? a.table[rid] : rid;
+        absent = my_slot == CW_NO_SLOT;
+        if (absent) my_slot = 0;
+        if (my_slot >= (uint32_t)a.n_slots) my_slot = 0xFFFFFFFFu;
+    }
+    if (wave == 0 && lane < K) {
+        pick_w[lane] = rw;
+        pick_e[lane] = rid;
+        if (blockIdx.x == 0) {
+            a.ids[lane] = rid;
+            a.w[lane] = rw;
+            if (absent && a.missing) atomicAdd(a.missing, 1u);
+        }
+    }
+
+    // gate / up items (pick j, 2*RPG rows) spread over every wave of the grid; the first
+    // item's weights and the block's first down rows are requested right after routing
+    const int row_items = (a.I + 2 * RPG - 1) / (2 * RPG);
+    const int n_items = K * row_items;
+    const int gwave = blockIdx.x * 4 + wave, total_waves = gridDim.x * 4;
+    typename FG::Raw rg[2][XG], ru[2][XG];
+    auto load_item = [&](int it) {
+        const int j = it / row_items, r0 = (it - j * row_items) * 2 * RPG + rsg;
+        const uint32_t slot = __shfl(my_slot, j);
+        const uint32_t sl = slot == 0xFFFFFFFFu ? 0 : slot;
+        const uint8_t *bg = a.wg + (int64_t)sl * a.sg;
+        const uint8_t *bu = a.wu + (int64_t)sl * a.su;
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int r = r0 + q * RPG;
+#pragma unroll
+            for (int i = 0; i < XG; i++) {
+                const int sb = subg + i * LG;
+                if (r < a.I && sb < nsbg) {
+                    rg[q][i] = FG::load(bg + (int64_t)r * a.rbg, sb);
+                    ru[q][i] = FG::load(bu + (int64_t)r * a.rbg, sb);
+                }
+            }
+        }
+    };
+    if (gwave < n_items) load_item(gwave);
+
+    const int subd = lane % LD, rsd = lane / LD, nsbd = a.P / 32;
+    typename FD::Raw draw[PPW][XD];
+    uint32_t dslot[PPW];
+    {
+        const int r = blockIdx.x * RPD + rsd;
+#pragma unroll
+        for (int q = 0; q < PPW; q++) {
+            const int j = wave + 4 * q;
+            dslot[q] = __shfl(my_slot, j < K ? j : 0);
+            if (j < K && dslot[q] != 0xFFFFFFFFu && r < a.H) {
+                const uint8_t *base = a.wd + (int64_t)dslot[q] * a.sd + (int64_t)r * a.rbd;
+#pragma unroll
+                for (int i = 0; i < XD; i++) {
+                    const int sb = subd + i * LD;
+                    if (sb < nsbd) draw[q][i] = FD::load(base, sb);
+                }
+            }
+        }
+    }
+    tg.store(ldsg, threadIdx.x);
+    td.store(ldsd, threadIdx.x);
+    __syncthreads();
+
+    for (int it = gwave; it < n_items; it += total_waves) {
+        if (it != gwave) load_item(it);
+        const int j = it / row_items, r0 = (it - j * row_items) * 2 * RPG + rsg;
+        const uint32_t slot = __shfl(my_slot, j);
+        const uint32_t expert = __shfl(rid, j);
+        const bool bad = slot == 0xFFFFFFFFu;
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int r = r0 + q * RPG;
+            float g = 0.f, u = 0.f;
+#pragma unroll
+            for (int i = 0; i < XG; i++) {
+                const int sb = subg + i * LG;
+                if (r < a.I && sb < nsbg) {
+                    g += FG::dot(rg[q][i], ldsg, xr[i]);
+                    u += FG::dot(ru[q][i], ldsg, xr[i]);
+                }
+            }
+            g = group_sum<LG>(g);
+            u = group_sum<LG>(u);
+            if (subg == 0 && r < a.I) {
+                float o;
+                if (a.act == CW_ACT_SILU) {
+                    o = g / (1.0f + expf(-g)) * u;
+                } else {
+                    if (a.bg) g += a.bg[(int64_t)expert * a.I + r];
+                    if (a.bu) u += a.bu[(int64_t)expert * a.I + r];
+                    g = fminf(g, a.limit);
+                    u = fminf(fmaxf(u, -a.limit), a.limit);
+                    o = (u + 1.0f) * (g * (1.0f / (1.0f + expf(-(g * a.alpha)))));
+                }
+                store_coherent(a.h + (int64_t)j * a.P + r, bad ? __int_as_float(0x7fc00000) : o);
+            }
+        }
+    }
+    // zero padding of hidden rows up to the width down reads
+    for (int c = gwave * 64 + lane; c < K * (a.P - a.I); c += total_waves * 64) {
+        const int j = c / (a.P - a.I);
+        store_coherent(a.h + (int64_t)j * a.P + a.I + (c - j * (a.P - a.I)), 0.f);
+    }
+
+    const bool ok = grid_barrier(gridDim.x);
+
+    // every hidden row into LDS once per block, read at the coherence point with 8 loads in
+    // flight per thread, and stored with the padding (36 floats per sub-block of 32) that keeps
+    // the 16 sub-block readers of a row on distinct LDS banks
+    {
+        const uint64_t *h64 = (const uint64_t *)a.h;
+        const int nh = K * a.P / 2, hp = a.P / 2;
+        for (int v0 = 0; v0 < nh; v0 += 256 * 8) {
+            uint64_t t[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int v = v0 + 256 * u + threadIdx.x;
+                if (v < nh) t[u] = __hip_atomic_load(h64 + v, __ATOMIC_RELAXED, CW_AGENT);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int v = v0 + 256 * u + threadIdx.x;
+                if (v < nh) {
+                    const int j = v / hp, c = 2 * (v - j * hp);
+                    *(uint64_t *)(hs + (j * nsbd + (c >> 5)) * 36 + (c & 31)) = t[u];
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // down + combine
+    for (int grp_i = blockIdx.x, first = 1; grp_i * RPD < a.H; grp_i += gridDim.x, first = 0) {
+        const int r = grp_i * RPD + rsd;
+        if (!first) {
+#pragma unroll
+            for (int q = 0; q < PPW; q++) {
+                const int j = wave + 4 * q;
+                if (j >= K) break;  // uniform across the wave
+                if (dslot[q] == 0xFFFFFFFFu || r >= a.H) continue;
+#pragma unroll
+                for (int i = 0; i < XD; i++) {
+                    const int sb = subd + i * LD;
+                    if (sb < nsbd) draw[q][i] = FD::load(a.wd + (int64_t)dslot[q] * a.sd + (int64_t)r * a.rbd, sb);
+                }
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < PPW; q++) {
+            const int j = wave + 4 * q;
+            if (j >= K) break;
+            const bool live = dslot[q] != 0xFFFFFFFFu && r < a.H;
+            float d = 0.f;
+#pragma unroll
+            for (int i = 0; i < XD; i++) {
+                const int sb = subd + i * LD;
+                if (live && sb < nsbd) {
+                    float hx[32];
+                    const float4 *src = (const float4 *)(hs + (j * nsbd + sb) * 36);
+#pragma unroll
+                    for (int c = 0; c < 8; c++) *(float4 *)(hx + 4 * c) = src[c];
+                    d += FD::dot(draw[q][i], ldsd, hx);
+                }
+            }
+            d = group_sum<LD>(d);
+            if (subd == 0) part[j * RPD + rsd] = (dslot[q] == 0xFFFFFFFFu || !ok) ? __int_as_float(0x7fc00000) : d;
+        }
+        __syncthreads();
+        if (threadIdx.x < RPD) {
+            const int rr = grp_i * RPD + threadIdx.x;
+            if (rr < a.H) {
+                float acc = 0.f;
+                for (int j = 0; j < K; j++) {
+                    float d = part[j * RPD + threadIdx.x];
+                    if (a.bd) d += a.bd[(int64_t)pick_e[j] * a.H + rr];
+                    acc += pick_w[j] * d;
+                }
+                a.out[rr] = acc;
+            }
+        }
+        __syncthreads();
+    }
+}
+
 // ------------------------------------------------------------------------------ dispatch
 
 static int lpr_for(int nsb) {
@@ -238,6 +525,62 @@ static int by_fmt(int dtype, const MoeArgs &a, int T, hipStream_t s) {
     case CW_IQ3_S: return by_shape<FIQ3_S, DOWN>(a, T, s);
     default: return set_error(CW_ENOTSUP, "moe: dtype %d is not supported", dtype);
     }
+}
+
+// LDS for the staged hidden rows of one decode call: K rows of P floats, 36 per 32
+static size_t decode_hidden_lds(const MoeArgs &a) { return (size_t)a.K * (a.P / 32) * 36 * sizeof(float); }
+static constexpr size_t DECODE_MAX_HIDDEN_LDS = 64 * 1024;
+
+template <class FG, int LG, int XG, class FD, int LD, int XD, int PPW>
+static int decode_launch(const MoeArgs &a, hipStream_t s) {
+    auto kern = a.E <= 256 ? k_moe_decode<FG, LG, XG, FD, LD, XD, 4, PPW> : k_moe_decode<FG, LG, XG, FD, LD, XD, 16, PPW>;
+    const size_t lds = decode_hidden_lds(a);
+    // every block must be resident at once for the barrier: size the grid from the occupancy
+    // at this call's LDS size (remembered per router width for the last size asked)
+    static int per_cu[2] = {0, 0}, cus = 0;
+    static size_t per_cu_lds[2] = {0, 0};
+    const int which = a.E <= 256 ? 0 : 1;
+    if (!per_cu[which] || per_cu_lds[which] != lds) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, 256, lds) != hipSuccess || n < 1)
+            return set_error(CW_EHIP, "moe decode: occupancy query failed");
+        per_cu[which] = n;
+        per_cu_lds[which] = lds;
+    }
+    const int RPD = 64 / LD;
+    const int want = (a.H + RPD - 1) / RPD;
+    int grid = per_cu[which] * cus;
+    if (grid > want) grid = want;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, s, a);
+    return check_launch("k_moe_decode");
+}
+
+template <class FG, int LG, int XG, class FD, int LD, int XD>
+static int decode_ppw(const MoeArgs &a, hipStream_t s) {
+    const int ppw = (a.K + 3) / 4;
+    if (ppw == 1) return decode_launch<FG, LG, XG, FD, LD, XD, 1>(a, s);
+    if (ppw == 2) return decode_launch<FG, LG, XG, FD, LD, XD, 2>(a, s);
+    if (ppw == 3) return decode_launch<FG, LG, XG, FD, LD, XD, 3>(a, s);
+    return CW_ENOTSUP;
+}
+
+// the format / shape pairs of the benchmark configurations; others take the two-kernel path
+int moe_decode(int dtg, int dtd, const MoeArgs &a, hipStream_t s) {
+    if (a.K > 12 || a.E > 1024 || decode_hidden_lds(a) > DECODE_MAX_HIDDEN_LDS) return CW_ENOTSUP;
+    const int nsg = a.H / 32, nsd = a.P / 32;
+    if (dtg == CW_IQ2_XXS && dtd == CW_IQ2_S && nsg == 64 && nsd == 16) return decode_ppw<FIQ2_XXS, 64, 1, FIQ2_S, 16, 1>(a, s);
+    if (dtg == CW_IQ2_XXS && dtd == CW_IQ2_XXS && nsg == 64 && nsd == 16) return decode_ppw<FIQ2_XXS, 64, 1, FIQ2_XXS, 16, 1>(a, s);
+    if (dtg == CW_IQ2_S && dtd == CW_IQ2_S && nsg == 64 && nsd == 16) return decode_ppw<FIQ2_S, 64, 1, FIQ2_S, 16, 1>(a, s);
+    if (dtg == CW_IQ3_S && dtd == CW_Q4_K && nsg == 64 && nsd == 16) return decode_ppw<FIQ3_S, 64, 1, FQ4_K, 16, 1>(a, s);
+    if (dtg == CW_MXFP4 && dtd == CW_MXFP4 && nsg == 90 && nsd == 90) return decode_ppw<FMXFP4, 64, 2, FMXFP4, 64, 2>(a, s);
+    return CW_ENOTSUP;
+}
+
+uint32_t decode_barrier_errors() {
+    DecodeBarrier b = {};
+    if (hipMemcpyFromSymbol(&b, HIP_SYMBOL(g_decode_barrier), sizeof b) != hipSuccess) return 0xFFFFFFFFu;
+    return b.errors;
 }
 
 int moe_gateup(int dtype, const MoeArgs &a, int T, hipStream_t s) { return T ? by_fmt<false>(dtype, a, T, s) : CW_OK; }

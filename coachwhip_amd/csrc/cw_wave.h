@@ -44,37 +44,40 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
 }
 
-// (value, index) order of the router: larger value first, the lower index among equals;
-// index ~0u marks an exhausted candidate.
-__device__ __forceinline__ bool route_better(float va, uint32_t ia, float vb, uint32_t ib) {
-    if (ia == 0xFFFFFFFFu) return false;
-    if (ib == 0xFFFFFFFFu) return true;
-    return va > vb || (va == vb && ia < ib);
+// Router key: the float's bits made order-preserving as an unsigned number, above the bitwise
+// complement of the expert index. The unsigned maximum is then the largest logit, the lowest
+// index among equal logits (the stable descending argsort's order), and 0 marks a taken or absent
+// candidate (every real key is above it).
+__device__ __forceinline__ uint64_t route_key(float v, uint32_t e) {
+    const uint32_t b = __float_as_uint(v);
+    const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((uint64_t)o << 32) | (uint64_t)(0xFFFFFFFFu - e);
 }
+__device__ __forceinline__ float key_value(uint64_t k) {
+    const uint32_t o = (uint32_t)(k >> 32);
+    return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
+}
+__device__ __forceinline__ uint32_t key_index(uint64_t k) { return 0xFFFFFFFFu - (uint32_t)k; }
 
 template <int CTRL>
-__device__ __forceinline__ void argmax_step(float &v, uint32_t &i) {
-    const float ov = dpp_f<CTRL>(v);
-    const uint32_t oi = dpp_u<CTRL>(i);
-    if (route_better(ov, oi, v, i)) { v = ov; i = oi; }
+__device__ __forceinline__ uint64_t max_step(uint64_t k) {
+    const uint64_t o = ((uint64_t)dpp_u<CTRL>((uint32_t)(k >> 32)) << 32) | dpp_u<CTRL>((uint32_t)k);
+    return o > k ? o : k;
 }
-
-// the best (value, index) of the wave, in every lane
-__device__ __forceinline__ void wave_argmax(float &v, uint32_t &i) {
-    argmax_step<0xB1>(v, i);
-    argmax_step<0x4E>(v, i);
-    argmax_step<0x141>(v, i);
-    argmax_step<0x140>(v, i);
-    float bv = readlane_f(v, 0);
-    uint32_t bi = (uint32_t)__builtin_amdgcn_readlane((int)i, 0);
-#pragma unroll
-    for (int row = 16; row < 64; row += 16) {
-        const float rv = readlane_f(v, row);
-        const uint32_t ri = (uint32_t)__builtin_amdgcn_readlane((int)i, row);
-        if (route_better(rv, ri, bv, bi)) { bv = rv; bi = ri; }
-    }
-    v = bv;
-    i = bi;
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t k, int lane) {
+    return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(k >> 32), lane) << 32) |
+           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, lane);
+}
+// the largest key of the wave, in every lane
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
+    k = max_step<0xB1>(k);
+    k = max_step<0x4E>(k);
+    k = max_step<0x141>(k);
+    k = max_step<0x140>(k);
+    uint64_t a = readlane_u64(k, 0), b = readlane_u64(k, 16), c = readlane_u64(k, 32), d = readlane_u64(k, 48);
+    a = a > b ? a : b;
+    c = c > d ? c : d;
+    return a > c ? a : c;
 }
 
 // One wavefront routes one token: softmax over E = 64*PER (or fewer) logits as candle-nn's
@@ -84,41 +87,54 @@ __device__ __forceinline__ void wave_argmax(float &v, uint32_t &i) {
 // monotone and comparing logits is exact. Lane j < K returns pick j's expert in *id and its
 // weight (renormalised over the K when norm) in *w; other lanes return id ~0u.
 template <int PER>
-__device__ __forceinline__ void wave_route(const float *logits, int E, int K, int norm, uint32_t *id, float *w) {
+__device__ __forceinline__ void route_load(const float *logits, int E, float (&v)[PER]) {
     const int lane = threadIdx.x & 63;
-    float v[PER];
 #pragma unroll
     for (int i = 0; i < PER; i++) {
         const int e = lane + 64 * i;
         v[i] = e < E ? logits[e] : -INFINITY;
     }
-    float m = v[0];
+}
+// the routing of logits already loaded by route_load
+template <int PER>
+__device__ __forceinline__ void wave_route(const float (&v)[PER], int E, int K, int norm, uint32_t *id, float *w) {
+    const int lane = threadIdx.x & 63;
+    uint64_t key[PER];
+    float m = -INFINITY;
 #pragma unroll
-    for (int i = 1; i < PER; i++) m = fmaxf(m, v[i]);
-    m = wave_max(m);
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < PER; i++) s += (lane + 64 * i < E) ? expf(v[i] - m) : 0.f;
-    s = wave_sum(s);
-    uint32_t taken = 0;  // bit i: v[i] already picked
-    uint32_t my_id = 0xFFFFFFFFu;
-    float my_v = 0.f;
-    for (int j = 0; j < K; j++) {
-        float bv = -INFINITY;
-        uint32_t bi = 0xFFFFFFFFu;
-#pragma unroll
-        for (int i = 0; i < PER; i++) {
-            const uint32_t e = (uint32_t)(lane + 64 * i);
-            if (e < (uint32_t)E && !((taken >> i) & 1u) && route_better(v[i], e, bv, bi)) { bv = v[i]; bi = e; }
-        }
-        wave_argmax(bv, bi);
-        if ((bi & 63u) == (uint32_t)lane) taken |= 1u << (bi >> 6);
-        if (lane == j) { my_id = bi; my_v = bv; }
+    for (int i = 0; i < PER; i++) {
+        const int e = lane + 64 * i;
+        key[i] = e < E ? route_key(v[i], (uint32_t)e) : 0ull;
+        m = fmaxf(m, v[i]);
     }
-    float p = lane < K ? expf(my_v - m) / s : 0.f;
-    if (norm) p = p / wave_sum(p);
-    *id = my_id;
+    m = wave_max(m);
+    uint64_t mine = 0;
+    for (int j = 0; j < K; j++) {
+        uint64_t best = key[0];
+#pragma unroll
+        for (int i = 1; i < PER; i++) best = key[i] > best ? key[i] : best;
+        best = wave_max_key(best);
+#pragma unroll
+        for (int i = 0; i < PER; i++) key[i] = key[i] == best ? 0ull : key[i];
+        mine = lane == j ? best : mine;
+    }
+    float p = lane < K ? expf(key_value(mine) - m) : 0.f;
+    if (norm) {
+        p = p / wave_sum(p);
+    } else {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < PER; i++) s += lane + 64 * i < E ? expf(v[i] - m) : 0.f;
+        p = p / wave_sum(s);
+    }
+    *id = lane < K ? key_index(mine) : 0xFFFFFFFFu;
     *w = p;
+}
+template <int PER>
+__device__ __forceinline__ void wave_route(const float *logits, int E, int K, int norm, uint32_t *id, float *w) {
+    float v[PER];
+    route_load<PER>(logits, E, v);
+    wave_route<PER>(v, E, K, norm, id, w);
 }
 
 }  // namespace cw

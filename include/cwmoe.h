@@ -23,8 +23,11 @@
  *    caller may fall back, as mv_id.rs:156-179 does with Ok(false)), CW_EINVAL (shape, stride
  *    or argument error, as candle::bail! in crates/engine/src/experts.rs:2204-2217), CW_EHIP
  *    (the HIP runtime failed). cw_last_error() describes the last failure on this thread.
- *  - Calls on distinct streams may run concurrently; the library keeps no mutable global
- *    state apart from one-time initialisation, which is thread-safe.
+ *  - Calls on distinct streams may run concurrently, with one exception: a one-token
+ *    cw_moe_layer call runs as a single persistent launch whose blocks meet at a device-wide
+ *    barrier kept in library state, so two such calls must not overlap on one device (issue
+ *    them on one stream). Set CWMOE_DECODE_KERNELS=2 in the environment to use the two-kernel
+ *    form instead, which has no such state.
  */
 #ifndef CWMOE_H
 #define CWMOE_H
@@ -168,6 +171,12 @@ size_t cw_moe_workspace_size(const cw_moe_desc *desc, int T);
 int cw_moe_layer(const cw_moe_desc *desc, const float *x, const float *logits, int T, float *out,
                  uint32_t *ids_out, float *w_out, uint32_t *missing, void *ws, size_t ws_bytes,
                  cw_stream_t stream);
+
+/* Device-side failures since the library loaded: a one-token layer runs as one persistent
+ * launch whose blocks meet at a device-wide barrier; a barrier wait that times out (a block
+ * could not be scheduled) makes the call's outputs NaN and is counted here. No counterpart in
+ * the reference (its layer is several dispatches). Synchronizes the device. */
+uint32_t cw_device_errors(void);
 
 /* ---- host bank bookkeeping (no GPU) ----------------------------------------------------- */
 
