@@ -28,6 +28,22 @@ def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
 
 
+COPY_BYTES = 1 << 30
+
+
+def copy_calibration(torch, dev):
+    """A plain copy kernel of known size: 1 GiB read, 1 GiB written per launch (an elementwise add
+    of zero, so it is a kernel dispatch and not a DMA copy). HBM counters read on it give the
+    factor that turns the same counters read on the MoE kernels into bytes."""
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.add(src, 0.0, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "launches": 3, "bytes_read_per_launch": COPY_BYTES,
+                      "bytes_written_per_launch": COPY_BYTES}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -38,6 +54,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=3)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain device copy of known size (for scaling HBM counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (experts would shard across GPUs "
@@ -56,6 +74,9 @@ def main():
     cw.lib()  # fails loudly when the HIP library is not built
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        copy_calibration(torch, dev)
+        return
     E, K, H, I = 256, 8, 2048, 512
     dts = (F.IQ2_XXS, F.IQ2_XXS, F.IQ2_S)
     L = args.layers

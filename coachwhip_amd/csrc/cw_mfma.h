@@ -5,8 +5,7 @@
 
 namespace cw {
 
-constexpr int MF_MT = 64;   // activation rows per tile (4 MFMA blocks of 16)
-constexpr int MF_NT = 64;   // weight rows per tile (4 waves x 16)
+constexpr int MF_MT = 64;   // picks per tile (4 MFMA blocks of 16)
 
 struct MfTile {
     int slot, pos0, m, pad;
@@ -35,9 +34,7 @@ struct MfArgs {
     const uint32_t *ids;          // expert of each pick (bias lookup)
     float *h;                     // gate/up: hidden rows in pile order (ldh floats)
     int ldh;
-    const float *w;               // down: routing weight of each pick
-    const float *bias_d;          // down: bias (E x n)
-    float *out;                   // down: (T x n), accumulated atomically
+    float *dn;                    // down: one row of n per pick, in pick order (t*K + j)
 };
 
 bool mfma_supported(int dtype);
@@ -50,5 +47,8 @@ int pack_rows_f16(const float *x, int rows, int k, int ldx, uint16_t *a16, float
 int fill_zero(float *p, int64_t n, hipStream_t s);
 int mfma_gateup(int dtype, const MfArgs &a, int tiles_max, hipStream_t s);
 int mfma_down(int dtype, const MfArgs &a, int tiles_max, hipStream_t s);
+// out[t] = sum_j w[t*K+j] * (dn[t*K+j] + bias[ids[t*K+j]]), picks in order (H a multiple of 4)
+int combine_picks(const float *dn, const float *w, const float *bias, const uint32_t *ids, int T, int K, int H, float *out,
+                  hipStream_t s);
 
 }  // namespace cw

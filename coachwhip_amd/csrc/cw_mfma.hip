@@ -22,8 +22,6 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int A_LD = 256 + 8;   // halves per staged activation row (padding breaks LDS bank conflicts)
-
 __device__ __forceinline__ uint32_t pk_mul_u(uint32_t v, uint32_t sc2) {
     f16x2 a = __builtin_bit_cast(f16x2, v), b = __builtin_bit_cast(f16x2, sc2);
     return __builtin_bit_cast(uint32_t, a * b);
@@ -110,243 +108,336 @@ __device__ __forceinline__ void copy_tab(uint8_t *lds, const Tab<N> &t, int tid,
 }
 
 // ------------------------------------------------------------------------------ formats
-// Per format: TS bytes per block, SBK weights per scale unit, LDS table bytes, the per-lane raw
-// data of one scale unit, the fp16 fragment (8 codes) of K-step ks for lane group grp (weights
-// 8*grp..8*grp+7 of the step's 32), and the unit's f32 scale.
+// Per format: TS bytes per block, SBK weights per scale unit, LDS table bytes, and the decode of
+// one K-step (32 weights) of a row from the row's stage window in LDS (the bytes of 8 K-steps:
+// one IQ super-block, or 8 MXFP4 blocks): lane group grp takes weights 8*grp..8*grp+7 of the
+// step, as 8 fp16 integer codes times a per-lane multiplier.
+
+__device__ __forceinline__ uint32_t lds_u8(const uint8_t *p) { return *p; }
+__device__ __forceinline__ uint32_t lds_u16(const uint8_t *p) { uint16_t v; __builtin_memcpy(&v, p, 2); return v; }
+__device__ __forceinline__ uint32_t lds_u32(const uint8_t *p) { uint32_t v; __builtin_memcpy(&v, p, 4); return v; }
+// 8 bytes at any LDS address: three aligned dwords and a byte shift (a misaligned ds_read_b64
+// measured ~2x slower for the whole stage)
+__device__ __forceinline__ uint2 lds_u64(const uint8_t *p) {
+    const uint32_t a = (uint32_t)(uintptr_t)p & 3;
+    const uint32_t *q = (const uint32_t *)(p - a);
+    const uint32_t d0 = q[0], d1 = q[1], d2 = q[2];
+    return make_uint2(__builtin_amdgcn_alignbyte(d1, d0, a), __builtin_amdgcn_alignbyte(d2, d1, a));
+}
 
 struct MIQ2_XXS {
     static constexpr int TS = 66, SBK = 256, LDS = 256 * 16 + 128 * 16;
-    struct Raw { uint32_t d; uint2 q[8]; };
     static __device__ void fill(uint8_t *lds, int tid, int nt) {
         copy_tab(lds, c_iq2xxs_f16, tid, nt);
         copy_tab(lds + 256 * 16, c_psigns, tid, nt);
     }
-    static __device__ __forceinline__ void load(Raw &r, const uint8_t *row, int u) {
-        const uint8_t *b = row + (int64_t)TS * u;
-        r.d = ld_u16(b);
-#pragma unroll
-        for (int i = 0; i < 8; i++) r.q[i] = ld_u64(b + 2 + 8 * i);
-    }
-    static __device__ __forceinline__ uint4 frag(const Raw &r, int ks, int grp, const uint8_t *lds) {
+    // zero: the super-block scale is 0, so the codes must not contribute
+    static __device__ __forceinline__ uint4 frag(const uint8_t *win, int kk, int grp, const uint8_t *lds, bool zero) {
+        const uint2 q = lds_u64(win + 2 + 8 * kk);
         const uint4 *g = (const uint4 *)lds, *sg = (const uint4 *)(lds + 256 * 16);
-        const uint32_t gi = (r.q[ks].x >> (8 * grp)) & 0xFF;
-        const uint32_t si = (r.q[ks].y >> (7 * grp)) & 127;
-        const uint32_t sc = 2 * (r.q[ks].y >> 28) + 1;
+        const uint32_t gi = (q.x >> (8 * grp)) & 0xFF;
+        const uint32_t si = (q.y >> (7 * grp)) & 127;
+        const uint32_t sc = zero ? 0u : 2 * (q.y >> 28) + 1;
         return scale4(xor4(g[gi], sg[si]), splat_f16((int)sc));
     }
-    static __device__ __forceinline__ float scale(const Raw &r) { return h2f(r.d) * 0.125f; }
+    static __device__ __forceinline__ float scale(const uint8_t *win) { return h2f(lds_u16(win)) * 0.125f; }
 };
 
 struct MIQ2_S {
     static constexpr int TS = 82, SBK = 256, LDS = 1024 * 16 + 256 * 16;
-    struct Raw { uint32_t d; uint32_t qs[8]; uint32_t sg[8]; uint2 qh; uint2 sc; };
     static __device__ void fill(uint8_t *lds, int tid, int nt) {
         copy_tab(lds, c_iq2s_f16, tid, nt);
         copy_tab(lds + 1024 * 16, c_signs, tid, nt);
     }
-    static __device__ __forceinline__ void load(Raw &r, const uint8_t *row, int u) {
-        const uint8_t *b = row + (int64_t)TS * u;
-        r.d = ld_u16(b);
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            r.qs[i] = ld_u32(b + 2 + 4 * i);
-            r.sg[i] = ld_u32(b + 34 + 4 * i);
-        }
-        r.qh = ld_u64(b + 66);
-        r.sc = ld_u64(b + 74);
-    }
-    static __device__ __forceinline__ uint32_t byte8(uint2 v, int i) { return ((i < 4 ? v.x : v.y) >> (8 * (i & 3))) & 0xFF; }
-    static __device__ __forceinline__ uint4 frag(const Raw &r, int ks, int grp, const uint8_t *lds) {
+    static __device__ __forceinline__ uint4 frag(const uint8_t *win, int kk, int grp, const uint8_t *lds, bool zero) {
+        const uint32_t qs = lds_u8(win + 2 + 4 * kk + grp), sgn = lds_u8(win + 34 + 4 * kk + grp);
+        const uint32_t qh = lds_u8(win + 66 + kk), scb = lds_u8(win + 74 + kk);
         const uint4 *g = (const uint4 *)lds, *sg = (const uint4 *)(lds + 1024 * 16);
-        const uint32_t qh = byte8(r.qh, ks);
-        const uint32_t gi = ((r.qs[ks] >> (8 * grp)) & 0xFF) | (((qh >> (2 * grp)) & 3) << 8);
-        const uint32_t si = (r.sg[ks] >> (8 * grp)) & 0xFF;
-        const uint32_t sc = 2 * ((byte8(r.sc, ks) >> (4 * (grp >> 1))) & 0xF) + 1;
-        return scale4(xor4(g[gi], sg[si]), splat_f16((int)sc));
+        const uint32_t gi = qs | (((qh >> (2 * grp)) & 3) << 8);
+        const uint32_t sc = zero ? 0u : 2 * ((scb >> (4 * (grp >> 1))) & 0xF) + 1;
+        return scale4(xor4(g[gi], sg[sgn]), splat_f16((int)sc));
     }
-    static __device__ __forceinline__ float scale(const Raw &r) { return h2f(r.d) * 0.125f; }
+    static __device__ __forceinline__ float scale(const uint8_t *win) { return h2f(lds_u16(win)) * 0.125f; }
 };
 
 struct MIQ3_S {
     static constexpr int TS = 110, SBK = 256, LDS = 512 * 8 + 256 * 16;
-    struct Raw { uint32_t d; uint32_t qs[8]; uint2 qh; uint32_t sg[8]; uint32_t sc; };
     static __device__ void fill(uint8_t *lds, int tid, int nt) {
         copy_tab(lds, c_iq3s_f16, tid, nt);   // entry i as 4 halves at byte 8*i
         copy_tab(lds + 512 * 8, c_signs, tid, nt);
     }
-    static __device__ __forceinline__ void load(Raw &r, const uint8_t *row, int u) {
-        const uint8_t *b = row + (int64_t)TS * u;
-        r.d = ld_u16(b);
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            r.qs[i] = 0;  // filled per lane group below
-            r.sg[i] = ld_u32(b + 74 + 4 * i);
-        }
-        r.qh = ld_u64(b + 66);
-        r.sc = ld_u32(b + 106);
-    }
-    // the two grid bytes of lane group grp in sub-block i sit at 2 + 8*i + 2*grp
-    static __device__ __forceinline__ void load_grp(Raw &r, const uint8_t *row, int u, int grp) {
-        const uint8_t *b = row + (int64_t)TS * u;
-#pragma unroll
-        for (int i = 0; i < 8; i++) r.qs[i] = ld_u16(b + 2 + 8 * i + 2 * grp);
-    }
-    static __device__ __forceinline__ uint4 frag(const Raw &r, int ks, int grp, const uint8_t *lds) {
+    static __device__ __forceinline__ uint4 frag(const uint8_t *win, int kk, int grp, const uint8_t *lds, bool zero) {
+        const uint32_t qs = lds_u16(win + 2 + 8 * kk + 2 * grp), qh = lds_u8(win + 66 + kk);
+        const uint32_t sgn = lds_u8(win + 74 + 4 * kk + grp), scb = lds_u8(win + 106 + (kk >> 1));
         const uint2 *g = (const uint2 *)lds;
         const uint4 *sg = (const uint4 *)(lds + 512 * 8);
-        const uint32_t qh = ((ks < 4 ? r.qh.x : r.qh.y) >> (8 * (ks & 3))) & 0xFF;
-        const uint32_t i0 = (r.qs[ks] & 0xFF) | (((qh >> (2 * grp)) & 1) << 8);
-        const uint32_t i1 = (r.qs[ks] >> 8) | (((qh >> (2 * grp + 1)) & 1) << 8);
-        const uint2 a = g[i0], c = g[i1];
-        const uint32_t si = (r.sg[ks] >> (8 * grp)) & 0xFF;
-        const uint32_t sc = 1 + 2 * ((r.sc >> (4 * ks)) & 0xF);   // nibble ks of the 4 scale bytes
-        return scale4(xor4(make_uint4(a.x, a.y, c.x, c.y), sg[si]), splat_f16((int)sc));
+        const uint32_t i0 = (qs & 0xFF) | (((qh >> (2 * grp)) & 1) << 8);
+        const uint32_t i1 = (qs >> 8) | (((qh >> (2 * grp + 1)) & 1) << 8);
+        const uint2 x = g[i0], y = g[i1];
+        const uint32_t sc = zero ? 0u : 1 + 2 * ((scb >> (4 * (kk & 1))) & 0xF);
+        return scale4(xor4(make_uint4(x.x, x.y, y.x, y.y), sg[sgn]), splat_f16((int)sc));
     }
-    static __device__ __forceinline__ float scale(const Raw &r) { return h2f(r.d); }
+    static __device__ __forceinline__ float scale(const uint8_t *win) { return h2f(lds_u16(win)); }
 };
+
+// MXFP4: one scale (e8m0) per 32 weights, so per K-step. The fragment carries the power of two
+// 2^(e - base) relative to the largest exponent of the row's stage, and the accumulator is
+// rescaled when that base changes; in fp16 the product code * 2^(e - base) is exact down to
+// 2^-24 of the stage's largest block scale (smaller contributions round).
+constexpr Tab<64> make_mxfp4_pairs() {  // fp16 pair of the doubled-E2M1 codes (lo, hi), index lo | hi << 4
+    Tab<64> t{};
+    const int kv[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
+    uint32_t w[256] = {};
+    for (int i = 0; i < 256; i++) {
+        uint32_t h[2] = {};
+        for (int q = 0; q < 2; q++) {
+            const int v = kv[(i >> (4 * q)) & 15];
+            h[q] = f16_int((uint32_t)(v < 0 ? -v : v)) | (v < 0 ? 0x8000u : 0u);
+        }
+        w[i] = h[0] | (h[1] << 16);
+    }
+    for (int i = 0; i < 64; i++) t.v[i] = U4{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]};
+    return t;
+}
+static __constant__ Tab<64> c_mxfp4_pairs = make_mxfp4_pairs();
 
 struct MMXFP4 {
-    static constexpr int TS = 17, SBK = 32, LDS = 16;
-    struct Raw { uint32_t e; uint2 q; };
-    static __device__ void fill(uint8_t *, int, int) {}
-    static __device__ __forceinline__ void load(Raw &r, const uint8_t *row, int u) {
-        r.e = 0;
-        r.q = make_uint2(0, 0);
-        (void)row; (void)u;
+    static constexpr int TS = 17, SBK = 32, LDS = 1024;
+    static __device__ void fill(uint8_t *lds, int tid, int nt) { copy_tab(lds, c_mxfp4_pairs, tid, nt); }
+    static __device__ __forceinline__ uint32_t expo(const uint8_t *win, int kk) { return lds_u8(win + TS * kk); }
+    static __device__ __forceinline__ uint32_t pair(const uint32_t *tab, uint32_t w) {
+        return tab[(w & 0xF) | ((w >> 4) & 0xF0)];
     }
-    // lane group grp takes the low (grp < 2) or high nibbles of bytes 8*(grp&1)..+8
-    static __device__ __forceinline__ void load_grp(Raw &r, const uint8_t *row, int u, int grp) {
-        const uint8_t *b = row + (int64_t)TS * u;
-        r.e = b[0];
-        r.q = ld_u64(b + 1 + 8 * (grp & 1));
-    }
-    static __device__ __forceinline__ uint32_t pair(uint32_t w, int b) {
-        // doubled-E2M1 codes in bytes b and b+1 of w, as two fp16 integers
-        const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)kv_mxfp4((w >> (8 * b)) & 0xF));
-        const uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16)kv_mxfp4((w >> (8 * b + 8)) & 0xF));
-        return lo | (hi << 16);
-    }
-    static __device__ __forceinline__ uint4 frag(const Raw &r, int ks, int grp, const uint8_t *) {
-        (void)ks;
+    // lane group grp takes the low (grp < 2) or high nibbles of bytes 8*(grp&1)..+8; mult is the
+    // splatted fp16 2^(e - base)
+    static __device__ __forceinline__ uint4 frag_mx(const uint8_t *win, int kk, int grp, const uint8_t *lds, uint32_t mult) {
+        const uint2 q = lds_u64(win + TS * kk + 1 + 8 * (grp & 1));
+        const uint32_t *tab = (const uint32_t *)lds;
         const int sh = 4 * (grp >> 1);
-        const uint32_t a = (r.q.x >> sh) & 0x0F0F0F0F, b = (r.q.y >> sh) & 0x0F0F0F0F;
-        return make_uint4(pair(a, 0), pair(a, 2), pair(b, 0), pair(b, 2));
+        const uint32_t a = (q.x >> sh) & 0x0F0F0F0F, b = (q.y >> sh) & 0x0F0F0F0F;
+        return scale4(make_uint4(pair(tab, a), pair(tab, a >> 16), pair(tab, b), pair(tab, b >> 16)), mult);
     }
-    static __device__ __forceinline__ float scale(const Raw &r) { return e8m0_half(r.e); }
 };
 
-template <class MF, typename = void>
-struct has_grp_load { static constexpr bool value = false; };
+// fp16 bits of 2^x for x <= 0 (0 below the subnormal range), splatted to both halves
+__device__ __forceinline__ uint32_t pow2_f16x2(int x) {
+    const uint32_t h = x >= -14 ? (uint32_t)(x + 15) << 10 : (x >= -24 ? 1u << (x + 24) : 0u);
+    return h | (h << 16);
+}
+
+// A stage is 8 K-steps (256 weights of k). The window of a row for a stage holds the stage's
+// bytes (an IQ super-block, or 8 MXFP4 blocks) from the 16-byte boundary at or below their
+// start, in PCS pieces of 16 bytes.
 template <class MF>
-struct has_grp_load<MF, decltype((void)&MF::load_grp, void())> { static constexpr bool value = true; };
+struct Win {
+    static constexpr int SEG = MF::SBK == 32 ? 8 * MF::TS : MF::TS;
+    static constexpr int PCS = (SEG + (MF::TS % 2 ? 15 : 14) + 15) / 16;
+    static constexpr int BYTES = 16 * PCS;
+};
 
 // ------------------------------------------------------------------------------ kernels
 
 __device__ __forceinline__ f16x8 as_f16x8(uint4 v) { return __builtin_bit_cast(f16x8, v); }
 
-// MODE 0: gate and up (two matrices) with the activation, hidden rows written in pile order.
-// MODE 1: down, the pick's routing weight (and bias) applied, accumulated into out[token].
-// A block owns one M-tile (up to 64 picks of a slot) and NTB consecutive N-tiles of 64 weight
-// rows; k streams through LDS in chunks of 256 (8 K-steps). Latency is hidden by occupancy
-// (several blocks per CU).
-template <class MF, int MODE, int NTB>
-__global__ __launch_bounds__(256) void k_mfma(const MfArgs a) {
+// 16 bytes from global memory to LDS without passing through registers: lane l of the wave
+// writes lds_base + 16*l (lds_base is the same for the whole wave)
+__device__ __forceinline__ void dma16(const void *g, uint8_t *lds_base) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)lds_base, 16, 0, 0);
+}
+
+// Tile shape of the grouped GEMM: a block owns one M-tile (up to 64 picks of a slot, in 16-row
+// pick blocks) and RPB weight rows per matrix. Each of the 4 waves takes NB blocks of 16 rows in
+// each of its NM matrices (gate and up together for MODE 0, so the activation sees both) and
+// every pick block: per K-step it reads one activation fragment per pick block, decodes NM*NB
+// weight fragments and issues up to 4*NM*NB MFMAs.
+template <class MF, int MODE>
+struct GmShape {
+    static constexpr int NM = MODE == 0 ? 2 : 1;
+    static constexpr int NB = MODE == 0 ? 2 : 4;
+    static constexpr int RPW = 16 * NB, RPB = 4 * RPW;
+    static constexpr int A_BYTES = 8 * 4 * 64 * 16;                 // one stage of activations
+    static constexpr int W_BYTES = NM * RPB * Win<MF>::BYTES;       // one stage of weight windows
+    static constexpr size_t lds_bytes() { return ((MF::LDS + 15) & ~15) + A_BYTES + W_BYTES; }
+};
+
+// MODE 0: gate and up with the activation, hidden rows written in pile order.
+// MODE 1: down, one output row per pick (combined per token by k_combine, in pick order, so the
+//         result does not depend on the order blocks finish in).
+//
+// Per stage of 8 K-steps, the block copies its activations and the weight bytes of its rows
+// into LDS with direct global-to-LDS loads: activations in MFMA fragment order ([K-step][pick
+// block][lane] x 16 bytes, so every fragment read is one conflict-free ds_read_b128), weights as
+// one window of whole 16-byte pieces per row (each load instruction covers 1 KB of consecutive
+// pieces, instead of a few bytes from each of 16 rows). Latency is hidden by the second block
+// on the CU. A piece is loaded only when it holds a byte of the row's stage; an aligned 16-byte
+// piece cannot cross a page boundary, so its other bytes are mapped memory too.
+//
+// Scales: the accumulator of a weight row carries a running scale. When a new scale unit starts
+// (an IQ super-block, or an MXFP4 stage), the accumulator is multiplied by old/new scale and the
+// unit's codes accumulate on top; the epilogue multiplies by the last scale. This keeps one
+// accumulator per output instead of a partial sum per scale unit.
+template <class MF, int MODE>
+__global__ __launch_bounds__(256, 2) void k_gmm(const MfArgs a) {
+    using S = GmShape<MF, MODE>;
+    using W = Win<MF>;
+    constexpr int NM = S::NM, NB = S::NB, KST = 8;
+    constexpr bool POW2 = MF::SBK == 32;
     extern __shared__ __align__(16) uint8_t smem[];
     uint8_t *tab = smem;
-    _Float16 *As = (_Float16 *)(smem + ((MF::LDS + 15) & ~15));
-    constexpr int UPC = 256 / MF::SBK;   // scale units per chunk
-    constexpr int KPU = MF::SBK / 32;    // K-steps per scale unit
-    const int n_nt = (a.n + MF_NT - 1) / MF_NT;
-    const int groups = (n_nt + NTB - 1) / NTB;
-    // blocks go to XCDs round-robin; block b of each run of 8*groups takes M-tile 8*run + b%8
-    // and N-group b/8, so an M-tile's N-groups share an XCD and every XCD gets valid tiles
-    const int run = blockIdx.x / (8 * groups), b = blockIdx.x - run * 8 * groups;
+    uint8_t *As = smem + ((MF::LDS + 15) & ~15);
+    uint8_t *Ws = As + S::A_BYTES;
+    const int n_nb = (a.n + S::RPB - 1) / S::RPB;
+    // blocks go to XCDs round-robin; block b of each run of 8*n_nb takes M-tile 8*run + b%8 and
+    // N-block b/8, so an M-tile's N-blocks share an XCD (and its L2 copy of the activations)
+    const int run = blockIdx.x / (8 * n_nb), b = blockIdx.x - run * 8 * n_nb;
     const int mt = run * 8 + (b & 7);
     if (mt >= *a.n_tiles) return;  // whole block exits before any barrier
-    const int nt_begin = (b >> 3) * NTB, nt_end = min(nt_begin + NTB, n_nt);
+    const int nblk = b >> 3;
     const MfTile tile = a.tiles[mt];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = lane >> 4, l16 = lane & 15;
+    const int mbs = (tile.m + 15) >> 4;
     MF::fill(tab, tid, 256);
-    const int n_ks = a.k / 32;
 
-    for (int nt = nt_begin; nt < nt_end; nt++) {
-        const int n = nt * MF_NT + wave * 16 + l16;   // this lane's weight row
-        const bool nv = n < a.n;
-        const uint8_t *r0 = a.w0 + (int64_t)tile.slot * a.s0 + (int64_t)(nv ? n : 0) * a.row_bytes;
-        const uint8_t *r1 = MODE == 0 ? a.w1 + (int64_t)tile.slot * a.s1 + (int64_t)(nv ? n : 0) * a.row_bytes : r0;
-        f32x4 acc0[4], acc1[4];
+    // the activation row this lane copies: pick block `wave`, row l16, k-group grp
+    const bool stager = wave < mbs;
+    const int apos = tile.pos0 + min(16 * wave + l16, tile.m - 1);
+    const uint16_t *asrc = a.a16 + (int64_t)(a.rows ? a.rows[apos] : apos) * a.lda + 8 * grp;
+
+    // row r of the block (r < NM*RPB: matrix r / RPB, row nblk*RPB + r % RPB; rows past n read row 0)
+    auto row_ptr = [&](int r) -> const uint8_t * {
+        const int m = r / S::RPB, n = nblk * S::RPB + (r - m * S::RPB);
+        const int64_t roff = (int64_t)(n < a.n ? n : 0) * a.row_bytes;
+        return (m == 0 ? a.w0 + (int64_t)tile.slot * a.s0 : a.w1 + (int64_t)tile.slot * a.s1) + roff;
+    };
+
+    const int n_ks = a.k / 32, n_st = (n_ks + KST - 1) / KST;
+    f32x4 acc[NM][NB][4];
+    float rs[NM][NB];     // running scale (IQ) ...
+    int rb[NM][NB];       // ... or running base exponent (MXFP4)
+    uint32_t lrow[NM][NB];  // this lane's window row within the block's windows
+    uintptr_t lptr[NM][NB]; // this lane's row in global memory (its alignment gives the shift)
 #pragma unroll
-        for (int mb = 0; mb < 4; mb++) { acc0[mb] = f32x4{0, 0, 0, 0}; acc1[mb] = f32x4{0, 0, 0, 0}; }
-        for (int c0 = 0; c0 < n_ks; c0 += 8) {
-            const int nks = min(8, n_ks - c0);
-            __syncthreads();  // previous chunk's readers are done
-            for (int idx = tid; idx < MF_MT * 32; idx += 256) {
-                const int r = idx >> 5, c = idx & 31;
-                uint4 v = make_uint4(0, 0, 0, 0);
-                if (r < tile.m && c < nks * 4) {
-                    const int pos = tile.pos0 + r;
-                    const int src = a.rows ? a.rows[pos] : pos;
-                    v = *(const uint4 *)(a.a16 + (int64_t)src * a.lda + (int64_t)c0 * 32 + c * 8);
-                }
-                *(uint4 *)(As + r * A_LD + c * 8) = v;
-            }
-            typename MF::Raw raw0[UPC], raw1[UPC];
+    for (int m = 0; m < NM; m++)
 #pragma unroll
-            for (int u = 0; u < UPC; u++) {
-                const int unit = c0 / KPU + u;
-                if (u * KPU < nks) {
-                    MF::load(raw0[u], r0, unit);
-                    if constexpr (has_grp_load<MF>::value) MF::load_grp(raw0[u], r0, unit, grp);
-                    if constexpr (MODE == 0) {
-                        MF::load(raw1[u], r1, unit);
-                        if constexpr (has_grp_load<MF>::value) MF::load_grp(raw1[u], r1, unit, grp);
-                    }
-                }
-            }
-            __syncthreads();
+        for (int q = 0; q < NB; q++) {
+            rs[m][q] = 1.f;
+            rb[m][q] = 0;
+            lrow[m][q] = m * S::RPB + wave * S::RPW + 16 * q + l16;
+            lptr[m][q] = (uintptr_t)row_ptr(lrow[m][q]);
 #pragma unroll
-            for (int u = 0; u < UPC; u++) {
-                if (u * KPU >= nks) break;
-                f32x4 p0[4], p1[4];
-#pragma unroll
-                for (int mb = 0; mb < 4; mb++) { p0[mb] = f32x4{0, 0, 0, 0}; p1[mb] = f32x4{0, 0, 0, 0}; }
-#pragma unroll
-                for (int ks = 0; ks < KPU; ks++) {
-                    const int kk = u * KPU + ks;
-                    const f16x8 b0 = as_f16x8(MF::frag(raw0[u], ks, grp, tab));
-                    f16x8 b1;
-                    if constexpr (MODE == 0) b1 = as_f16x8(MF::frag(raw1[u], ks, grp, tab));
-#pragma unroll
-                    for (int mb = 0; mb < 4; mb++) {
-                        const f16x8 av = as_f16x8(*(const uint4 *)(As + (16 * mb + l16) * A_LD + kk * 32 + 8 * grp));
-                        p0[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b0, p0[mb], 0, 0, 0);
-                        if constexpr (MODE == 0) p1[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b1, p1[mb], 0, 0, 0);
-                    }
-                }
-                const float s0 = MF::scale(raw0[u]);
-                const float s1 = MODE == 0 ? MF::scale(raw1[u]) : 0.f;
-#pragma unroll
-                for (int mb = 0; mb < 4; mb++) {
-                    acc0[mb] += s0 * p0[mb];
-                    if constexpr (MODE == 0) acc1[mb] += s1 * p1[mb];
-                }
-            }
+            for (int mb = 0; mb < 4; mb++) acc[m][q][mb] = f32x4{0, 0, 0, 0};
         }
 
-        // epilogue: lane holds rows 16*mb + 4*grp + i (i < 4) of weight row n
-        if (!nv) continue;
+    for (int st = 0; st < n_st; st++) {
+        if (st) __syncthreads();  // every wave is done with the previous stage's LDS
+        const int nk = min(KST, n_ks - st * KST);   // K-steps in this stage
+        const int seg = POW2 ? MF::TS * nk : MF::TS; // bytes of a row in this stage
+        if (stager) {
 #pragma unroll
-        for (int mb = 0; mb < 4; mb++) {
+            for (int kk = 0; kk < KST; kk++)
+                if (kk < nk) dma16(asrc + (st * KST + kk) * 32, As + ((kk * 4 + wave) * 64) * 16);
+        }
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int r = 16 * mb + 4 * grp + i;
-                if (r >= tile.m) continue;
-                const int pos = tile.pos0 + r;
-                const int src = a.rows ? a.rows[pos] : pos;
-                const float sa = a.ascale[src];
-                const int pick = a.pile_pick[pos];
+        for (int t = 0; t < W::PCS; t++) {
+            const int i = tid + 256 * t, r = i / W::PCS, p = i - r * W::PCS;
+            const uint8_t *o = row_ptr(r) + (int64_t)W::SEG * st;
+            const uint8_t *base = (const uint8_t *)((uintptr_t)o & ~(uintptr_t)15);
+            if (base + 16 * p < o + seg) dma16(base + 16 * p, Ws + (256 * t + 64 * wave) * 16);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+
+        // this lane's windows
+        const uint8_t *win[NM][NB];
+#pragma unroll
+        for (int m = 0; m < NM; m++)
+#pragma unroll
+            for (int q = 0; q < NB; q++)
+                win[m][q] = Ws + lrow[m][q] * W::BYTES + ((lptr[m][q] + (uintptr_t)W::SEG * st) & 15);
+
+        bool zero[NM][NB];
+        if constexpr (POW2) {
+#pragma unroll
+            for (int m = 0; m < NM; m++)
+#pragma unroll
+                for (int q = 0; q < NB; q++) {
+                    zero[m][q] = false;
+                    int base = 0;
+#pragma unroll
+                    for (int kk = 0; kk < KST; kk++)
+                        if (kk < nk) base = max(base, (int)MF::expo(win[m][q], kk));
+                    if (st > 0 && base != rb[m][q]) {
+#pragma unroll
+                        for (int mb = 0; mb < 4; mb++)
+#pragma unroll
+                            for (int i = 0; i < 4; i++) acc[m][q][mb][i] = ldexpf(acc[m][q][mb][i], rb[m][q] - base);
+                    }
+                    rb[m][q] = base;
+                }
+        } else {
+#pragma unroll
+            for (int m = 0; m < NM; m++)
+#pragma unroll
+                for (int q = 0; q < NB; q++) {
+                    const float d = MF::scale(win[m][q]);
+                    zero[m][q] = d == 0.f;
+                    if (d != 0.f) {
+                        const float ratio = __fdividef(rs[m][q], d);
+#pragma unroll
+                        for (int mb = 0; mb < 4; mb++) acc[m][q][mb] *= ratio;
+                        rs[m][q] = d;
+                    }
+                }
+        }
+
+#pragma unroll
+        for (int kk = 0; kk < KST; kk++) {
+            if (kk >= nk) break;
+            f16x8 bf[NM][NB];
+#pragma unroll
+            for (int m = 0; m < NM; m++)
+#pragma unroll
+                for (int q = 0; q < NB; q++) {
+                    if constexpr (POW2)
+                        bf[m][q] = as_f16x8(MF::frag_mx(win[m][q], kk, grp, tab, pow2_f16x2((int)MF::expo(win[m][q], kk) - rb[m][q])));
+                    else
+                        bf[m][q] = as_f16x8(MF::frag(win[m][q], kk, grp, tab, zero[m][q]));
+                }
+#pragma unroll
+            for (int mb = 0; mb < 4; mb++) {
+                if (mb >= mbs) break;
+                const f16x8 av = *(const f16x8 *)(As + ((kk * 4 + mb) * 64 + lane) * 16);
+#pragma unroll
+                for (int m = 0; m < NM; m++)
+#pragma unroll
+                    for (int q = 0; q < NB; q++)
+                        acc[m][q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bf[m][q], acc[m][q][mb], 0, 0, 0);
+            }
+        }
+    }
+
+    // epilogue: lane holds picks 16*mb + 4*grp + i (i < 4) of weight row n (block q)
+    float fs[NM][NB];
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+#pragma unroll
+        for (int q = 0; q < NB; q++) fs[m][q] = POW2 ? ldexpf(1.0f, rb[m][q] - 128) : rs[m][q];
+#pragma unroll
+    for (int mb = 0; mb < 4; mb++) {
+        if (mb >= mbs) break;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = 16 * mb + 4 * grp + i;
+            if (r >= tile.m) continue;
+            const int pos = tile.pos0 + r;
+            const float sa = a.ascale[a.rows ? a.rows[pos] : pos];
+            const int pick = a.pile_pick[pos];
+#pragma unroll
+            for (int q = 0; q < NB; q++) {
+                const int n = nblk * S::RPB + wave * S::RPW + 16 * q + l16;
+                if (n >= a.n) continue;
                 if constexpr (MODE == 0) {
-                    float g = acc0[mb][i] * sa, u = acc1[mb][i] * sa, o;
+                    float g = acc[0][q][mb][i] * fs[0][q] * sa, u = acc[NM - 1][q][mb][i] * fs[NM - 1][q] * sa, o;
                     if (a.act == CW_ACT_SILU) {
                         o = g / (1.0f + expf(-g)) * u;
                     } else {
@@ -359,9 +450,7 @@ __global__ __launch_bounds__(256) void k_mfma(const MfArgs a) {
                     }
                     a.h[(int64_t)pos * a.ldh + n] = o;
                 } else {
-                    float v = acc0[mb][i] * sa;
-                    if (a.bias_d) v += a.bias_d[(int64_t)a.ids[pick] * a.n + n];
-                    atomicAdd(a.out + (int64_t)(pick / a.K) * a.n + n, a.w[pick] * v);
+                    a.dn[(int64_t)pick * a.n + n] = acc[0][q][mb][i] * fs[0][q] * sa;
                 }
             }
         }
@@ -371,28 +460,40 @@ __global__ __launch_bounds__(256) void k_mfma(const MfArgs a) {
 // ------------------------------------------------------------------------------ helpers
 
 // One block: histogram of slots, exclusive scans, scatter of picks into per-slot piles, tiles.
+// Each thread reads its (up to) PILE_PER slots of a chunk into registers before using any, so
+// the loads overlap; the order of picks inside a pile does not matter (every pick's outputs are
+// computed independently of the other rows of its tile).
+constexpr int PILE_PER = 16;
 __global__ __launch_bounds__(1024) void k_piles(const uint32_t *slots, int TK, int K, int n_slots, int *pile_pick,
                                                  int *pile_tok, MfTile *tiles, int *n_tiles) {
     __shared__ int cnt[1024], off[1024], toff[1024], cur[1024];
     const int tid = threadIdx.x;
-    for (int s = tid; s < 1024; s += blockDim.x) { cnt[s] = 0; cur[s] = 0; }
+    cnt[tid] = 0;
+    cur[tid] = 0;
     __syncthreads();
-    for (int i = tid; i < TK; i += blockDim.x) {
-        const uint32_t s = slots[i];
-        if (s < (uint32_t)n_slots) atomicAdd(&cnt[s], 1);
+    for (int c0 = 0; c0 < TK; c0 += 1024 * PILE_PER) {
+        uint32_t v[PILE_PER];
+#pragma unroll
+        for (int q = 0; q < PILE_PER; q++) {
+            const int i = c0 + q * 1024 + tid;
+            v[q] = i < TK ? slots[i] : 0xFFFFFFFFu;
+        }
+#pragma unroll
+        for (int q = 0; q < PILE_PER; q++)
+            if (v[q] < (uint32_t)n_slots) atomicAdd(&cnt[v[q]], 1);
     }
     __syncthreads();
     // inclusive scans of counts and tile counts (Hillis-Steele over 1024 entries)
-    int c = tid < n_slots ? cnt[tid] : 0;
-    int tc = (c + MF_MT - 1) / MF_MT;
+    const int c = tid < n_slots ? cnt[tid] : 0;
+    const int tc = (c + MF_MT - 1) / MF_MT;
     off[tid] = c;
     toff[tid] = tc;
     __syncthreads();
     for (int d = 1; d < 1024; d <<= 1) {
-        const int a = tid >= d ? off[tid - d] : 0, b = tid >= d ? toff[tid - d] : 0;
+        const int x = tid >= d ? off[tid - d] : 0, y = tid >= d ? toff[tid - d] : 0;
         __syncthreads();
-        off[tid] += a;
-        toff[tid] += b;
+        off[tid] += x;
+        toff[tid] += y;
         __syncthreads();
     }
     const int my_off = off[tid] - c, my_toff = toff[tid] - tc;
@@ -402,31 +503,75 @@ __global__ __launch_bounds__(1024) void k_piles(const uint32_t *slots, int TK, i
     __syncthreads();
     if (tid < n_slots)
         for (int q = 0; q < tc; q++) tiles[my_toff + q] = MfTile{tid, my_off + q * MF_MT, min(MF_MT, c - q * MF_MT), 0};
-    for (int i = tid; i < TK; i += blockDim.x) {
-        const uint32_t s = slots[i];
-        if (s < (uint32_t)n_slots) {
-            const int pos = off[s] + atomicAdd(&cur[s], 1);
-            pile_pick[pos] = i;
-            pile_tok[pos] = i / K;
+    for (int c0 = 0; c0 < TK; c0 += 1024 * PILE_PER) {
+        uint32_t v[PILE_PER];
+#pragma unroll
+        for (int q = 0; q < PILE_PER; q++) {
+            const int i = c0 + q * 1024 + tid;
+            v[q] = i < TK ? slots[i] : 0xFFFFFFFFu;
+        }
+#pragma unroll
+        for (int q = 0; q < PILE_PER; q++) {
+            const int i = c0 + q * 1024 + tid;
+            if (v[q] < (uint32_t)n_slots) {
+                const int pos = off[v[q]] + atomicAdd(&cur[v[q]], 1);
+                pile_pick[pos] = i;
+                pile_tok[pos] = i / K;
+            }
         }
     }
 }
 
-// one wave per row: scale = 2^(14 - floor(log2 max|x|)) keeps the row's largest value in
-// [2^14, 2^15) of fp16; ascale receives 1/scale
+// One wave per row, the row held in registers (NV float4 per lane, k <= 256*NV): scale =
+// 2^(15 - e) with max|x| in [2^(e-1), 2^e) keeps the row's largest value in [2^14, 2^15) of
+// fp16; ascale receives 1/scale.
+template <int NV>
 __global__ __launch_bounds__(256) void k_pack_f16(const float *x, int rows, int k, int ldx, uint16_t *a16, float *ascale) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= rows) return;
     const float *xr = x + (int64_t)row * ldx;
+    float4 v[NV];
     float m = 0.f;
-    for (int c = lane; c < k; c += 64) m = fmaxf(m, fabsf(xr[c]));
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int c = 4 * lane + 256 * i;
+        v[i] = c < k ? *(const float4 *)(xr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    }
     m = wave_max(m);
     int ex = 0;
-    if (m > 0.f && m < INFINITY) { frexpf(m, &ex); ex = 15 - ex; }  // m in [2^(e-1), 2^e)
+    if (m > 0.f && m < INFINITY) { frexpf(m, &ex); ex = 15 - ex; }
     const float sc = ldexpf(1.0f, ex);
     uint16_t *o = a16 + (int64_t)row * k;
-    for (int c = lane; c < k; c += 64) o[c] = __builtin_bit_cast(uint16_t, (_Float16)(xr[c] * sc));
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int c = 4 * lane + 256 * i;
+        if (c < k) {
+            const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)(v[i].x * sc)) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(v[i].y * sc)) << 16);
+            const uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16)(v[i].z * sc)) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(v[i].w * sc)) << 16);
+            *(uint2 *)(o + c) = make_uint2(lo, hi);
+        }
+    }
     if (lane == 0) ascale[row] = ldexpf(1.0f, -ex);
+}
+
+// one thread per 4 outputs of a token: the weighted sum of its K picks' rows, bias added per pick
+__global__ __launch_bounds__(256) void k_combine(const float *dn, const float *w, const float *bias, const uint32_t *ids, int K,
+                                                 int H, float *out) {
+    const int t = blockIdx.y, j = 4 * (blockIdx.x * 256 + threadIdx.x);
+    if (j >= H) return;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int e = 0; e < K; e++) {
+        const int64_t pick = (int64_t)t * K + e;
+        float4 d = *(const float4 *)(dn + pick * H + j);
+        if (bias) {
+            const float4 b = *(const float4 *)(bias + (int64_t)ids[pick] * H + j);
+            d.x += b.x; d.y += b.y; d.z += b.z; d.w += b.w;
+        }
+        const float we = w[pick];
+        acc.x += d.x * we; acc.y += d.y * we; acc.z += d.z * we; acc.w += d.w * we;
+    }
+    *(float4 *)(out + (int64_t)t * H + j) = acc;
 }
 
 __global__ void k_fill_zero(float *p, int64_t n) {
@@ -448,8 +593,22 @@ int mfma_piles(const uint32_t *slots, int TK, int K, int n_slots, int *pile_pick
 
 int pack_rows_f16(const float *x, int rows, int k, int ldx, uint16_t *a16, float *ascale, hipStream_t s) {
     if (rows == 0) return CW_OK;
-    hipLaunchKernelGGL(k_pack_f16, dim3((rows + 3) / 4), dim3(256), 0, s, x, rows, k, ldx, a16, ascale);
-    return check_launch("k_pack_f16");
+    if (k % 4 || ldx % 4) return set_error(CW_ENOTSUP, "pack: row of %d (stride %d) is not whole float4s", k, ldx);
+    const dim3 grid((rows + 3) / 4);
+    const int nv = (k + 255) / 256;
+#define CW_PACK(N) \
+    if (nv <= N) { hipLaunchKernelGGL(k_pack_f16<N>, grid, dim3(256), 0, s, x, rows, k, ldx, a16, ascale); return check_launch("k_pack_f16"); }
+    CW_PACK(2) CW_PACK(4) CW_PACK(8) CW_PACK(12) CW_PACK(16) CW_PACK(32)
+#undef CW_PACK
+    return set_error(CW_ENOTSUP, "pack: rows of %d above 8192", k);
+}
+
+int combine_picks(const float *dn, const float *w, const float *bias, const uint32_t *ids, int T, int K, int H, float *out,
+                  hipStream_t s) {
+    if (T == 0) return CW_OK;
+    if (H % 4) return set_error(CW_ENOTSUP, "combine: width %d is not a multiple of 4", H);
+    hipLaunchKernelGGL(k_combine, dim3((H / 4 + 255) / 256, T), dim3(256), 0, s, dn, w, bias, ids, K, H, out);
+    return check_launch("k_combine");
 }
 
 int fill_zero(float *p, int64_t n, hipStream_t s) {
@@ -459,21 +618,20 @@ int fill_zero(float *p, int64_t n, hipStream_t s) {
     return check_launch("k_fill_zero");
 }
 
-template <class MF, int MODE, int NTB>
-static int launch_v(const MfArgs &a, int tiles_max, hipStream_t s) {
-    const size_t shmem = ((MF::LDS + 15) & ~15) + (size_t)MF_MT * A_LD * 2;
-    const int n_nt = (a.n + MF_NT - 1) / MF_NT;
-    const int64_t blocks = (int64_t)((tiles_max + 7) / 8) * 8 * ((n_nt + NTB - 1) / NTB);
-    hipLaunchKernelGGL((k_mfma<MF, MODE, NTB>), dim3((unsigned)blocks), dim3(256), shmem, s, a);
-    return check_launch("k_mfma");
-}
-
 template <class MF, int MODE>
 static int launch(const MfArgs &a, int tiles_max, hipStream_t s) {
-    if (a.k % 32) return set_error(CW_ENOTSUP, "mfma: k %d is not a multiple of 32", a.k);
-    // short rows (down's k = expert FFN) do little work per N-tile: a block takes four
-    if (a.k <= 1024) return launch_v<MF, MODE, 4>(a, tiles_max, s);
-    return launch_v<MF, MODE, 1>(a, tiles_max, s);
+    using S = GmShape<MF, MODE>;
+    if (a.k % MF::SBK) return set_error(CW_ENOTSUP, "mfma: k %d is not a multiple of %d", a.k, MF::SBK);
+    const int n_nb = (a.n + S::RPB - 1) / S::RPB;
+    const int64_t blocks = (int64_t)((tiles_max + 7) / 8) * 8 * n_nb;
+    static bool lds_set = false;  // dynamic LDS above 64 KB is opted into once per kernel
+    if (!lds_set) {
+        if (hipFuncSetAttribute((const void *)k_gmm<MF, MODE>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::lds_bytes()) != hipSuccess)
+            return set_error(CW_EHIP, "mfma: cannot reserve %zu bytes of LDS", S::lds_bytes());
+        lds_set = true;
+    }
+    hipLaunchKernelGGL((k_gmm<MF, MODE>), dim3((unsigned)blocks), dim3(256), S::lds_bytes(), s, a);
+    return check_launch("k_gmm");
 }
 
 template <int MODE>

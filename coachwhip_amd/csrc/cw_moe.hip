@@ -99,7 +99,7 @@ struct MoeLayout {
     size_t ids, w, slots, g, u, h, total;
     // grouped (MFMA) path
     bool grouped;
-    size_t pile_pick, pile_tok, tiles, n_tiles, x16, xscale, h16, hscale;
+    size_t pile_pick, pile_tok, tiles, n_tiles, x16, xscale, h16, hscale, dn;
 };
 
 // Token count from which the layer runs as grouped MFMA GEMMs instead of per-pick matvecs
@@ -175,6 +175,7 @@ static MoeLayout layout(const cw_moe_desc *d, int T) {
         L.xscale = off; off = align256(off + (size_t)T * 4);
         L.h16 = off; off = align256(off + TK * (size_t)P * 2);
         L.hscale = off; off = align256(off + TK * 4);
+        L.dn = off; off = align256(off + TK * (size_t)d->hidden * 4);
     }
     L.total = off;
     return L;
@@ -226,7 +227,6 @@ static int moe_grouped(const cw_moe_desc *d, const MoeArgs &a, const MoeLayout &
     g.ldh = P;
     if ((rc = mfma_gateup(d->dtype[0], g, tmax, s))) return rc;
     if ((rc = pack_rows_f16(a.h, TK, P, P, h16, hscale, s))) return rc;
-    if ((rc = fill_zero(a.out, (int64_t)T * a.H, s))) return rc;
 
     MfArgs dn = {};
     dn.w0 = a.wd;
@@ -242,11 +242,9 @@ static int moe_grouped(const cw_moe_desc *d, const MoeArgs &a, const MoeLayout &
     dn.n_tiles = n_tiles;
     dn.pile_pick = pile_pick;
     dn.K = K;
-    dn.ids = a.ids;
-    dn.w = a.w;
-    dn.bias_d = a.bd;
-    dn.out = a.out;
-    return mfma_down(d->dtype[2], dn, tmax, s);
+    dn.dn = (float *)(base + L.dn);
+    if ((rc = mfma_down(d->dtype[2], dn, tmax, s))) return rc;
+    return combine_picks(dn.dn, a.w, a.bd, a.ids, T, K, a.H, a.out, s);
 }
 
 static int moe_layer(const cw_moe_desc *d, const float *x, const float *logits, int T, float *out, uint32_t *ids_out,
