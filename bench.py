@@ -31,6 +31,22 @@ def log(*a):
 COPY_BYTES = 1 << 30
 
 
+TRAFFIC_PROFILE = "profiles/moe_c3_hbm_traffic.md"
+
+
+def measured_traffic(root):
+    """HBM bytes per decode-layer launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+    (counters scaled by a copy kernel of known size), or None when the summary is absent."""
+    try:
+        with open(os.path.join(root, TRAFFIC_PROFILE)) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def copy_calibration(torch, dev):
     """A plain copy kernel of known size: 1 GiB read, 1 GiB written per launch (an elementwise add
     of zero, so it is a kernel dispatch and not a DMA copy). HBM counters read on it give the
@@ -206,7 +222,8 @@ def main():
                    "expert_ffn": I, "gate_up": "iq2_xxs", "down": "iq2_s", "layers": L, "tokens": 1},
         "us_per_layer": round(us_per_layer, 3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(root),
+                     "traffic_source": TRAFFIC_PROFILE,
                      "kernel": "MoE decode layer (route + fused gate/up+SwiGLU + fused down+combine)",
                      "bytes_per_launch": layer_bytes},
         "prefill": prefill,
