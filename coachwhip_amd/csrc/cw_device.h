@@ -338,7 +338,7 @@ struct TableRegs {
 #pragma unroll
         for (int q = 0; q < PER; q++) {
             const int i = tid + 256 * q;
-            if (i < WORDS) r[q] = F::table_word(i);
+            if constexpr (WORDS > 0) r[q] = F::table_word(i < WORDS ? i : WORDS - 1);  // clamped, not branched
         }
     }
     __device__ __forceinline__ void store(void *lds, int tid) const {

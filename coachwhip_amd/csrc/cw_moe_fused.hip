@@ -21,17 +21,17 @@ template <int NX>
 __device__ __forceinline__ void load_xs(float (&xr)[NX][32], const float *xrow, int sub, int lpr, int nsb) {
 #pragma unroll
     for (int i = 0; i < NX; i++) {
+        // clamped, not branched, so later waits on other loads stay exact
         const int sb = sub + i * lpr;
-        if (sb < nsb) {
-            const float4 *p = (const float4 *)(xrow + 32 * sb);
+        const bool in = sb < nsb;
+        const float4 *p = (const float4 *)(xrow + 32 * (in ? sb : nsb - 1));
 #pragma unroll
-            for (int v = 0; v < 8; v++) {
-                const float4 f = p[v];
-                xr[i][4 * v] = f.x; xr[i][4 * v + 1] = f.y; xr[i][4 * v + 2] = f.z; xr[i][4 * v + 3] = f.w;
-            }
-        } else {
-#pragma unroll
-            for (int v = 0; v < 32; v++) xr[i][v] = 0.f;
+        for (int v = 0; v < 8; v++) {
+            const float4 f = p[v];
+            xr[i][4 * v] = in ? f.x : 0.f;
+            xr[i][4 * v + 1] = in ? f.y : 0.f;
+            xr[i][4 * v + 2] = in ? f.z : 0.f;
+            xr[i][4 * v + 3] = in ? f.w : 0.f;
         }
     }
 }
@@ -267,10 +267,13 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoeArgs a) {
     extern __shared__ __align__(16) float hs[];  // hidden rows, sub-blocks of 32 floats 36 apart
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int K = a.K;
-    // the logits first (waits on loads count in issue order), then the loads that need nothing
-    // from the routing: LDS tables and this lane's x slice
+    // the logits alone first: every wave of the grid starts at once, and the table and x loads
+    // of 2048 waves queued in front of them in L2 (~2.5 us to the first logit). Those loads are
+    // issued once the logits are in and complete during the top-k.
     float lv[PER];
     route_load<PER>(a.logits, a.E, lv);
+    RouteState<PER> rst;
+    route_keys<PER>(lv, a.E, rst);
     TableRegs<FG> tg;
     TableRegs<FD> td;
     tg.load(threadIdx.x);
@@ -281,7 +284,7 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoeArgs a) {
 
     uint32_t rid;
     float rw;
-    wave_route<PER>(lv, a.E, K, a.norm, &rid, &rw);
+    route_pick<PER>(lv, rst, a.E, K, a.norm, &rid, &rw);
     uint32_t my_slot = 0xFFFFFFFFu;  // lane j < K: slot of pick j
     bool absent = false;
     if (lane < K) {

@@ -44,91 +44,123 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
 }
 
-// Router key: the float's bits made order-preserving as an unsigned number, above the bitwise
-// complement of the expert index. The unsigned maximum is then the largest logit, the lowest
-// index among equal logits (the stable descending argsort's order), and 0 marks a taken or absent
-// candidate (every real key is above it).
-__device__ __forceinline__ uint64_t route_key(float v, uint32_t e) {
-    const uint32_t b = __float_as_uint(v);
+// Router key: the float's bits made order-preserving as an unsigned number, so the unsigned
+// maximum is the largest logit and equal logits have equal keys (-0 is keyed as +0); 0 marks a
+// taken or absent candidate (the one float that maps to 0, a negative NaN, is raised to 1,
+// among the other NaNs).
+__device__ __forceinline__ uint32_t route_key(float v) {
+    uint32_t b = __float_as_uint(v);
+    if (b == 0x80000000u) b = 0u;
     const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    return ((uint64_t)o << 32) | (uint64_t)(0xFFFFFFFFu - e);
+    return o ? o : 1u;
 }
-__device__ __forceinline__ float key_value(uint64_t k) {
-    const uint32_t o = (uint32_t)(k >> 32);
+__device__ __forceinline__ float key_value(uint32_t o) {
     return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
 }
-__device__ __forceinline__ uint32_t key_index(uint64_t k) { return 0xFFFFFFFFu - (uint32_t)k; }
 
-template <int CTRL>
-__device__ __forceinline__ uint64_t max_step(uint64_t k) {
-    const uint64_t o = ((uint64_t)dpp_u<CTRL>((uint32_t)(k >> 32)) << 32) | dpp_u<CTRL>((uint32_t)k);
-    return o > k ? o : k;
+// the largest key of the wave, in every lane: the row maximum (four DPP steps), then
+// row_bcast:15 into rows 1 and 3 and row_bcast:31 into rows 2 and 3 (gfx9 DPP), so lane 63
+// holds the wave's maximum and one readlane returns it (unsigned max: 0 is the identity for the
+// lanes a broadcast does not write)
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_rows_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xF, false);
 }
-__device__ __forceinline__ uint64_t readlane_u64(uint64_t k, int lane) {
-    return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(k >> 32), lane) << 32) |
-           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, lane);
+__device__ __forceinline__ uint32_t wave_max_key(uint32_t k) {
+    k = max(k, dpp_u<0xB1>(k));
+    k = max(k, dpp_u<0x4E>(k));
+    k = max(k, dpp_u<0x141>(k));
+    k = max(k, dpp_u<0x140>(k));
+    k = max(k, dpp_rows_u<0x142, 0xA>(k));
+    k = max(k, dpp_rows_u<0x143, 0xC>(k));
+    return (uint32_t)__builtin_amdgcn_readlane((int)k, 63);
 }
-// the largest key of the wave, in every lane
-__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
-    k = max_step<0xB1>(k);
-    k = max_step<0x4E>(k);
-    k = max_step<0x141>(k);
-    k = max_step<0x140>(k);
-    uint64_t a = readlane_u64(k, 0), b = readlane_u64(k, 16), c = readlane_u64(k, 32), d = readlane_u64(k, 48);
-    a = a > b ? a : b;
-    c = c > d ? c : d;
-    return a > c ? a : c;
+
+// lane l loads logits l, l + 64, ... (-inf past E)
+template <int PER>
+__device__ __forceinline__ void route_load(const float *logits, int E, float (&v)[PER]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        // clamped, not branched: loads in branches make the compiler wait for every later load
+        // before the first use
+        const int e = lane + 64 * i;
+        const float t = logits[e < E ? e : E - 1];
+        v[i] = e < E ? t : -INFINITY;
+    }
 }
 
 // One wavefront routes one token: softmax over E = 64*PER (or fewer) logits as candle-nn's
 // softmax_last_dim computes it (max, exp of the differences, sum, divide), then the K best
 // picks, best first, the lowest index winning ties (the stable descending argsort of
 // crates/engine/src/experts.rs:2364-2372). Picks are made on the logits themselves: softmax is
-// monotone and comparing logits is exact. Lane j < K returns pick j's expert in *id and its
-// weight (renormalised over the K when norm) in *w; other lanes return id ~0u.
+// monotone and comparing logits is exact. Each round takes the wave maximum of 32-bit keys, then
+// the lowest expert index holding it from one ballot per candidate slot (expert e sits in lane
+// e % 64, slot e / 64). Lane j < K returns pick j's expert in *id and its weight (renormalised
+// over the K when norm) in *w; other lanes return id ~0u.
+// The routing in two parts, so a caller can issue other loads once the logits are in:
+// route_keys turns the loaded logits into keys and their maximum (waiting for the logits),
+// route_pick makes the K picks and their weights.
 template <int PER>
-__device__ __forceinline__ void route_load(const float *logits, int E, float (&v)[PER]) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int i = 0; i < PER; i++) {
-        const int e = lane + 64 * i;
-        v[i] = e < E ? logits[e] : -INFINITY;
-    }
-}
-// the routing of logits already loaded by route_load
+struct RouteState {
+    uint32_t key[PER];
+    float m;
+};
 template <int PER>
-__device__ __forceinline__ void wave_route(const float (&v)[PER], int E, int K, int norm, uint32_t *id, float *w) {
+__device__ __forceinline__ void route_keys(const float (&v)[PER], int E, RouteState<PER> &r) {
     const int lane = threadIdx.x & 63;
-    uint64_t key[PER];
     float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < PER; i++) {
-        const int e = lane + 64 * i;
-        key[i] = e < E ? route_key(v[i], (uint32_t)e) : 0ull;
+        r.key[i] = lane + 64 * i < E ? route_key(v[i]) : 0u;
         m = fmaxf(m, v[i]);
     }
-    m = wave_max(m);
-    uint64_t mine = 0;
+    r.m = wave_max(m);
+}
+template <int PER>
+__device__ __forceinline__ void route_pick(const float (&v)[PER], RouteState<PER> &r, int E, int K, int norm, uint32_t *id,
+                                           float *w) {
+    const int lane = threadIdx.x & 63;
+    uint32_t mine_k = 0, mine_e = 0xFFFFFFFFu;
     for (int j = 0; j < K; j++) {
-        uint64_t best = key[0];
+        uint32_t best = r.key[0];
 #pragma unroll
-        for (int i = 1; i < PER; i++) best = key[i] > best ? key[i] : best;
+        for (int i = 1; i < PER; i++) best = max(best, r.key[i]);
         best = wave_max_key(best);
+        int slot = PER, at = 0;
 #pragma unroll
-        for (int i = 0; i < PER; i++) key[i] = key[i] == best ? 0ull : key[i];
-        mine = lane == j ? best : mine;
+        for (int i = PER - 1; i >= 0; i--) {  // the lowest slot holding best wins, then the lowest lane
+            const uint64_t bal = __ballot(r.key[i] == best);
+            if (bal) {
+                slot = i;
+                at = __builtin_ctzll(bal);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < PER; i++)
+            if (i == slot && lane == at) r.key[i] = 0u;
+        if (lane == j) {
+            mine_k = best;
+            mine_e = (uint32_t)(64 * slot + at);
+        }
     }
-    float p = lane < K ? expf(key_value(mine) - m) : 0.f;
+    float p = lane < K ? expf(key_value(mine_k) - r.m) : 0.f;
     if (norm) {
         p = p / wave_sum(p);
     } else {
         float s = 0.f;
 #pragma unroll
-        for (int i = 0; i < PER; i++) s += lane + 64 * i < E ? expf(v[i] - m) : 0.f;
+        for (int i = 0; i < PER; i++) s += lane + 64 * i < E ? expf(v[i] - r.m) : 0.f;
         p = p / wave_sum(s);
     }
-    *id = lane < K ? key_index(mine) : 0xFFFFFFFFu;
+    *id = lane < K ? mine_e : 0xFFFFFFFFu;
     *w = p;
+}
+template <int PER>
+__device__ __forceinline__ void wave_route(const float (&v)[PER], int E, int K, int norm, uint32_t *id, float *w) {
+    RouteState<PER> r;
+    route_keys<PER>(v, E, r);
+    route_pick<PER>(v, r, E, K, norm, id, w);
 }
 template <int PER>
 __device__ __forceinline__ void wave_route(const float *logits, int E, int K, int norm, uint32_t *id, float *w) {

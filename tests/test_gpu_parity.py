@@ -135,6 +135,24 @@ def test_route_reference_known_answers():
     assert host(ids).tolist() == [[1, 2, 4]]
 
 
+def test_route_ties_across_signed_zero_and_slots():
+    # -0 and +0 are equal logits: the stable argsort keeps index order among them; equal logits
+    # in different 64-wide slots (index 3 and 131) and in the same lane (3 and 67) tie too
+    lg = np.full((1, 256), -1.0, np.float32)
+    lg[0, [3, 5, 10]] = [0.0, -0.0, 0.0]
+    lg[0, [67, 131, 200]] = 2.5
+    ids, w = ops.route(dev(lg), 5, True)
+    wids, ww = O.route(lg, 5, True)
+    assert wids.tolist() == [[67, 131, 200, 3, 5]]
+    assert np.array_equal(host(ids).view(np.uint32), wids)
+    assert np.max(np.abs(host(w) - ww)) < 1e-6
+    # ties in every round: 9 equal maxima, K = 8 takes the 8 lowest indices
+    lg = np.zeros((2, 512), np.float32)
+    lg[:, ::57] = 1.0
+    ids, _ = ops.route(dev(lg), 8, False)
+    assert host(ids).tolist() == [list(range(0, 57 * 8, 57))] * 2
+
+
 @pytest.mark.parametrize("E,K,norm", [(256, 8, True), (128, 4, True), (512, 10, True), (1024, 32, False), (20, 20, True)])
 def test_route_matches_the_oracle(E, K, norm):
     rng = np.random.default_rng(E + K)
