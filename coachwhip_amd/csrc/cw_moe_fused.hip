@@ -206,6 +206,11 @@ struct DecodeBarrier {
 static __device__ DecodeBarrier g_decode_barrier;
 
 #define CW_AGENT __HIP_MEMORY_SCOPE_AGENT
+// buffer descriptor word 3 for raw byte-addressed buffers on gfx9, and the cache policy bit of
+// agent-scope coherent loads (sc1)
+#define CW_BUFFER_DWORD3 0x00020000
+#define CW_CPOL_SC1 16
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 __device__ bool grid_barrier(uint32_t nblocks) {
     __builtin_amdgcn_s_waitcnt(0);  // this thread's coherent stores have landed
     __syncthreads();
@@ -396,25 +401,26 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoeArgs a) {
 
     const bool ok = grid_barrier(gridDim.x);
 
-    // every hidden row into LDS once per block, read at the coherence point with 8 loads in
-    // flight per thread, and stored with the padding (36 floats per sub-block of 32) that keeps
-    // the 16 sub-block readers of a row on distinct LDS banks
+    // every hidden row into LDS once per block, read at the coherence point (16-byte buffer
+    // loads with the sc1 policy, the form of an agent-scope atomic load, 8 in flight per thread),
+    // and stored with the padding (36 floats per sub-block of 32) that keeps the 16 sub-block
+    // readers of a row on distinct LDS banks
     {
-        const uint64_t *h64 = (const uint64_t *)a.h;
-        const int nh = K * a.P / 2, hp = a.P / 2;
-        for (int v0 = 0; v0 < nh; v0 += 256 * 8) {
-            uint64_t t[8];
+        const int nbytes = K * a.P * 4, hp = a.P / 4;
+        const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc((void *)a.h, (short)0, nbytes, CW_BUFFER_DWORD3);
+        for (int v0 = 0; v0 < nbytes / 16; v0 += 256 * 8) {
+            f32x4 t[8];
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 const int v = v0 + 256 * u + threadIdx.x;
-                if (v < nh) t[u] = __hip_atomic_load(h64 + v, __ATOMIC_RELAXED, CW_AGENT);
+                t[u] = __builtin_amdgcn_raw_buffer_load_b128(hr, 16 * v, 0, CW_CPOL_SC1);  // past the end: 0, unused
             }
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 const int v = v0 + 256 * u + threadIdx.x;
-                if (v < nh) {
-                    const int j = v / hp, c = 2 * (v - j * hp);
-                    *(uint64_t *)(hs + (j * nsbd + (c >> 5)) * 36 + (c & 31)) = t[u];
+                if (v < nbytes / 16) {
+                    const int j = v / hp, c = 4 * (v - j * hp);
+                    *(f32x4 *)(hs + (j * nsbd + (c >> 5)) * 36 + (c & 31)) = t[u];
                 }
             }
         }
