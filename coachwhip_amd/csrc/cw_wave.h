@@ -76,7 +76,7 @@ __device__ __forceinline__ uint32_t wave_max_key(uint32_t k) {
     return (uint32_t)__builtin_amdgcn_readlane((int)k, 63);
 }
 
-// lane l loads logits l, l + 64, ... (-inf past E)
+// lane l loads logits PER*l .. PER*l + PER-1 (-inf past E)
 template <int PER>
 __device__ __forceinline__ void route_load(const float *logits, int E, float (&v)[PER]) {
     const int lane = threadIdx.x & 63;
@@ -84,7 +84,7 @@ __device__ __forceinline__ void route_load(const float *logits, int E, float (&v
     for (int i = 0; i < PER; i++) {
         // clamped, not branched: loads in branches make the compiler wait for every later load
         // before the first use
-        const int e = lane + 64 * i;
+        const int e = PER * lane + i;
         const float t = logits[e < E ? e : E - 1];
         v[i] = e < E ? t : -INFINITY;
     }
@@ -94,11 +94,12 @@ __device__ __forceinline__ void route_load(const float *logits, int E, float (&v
 // softmax_last_dim computes it (max, exp of the differences, sum, divide), then the K best
 // picks, best first, the lowest index winning ties (the stable descending argsort of
 // crates/engine/src/experts.rs:2364-2372). Picks are made on the logits themselves: softmax is
-// monotone and comparing logits is exact. Each round takes the wave maximum of 32-bit keys, then
-// the lowest expert index holding it from one ballot per candidate slot (expert e sits in lane
-// e % 64, slot e / 64). Lane j < K returns pick j's expert in *id and its weight (renormalised
-// over the K when norm) in *w; other lanes return id ~0u.
-// The routing in two parts, so a caller can issue other loads once the logits are in:
+// monotone and comparing logits is exact. Lane l holds experts PER*l .. PER*l + PER-1, so the
+// lowest index holding a round's maximum is in the lowest lane holding it, at that lane's lowest
+// slot holding it: per round one wave maximum of 32-bit keys, one ballot, one find-first-set and
+// one readlane. Lane j < K returns pick j's expert in *id and its weight (renormalised over the
+// K when norm) in *w; other lanes return id ~0u.
+// The routing is in two parts, so a caller can issue other loads once the logits are in:
 // route_keys turns the loaded logits into keys and their maximum (waiting for the logits),
 // route_pick makes the K picks and their weights.
 template <int PER>
@@ -112,36 +113,71 @@ __device__ __forceinline__ void route_keys(const float (&v)[PER], int E, RouteSt
     float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < PER; i++) {
-        r.key[i] = lane + 64 * i < E ? route_key(v[i]) : 0u;
+        r.key[i] = PER * lane + i < E ? route_key(v[i]) : 0u;
         m = fmaxf(m, v[i]);
     }
     r.m = wave_max(m);
 }
+// the K picks for PER = 4: each lane first sorts its four keys (by key, then by slot, so equal
+// keys keep index order); a round then needs only the wave maximum of the lanes' heads, the
+// lowest lane holding it, and a pop of that lane's list
+__device__ __forceinline__ void route_tournament(uint32_t (&key)[4], int K, uint32_t &mine_k, uint32_t &mine_e) {
+    const int lane = threadIdx.x & 63;
+    // 64-bit sort keys: key above the slot's complement, so larger is better and ties go to the lower slot
+    uint64_t q[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) q[i] = ((uint64_t)key[i] << 8) | (uint64_t)(255 - i);
+    auto cx = [&](int a, int b) {
+        const uint64_t x = q[a], y = q[b];
+        q[a] = x > y ? x : y;
+        q[b] = x > y ? y : x;
+    };
+    cx(0, 1); cx(2, 3); cx(0, 2); cx(1, 3); cx(1, 2);
+    uint32_t k[4], sl[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        k[i] = (uint32_t)(q[i] >> 8);
+        sl[i] = 255u - (uint32_t)(q[i] & 0xFF);
+    }
+    for (int j = 0; j < K; j++) {
+        const uint32_t best = wave_max_key(k[0]);
+        const int at = __builtin_ctzll(__ballot(k[0] == best));  // the lowest lane holding it
+        const uint32_t slot = __builtin_amdgcn_readlane((int)sl[0], at);
+        if (lane == at) {
+            k[0] = k[1]; sl[0] = sl[1];
+            k[1] = k[2]; sl[1] = sl[2];
+            k[2] = k[3]; sl[2] = sl[3];
+            k[3] = 0u;
+        }
+        if (lane == j) {
+            mine_k = best;
+            mine_e = 4u * (uint32_t)at + slot;
+        }
+    }
+}
+
 template <int PER>
 __device__ __forceinline__ void route_pick(const float (&v)[PER], RouteState<PER> &r, int E, int K, int norm, uint32_t *id,
                                            float *w) {
     const int lane = threadIdx.x & 63;
     uint32_t mine_k = 0, mine_e = 0xFFFFFFFFu;
-    for (int j = 0; j < K; j++) {
+    if constexpr (PER == 4) route_tournament(r.key, K, mine_k, mine_e);
+    else for (int j = 0; j < K; j++) {
         uint32_t best = r.key[0];
 #pragma unroll
         for (int i = 1; i < PER; i++) best = max(best, r.key[i]);
         best = wave_max_key(best);
-        int slot = PER, at = 0;
+        int c = PER;  // this lane's lowest slot holding best
 #pragma unroll
-        for (int i = PER - 1; i >= 0; i--) {  // the lowest slot holding best wins, then the lowest lane
-            const uint64_t bal = __ballot(r.key[i] == best);
-            if (bal) {
-                slot = i;
-                at = __builtin_ctzll(bal);
-            }
-        }
+        for (int i = PER - 1; i >= 0; i--) c = r.key[i] == best ? i : c;
+        const int at = __builtin_ctzll(__ballot(c < PER));  // the lowest lane holding it
+        const int slot = __builtin_amdgcn_readlane(c, at);
 #pragma unroll
         for (int i = 0; i < PER; i++)
-            if (i == slot && lane == at) r.key[i] = 0u;
+            if (lane == at && i == slot) r.key[i] = 0u;
         if (lane == j) {
             mine_k = best;
-            mine_e = (uint32_t)(64 * slot + at);
+            mine_e = (uint32_t)(PER * at + slot);
         }
     }
     float p = lane < K ? expf(key_value(mine_k) - r.m) : 0.f;
@@ -150,7 +186,7 @@ __device__ __forceinline__ void route_pick(const float (&v)[PER], RouteState<PER
     } else {
         float s = 0.f;
 #pragma unroll
-        for (int i = 0; i < PER; i++) s += lane + 64 * i < E ? expf(v[i] - r.m) : 0.f;
+        for (int i = 0; i < PER; i++) s += PER * lane + i < E ? expf(v[i] - r.m) : 0.f;
         p = p / wave_sum(s);
     }
     *id = lane < K ? mine_e : 0xFFFFFFFFu;
