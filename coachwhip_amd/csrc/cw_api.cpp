@@ -2,10 +2,12 @@
 // library's error reporting. The MoE-layer, routing and activation entry points live in
 // cw_moe.hip; the host bank bookkeeping in cw_slots.cpp.
 #include <stdarg.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "cw_common.h"
 #include "cw_gemv.h"
+#include "cw_mfma.h"
 
 namespace cw {
 
@@ -71,14 +73,26 @@ int cw_dequantize(int dtype, const void *blocks, int64_t n_elems, float *out, cw
     return dequantize(dtype, blocks, n_elems, out, (hipStream_t)stream);
 }
 
+// Rows of x from which cw_qmatmul runs as an MFMA GEMM instead of one matvec per row
+// (CWMOE_MM_MIN_ROWS overrides; the reference switches to its simdgroup-matrix kernel above 8
+// rows, vendor/candle-core/src/quantized/metal.rs:339-353).
+static int64_t mm_min_rows() {
+    const char *e = getenv("CWMOE_MM_MIN_ROWS");
+    return e ? atoll(e) : 32;
+}
+static bool qmatmul_mfma(int dtype, int64_t k, int64_t m) {
+    return m >= mm_min_rows() && cw::mfma_supported(dtype) && k % cw_block_size(dtype) == 0 && k % 32 == 0 &&
+           (dtype == CW_Q8_0 || dtype == CW_MXFP4 || k % 256 == 0);
+}
+
 size_t cw_qmatmul_workspace_size(int dtype, int64_t n, int64_t k, int64_t m) {
-    (void)dtype; (void)n; (void)k; (void)m;
-    return 0;
+    (void)n;
+    if (!is_weight_type(dtype) || k <= 0 || m <= 0 || !qmatmul_mfma(dtype, k, m)) return 0;
+    return cw::mfma_dense_workspace(m, k);
 }
 
 int cw_qmatmul(int dtype, const void *w, int64_t n, int64_t k, const float *x, int64_t m, float *y, void *ws,
                size_t ws_bytes, cw_stream_t stream) {
-    (void)ws; (void)ws_bytes;
     if (!is_weight_type(dtype)) return set_error(CW_ENOTSUP, "qmatmul: dtype %d is not supported", dtype);
     const int bs = cw_block_size(dtype);
     CW_REQUIRE(n >= 0 && m >= 0 && k > 0, "qmatmul: n %lld, k %lld, m %lld", (long long)n, (long long)k, (long long)m);
@@ -88,6 +102,9 @@ int cw_qmatmul(int dtype, const void *w, int64_t n, int64_t k, const float *x, i
     if (n == 0 || m == 0) return CW_OK;
     CW_REQUIRE(w && x && y, "qmatmul: null pointer");
     CW_REQUIRE(aligned16(x), "qmatmul: x must be 16-byte aligned");
+    if (qmatmul_mfma(dtype, k, m))
+        return cw::mfma_dense(dtype, (const uint8_t *)w, k / bs * cw_type_size(dtype), (int)n, (int)k, x, (int)m, y, ws,
+                              ws_bytes, (hipStream_t)stream);
     GemvArgs a = {};
     a.w0 = (const uint8_t *)w;
     a.row_bytes = k / bs * cw_type_size(dtype);

@@ -47,6 +47,10 @@ int pack_rows_f16(const float *x, int rows, int k, int ldx, uint16_t *a16, float
 int fill_zero(float *p, int64_t n, hipStream_t s);
 int mfma_gateup(int dtype, const MfArgs &a, int tiles_max, hipStream_t s);
 int mfma_down(int dtype, const MfArgs &a, int tiles_max, hipStream_t s);
+// y (m x n) = x (m x k) . W^T for one quantized matrix, through the same GEMM (fp16 activations)
+size_t mfma_dense_workspace(int64_t m, int64_t k);
+int mfma_dense(int dtype, const uint8_t *w, int64_t row_bytes, int n, int k, const float *x, int m, float *y, void *ws,
+               size_t ws_bytes, hipStream_t s);
 // out[t] = sum_j w[t*K+j] * (dn[t*K+j] + bias[ids[t*K+j]]), picks in order (H a multiple of 4)
 int combine_picks(const float *dn, const float *w, const float *bias, const uint32_t *ids, int T, int K, int H, float *out,
                   hipStream_t s);

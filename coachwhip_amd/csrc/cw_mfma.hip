@@ -125,8 +125,13 @@ __device__ __forceinline__ uint2 lds_u64(const uint8_t *p) {
     return make_uint2(__builtin_amdgcn_alignbyte(d1, d0, a), __builtin_amdgcn_alignbyte(d2, d1, a));
 }
 
+// Traits common to the formats: KST K-steps per stage; SCALE 0 = one f16 scale per super-block
+// (read by scale()), 1 = MXFP4's power-of-two block scales, 2 = one f16 scale per 32-weight block
+// (read by step_scale()); HAS_MIN = an f16 dmin per super-block and a 6-bit m per sub-block.
 struct MIQ2_XXS {
     static constexpr int TS = 66, SBK = 256, LDS = 256 * 16 + 128 * 16;
+    static constexpr int KST = 8, SCALE = 0;
+    static constexpr bool HAS_MIN = false;
     static __device__ void fill(uint8_t *lds, int tid, int nt) {
         copy_tab(lds, c_iq2xxs_f16, tid, nt);
         copy_tab(lds + 256 * 16, c_psigns, tid, nt);
@@ -145,6 +150,8 @@ struct MIQ2_XXS {
 
 struct MIQ2_S {
     static constexpr int TS = 82, SBK = 256, LDS = 1024 * 16 + 256 * 16;
+    static constexpr int KST = 8, SCALE = 0;
+    static constexpr bool HAS_MIN = false;
     static __device__ void fill(uint8_t *lds, int tid, int nt) {
         copy_tab(lds, c_iq2s_f16, tid, nt);
         copy_tab(lds + 1024 * 16, c_signs, tid, nt);
@@ -162,6 +169,8 @@ struct MIQ2_S {
 
 struct MIQ3_S {
     static constexpr int TS = 110, SBK = 256, LDS = 512 * 8 + 256 * 16;
+    static constexpr int KST = 8, SCALE = 0;
+    static constexpr bool HAS_MIN = false;
     static __device__ void fill(uint8_t *lds, int tid, int nt) {
         copy_tab(lds, c_iq3s_f16, tid, nt);   // entry i as 4 halves at byte 8*i
         copy_tab(lds + 512 * 8, c_signs, tid, nt);
@@ -203,6 +212,8 @@ static __constant__ Tab<64> c_mxfp4_pairs = make_mxfp4_pairs();
 
 struct MMXFP4 {
     static constexpr int TS = 17, SBK = 32, LDS = 1024;
+    static constexpr int KST = 8, SCALE = 1;
+    static constexpr bool HAS_MIN = false;
     static __device__ void fill(uint8_t *lds, int tid, int nt) { copy_tab(lds, c_mxfp4_pairs, tid, nt); }
     static __device__ __forceinline__ uint32_t expo(const uint8_t *win, int kk) { return lds_u8(win + TS * kk); }
     static __device__ __forceinline__ uint32_t pair(const uint32_t *tab, uint32_t w) {
@@ -219,18 +230,95 @@ struct MMXFP4 {
     }
 };
 
+// 8 small unsigned byte values (v < 1024) of two dwords -> fp16 (1024 + v), by placing each byte
+// under an 0x64 high byte
+__device__ __forceinline__ uint4 bytes_plus_1024(uint32_t w0, uint32_t w1) {
+    return make_uint4(__builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u), __builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u),
+                      __builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u), __builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u));
+}
+// x * mul + add on each fp16 pair (one rounding: exact when the result is a small integer)
+__device__ __forceinline__ uint32_t pk_fma_u(uint32_t x, uint32_t mul, uint32_t add) {
+    const f16x2 r = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, x), __builtin_bit_cast(f16x2, mul), __builtin_bit_cast(f16x2, add));
+    return __builtin_bit_cast(uint32_t, r);
+}
+__device__ __forceinline__ uint4 fma4(uint4 v, uint32_t mul, uint32_t add) {
+    return make_uint4(pk_fma_u(v.x, mul, add), pk_fma_u(v.y, mul, add), pk_fma_u(v.z, mul, add), pk_fma_u(v.w, mul, add));
+}
+__device__ __forceinline__ uint32_t splat_f16f(float v) {
+    const uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)v);
+    return h | (h << 16);
+}
+
+// Q8_0: codes are the int8 quants themselves (exact in fp16), one f16 scale per block (per K-step)
+struct MQ8_0 {
+    static constexpr int TS = 34, SBK = 32, LDS = 16;
+    static constexpr int KST = 4, SCALE = 2;
+    static constexpr bool HAS_MIN = false;
+    static __device__ void fill(uint8_t *, int, int) {}
+    static __device__ __forceinline__ float step_scale(const uint8_t *win, int kk) { return h2f(lds_u16(win + TS * kk)); }
+    // (q + 128) + 1024 from the byte pattern, then x - 1152 (or 0 when the block's scale is 0)
+    static __device__ __forceinline__ uint4 frag(const uint8_t *win, int kk, int grp, const uint8_t *, bool zero) {
+        const uint2 q = lds_u64(win + TS * kk + 2 + 8 * grp);
+        const uint4 x = bytes_plus_1024(q.x ^ 0x80808080u, q.y ^ 0x80808080u);
+        const uint32_t one = zero ? 0u : 0x3C003C00u, off = zero ? 0u : 0xE480E480u;  // 1.0, -1152.0
+        return fma4(x, one, off);
+    }
+};
+
+// Q4_K: y = d*sc*q - dmin*m per sub-block of 32 (k_quants.rs:1821-1849, get_scale_min_k4 in
+// quantized/utils.rs:50-60). Codes sc*q (<= 945) are exact in fp16 with d as the running scale;
+// the minimum term is a second product of the same activations with codes -m (<= 63) and dmin as
+// its running scale.
+struct MQ4_K {
+    static constexpr int TS = 144, SBK = 256, LDS = 16;
+    static constexpr int KST = 8, SCALE = 0;
+    static constexpr bool HAS_MIN = true;
+    static __device__ void fill(uint8_t *, int, int) {}
+    static __device__ __forceinline__ float scale(const uint8_t *win) { return h2f(lds_u16(win)); }
+    static __device__ __forceinline__ float dmin(const uint8_t *win) { return h2f(lds_u16(win + 2)); }
+    // 6-bit scale and min of sub-block j
+    static __device__ __forceinline__ void sc_m(const uint8_t *win, int j, uint32_t &sc, uint32_t &m) {
+        const uint8_t *q = win + 4;
+        if (j < 4) {
+            sc = lds_u8(q + j) & 63;
+            m = lds_u8(q + j + 4) & 63;
+        } else {
+            const uint32_t a = lds_u8(q + j + 4), lo = lds_u8(q + j - 4), hi = lds_u8(q + j);
+            sc = (a & 0xF) | ((lo >> 6) << 4);
+            m = (a >> 4) | ((hi >> 6) << 4);
+        }
+    }
+    // codes sc*q of sub-block kk (sub-blocks 2c, 2c+1 are the low and high nibbles of qs[32c..32c+32))
+    static __device__ __forceinline__ uint4 frag(const uint8_t *win, int kk, int grp, const uint8_t *, bool zero) {
+        uint32_t sc, m;
+        sc_m(win, kk, sc, m);
+        if (zero) sc = 0;
+        const uint2 q = lds_u64(win + 16 + 32 * (kk >> 1) + 8 * grp);
+        const int sh = 4 * (kk & 1);
+        const uint4 x = bytes_plus_1024((q.x >> sh) & 0x0F0F0F0Fu, (q.y >> sh) & 0x0F0F0F0Fu);
+        return fma4(x, splat_f16f((float)sc), splat_f16f(-1024.0f * (float)sc));
+    }
+    // codes -m for all 8 weights (the minimum term)
+    static __device__ __forceinline__ uint4 min_frag(const uint8_t *win, int kk, bool zero) {
+        uint32_t sc, m;
+        sc_m(win, kk, sc, m);
+        const uint32_t v = zero ? 0u : splat_f16f(-(float)m);
+        return make_uint4(v, v, v, v);
+    }
+};
+
 // fp16 bits of 2^x for x <= 0 (0 below the subnormal range), splatted to both halves
 __device__ __forceinline__ uint32_t pow2_f16x2(int x) {
     const uint32_t h = x >= -14 ? (uint32_t)(x + 15) << 10 : (x >= -24 ? 1u << (x + 24) : 0u);
     return h | (h << 16);
 }
 
-// A stage is 8 K-steps (256 weights of k). The window of a row for a stage holds the stage's
-// bytes (an IQ super-block, or 8 MXFP4 blocks) from the 16-byte boundary at or below their
-// start, in PCS pieces of 16 bytes.
+// A stage is KST K-steps (8: 256 weights of k; 4 for Q8_0). The window of a row for a stage
+// holds the stage's bytes (an IQ or Q4_K super-block, or KST MXFP4 / Q8_0 blocks) from the
+// 16-byte boundary at or below their start, in PCS pieces of 16 bytes.
 template <class MF>
 struct Win {
-    static constexpr int SEG = MF::SBK == 32 ? 8 * MF::TS : MF::TS;
+    static constexpr int SEG = MF::SBK == 32 ? MF::KST * MF::TS : MF::TS;
     static constexpr int PCS = (SEG + (MF::TS % 2 ? 15 : 14) + 15) / 16;
     static constexpr int BYTES = 16 * PCS;
 };
@@ -253,9 +341,10 @@ __device__ __forceinline__ void dma16(const void *g, uint8_t *lds_base) {
 template <class MF, int MODE>
 struct GmShape {
     static constexpr int NM = MODE == 0 ? 2 : 1;
-    static constexpr int NB = MODE == 0 ? 2 : 4;
+    // MODE 2 (dense matmul) uses narrower N-blocks than MODE 1 so one matrix still fills the chip
+    static constexpr int NB = (MODE == 1 ? 4 : 2) / (MF::HAS_MIN ? 2 : 1);  // a second accumulator set for the minimum
     static constexpr int RPW = 16 * NB, RPB = 4 * RPW;
-    static constexpr int A_BYTES = 8 * 4 * 64 * 16;                 // one stage of activations
+    static constexpr int A_BYTES = MF::KST * 4 * 64 * 16;           // one stage of activations
     static constexpr int W_BYTES = NM * RPB * Win<MF>::BYTES;       // one stage of weight windows
     static constexpr size_t lds_bytes() { return ((MF::LDS + 15) & ~15) + A_BYTES + W_BYTES; }
 };
@@ -263,6 +352,7 @@ struct GmShape {
 // MODE 0: gate and up with the activation, hidden rows written in pile order.
 // MODE 1: down, one output row per pick (combined per token by k_combine, in pick order, so the
 //         result does not depend on the order blocks finish in).
+// MODE 2: a dense matmul, the same output as MODE 1 (pile_pick NULL: one row per position).
 //
 // Per stage of 8 K-steps, the block copies its activations and the weight bytes of its rows
 // into LDS with direct global-to-LDS loads: activations in MFMA fragment order ([K-step][pick
@@ -280,8 +370,9 @@ template <class MF, int MODE>
 __global__ __launch_bounds__(256, 2) void k_gmm(const MfArgs a) {
     using S = GmShape<MF, MODE>;
     using W = Win<MF>;
-    constexpr int NM = S::NM, NB = S::NB, KST = 8;
-    constexpr bool POW2 = MF::SBK == 32;
+    constexpr int NM = S::NM, NB = S::NB, KST = MF::KST;
+    constexpr bool POW2 = MF::SCALE == 1, STEP = MF::SCALE == 2, MIN = MF::HAS_MIN;
+    constexpr int NA = MIN ? NB : 1;  // accumulator sets of the minimum term
     extern __shared__ __align__(16) uint8_t smem[];
     uint8_t *tab = smem;
     uint8_t *As = smem + ((MF::LDS + 15) & ~15);
@@ -312,8 +403,10 @@ __global__ __launch_bounds__(256, 2) void k_gmm(const MfArgs a) {
 
     const int n_ks = a.k / 32, n_st = (n_ks + KST - 1) / KST;
     f32x4 acc[NM][NB][4];
-    float rs[NM][NB];     // running scale (IQ) ...
+    f32x4 accm[NM][NA][4];  // minimum term (Q4_K)
+    float rs[NM][NB];     // running scale (f16 scales) ...
     int rb[NM][NB];       // ... or running base exponent (MXFP4)
+    float rsm[NM][NA];    // running dmin (Q4_K)
     uint32_t lrow[NM][NB];  // this lane's window row within the block's windows
     uintptr_t lptr[NM][NB]; // this lane's row in global memory (its alignment gives the shift)
 #pragma unroll
@@ -325,21 +418,40 @@ __global__ __launch_bounds__(256, 2) void k_gmm(const MfArgs a) {
             lrow[m][q] = m * S::RPB + wave * S::RPW + 16 * q + l16;
             lptr[m][q] = (uintptr_t)row_ptr(lrow[m][q]);
 #pragma unroll
-            for (int mb = 0; mb < 4; mb++) acc[m][q][mb] = f32x4{0, 0, 0, 0};
+            for (int mb = 0; mb < 4; mb++) {
+                acc[m][q][mb] = f32x4{0, 0, 0, 0};
+                asm volatile("" : "+v"(acc[m][q][mb]));  // see accm below
+            }
+        }
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+#pragma unroll
+        for (int q = 0; q < NA; q++) {
+            rsm[m][q] = 1.f;
+#pragma unroll
+            for (int mb = 0; mb < 4; mb++) {
+                accm[m][q][mb] = f32x4{0, 0, 0, 0};
+                // the compiler must not treat the four elements as one value from here on: with
+                // that assumption it fed later MFMAs three stale copies (wrong rows 1-3 of each
+                // 4-row group); the empty asm emits nothing
+                asm volatile("" : "+v"(accm[m][q][mb]));
+            }
         }
 
     for (int st = 0; st < n_st; st++) {
         if (st) __syncthreads();  // every wave is done with the previous stage's LDS
-        const int nk = min(KST, n_ks - st * KST);   // K-steps in this stage
-        const int seg = POW2 ? MF::TS * nk : MF::TS; // bytes of a row in this stage
+        const int nk = min(KST, n_ks - st * KST);              // K-steps in this stage
+        const int seg = MF::SBK == 32 ? MF::TS * nk : MF::TS;  // bytes of a row in this stage
         if (stager) {
 #pragma unroll
             for (int kk = 0; kk < KST; kk++)
                 if (kk < nk) dma16(asrc + (st * KST + kk) * 32, As + ((kk * 4 + wave) * 64) * 16);
         }
+        constexpr int NP = NM * S::RPB * W::PCS;  // pieces of the block's windows, a multiple of 64
 #pragma unroll
-        for (int t = 0; t < W::PCS; t++) {
+        for (int t = 0; t < (NP + 255) / 256; t++) {
             const int i = tid + 256 * t, r = i / W::PCS, p = i - r * W::PCS;
+            if (i >= NP) break;  // uniform across the wave
             const uint8_t *o = row_ptr(r) + (int64_t)W::SEG * st;
             const uint8_t *base = (const uint8_t *)((uintptr_t)o & ~(uintptr_t)15);
             if (base + 16 * p < o + seg) dma16(base + 16 * p, Ws + (256 * t + 64 * wave) * 16);
@@ -355,8 +467,13 @@ __global__ __launch_bounds__(256, 2) void k_gmm(const MfArgs a) {
             for (int q = 0; q < NB; q++)
                 win[m][q] = Ws + lrow[m][q] * W::BYTES + ((lptr[m][q] + (uintptr_t)W::SEG * st) & 15);
 
-        bool zero[NM][NB];
-        if constexpr (POW2) {
+        bool zero[NM][NB], zerom[NM][NA];
+        if constexpr (STEP) {
+#pragma unroll
+            for (int m = 0; m < NM; m++)
+#pragma unroll
+                for (int q = 0; q < NB; q++) zero[m][q] = false;
+        } else if constexpr (POW2) {
 #pragma unroll
             for (int m = 0; m < NM; m++)
 #pragma unroll
@@ -387,13 +504,44 @@ __global__ __launch_bounds__(256, 2) void k_gmm(const MfArgs a) {
                         for (int mb = 0; mb < 4; mb++) acc[m][q][mb] *= ratio;
                         rs[m][q] = d;
                     }
+                    if constexpr (MIN) {
+                        const float dm = MF::dmin(win[m][q]);
+                        zerom[m][q] = dm == 0.f;
+                        if (dm != 0.f) {
+                            const float ratio = __fdividef(rsm[m][q], dm);
+#pragma unroll
+                            for (int mb = 0; mb < 4; mb++) accm[m][q][mb] *= ratio;
+                            rsm[m][q] = dm;
+                        }
+                    }
                 }
         }
 
 #pragma unroll
         for (int kk = 0; kk < KST; kk++) {
             if (kk >= nk) break;
-            f16x8 bf[NM][NB];
+            if constexpr (STEP) {
+                // a scale per K-step: move each accumulator onto it
+#pragma unroll
+                for (int m = 0; m < NM; m++)
+#pragma unroll
+                    for (int q = 0; q < NB; q++) {
+                        const float d = MF::step_scale(win[m][q], kk);
+                        zero[m][q] = d == 0.f;
+                        if (d != 0.f) {
+                            const float ratio = __fdividef(rs[m][q], d);
+#pragma unroll
+                            for (int mb = 0; mb < 4; mb++) acc[m][q][mb] *= ratio;
+                            rs[m][q] = d;
+                        }
+                    }
+            }
+            f16x8 bf[NM][NB], bm[NM][NA];
+#pragma unroll
+            for (int m = 0; m < NM; m++)
+#pragma unroll
+                for (int q = 0; q < NA; q++)
+                    if constexpr (MIN) bm[m][q] = as_f16x8(MF::min_frag(win[m][q], kk, zerom[m][q]));
 #pragma unroll
             for (int m = 0; m < NM; m++)
 #pragma unroll
@@ -410,8 +558,10 @@ __global__ __launch_bounds__(256, 2) void k_gmm(const MfArgs a) {
 #pragma unroll
                 for (int m = 0; m < NM; m++)
 #pragma unroll
-                    for (int q = 0; q < NB; q++)
+                    for (int q = 0; q < NB; q++) {
                         acc[m][q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bf[m][q], acc[m][q][mb], 0, 0, 0);
+                        if constexpr (MIN) accm[m][q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bm[m][q], accm[m][q][mb], 0, 0, 0);
+                    }
             }
         }
     }
@@ -431,13 +581,20 @@ __global__ __launch_bounds__(256, 2) void k_gmm(const MfArgs a) {
             if (r >= tile.m) continue;
             const int pos = tile.pos0 + r;
             const float sa = a.ascale[a.rows ? a.rows[pos] : pos];
-            const int pick = a.pile_pick[pos];
+            const int pick = a.pile_pick ? a.pile_pick[pos] : pos;
 #pragma unroll
             for (int q = 0; q < NB; q++) {
                 const int n = nblk * S::RPB + wave * S::RPW + 16 * q + l16;
                 if (n >= a.n) continue;
+                float v[NM];
+#pragma unroll
+                for (int m = 0; m < NM; m++) {
+                    v[m] = acc[m][q][mb][i] * fs[m][q];
+                    if constexpr (MIN) v[m] += accm[m][q][mb][i] * rsm[m][q];
+                    v[m] *= sa;
+                }
                 if constexpr (MODE == 0) {
-                    float g = acc[0][q][mb][i] * fs[0][q] * sa, u = acc[NM - 1][q][mb][i] * fs[NM - 1][q] * sa, o;
+                    float g = v[0], u = v[NM - 1], o;
                     if (a.act == CW_ACT_SILU) {
                         o = g / (1.0f + expf(-g)) * u;
                     } else {
@@ -450,7 +607,7 @@ __global__ __launch_bounds__(256, 2) void k_gmm(const MfArgs a) {
                     }
                     a.h[(int64_t)pos * a.ldh + n] = o;
                 } else {
-                    a.dn[(int64_t)pick * a.n + n] = acc[0][q][mb][i] * fs[0][q] * sa;
+                    a.dn[(int64_t)pick * a.n + n] = v[0];
                 }
             }
         }
@@ -580,7 +737,9 @@ __global__ void k_fill_zero(float *p, int64_t n) {
 
 // ------------------------------------------------------------------------------ launchers
 
-bool mfma_supported(int dtype) { return dtype == CW_IQ2_XXS || dtype == CW_IQ2_S || dtype == CW_IQ3_S || dtype == CW_MXFP4; }
+bool mfma_supported(int dtype) {
+    return dtype == CW_IQ2_XXS || dtype == CW_IQ2_S || dtype == CW_IQ3_S || dtype == CW_MXFP4 || dtype == CW_Q4_K || dtype == CW_Q8_0;
+}
 
 int max_tiles(int TK, int n_slots) { return (TK + MF_MT - 1) / MF_MT + (n_slots < TK ? n_slots : TK); }
 
@@ -641,8 +800,50 @@ static int by_fmt(int dtype, const MfArgs &a, int tiles_max, hipStream_t s) {
     case CW_IQ2_S: return launch<MIQ2_S, MODE>(a, tiles_max, s);
     case CW_IQ3_S: return launch<MIQ3_S, MODE>(a, tiles_max, s);
     case CW_MXFP4: return launch<MMXFP4, MODE>(a, tiles_max, s);
+    case CW_Q4_K: return launch<MQ4_K, MODE>(a, tiles_max, s);
+    case CW_Q8_0: return launch<MQ8_0, MODE>(a, tiles_max, s);
     default: return set_error(CW_ENOTSUP, "mfma: dtype %d has no MFMA path", dtype);
     }
+}
+
+// tile i of a dense matmul: rows 64i .. 64i + 63 of x, "slot" 0
+__global__ void k_dense_tiles(MfTile *tiles, int *n_tiles, int m) {
+    const int nt = (m + MF_MT - 1) / MF_MT;
+    for (int i = threadIdx.x; i < nt; i += blockDim.x) tiles[i] = MfTile{0, i * MF_MT, min(MF_MT, m - i * MF_MT), 0};
+    if (threadIdx.x == 0) *n_tiles = nt;
+}
+
+static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
+size_t mfma_dense_workspace(int64_t m, int64_t k) {
+    return al256(m * k * 2) + al256(m * 4) + al256((m + MF_MT - 1) / MF_MT * sizeof(MfTile)) + al256(4);
+}
+
+int mfma_dense(int dtype, const uint8_t *w, int64_t row_bytes, int n, int k, const float *x, int m, float *y, void *ws,
+               size_t ws_bytes, hipStream_t s) {
+    if (ws_bytes < mfma_dense_workspace(m, k) || !ws) return set_error(CW_EINVAL, "qmatmul: workspace of %zu bytes, %zu needed", ws_bytes, mfma_dense_workspace(m, k));
+    uint8_t *p = (uint8_t *)ws;
+    uint16_t *x16 = (uint16_t *)p; p += al256((size_t)m * k * 2);
+    float *xs = (float *)p; p += al256((size_t)m * 4);
+    MfTile *tiles = (MfTile *)p; p += al256((size_t)(m + MF_MT - 1) / MF_MT * sizeof(MfTile));
+    int *n_tiles = (int *)p;
+    hipLaunchKernelGGL(k_dense_tiles, dim3(1), dim3(256), 0, s, tiles, n_tiles, m);
+    int rc = check_launch("k_dense_tiles");
+    if (rc) return rc;
+    if ((rc = pack_rows_f16(x, m, k, k, x16, xs, s))) return rc;
+    MfArgs a = {};
+    a.w0 = w;
+    a.s0 = 0;
+    a.row_bytes = row_bytes;
+    a.n = n;
+    a.k = k;
+    a.a16 = x16;
+    a.ascale = xs;
+    a.lda = k;
+    a.tiles = tiles;
+    a.n_tiles = n_tiles;
+    a.K = 1;
+    a.dn = y;
+    return by_fmt<2>(dtype, a, (m + MF_MT - 1) / MF_MT, s);
 }
 
 int mfma_gateup(int dtype, const MfArgs &a, int tiles_max, hipStream_t s) { return by_fmt<0>(dtype, a, tiles_max, s); }

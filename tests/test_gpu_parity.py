@@ -18,6 +18,7 @@ pytestmark = pytest.mark.gpu
 
 REL_L2_GATE = 1e-3      # north-star tolerance for matmul / MoE outputs
 REL_L2_F32 = 2e-5       # what an f32-activation path must reach
+MFMA_TYPES = (F.IQ2_XXS, F.IQ2_S, F.IQ3_S, F.MXFP4, F.Q4_K, F.Q8_0)  # formats of the grouped / dense GEMM
 
 
 def dev(a):
@@ -72,9 +73,26 @@ QMM_CASES = [
 ]
 
 
-@pytest.mark.parametrize("dtype,n,k,m", QMM_CASES)
-def test_qmatmul_matches_the_oracle(dtype, n, k, m):
-    say("qmatmul", F.NAMES[dtype], n, k, m)
+# the MFMA GEMM path (from CWMOE_MM_MIN_ROWS rows) rounds activations to fp16 once and is held to
+# the 1e-3 gate; the matvec path keeps f32 activations and is held to the f32 bar as well
+MM_PATHS = {"matvec": "1000000", "mfma": "1"}
+MM_CASES = [
+    (F.Q4_K, 4096, 4096, 128),    # config 2, M = 128
+    (F.Q4_K, 4096, 4096, 512),    # config 2, M = 512
+    (F.Q8_0, 2048, 2048, 77),     # config 1 rows, a ragged last tile
+    (F.Q4_K, 200, 512, 70),       # N-blocks past the last row, two super-blocks per row
+    (F.Q8_0, 96, 1056, 33),       # 33 blocks per row: a partial last stage
+    (F.MXFP4, 512, 2880, 40),
+    (F.IQ2_XXS, 512, 2048, 20),
+    (F.IQ3_S, 300, 1024, 65),
+]
+
+
+@pytest.mark.parametrize("path", sorted(MM_PATHS))
+@pytest.mark.parametrize("dtype,n,k,m", QMM_CASES + MM_CASES)
+def test_qmatmul_matches_the_oracle(dtype, n, k, m, path, monkeypatch):
+    monkeypatch.setenv("CWMOE_MM_MIN_ROWS", MM_PATHS[path])
+    say("qmatmul", F.NAMES[dtype], n, k, m, path)
     rng = np.random.default_rng(n * 7 + k + m)
     raw = synth.random_blocks(dtype, n * k, rng)
     x = rng.standard_normal((m, k)).astype(np.float32)
@@ -82,7 +100,29 @@ def test_qmatmul_matches_the_oracle(dtype, n, k, m):
     want = O.qmatmul_f64(dtype, raw, n, k, x)
     err = O.rel_l2(y, want)
     say("  rel_l2", err)
-    assert err <= REL_L2_GATE and err <= REL_L2_F32
+    assert err <= REL_L2_GATE
+    if path == "matvec":
+        assert err <= REL_L2_F32
+
+
+@pytest.mark.parametrize("path", sorted(MM_PATHS))
+def test_qmatmul_edge_scales(path, monkeypatch):
+    # zero and subnormal f16 scales (and a zero dmin) take the kernels' zero-scale branches
+    monkeypatch.setenv("CWMOE_MM_MIN_ROWS", MM_PATHS[path])
+    rng = np.random.default_rng(77)
+    for dtype, n, k in ((F.Q4_K, 64, 1024), (F.Q8_0, 64, 512)):
+        raw = synth.random_blocks(dtype, n * k, rng).reshape(-1, F.type_size(dtype)).copy()
+        raw[::3, 0:2] = 0                    # d = 0
+        raw[1::5, 0:2] = [0x01, 0x00]        # smallest subnormal d
+        if dtype == F.Q4_K:
+            raw[2::7, 2:4] = 0               # dmin = 0
+        raw = raw.reshape(-1)
+        x = rng.standard_normal((48, k)).astype(np.float32)
+        y = host(ops.QMatMul(ops.QTensor.from_blocks(raw, dtype, (n, k))).forward(dev(x)))
+        want = O.qmatmul_f64(dtype, raw, n, k, x)
+        err = O.rel_l2(y, want)
+        say("edge scales", F.NAMES[dtype], path, err)
+        assert err <= REL_L2_GATE
 
 
 def test_qmatmul_rejects_bad_shapes():
@@ -240,7 +280,7 @@ def test_moe_layer_matches_the_oracle(name, E, K, h, I, dts, act, pad, T, path, 
     err = O.rel_l2(host(out), want)
     say("  rel_l2", err)
     assert err <= REL_L2_GATE
-    grouped = path == "grouped" and dts[0] == dts[1] and all(d in (F.IQ2_XXS, F.IQ2_S, F.IQ3_S, F.MXFP4) for d in (dts[0], dts[2]))
+    grouped = path == "grouped" and dts[0] == dts[1] and all(d in MFMA_TYPES for d in (dts[0], dts[2]))
     if not grouped:
         assert err <= REL_L2_F32
 
