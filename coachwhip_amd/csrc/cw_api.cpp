@@ -88,7 +88,7 @@ static bool qmatmul_mfma(int dtype, int64_t k, int64_t m) {
 size_t cw_qmatmul_workspace_size(int dtype, int64_t n, int64_t k, int64_t m) {
     (void)n;
     if (!is_weight_type(dtype) || k <= 0 || m <= 0 || !qmatmul_mfma(dtype, k, m)) return 0;
-    return cw::mfma_dense_workspace(m, k);
+    return cw::mfma_dense_workspace(dtype, m, n, k);
 }
 
 int cw_qmatmul(int dtype, const void *w, int64_t n, int64_t k, const float *x, int64_t m, float *y, void *ws,

@@ -35,6 +35,10 @@ struct MfArgs {
     float *h;                     // gate/up: hidden rows in pile order (ldh floats)
     int ldh;
     float *dn;                    // down: one row of n per pick, in pick order (t*K + j)
+    // split-K (dense matmul): block row blockIdx.y takes stages [y*split_st, (y+1)*split_st) and
+    // writes its partial rows at dn + y*split_stride; 0 = no split
+    int split_st;
+    int64_t split_stride;
 };
 
 bool mfma_supported(int dtype);
@@ -48,7 +52,7 @@ int fill_zero(float *p, int64_t n, hipStream_t s);
 int mfma_gateup(int dtype, const MfArgs &a, int tiles_max, hipStream_t s);
 int mfma_down(int dtype, const MfArgs &a, int tiles_max, hipStream_t s);
 // y (m x n) = x (m x k) . W^T for one quantized matrix, through the same GEMM (fp16 activations)
-size_t mfma_dense_workspace(int64_t m, int64_t k);
+size_t mfma_dense_workspace(int dtype, int64_t m, int64_t n, int64_t k);
 int mfma_dense(int dtype, const uint8_t *w, int64_t row_bytes, int n, int k, const float *x, int m, float *y, void *ws,
                size_t ws_bytes, hipStream_t s);
 // out[t] = sum_j w[t*K+j] * (dn[t*K+j] + bias[ids[t*K+j]]), picks in order (H a multiple of 4)

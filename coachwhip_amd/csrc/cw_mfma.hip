@@ -438,8 +438,10 @@ __global__ __launch_bounds__(256, 2) void k_gmm(const MfArgs a) {
             }
         }
 
-    for (int st = 0; st < n_st; st++) {
-        if (st) __syncthreads();  // every wave is done with the previous stage's LDS
+    const int st_lo = a.split_st ? blockIdx.y * a.split_st : 0;
+    const int st_hi = a.split_st ? min(n_st, st_lo + a.split_st) : n_st;
+    for (int st = st_lo; st < st_hi; st++) {
+        if (st != st_lo) __syncthreads();  // every wave is done with the previous stage's LDS
         const int nk = min(KST, n_ks - st * KST);              // K-steps in this stage
         const int seg = MF::SBK == 32 ? MF::TS * nk : MF::TS;  // bytes of a row in this stage
         if (stager) {
@@ -483,7 +485,7 @@ __global__ __launch_bounds__(256, 2) void k_gmm(const MfArgs a) {
 #pragma unroll
                     for (int kk = 0; kk < KST; kk++)
                         if (kk < nk) base = max(base, (int)MF::expo(win[m][q], kk));
-                    if (st > 0 && base != rb[m][q]) {
+                    if (st > st_lo && base != rb[m][q]) {
 #pragma unroll
                         for (int mb = 0; mb < 4; mb++)
 #pragma unroll
@@ -607,7 +609,7 @@ __global__ __launch_bounds__(256, 2) void k_gmm(const MfArgs a) {
                     }
                     a.h[(int64_t)pos * a.ldh + n] = o;
                 } else {
-                    a.dn[(int64_t)pick * a.n + n] = v[0];
+                    a.dn[blockIdx.y * a.split_stride + (int64_t)pick * a.n + n] = v[0];
                 }
             }
         }
@@ -778,7 +780,7 @@ int fill_zero(float *p, int64_t n, hipStream_t s) {
 }
 
 template <class MF, int MODE>
-static int launch(const MfArgs &a, int tiles_max, hipStream_t s) {
+static int launch(const MfArgs &a, int tiles_max, int splits, hipStream_t s) {
     using S = GmShape<MF, MODE>;
     if (a.k % MF::SBK) return set_error(CW_ENOTSUP, "mfma: k %d is not a multiple of %d", a.k, MF::SBK);
     const int n_nb = (a.n + S::RPB - 1) / S::RPB;
@@ -789,19 +791,19 @@ static int launch(const MfArgs &a, int tiles_max, hipStream_t s) {
             return set_error(CW_EHIP, "mfma: cannot reserve %zu bytes of LDS", S::lds_bytes());
         lds_set = true;
     }
-    hipLaunchKernelGGL((k_gmm<MF, MODE>), dim3((unsigned)blocks), dim3(256), S::lds_bytes(), s, a);
+    hipLaunchKernelGGL((k_gmm<MF, MODE>), dim3((unsigned)blocks, (unsigned)splits), dim3(256), S::lds_bytes(), s, a);
     return check_launch("k_gmm");
 }
 
 template <int MODE>
-static int by_fmt(int dtype, const MfArgs &a, int tiles_max, hipStream_t s) {
+static int by_fmt(int dtype, const MfArgs &a, int tiles_max, int splits, hipStream_t s) {
     switch (dtype) {
-    case CW_IQ2_XXS: return launch<MIQ2_XXS, MODE>(a, tiles_max, s);
-    case CW_IQ2_S: return launch<MIQ2_S, MODE>(a, tiles_max, s);
-    case CW_IQ3_S: return launch<MIQ3_S, MODE>(a, tiles_max, s);
-    case CW_MXFP4: return launch<MMXFP4, MODE>(a, tiles_max, s);
-    case CW_Q4_K: return launch<MQ4_K, MODE>(a, tiles_max, s);
-    case CW_Q8_0: return launch<MQ8_0, MODE>(a, tiles_max, s);
+    case CW_IQ2_XXS: return launch<MIQ2_XXS, MODE>(a, tiles_max, splits, s);
+    case CW_IQ2_S: return launch<MIQ2_S, MODE>(a, tiles_max, splits, s);
+    case CW_IQ3_S: return launch<MIQ3_S, MODE>(a, tiles_max, splits, s);
+    case CW_MXFP4: return launch<MMXFP4, MODE>(a, tiles_max, splits, s);
+    case CW_Q4_K: return launch<MQ4_K, MODE>(a, tiles_max, splits, s);
+    case CW_Q8_0: return launch<MQ8_0, MODE>(a, tiles_max, splits, s);
     default: return set_error(CW_ENOTSUP, "mfma: dtype %d has no MFMA path", dtype);
     }
 }
@@ -814,18 +816,53 @@ __global__ void k_dense_tiles(MfTile *tiles, int *n_tiles, int m) {
 }
 
 static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
-size_t mfma_dense_workspace(int64_t m, int64_t k) {
-    return al256(m * k * 2) + al256(m * 4) + al256((m + MF_MT - 1) / MF_MT * sizeof(MfTile)) + al256(4);
+
+// y[i] = sum over the S partial products, in split order
+__global__ void k_sum_splits(const float *part, int S, int64_t n, float *y) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        float acc = part[i];
+        for (int s = 1; s < S; s++) acc += part[s * n + i];
+        y[i] = acc;
+    }
+}
+
+// the dense GEMM's N-block rows and stage size for a format (GmShape<MF, 2>)
+static void dense_shape(int dtype, int &rpb, int &kst) {
+    rpb = dtype == CW_Q4_K ? 64 : 128;
+    kst = dtype == CW_Q8_0 ? 4 : 8;
+}
+// K splits: enough blocks to cover the chip twice, at least one stage each
+static int dense_splits(int dtype, int64_t m, int64_t n, int64_t k, int &split_st) {
+    int rpb, kst;
+    dense_shape(dtype, rpb, kst);
+    const int64_t blocks = (m + MF_MT - 1) / MF_MT * ((n + rpb - 1) / rpb);
+    const int n_st = (int)((k / 32 + kst - 1) / kst);
+    int S = (int)((512 + blocks - 1) / blocks);
+    if (S > n_st) S = n_st;
+    if (S < 1) S = 1;
+    split_st = (n_st + S - 1) / S;
+    return (n_st + split_st - 1) / split_st;
+}
+
+size_t mfma_dense_workspace(int dtype, int64_t m, int64_t n, int64_t k) {
+    int split_st;
+    const int S = dense_splits(dtype, m, n, k, split_st);
+    return al256(m * k * 2) + al256(m * 4) + al256((m + MF_MT - 1) / MF_MT * sizeof(MfTile)) + al256(4) +
+           (S > 1 ? al256((size_t)S * m * n * 4) : 0);
 }
 
 int mfma_dense(int dtype, const uint8_t *w, int64_t row_bytes, int n, int k, const float *x, int m, float *y, void *ws,
                size_t ws_bytes, hipStream_t s) {
-    if (ws_bytes < mfma_dense_workspace(m, k) || !ws) return set_error(CW_EINVAL, "qmatmul: workspace of %zu bytes, %zu needed", ws_bytes, mfma_dense_workspace(m, k));
+    const size_t need = mfma_dense_workspace(dtype, m, n, k);
+    if (ws_bytes < need || !ws) return set_error(CW_EINVAL, "qmatmul: workspace of %zu bytes, %zu needed", ws_bytes, need);
+    int split_st;
+    const int S = dense_splits(dtype, m, n, k, split_st);
     uint8_t *p = (uint8_t *)ws;
     uint16_t *x16 = (uint16_t *)p; p += al256((size_t)m * k * 2);
     float *xs = (float *)p; p += al256((size_t)m * 4);
     MfTile *tiles = (MfTile *)p; p += al256((size_t)(m + MF_MT - 1) / MF_MT * sizeof(MfTile));
-    int *n_tiles = (int *)p;
+    int *n_tiles = (int *)p; p += al256(4);
+    float *part = S > 1 ? (float *)p : nullptr;
     hipLaunchKernelGGL(k_dense_tiles, dim3(1), dim3(256), 0, s, tiles, n_tiles, m);
     int rc = check_launch("k_dense_tiles");
     if (rc) return rc;
@@ -842,11 +879,17 @@ int mfma_dense(int dtype, const uint8_t *w, int64_t row_bytes, int n, int k, con
     a.tiles = tiles;
     a.n_tiles = n_tiles;
     a.K = 1;
-    a.dn = y;
-    return by_fmt<2>(dtype, a, (m + MF_MT - 1) / MF_MT, s);
+    a.dn = S > 1 ? part : y;
+    a.split_st = S > 1 ? split_st : 0;
+    a.split_stride = (int64_t)m * n;
+    if ((rc = by_fmt<2>(dtype, a, (m + MF_MT - 1) / MF_MT, S, s))) return rc;
+    if (S == 1) return CW_OK;
+    const int64_t total = (int64_t)m * n, blocks = (total + 255) / 256;
+    hipLaunchKernelGGL(k_sum_splits, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s, part, S, total, y);
+    return check_launch("k_sum_splits");
 }
 
-int mfma_gateup(int dtype, const MfArgs &a, int tiles_max, hipStream_t s) { return by_fmt<0>(dtype, a, tiles_max, s); }
-int mfma_down(int dtype, const MfArgs &a, int tiles_max, hipStream_t s) { return by_fmt<1>(dtype, a, tiles_max, s); }
+int mfma_gateup(int dtype, const MfArgs &a, int tiles_max, hipStream_t s) { return by_fmt<0>(dtype, a, tiles_max, 1, s); }
+int mfma_down(int dtype, const MfArgs &a, int tiles_max, hipStream_t s) { return by_fmt<1>(dtype, a, tiles_max, 1, s); }
 
 }  // namespace cw
