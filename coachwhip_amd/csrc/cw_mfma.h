@@ -5,7 +5,9 @@
 
 namespace cw {
 
-constexpr int MF_MT = 64;   // picks per tile (4 MFMA blocks of 16)
+constexpr int MF_MB = 5;            // MFMA blocks of 16 picks per tile
+constexpr int MF_MT = 16 * MF_MB;   // picks per tile: 80 keeps the piles of a 1,500-token batch over
+                                    // 256 experts (about 47 picks each) at one tile per expert
 
 struct MfTile {
     int slot, pos0, m, pad;
@@ -25,6 +27,8 @@ struct MfArgs {
     // piles
     const MfTile *tiles;
     const int *n_tiles;
+    int run_tiles;             // M-tiles per run of work items (1, 2, 4 or 8; set by the launch)
+    int n_items;               // work items (M-tile, N-block) of the launch (set by the launch)
     const int *pile_pick;      // pick index (t*K + j) of each pile position
     int K;
     // epilogues

@@ -1,7 +1,8 @@
 // Grouped expert GEMMs on MFMA (gfx950, v_mfma_f32_16x16x32_f16) for the MoE layer's prefill.
 //
 // Picks are grouped by the slot they read (mfma_piles); a tile is up to 64 picks of one slot by
-// 64 weight rows. Each of the 4 waves owns 16 weight rows and all 64 picks (4 MFMA blocks).
+// 128 or 256 weight rows. Each of the 8 waves of a block owns 16 or 32 weight rows and all 64
+// picks (4 MFMA blocks).
 //
 // Exactness: a weight is (f16 super-block scale) x (small integer code). The codes go through
 // MFMA as fp16 integers, which they represent exactly: IQ2_XXS / IQ2_S codes (2s+1)*grid*sign
@@ -26,18 +27,30 @@ __device__ __forceinline__ uint32_t pk_mul_u(uint32_t v, uint32_t sc2) {
     f16x2 a = __builtin_bit_cast(f16x2, v), b = __builtin_bit_cast(f16x2, sc2);
     return __builtin_bit_cast(uint32_t, a * b);
 }
-__device__ __forceinline__ uint32_t splat_f16(int v) {
-    const uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)v);
-    return h | (h << 16);
-}
 __device__ __forceinline__ uint4 scale4(uint4 v, uint32_t sc2) {
     return make_uint4(pk_mul_u(v.x, sc2), pk_mul_u(v.y, sc2), pk_mul_u(v.z, sc2), pk_mul_u(v.w, sc2));
 }
-__device__ __forceinline__ uint4 xor4(uint4 a, uint4 b) { return make_uint4(a.x ^ b.x, a.y ^ b.y, a.z ^ b.z, a.w ^ b.w); }
+// Signs of 8 fp16 codes (dword i holds weights 2i, 2i+1; sign bits clear): bit j of b negates
+// weight j. With y = b | b << 15, y << (15 - 2i) has bit 2i of b at bit 15 and bit 2i+1 at bit
+// 31; a bit-field insert takes exactly those two bits (bits 8 and up of b never reach them).
+__device__ __forceinline__ uint32_t bfi_sign(uint32_t s, uint32_t g) { return (s & 0x80008000u) | (g & 0x7FFF7FFFu); }
+__device__ __forceinline__ uint4 apply_signs(uint4 g, uint32_t b) {
+    // an opaque b keeps the shifts as shifts: with b known to be small the compiler turns
+    // (b | b << 15) << c into one quarter-rate 32-bit multiply per dword
+    asm("" : "+v"(b));
+    const uint32_t y = b | (b << 15);
+    return make_uint4(bfi_sign(y << 15, g.x), bfi_sign(y << 13, g.y), bfi_sign(y << 11, g.z), bfi_sign(y << 9, g.w));
+}
+// fp16 pair of a small integer multiplier (exact below 2048)
+__device__ __forceinline__ uint32_t splat_mult(uint32_t v) {
+    const float m = (float)v;
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(m, m));
+}
 
 // ------------------------------------------------------------------------------ code tables
-// Lattice entries as fp16 integers and sign masks as fp16 sign bits, built at compile time; a
-// kernel copies the ones its format needs into LDS.
+// Lattice entries as fp16 integers, built at compile time; a kernel copies the one its format
+// needs into LDS. Signs are applied arithmetically (apply_signs), not through a table: a random
+// 16-byte LDS lookup costs about as much LDS time as two conflict-free ones.
 struct U4 { uint32_t x, y, z, w; };
 template <int N> struct Tab { U4 v[N]; };
 
@@ -51,17 +64,6 @@ constexpr U4 pack8(uint64_t bytes) {
     uint32_t h[8] = {};
     for (int b = 0; b < 8; b++) h[b] = f16_int((uint32_t)(bytes >> (8 * b)) & 0xFF);
     return U4{h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16};
-}
-constexpr U4 signs8(uint32_t s) {
-    uint32_t w[4] = {};
-    for (int i = 0; i < 4; i++) w[i] = (((s >> (2 * i)) & 1u) << 15) | (((s >> (2 * i + 1)) & 1u) << 31);
-    return U4{w[0], w[1], w[2], w[3]};
-}
-constexpr uint32_t parity_signs(uint32_t i7) {  // ksigns_iq2xs: 7 bits plus an even-parity bit
-    uint32_t p = i7 ^ (i7 >> 4);
-    p ^= p >> 2;
-    p ^= p >> 1;
-    return i7 | ((p & 1u) << 7);
 }
 constexpr Tab<256> make_iq2xxs_f16() {
     constexpr uint64_t g[256] = {CW_IQ2XXS_GRID_VALUES};
@@ -84,21 +86,28 @@ constexpr Tab<256> make_iq3s_f16() {  // two 4-value entries per U4: entry 2i in
     }
     return t;
 }
-constexpr Tab<128> make_parity_signs() {
-    Tab<128> t{};
-    for (int i = 0; i < 128; i++) t.v[i] = signs8(parity_signs((uint32_t)i));
-    return t;
-}
-constexpr Tab<256> make_signs() {
-    Tab<256> t{};
-    for (int i = 0; i < 256; i++) t.v[i] = signs8((uint32_t)i);
+// IQ2_XXS sign-and-scale multipliers: entry (s << 7) | s7 holds the 8 fp16 values +-8(2s+1),
+// negative where bit j of s7 | parity(s7) << 7 is set (ksigns_iq2xs: the 8th sign is the even
+// parity of the other 7); entry 2048 is all zeros (a super-block whose scale is 0).
+constexpr Tab<2049> make_iq2xxs_sm() {
+    Tab<2049> t{};
+    for (int s = 0; s < 16; s++)
+        for (uint32_t s7 = 0; s7 < 128; s7++) {
+            uint32_t p = s7 ^ (s7 >> 4);
+            p ^= p >> 2;
+            p ^= p >> 1;
+            const uint32_t b = s7 | ((p & 1u) << 7), m = f16_int(8 * (2 * s + 1));
+            uint32_t w[4] = {};
+            for (int i = 0; i < 4; i++)
+                w[i] = (m | (((b >> (2 * i)) & 1u) << 15)) | ((m | (((b >> (2 * i + 1)) & 1u) << 15)) << 16);
+            t.v[(s << 7) | s7] = U4{w[0], w[1], w[2], w[3]};
+        }
     return t;
 }
 static __constant__ Tab<256> c_iq2xxs_f16 = make_iq2xxs_f16();
+static __constant__ Tab<2049> c_iq2xxs_sm = make_iq2xxs_sm();
 static __constant__ Tab<1024> c_iq2s_f16 = make_iq2s_f16();
 static __constant__ Tab<256> c_iq3s_f16 = make_iq3s_f16();
-static __constant__ Tab<128> c_psigns = make_parity_signs();
-static __constant__ Tab<256> c_signs = make_signs();
 
 template <int N>
 __device__ __forceinline__ void copy_tab(uint8_t *lds, const Tab<N> &t, int tid, int nt) {
@@ -125,68 +134,130 @@ __device__ __forceinline__ uint2 lds_u64(const uint8_t *p) {
     return make_uint2(__builtin_amdgcn_alignbyte(d1, d0, a), __builtin_amdgcn_alignbyte(d2, d1, a));
 }
 
+// A row's stage window in LDS, with the dword address and byte shift of its 8-byte reads
+// (which start ORG bytes into the window) worked out once per stage instead of per read
+struct WinRef {
+    const uint8_t *p;     // the window: the row's bytes of this stage
+    const uint32_t *qa;   // p + ORG rounded down to a dword
+    uint32_t sh;          // (p + ORG) & 3
+    template <int ORG>
+    static __device__ __forceinline__ WinRef at(const uint8_t *p) {
+        const uint32_t o = (uint32_t)(uintptr_t)(p + ORG);
+        return WinRef{p, (const uint32_t *)(p + ORG - (o & 3)), o & 3};
+    }
+    // 8 bytes at p + ORG + off, off a multiple of 4 (the shift stays sh)
+    __device__ __forceinline__ uint2 u64(int off) const {
+        const uint32_t *q = qa + off / 4;
+        const uint32_t d0 = q[0], d1 = q[1], d2 = q[2];
+        return make_uint2(__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh));
+    }
+    // 8 bytes at p + ORG + off, any off
+    __device__ __forceinline__ uint2 u64x(int off) const {
+        const uint32_t t = sh + (uint32_t)off, a = t & 3;
+        const uint32_t *q = qa + (t >> 2);
+        const uint32_t d0 = q[0], d1 = q[1], d2 = q[2];
+        return make_uint2(__builtin_amdgcn_alignbyte(d1, d0, a), __builtin_amdgcn_alignbyte(d2, d1, a));
+    }
+};
+
 // Traits common to the formats: KST K-steps per stage; SCALE 0 = one f16 scale per super-block
 // (read by scale()), 1 = MXFP4's power-of-two block scales, 2 = one f16 scale per 32-weight block
 // (read by step_scale()); HAS_MIN = an f16 dmin per super-block and a 6-bit m per sub-block.
 struct MIQ2_XXS {
-    static constexpr int TS = 66, SBK = 256, LDS = 256 * 16 + 128 * 16;
-    static constexpr int KST = 8, SCALE = 0;
+    static constexpr int TS = 66, SBK = 256, LDS = 256 * 16 + 2049 * 16;
+    static constexpr int KST = 8, SCALE = 0, ORG = 2;
     static constexpr bool HAS_MIN = false;
     static __device__ void fill(uint8_t *lds, int tid, int nt) {
         copy_tab(lds, c_iq2xxs_f16, tid, nt);
-        copy_tab(lds + 256 * 16, c_psigns, tid, nt);
+        copy_tab(lds + 256 * 16, c_iq2xxs_sm, tid, nt);
     }
-    // zero: the super-block scale is 0, so the codes must not contribute
-    static __device__ __forceinline__ uint4 frag(const uint8_t *win, int kk, int grp, const uint8_t *lds, bool zero) {
-        const uint2 q = lds_u64(win + 2 + 8 * kk);
-        const uint4 *g = (const uint4 *)lds, *sg = (const uint4 *)(lds + 256 * 16);
-        const uint32_t gi = (q.x >> (8 * grp)) & 0xFF;
-        const uint32_t si = (q.y >> (7 * grp)) & 127;
-        const uint32_t sc = zero ? 0u : 2 * (q.y >> 28) + 1;
-        return scale4(xor4(g[gi], sg[si]), splat_f16((int)sc));
+    struct Stage {
+        __device__ __forceinline__ void load(const WinRef &, int) {}
+    };
+    // A fragment is the grid entry times a sign-and-scale entry (two lookups and 4 packed
+    // multiplies). The multiplier is 8*(2s+1), exact in fp16 with the grid values (at most
+    // 43*248 = 1333*8); scale() takes the 8 back out. zero: the super-block scale is 0, so the
+    // codes must not contribute (the all-zero entry).
+    struct Raw { uint2 q; };
+    struct Look { uint4 g, m; };
+    static __device__ __forceinline__ Raw raw(const WinRef &w, const Stage &, int kk, int) { return Raw{w.u64(8 * kk)}; }
+    static __device__ __forceinline__ Look look(const Raw &r, const Stage &, int, int grp, const uint8_t *lds, bool zero) {
+        const uint32_t sm = zero ? 2048u : ((r.q.y >> 28) << 7) | ((r.q.y >> (7 * grp)) & 127);
+        return Look{((const uint4 *)lds)[(r.q.x >> (8 * grp)) & 0xFF], ((const uint4 *)(lds + 256 * 16))[sm]};
     }
-    static __device__ __forceinline__ float scale(const uint8_t *win) { return h2f(lds_u16(win)) * 0.125f; }
+    static __device__ __forceinline__ uint4 make(const Raw &, const Look &l, const Stage &, int, int, bool) {
+        return make_uint4(pk_mul_u(l.g.x, l.m.x), pk_mul_u(l.g.y, l.m.y), pk_mul_u(l.g.z, l.m.z), pk_mul_u(l.g.w, l.m.w));
+    }
+    static __device__ __forceinline__ float scale(const uint8_t *win) { return h2f(lds_u16(win)) * (0.125f / 8); }
 };
 
 struct MIQ2_S {
-    static constexpr int TS = 82, SBK = 256, LDS = 1024 * 16 + 256 * 16;
-    static constexpr int KST = 8, SCALE = 0;
+    static constexpr int TS = 82, SBK = 256, LDS = 1024 * 16;
+    static constexpr int KST = 8, SCALE = 0, ORG = 66;
     static constexpr bool HAS_MIN = false;
-    static __device__ void fill(uint8_t *lds, int tid, int nt) {
-        copy_tab(lds, c_iq2s_f16, tid, nt);
-        copy_tab(lds + 1024 * 16, c_signs, tid, nt);
+    static __device__ void fill(uint8_t *lds, int tid, int nt) { copy_tab(lds, c_iq2s_f16, tid, nt); }
+    // The lane's bits of qh[8] and scales[8] (bytes 66..81), read once per stage: qh bits 2grp,
+    // 2grp+1 of byte kk at bits 8(kk&3) + 2(kk>>2) of qh; the scale nibble of byte kk for this
+    // lane's half at bits 8(kk&3) + 4(kk>>2) of sc.
+    struct Stage {
+        uint32_t qh, sc;
+        __device__ __forceinline__ void load(const WinRef &w, int grp) {
+            const uint2 h = w.u64(0), c = w.u64(8);
+            const int hs = 2 * grp, cs = 4 * (grp >> 1);
+            qh = ((h.x >> hs) & 0x03030303u) | (((h.y >> hs) & 0x03030303u) << 2);
+            sc = ((c.x >> cs) & 0x0F0F0F0Fu) | (((c.y >> cs) & 0x0F0F0F0Fu) << 4);
+        }
+    };
+    // multiplier 8*(2s+1) for the 4-bit scale s, as (s << 4) | 8; scale() takes the 8 back out
+    struct Raw { uint32_t qs, sgn; };
+    struct Look { uint4 g; };
+    static __device__ __forceinline__ Raw raw(const WinRef &w, const Stage &, int kk, int grp) {
+        return Raw{lds_u8(w.p + 2 + 4 * kk + grp), lds_u8(w.p + 34 + 4 * kk + grp)};
     }
-    static __device__ __forceinline__ uint4 frag(const uint8_t *win, int kk, int grp, const uint8_t *lds, bool zero) {
-        const uint32_t qs = lds_u8(win + 2 + 4 * kk + grp), sgn = lds_u8(win + 34 + 4 * kk + grp);
-        const uint32_t qh = lds_u8(win + 66 + kk), scb = lds_u8(win + 74 + kk);
-        const uint4 *g = (const uint4 *)lds, *sg = (const uint4 *)(lds + 1024 * 16);
-        const uint32_t gi = qs | (((qh >> (2 * grp)) & 3) << 8);
-        const uint32_t sc = zero ? 0u : 2 * ((scb >> (4 * (grp >> 1))) & 0xF) + 1;
-        return scale4(xor4(g[gi], sg[sgn]), splat_f16((int)sc));
+    static __device__ __forceinline__ Look look(const Raw &r, const Stage &st, int kk, int, const uint8_t *lds, bool) {
+        const uint32_t qh = (st.qh >> (8 * (kk & 3) + 2 * (kk >> 2))) & 3;
+        return Look{((const uint4 *)lds)[r.qs | (qh << 8)]};
     }
-    static __device__ __forceinline__ float scale(const uint8_t *win) { return h2f(lds_u16(win)) * 0.125f; }
+    static __device__ __forceinline__ uint4 make(const Raw &r, const Look &l, const Stage &st, int kk, int, bool zero) {
+        const uint32_t s4 = (st.sc >> (8 * (kk & 3) + 4 * (kk >> 2))) & 0xF;
+        return scale4(apply_signs(l.g, r.sgn), splat_mult(zero ? 0u : (s4 << 4) | 8));
+    }
+    static __device__ __forceinline__ float scale(const uint8_t *win) { return h2f(lds_u16(win)) * (0.125f / 8); }
 };
 
 struct MIQ3_S {
-    static constexpr int TS = 110, SBK = 256, LDS = 512 * 8 + 256 * 16;
-    static constexpr int KST = 8, SCALE = 0;
+    static constexpr int TS = 110, SBK = 256, LDS = 512 * 8;
+    static constexpr int KST = 8, SCALE = 0, ORG = 66;
     static constexpr bool HAS_MIN = false;
-    static __device__ void fill(uint8_t *lds, int tid, int nt) {
-        copy_tab(lds, c_iq3s_f16, tid, nt);   // entry i as 4 halves at byte 8*i
-        copy_tab(lds + 512 * 8, c_signs, tid, nt);
+    static __device__ void fill(uint8_t *lds, int tid, int nt) { copy_tab(lds, c_iq3s_f16, tid, nt); }  // entry i: 4 halves at byte 8*i
+    // The lane's bits of qh[8] (bytes 66..73: bits 2grp, 2grp+1 of byte kk at bits 8(kk&3) +
+    // 2(kk>>2)) and scales[4] (bytes 106..109), read once per stage (the read of the scales also
+    // takes 4 bytes past the block, which stay unused)
+    struct Stage {
+        uint32_t qh, sc;
+        __device__ __forceinline__ void load(const WinRef &w, int grp) {
+            const uint2 h = w.u64(0);
+            const int hs = 2 * grp;
+            qh = ((h.x >> hs) & 0x03030303u) | (((h.y >> hs) & 0x03030303u) << 2);
+            sc = w.u64(40).x;
+        }
+    };
+    // multiplier 8*(2s+1), as (s << 4) | 8; scale() takes the 8 back out
+    struct Raw { uint32_t qs, sgn; };
+    struct Look { uint2 x, y; };
+    static __device__ __forceinline__ Raw raw(const WinRef &w, const Stage &, int kk, int grp) {
+        return Raw{lds_u16(w.p + 2 + 8 * kk + 2 * grp), lds_u8(w.p + 74 + 4 * kk + grp)};
     }
-    static __device__ __forceinline__ uint4 frag(const uint8_t *win, int kk, int grp, const uint8_t *lds, bool zero) {
-        const uint32_t qs = lds_u16(win + 2 + 8 * kk + 2 * grp), qh = lds_u8(win + 66 + kk);
-        const uint32_t sgn = lds_u8(win + 74 + 4 * kk + grp), scb = lds_u8(win + 106 + (kk >> 1));
+    static __device__ __forceinline__ Look look(const Raw &r, const Stage &st, int kk, int, const uint8_t *lds, bool) {
+        const uint32_t qh = st.qh >> (8 * (kk & 3) + 2 * (kk >> 2));
         const uint2 *g = (const uint2 *)lds;
-        const uint4 *sg = (const uint4 *)(lds + 512 * 8);
-        const uint32_t i0 = (qs & 0xFF) | (((qh >> (2 * grp)) & 1) << 8);
-        const uint32_t i1 = (qs >> 8) | (((qh >> (2 * grp + 1)) & 1) << 8);
-        const uint2 x = g[i0], y = g[i1];
-        const uint32_t sc = zero ? 0u : 1 + 2 * ((scb >> (4 * (kk & 1))) & 0xF);
-        return scale4(xor4(make_uint4(x.x, x.y, y.x, y.y), sg[sgn]), splat_f16((int)sc));
+        return Look{g[(r.qs & 0xFF) | ((qh & 1) << 8)], g[(r.qs >> 8) | (((qh >> 1) & 1) << 8)]};
     }
-    static __device__ __forceinline__ float scale(const uint8_t *win) { return h2f(lds_u16(win)); }
+    static __device__ __forceinline__ uint4 make(const Raw &r, const Look &l, const Stage &st, int kk, int, bool zero) {
+        const uint32_t s4 = (st.sc >> (4 * kk)) & 0xF;
+        return scale4(apply_signs(make_uint4(l.x.x, l.x.y, l.y.x, l.y.y), r.sgn), splat_mult(zero ? 0u : (s4 << 4) | 8));
+    }
+    static __device__ __forceinline__ float scale(const uint8_t *win) { return h2f(lds_u16(win)) * 0.125f; }
 };
 
 // MXFP4: one scale (e8m0) per 32 weights, so per K-step. The fragment carries the power of two
@@ -212,22 +283,30 @@ static __constant__ Tab<64> c_mxfp4_pairs = make_mxfp4_pairs();
 
 struct MMXFP4 {
     static constexpr int TS = 17, SBK = 32, LDS = 1024;
-    static constexpr int KST = 8, SCALE = 1;
+    static constexpr int KST = 8, SCALE = 1, ORG = 1;
     static constexpr bool HAS_MIN = false;
     static __device__ void fill(uint8_t *lds, int tid, int nt) { copy_tab(lds, c_mxfp4_pairs, tid, nt); }
+    struct Stage {
+        __device__ __forceinline__ void load(const WinRef &, int) {}
+    };
     static __device__ __forceinline__ uint32_t expo(const uint8_t *win, int kk) { return lds_u8(win + TS * kk); }
     static __device__ __forceinline__ uint32_t pair(const uint32_t *tab, uint32_t w) {
         return tab[(w & 0xF) | ((w >> 4) & 0xF0)];
     }
-    // lane group grp takes the low (grp < 2) or high nibbles of bytes 8*(grp&1)..+8; mult is the
-    // splatted fp16 2^(e - base)
-    static __device__ __forceinline__ uint4 frag_mx(const uint8_t *win, int kk, int grp, const uint8_t *lds, uint32_t mult) {
-        const uint2 q = lds_u64(win + TS * kk + 1 + 8 * (grp & 1));
+    // lane group grp takes the low (grp < 2) or high nibbles of bytes 8*(grp&1)..+8; the
+    // multiplier is the splatted fp16 2^(e - base)
+    struct Raw { uint2 q; uint32_t e; };
+    struct Look { uint4 p; };
+    static __device__ __forceinline__ Raw raw(const WinRef &w, const Stage &, int kk, int grp) {
+        return Raw{w.u64x(TS * kk + 8 * (grp & 1)), expo(w.p, kk)};
+    }
+    static __device__ __forceinline__ Look look(const Raw &r, const Stage &, int, int grp, const uint8_t *lds, bool) {
         const uint32_t *tab = (const uint32_t *)lds;
         const int sh = 4 * (grp >> 1);
-        const uint32_t a = (q.x >> sh) & 0x0F0F0F0F, b = (q.y >> sh) & 0x0F0F0F0F;
-        return scale4(make_uint4(pair(tab, a), pair(tab, a >> 16), pair(tab, b), pair(tab, b >> 16)), mult);
+        const uint32_t a = (r.q.x >> sh) & 0x0F0F0F0F, b = (r.q.y >> sh) & 0x0F0F0F0F;
+        return Look{make_uint4(pair(tab, a), pair(tab, a >> 16), pair(tab, b), pair(tab, b >> 16))};
     }
+    static __device__ __forceinline__ uint4 make_mx(const Look &l, uint32_t mult) { return scale4(l.p, mult); }
 };
 
 // 8 small unsigned byte values (v < 1024) of two dwords -> fp16 (1024 + v), by placing each byte
@@ -252,14 +331,22 @@ __device__ __forceinline__ uint32_t splat_f16f(float v) {
 // Q8_0: codes are the int8 quants themselves (exact in fp16), one f16 scale per block (per K-step)
 struct MQ8_0 {
     static constexpr int TS = 34, SBK = 32, LDS = 16;
-    static constexpr int KST = 4, SCALE = 2;
+    static constexpr int KST = 4, SCALE = 2, ORG = 2;
     static constexpr bool HAS_MIN = false;
     static __device__ void fill(uint8_t *, int, int) {}
-    static __device__ __forceinline__ float step_scale(const uint8_t *win, int kk) { return h2f(lds_u16(win + TS * kk)); }
+    struct Stage {
+        __device__ __forceinline__ void load(const WinRef &, int) {}
+    };
     // (q + 128) + 1024 from the byte pattern, then x - 1152 (or 0 when the block's scale is 0)
-    static __device__ __forceinline__ uint4 frag(const uint8_t *win, int kk, int grp, const uint8_t *, bool zero) {
-        const uint2 q = lds_u64(win + TS * kk + 2 + 8 * grp);
-        const uint4 x = bytes_plus_1024(q.x ^ 0x80808080u, q.y ^ 0x80808080u);
+    struct Raw { uint2 q; float d; };
+    struct Look {};
+    static __device__ __forceinline__ Raw raw(const WinRef &w, const Stage &, int kk, int grp) {
+        return Raw{w.u64x(TS * kk + 8 * grp), h2f(lds_u16(w.p + TS * kk))};
+    }
+    static __device__ __forceinline__ Look look(const Raw &, const Stage &, int, int, const uint8_t *, bool) { return Look{}; }
+    static __device__ __forceinline__ float step_scale(const Raw &r) { return r.d; }
+    static __device__ __forceinline__ uint4 make(const Raw &r, const Look &, const Stage &, int, int, bool zero) {
+        const uint4 x = bytes_plus_1024(r.q.x ^ 0x80808080u, r.q.y ^ 0x80808080u);
         const uint32_t one = zero ? 0u : 0x3C003C00u, off = zero ? 0u : 0xE480E480u;  // 1.0, -1152.0
         return fma4(x, one, off);
     }
@@ -271,37 +358,51 @@ struct MQ8_0 {
 // its running scale.
 struct MQ4_K {
     static constexpr int TS = 144, SBK = 256, LDS = 16;
-    static constexpr int KST = 8, SCALE = 0;
+    static constexpr int KST = 8, SCALE = 0, ORG = 16;
     static constexpr bool HAS_MIN = true;
     static __device__ void fill(uint8_t *, int, int) {}
+    // the 12 scale bytes (4..15) of the super-block, read once per stage
+    struct Stage {
+        uint32_t b[3];
+        __device__ __forceinline__ void load(const WinRef &w, int) {
+            const uint2 lo = w.u64(-12);
+            b[0] = lo.x;
+            b[1] = lo.y;
+            b[2] = w.u64(-4).x;
+        }
+        __device__ __forceinline__ uint32_t byte(int i) const { return (b[i >> 2] >> (8 * (i & 3))) & 0xFF; }
+    };
     static __device__ __forceinline__ float scale(const uint8_t *win) { return h2f(lds_u16(win)); }
     static __device__ __forceinline__ float dmin(const uint8_t *win) { return h2f(lds_u16(win + 2)); }
     // 6-bit scale and min of sub-block j
-    static __device__ __forceinline__ void sc_m(const uint8_t *win, int j, uint32_t &sc, uint32_t &m) {
-        const uint8_t *q = win + 4;
+    static __device__ __forceinline__ void sc_m(const Stage &st, int j, uint32_t &sc, uint32_t &m) {
         if (j < 4) {
-            sc = lds_u8(q + j) & 63;
-            m = lds_u8(q + j + 4) & 63;
+            sc = st.byte(j) & 63;
+            m = st.byte(j + 4) & 63;
         } else {
-            const uint32_t a = lds_u8(q + j + 4), lo = lds_u8(q + j - 4), hi = lds_u8(q + j);
+            const uint32_t a = st.byte(j + 4), lo = st.byte(j - 4), hi = st.byte(j);
             sc = (a & 0xF) | ((lo >> 6) << 4);
             m = (a >> 4) | ((hi >> 6) << 4);
         }
     }
     // codes sc*q of sub-block kk (sub-blocks 2c, 2c+1 are the low and high nibbles of qs[32c..32c+32))
-    static __device__ __forceinline__ uint4 frag(const uint8_t *win, int kk, int grp, const uint8_t *, bool zero) {
+    struct Raw { uint2 q; };
+    struct Look {};
+    static __device__ __forceinline__ Raw raw(const WinRef &w, const Stage &, int kk, int grp) { return Raw{w.u64(32 * (kk >> 1) + 8 * grp)}; }
+    static __device__ __forceinline__ Look look(const Raw &, const Stage &, int, int, const uint8_t *, bool) { return Look{}; }
+    static __device__ __forceinline__ uint4 make(const Raw &r, const Look &, const Stage &stg, int kk, int, bool zero) {
         uint32_t sc, m;
-        sc_m(win, kk, sc, m);
+        sc_m(stg, kk, sc, m);
         if (zero) sc = 0;
-        const uint2 q = lds_u64(win + 16 + 32 * (kk >> 1) + 8 * grp);
+        const uint2 q = r.q;
         const int sh = 4 * (kk & 1);
         const uint4 x = bytes_plus_1024((q.x >> sh) & 0x0F0F0F0Fu, (q.y >> sh) & 0x0F0F0F0Fu);
         return fma4(x, splat_f16f((float)sc), splat_f16f(-1024.0f * (float)sc));
     }
     // codes -m for all 8 weights (the minimum term)
-    static __device__ __forceinline__ uint4 min_frag(const uint8_t *win, int kk, bool zero) {
+    static __device__ __forceinline__ uint4 min_frag(const Stage &stg, int kk, bool zero) {
         uint32_t sc, m;
-        sc_m(win, kk, sc, m);
+        sc_m(stg, kk, sc, m);
         const uint32_t v = zero ? 0u : splat_f16f(-(float)m);
         return make_uint4(v, v, v, v);
     }
@@ -325,6 +426,8 @@ struct Win {
 
 // ------------------------------------------------------------------------------ kernels
 
+template <int V> struct Ic { static constexpr int value = V; };
+
 __device__ __forceinline__ f16x8 as_f16x8(uint4 v) { return __builtin_bit_cast(f16x8, v); }
 
 // 16 bytes from global memory to LDS without passing through registers: lane l of the wave
@@ -333,20 +436,40 @@ __device__ __forceinline__ void dma16(const void *g, uint8_t *lds_base) {
     __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)lds_base, 16, 0, 0);
 }
 
-// Tile shape of the grouped GEMM: a block owns one M-tile (up to 64 picks of a slot, in 16-row
-// pick blocks) and RPB weight rows per matrix. Each of the 4 waves takes NB blocks of 16 rows in
-// each of its NM matrices (gate and up together for MODE 0, so the activation sees both) and
-// every pick block: per K-step it reads one activation fragment per pick block, decodes NM*NB
-// weight fragments and issues up to 4*NM*NB MFMAs.
+// Tile shape of the grouped GEMM: a block of NW = 16 waves (one block per CU, four waves per
+// SIMD at 128 registers) owns one M-tile (up to 64 picks of a slot, in 16-row pick blocks) and
+// RPB weight rows per matrix. Each wave takes NB blocks of 16 rows in each of its NM matrices
+// (gate and up together for MODE 0, so the activation sees both) and every pick block: per
+// K-step it reads one activation fragment per pick block, decodes NM*NB weight fragments and
+// issues up to 4*NM*NB MFMAs. The decode is VALU-bound, so the block keeps the whole LDS for
+// code tables that take work off the VALU, with the activations shared by all 16 waves.
 template <class MF, int MODE>
 struct GmShape {
+    static constexpr int LDS_MAX = 160 * 1024;
     static constexpr int NM = MODE == 0 ? 2 : 1;
-    // MODE 2 (dense matmul) uses narrower N-blocks than MODE 1 so one matrix still fills the chip
-    static constexpr int NB = (MODE == 1 ? 4 : 2) / (MF::HAS_MIN ? 2 : 1);  // a second accumulator set for the minimum
-    static constexpr int RPW = 16 * NB, RPB = 4 * RPW;
-    static constexpr int A_BYTES = MF::KST * 4 * 64 * 16;           // one stage of activations
+    static constexpr int NB = 1;
+    static constexpr int KA = 4, HPS = MF::KST / KA;                // K-steps per activation buffer, buffers per stage
+    static constexpr int A_HALF = KA * MF_MB * 64 * 16, A_BYTES = 2 * A_HALF;  // two activation buffers
+    static constexpr int META_BYTES = MF_MT * 8;                     // scale and pick of each row of the tile
+    static constexpr int FIXED = ((MF::LDS + 15) & ~15) + A_BYTES + META_BYTES;
+    // Gate/up: 16 waves (one block per CU), where their windows fit beside the tables. Down and
+    // dense: 8 waves, two blocks per CU where the LDS allows, so one block's item start and end
+    // (with a short K: down's is 512) overlap the other's K-steps. A wave works on one matrix:
+    // the first WPM waves on gate, the others on up (MODE 0), which keeps its registers to one
+    // accumulator set.
+    static constexpr int NW = MODE == 0 && FIXED + 16 * 16 * Win<MF>::BYTES <= LDS_MAX ? 16 : 8, NT = 64 * NW;
+    static constexpr int WPM = NW / NM;                              // waves per matrix
+    static constexpr int RPW = 16 * NB, RPB = WPM * RPW;
     static constexpr int W_BYTES = NM * RPB * Win<MF>::BYTES;       // one stage of weight windows
-    static constexpr size_t lds_bytes() { return ((MF::LDS + 15) & ~15) + A_BYTES + W_BYTES; }
+    // 8-wave blocks run two per CU where two fit. Two window buffers are taken where they fit
+    // beside the rest (without costing the second block): the weights of stage st+1 then load
+    // while stage st computes.
+    static constexpr int BASE_BYTES = FIXED + W_BYTES;
+    static constexpr int PER_CU = NW == 8 && 2 * BASE_BYTES <= LDS_MAX ? 2 : 1;  // resident blocks per CU
+    static constexpr bool WDB = PER_CU * (BASE_BYTES + W_BYTES) <= LDS_MAX;
+    static constexpr size_t lds_bytes() { return BASE_BYTES + (WDB ? W_BYTES : 0); }
+    static_assert(BASE_BYTES <= LDS_MAX, "the GEMM's LDS does not fit");
+    static_assert(MODE != 0 || MF_MT * RPB * 4 <= A_BYTES, "the gate/up exchange does not fit the activation buffers");
 };
 
 // MODE 0: gate and up with the activation, hidden rows written in pile order.
@@ -367,249 +490,400 @@ struct GmShape {
 // unit's codes accumulate on top; the epilogue multiplies by the last scale. This keeps one
 // accumulator per output instead of a partial sum per scale unit.
 template <class MF, int MODE>
-__global__ __launch_bounds__(256, 2) void k_gmm(const MfArgs a) {
+__global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
     using S = GmShape<MF, MODE>;
     using W = Win<MF>;
-    constexpr int NM = S::NM, NB = S::NB, KST = MF::KST;
+    constexpr int NB = S::NB, KST = MF::KST;
+    constexpr int NM = 1;  // matrices per wave (a block has S::NM: gate/up waves are split)
     constexpr bool POW2 = MF::SCALE == 1, STEP = MF::SCALE == 2, MIN = MF::HAS_MIN;
     constexpr int NA = MIN ? NB : 1;  // accumulator sets of the minimum term
     extern __shared__ __align__(16) uint8_t smem[];
     uint8_t *tab = smem;
     uint8_t *As = smem + ((MF::LDS + 15) & ~15);
-    uint8_t *Ws = As + S::A_BYTES;
+    uint8_t *Ws = As + S::A_BYTES;  // window buffer(s): stage st uses Ws + (WDB ? st & 1 : 0) * W_BYTES
+    float *meta_sa = (float *)(Ws + (S::WDB ? 2 : 1) * S::W_BYTES);
+    int *meta_pick = (int *)(meta_sa + MF_MT);
     const int n_nb = (a.n + S::RPB - 1) / S::RPB;
-    // blocks go to XCDs round-robin; block b of each run of 8*n_nb takes M-tile 8*run + b%8 and
-    // N-block b/8, so an M-tile's N-blocks share an XCD (and its L2 copy of the activations)
-    const int run = blockIdx.x / (8 * n_nb), b = blockIdx.x - run * 8 * n_nb;
-    const int mt = run * 8 + (b & 7);
-    if (mt >= *a.n_tiles) return;  // whole block exits before any barrier
-    const int nblk = b >> 3;
-    const MfTile tile = a.tiles[mt];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = lane >> 4, l16 = lane & 15;
-    const int mbs = (tile.m + 15) >> 4;
-    MF::fill(tab, tid, 256);
+    // blocks go to the 8 XCDs round-robin; item b of each run of R*n_nb (R = run_tiles) takes
+    // M-tile R*run + b%R and N-block b/R. With R = 8 an M-tile's N-blocks share an XCD (and its
+    // L2 copy of the activations); with fewer tiles than 8, R < 8 spreads each tile's N-blocks
+    // over R-strided XCDs instead of leaving XCDs idle.
+    MF::fill(tab, threadIdx.x, S::NT);
+    // Persistent blocks: block b takes work items b, b + gridDim.x, ... (gridDim.x is a multiple of
+    // 8, so every item of a block maps to the block's XCD), and fills the code tables once.
+    const int R = a.run_tiles, n_tiles = *a.n_tiles;
+    for (int item = blockIdx.x; item < a.n_items; item += gridDim.x) {
+        const int run = item / (R * n_nb), b = item - run * R * n_nb;
+        const int mt = run * R + (b & (R - 1));
+        if (mt >= n_tiles) continue;  // uniform across the block
+        const int nblk = b / R;
+        __syncthreads();  // the tables are in, and every wave is done with the previous item's LDS
+        // lane values from an opaque copy of the thread index, so that nothing derived from them
+        // is hoisted out of the item loop and kept in registers across items
+        int tidi = threadIdx.x;
+        asm("" : "+v"(tidi));
+        const int tid = tidi, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), grp = lane >> 4, l16 = lane & 15;
+        const MfTile tile = a.tiles[mt];
+        const int mbs = (tile.m + 15) >> 4;
 
-    // the activation row this lane copies: pick block `wave`, row l16, k-group grp
-    const bool stager = wave < mbs;
-    const int apos = tile.pos0 + min(16 * wave + l16, tile.m - 1);
-    const uint16_t *asrc = a.a16 + (int64_t)(a.rows ? a.rows[apos] : apos) * a.lda + 8 * grp;
-
-    // row r of the block (r < NM*RPB: matrix r / RPB, row nblk*RPB + r % RPB; rows past n read row 0)
-    auto row_ptr = [&](int r) -> const uint8_t * {
-        const int m = r / S::RPB, n = nblk * S::RPB + (r - m * S::RPB);
-        const int64_t roff = (int64_t)(n < a.n ? n : 0) * a.row_bytes;
-        return (m == 0 ? a.w0 + (int64_t)tile.slot * a.s0 : a.w1 + (int64_t)tile.slot * a.s1) + roff;
-    };
-
-    const int n_ks = a.k / 32, n_st = (n_ks + KST - 1) / KST;
-    f32x4 acc[NM][NB][4];
-    f32x4 accm[NM][NA][4];  // minimum term (Q4_K)
-    float rs[NM][NB];     // running scale (f16 scales) ...
-    int rb[NM][NB];       // ... or running base exponent (MXFP4)
-    float rsm[NM][NA];    // running dmin (Q4_K)
-    uint32_t lrow[NM][NB];  // this lane's window row within the block's windows
-    uintptr_t lptr[NM][NB]; // this lane's row in global memory (its alignment gives the shift)
-#pragma unroll
-    for (int m = 0; m < NM; m++)
-#pragma unroll
-        for (int q = 0; q < NB; q++) {
-            rs[m][q] = 1.f;
-            rb[m][q] = 0;
-            lrow[m][q] = m * S::RPB + wave * S::RPW + 16 * q + l16;
-            lptr[m][q] = (uintptr_t)row_ptr(lrow[m][q]);
-#pragma unroll
-            for (int mb = 0; mb < 4; mb++) {
-                acc[m][q][mb] = f32x4{0, 0, 0, 0};
-                asm volatile("" : "+v"(acc[m][q][mb]));  // see accm below
-            }
-        }
-#pragma unroll
-    for (int m = 0; m < NM; m++)
-#pragma unroll
-        for (int q = 0; q < NA; q++) {
-            rsm[m][q] = 1.f;
-#pragma unroll
-            for (int mb = 0; mb < 4; mb++) {
-                accm[m][q][mb] = f32x4{0, 0, 0, 0};
-                // the compiler must not treat the four elements as one value from here on: with
-                // that assumption it fed later MFMAs three stale copies (wrong rows 1-3 of each
-                // 4-row group); the empty asm emits nothing
-                asm volatile("" : "+v"(accm[m][q][mb]));
-            }
+        // the epilogue's activation scale and pick index of tile row tid, fetched now and put in LDS
+        // with the first stage
+        float my_sa = 0.f;
+        int my_pick = 0;
+        if (tid < tile.m) {
+            const int pos = tile.pos0 + tid;
+            my_sa = a.ascale[a.rows ? a.rows[pos] : pos];
+            my_pick = a.pile_pick ? a.pile_pick[pos] : pos;
         }
 
-    const int st_lo = a.split_st ? blockIdx.y * a.split_st : 0;
-    const int st_hi = a.split_st ? min(n_st, st_lo + a.split_st) : n_st;
-    for (int st = st_lo; st < st_hi; st++) {
-        if (st != st_lo) __syncthreads();  // every wave is done with the previous stage's LDS
-        const int nk = min(KST, n_ks - st * KST);              // K-steps in this stage
-        const int seg = MF::SBK == 32 ? MF::TS * nk : MF::TS;  // bytes of a row in this stage
-        if (stager) {
-#pragma unroll
-            for (int kk = 0; kk < KST; kk++)
-                if (kk < nk) dma16(asrc + (st * KST + kk) * 32, As + ((kk * 4 + wave) * 64) * 16);
-        }
-        constexpr int NP = NM * S::RPB * W::PCS;  // pieces of the block's windows, a multiple of 64
-#pragma unroll
-        for (int t = 0; t < (NP + 255) / 256; t++) {
-            const int i = tid + 256 * t, r = i / W::PCS, p = i - r * W::PCS;
-            if (i >= NP) break;  // uniform across the wave
-            const uint8_t *o = row_ptr(r) + (int64_t)W::SEG * st;
-            const uint8_t *base = (const uint8_t *)((uintptr_t)o & ~(uintptr_t)15);
-            if (base + 16 * p < o + seg) dma16(base + 16 * p, Ws + (256 * t + 64 * wave) * 16);
-        }
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
+        // the activation row this lane copies: pick block `wave`, row l16, k-group grp
+        const bool stager = wave < mbs;
+        const int apos = tile.pos0 + min(16 * wave + l16, tile.m - 1);
+        const uint16_t *asrc = a.a16 + (int64_t)(a.rows ? a.rows[apos] : apos) * a.lda + 8 * grp;
 
-        // this lane's windows
-        const uint8_t *win[NM][NB];
+        // Row r of the block is row nblk*RPB + r % RPB of matrix r / RPB (rows past n read row 0).
+        // Addresses are the block's matrix base (uniform) plus 32-bit offsets (a matrix is under
+        // 4 GiB: checked at launch), so they need no 64-bit registers per row.
+        const uint8_t *wb0 = a.w0 + (int64_t)tile.slot * a.s0;
+        const uint8_t *wb1 = S::NM > 1 ? a.w1 + (int64_t)tile.slot * a.s1 : wb0;
+        const int mw = S::NM > 1 ? wave / S::WPM : 0;  // this wave's matrix
+        const int wrow = (wave - mw * S::WPM) * S::RPW;  // its first row within the matrix's N-block
+        auto row_off = [&](int r, int m) -> uint32_t {  // byte offset of row r within matrix m
+            const int n = nblk * S::RPB + (r - m * S::RPB);
+            return (uint32_t)(n < a.n ? n : 0) * (uint32_t)a.row_bytes;
+        };
+
+        const int n_ks = a.k / 32, n_st = (n_ks + KST - 1) / KST;
+        f32x4 acc[NM][NB][MF_MB];
+        f32x4 accm[NM][NA][MF_MB];  // minimum term (Q4_K)
+        float rs[NM][NB];     // running scale (f16 scales) ...
+        int rb[NM][NB];       // ... or running base exponent (MXFP4)
+        float rsm[NM][NA];    // running dmin (Q4_K)
 #pragma unroll
         for (int m = 0; m < NM; m++)
 #pragma unroll
-            for (int q = 0; q < NB; q++)
-                win[m][q] = Ws + lrow[m][q] * W::BYTES + ((lptr[m][q] + (uintptr_t)W::SEG * st) & 15);
+            for (int q = 0; q < NB; q++) {
+                rs[m][q] = 1.f;
+                rb[m][q] = 0;
+#pragma unroll
+                for (int mb = 0; mb < MF_MB; mb++) {
+                    acc[m][q][mb] = f32x4{0, 0, 0, 0};
+                    asm volatile("" : "+v"(acc[m][q][mb]));  // see accm below
+                }
+            }
+#pragma unroll
+        for (int m = 0; m < NM; m++)
+#pragma unroll
+            for (int q = 0; q < NA; q++) {
+                rsm[m][q] = 1.f;
+#pragma unroll
+                for (int mb = 0; mb < MF_MB; mb++) {
+                    accm[m][q][mb] = f32x4{0, 0, 0, 0};
+                    // the compiler must not treat the four elements as one value from here on: with
+                    // that assumption it fed later MFMAs three stale copies (wrong rows 1-3 of each
+                    // 4-row group); the empty asm emits nothing
+                    asm volatile("" : "+v"(accm[m][q][mb]));
+                }
+            }
 
-        bool zero[NM][NB], zerom[NM][NA];
-        if constexpr (STEP) {
+        // The weight windows of stage st_w into buffer wbuf: every wave issues exactly NTW loads
+        // (waves past the last piece repeat the first ones, writing the same bytes to the same place,
+        // and pieces past a row's last one re-load that one into a slot nothing reads), so the
+        // stage's wait can leave exactly the next stage's loads in flight. RPB*PCS is a multiple of
+        // 64: a wave's pieces lie in one matrix and the matrix base stays scalar.
+        constexpr int NP = S::NM * S::RPB * W::PCS, NTW = (NP + S::NT - 1) / S::NT;
+        auto issue_w = [&](int st_w, uint8_t *wbuf, int tido) __attribute__((always_inline)) {
+            const int nk_w = min(KST, n_ks - st_w * KST);
+            const uint32_t seg_w = MF::SBK == 32 ? MF::TS * nk_w : MF::TS;  // bytes of a row in this stage
 #pragma unroll
-            for (int m = 0; m < NM; m++)
+            for (int t = 0; t < NTW; t++) {
+                const int i0 = tido + S::NT * t, i = i0 < NP ? i0 : i0 - NP;  // the wrap is uniform across the wave
+                const int r = i / W::PCS, p = i - r * W::PCS;
+                const int m = __builtin_amdgcn_readfirstlane(r / S::RPB);
+                const uint8_t *mb = m == 0 ? wb0 : wb1;
+                const uint32_t o = row_off(r, m) + (uint32_t)(W::SEG * st_w);  // the row's stage bytes
+                const uint32_t mis = ((uint32_t)(uintptr_t)mb + o) & 15;      // ... from a 16-byte boundary
+                const uint32_t pc = min((uint32_t)p, (mis + seg_w - 1) >> 4);
+                dma16(mb + (o - mis + 16 * pc), wbuf + (i - (tido & 63)) * 16);
+            }
+        };
+        // Activations of half-stage h (K-steps h*KA .. h*KA+KA-1, clamped to the row: a clamped load
+        // fills a slot nothing reads) into buffer h & 1, by the waves that own a pick block.
+        auto issue_a = [&](int h) __attribute__((always_inline)) {
+            if (stager) {
 #pragma unroll
-                for (int q = 0; q < NB; q++) zero[m][q] = false;
-        } else if constexpr (POW2) {
+                for (int kk = 0; kk < S::KA; kk++)
+                    dma16(asrc + min(h * S::KA + kk, n_ks - 1) * 32, As + (h & 1) * S::A_HALF + ((kk * MF_MB + wave) * 64) * 16);
+            }
+        };
+        // vmcnt(NTW) alone: every load but this wave's last NTW (the next stage's windows) is done
+        constexpr int WAIT_BUT_W = (NTW & 15) | ((NTW >> 4) << 14) | (7 << 4) | (15 << 8);
+
+        // Pipeline: the activations of the next half-stage load while this one computes (two
+        // buffers), and where two window buffers fit, the next stage's windows load during the whole
+        // stage. One barrier per half-stage both publishes its loads and frees the buffer they
+        // replace; a single window buffer needs a second barrier before it is refilled.
+        const int st_lo = a.split_st ? blockIdx.y * a.split_st : 0;
+        const int st_hi = a.split_st ? min(n_st, st_lo + a.split_st) : n_st;
+        issue_a(st_lo * S::HPS);
+        if constexpr (S::WDB) issue_w(st_lo, Ws + (st_lo & 1) * S::W_BYTES, tid);
+        for (int st = st_lo; st < st_hi; st++) {
+            // Per-lane addressing is recomputed from an opaque copy of the thread index each stage
+            // (a few integer operations) rather than kept in registers across the stage loop.
+            int tido = tid;
+            asm("" : "+v"(tido));
+            const int l16o = tido & 15;
+            const int nk = min(KST, n_ks - st * KST);              // K-steps in this stage
+            uint8_t *const Wst = Ws + (S::WDB ? (st & 1) * S::W_BYTES : 0);
+            if (st == st_lo && tid < MF_MT) {
+                meta_sa[tid] = my_sa;
+                meta_pick[tid] = my_pick;
+            }
+            if constexpr (!S::WDB) {
+                if (st != st_lo) __syncthreads();  // every wave is done with the previous stage's windows
+                issue_w(st, Wst, tido);
+            }
+            __builtin_amdgcn_s_waitcnt(0);  // this stage's windows and first activations
+            __syncthreads();
+            if (S::HPS == 2)
+                issue_a(2 * st + 1);
+            else if (st + 1 < st_hi)
+                issue_a(st + 1);
+            if constexpr (S::WDB)
+                if (st + 1 < st_hi) issue_w(st + 1, Ws + ((st + 1) & 1) * S::W_BYTES, tido);
+
+            // this lane's windows
+            const uint8_t *win[NM][NB];
+            WinRef wr[NM][NB];
+            typename MF::Stage stg[NM][NB];
 #pragma unroll
             for (int m = 0; m < NM; m++)
 #pragma unroll
                 for (int q = 0; q < NB; q++) {
-                    zero[m][q] = false;
-                    int base = 0;
-#pragma unroll
-                    for (int kk = 0; kk < KST; kk++)
-                        if (kk < nk) base = max(base, (int)MF::expo(win[m][q], kk));
-                    if (st > st_lo && base != rb[m][q]) {
-#pragma unroll
-                        for (int mb = 0; mb < 4; mb++)
-#pragma unroll
-                            for (int i = 0; i < 4; i++) acc[m][q][mb][i] = ldexpf(acc[m][q][mb][i], rb[m][q] - base);
-                    }
-                    rb[m][q] = base;
+                    // this lane's row within the block's windows, and its start in global memory mod 16
+                    const int lrow = mw * S::RPB + wrow + 16 * q + l16o;
+                    const uint32_t lmis = (uint32_t)(uintptr_t)(mw == 0 ? wb0 : wb1) + row_off(lrow, mw);
+                    win[m][q] = Wst + lrow * W::BYTES + ((lmis + (uint32_t)(W::SEG * st)) & 15);
+                    wr[m][q] = WinRef::at<MF::ORG>(win[m][q]);
+                    stg[m][q].load(wr[m][q], grp);
                 }
-        } else {
-#pragma unroll
-            for (int m = 0; m < NM; m++)
-#pragma unroll
-                for (int q = 0; q < NB; q++) {
-                    const float d = MF::scale(win[m][q]);
-                    zero[m][q] = d == 0.f;
-                    if (d != 0.f) {
-                        const float ratio = __fdividef(rs[m][q], d);
-#pragma unroll
-                        for (int mb = 0; mb < 4; mb++) acc[m][q][mb] *= ratio;
-                        rs[m][q] = d;
-                    }
-                    if constexpr (MIN) {
-                        const float dm = MF::dmin(win[m][q]);
-                        zerom[m][q] = dm == 0.f;
-                        if (dm != 0.f) {
-                            const float ratio = __fdividef(rsm[m][q], dm);
-#pragma unroll
-                            for (int mb = 0; mb < 4; mb++) accm[m][q][mb] *= ratio;
-                            rsm[m][q] = dm;
-                        }
-                    }
-                }
-        }
 
-#pragma unroll
-        for (int kk = 0; kk < KST; kk++) {
-            if (kk >= nk) break;
+            bool zero[NM][NB], zerom[NM][NA];
             if constexpr (STEP) {
-                // a scale per K-step: move each accumulator onto it
+#pragma unroll
+                for (int m = 0; m < NM; m++)
+#pragma unroll
+                    for (int q = 0; q < NB; q++) zero[m][q] = false;
+            } else if constexpr (POW2) {
 #pragma unroll
                 for (int m = 0; m < NM; m++)
 #pragma unroll
                     for (int q = 0; q < NB; q++) {
-                        const float d = MF::step_scale(win[m][q], kk);
+                        zero[m][q] = false;
+                        int base = 0;
+#pragma unroll
+                        for (int kk = 0; kk < KST; kk++)
+                            if (kk < nk) base = max(base, (int)MF::expo(win[m][q], kk));
+                        if (st > st_lo && base != rb[m][q]) {
+#pragma unroll
+                            for (int mb = 0; mb < MF_MB; mb++)
+#pragma unroll
+                                for (int i = 0; i < 4; i++) acc[m][q][mb][i] = ldexpf(acc[m][q][mb][i], rb[m][q] - base);
+                        }
+                        rb[m][q] = base;
+                    }
+            } else {
+#pragma unroll
+                for (int m = 0; m < NM; m++)
+#pragma unroll
+                    for (int q = 0; q < NB; q++) {
+                        const float d = MF::scale(win[m][q]);
                         zero[m][q] = d == 0.f;
                         if (d != 0.f) {
                             const float ratio = __fdividef(rs[m][q], d);
 #pragma unroll
-                            for (int mb = 0; mb < 4; mb++) acc[m][q][mb] *= ratio;
+                            for (int mb = 0; mb < MF_MB; mb++) acc[m][q][mb] *= ratio;
                             rs[m][q] = d;
+                        }
+                        if constexpr (MIN) {
+                            const float dm = MF::dmin(win[m][q]);
+                            zerom[m][q] = dm == 0.f;
+                            if (dm != 0.f) {
+                                const float ratio = __fdividef(rsm[m][q], dm);
+#pragma unroll
+                                for (int mb = 0; mb < MF_MB; mb++) accm[m][q][mb] *= ratio;
+                                rsm[m][q] = dm;
+                            }
                         }
                     }
             }
-            f16x8 bf[NM][NB], bm[NM][NA];
+
+            // The K-steps, with the tile's count of 16-pick MFMA blocks as a constant, software
+            // pipelined: the window bytes of a step are requested two steps ahead (step kk asks for
+            // those of kk+2 once its own are decoded), so only the table lookups and activation loads
+            // of a step wait on LDS within it. A scheduling fence closes each step (without it the
+            // compiler interleaves all eight steps and runs out of registers).
+            auto ksteps = [&](auto mbs_c) __attribute__((always_inline)) {
+                constexpr int MBS = decltype(mbs_c)::value;
+                const int nke = MF::SBK == 32 ? nk : KST;  // super-block formats: every stage is whole
+                typename MF::Raw rw[2][NM][NB];
+                typename MF::Look lk[NM][NB];
+                auto issue_raw = [&](int kk) __attribute__((always_inline)) {
 #pragma unroll
-            for (int m = 0; m < NM; m++)
+                    for (int m = 0; m < NM; m++)
 #pragma unroll
-                for (int q = 0; q < NA; q++)
-                    if constexpr (MIN) bm[m][q] = as_f16x8(MF::min_frag(win[m][q], kk, zerom[m][q]));
+                        for (int q = 0; q < NB; q++) rw[kk & 1][m][q] = MF::raw(wr[m][q], stg[m][q], kk, grp);
+                };
+                auto issue_look = [&](int kk) __attribute__((always_inline)) {
 #pragma unroll
-            for (int m = 0; m < NM; m++)
+                    for (int m = 0; m < NM; m++)
 #pragma unroll
-                for (int q = 0; q < NB; q++) {
-                    if constexpr (POW2)
-                        bf[m][q] = as_f16x8(MF::frag_mx(win[m][q], kk, grp, tab, pow2_f16x2((int)MF::expo(win[m][q], kk) - rb[m][q])));
-                    else
-                        bf[m][q] = as_f16x8(MF::frag(win[m][q], kk, grp, tab, zero[m][q]));
-                }
+                        for (int q = 0; q < NB; q++) lk[m][q] = MF::look(rw[kk & 1][m][q], stg[m][q], kk, grp, tab, zero[m][q]);
+                };
+                issue_raw(0);
+                if (1 < nke) issue_raw(1);
 #pragma unroll
-            for (int mb = 0; mb < 4; mb++) {
-                if (mb >= mbs) break;
-                const f16x8 av = *(const f16x8 *)(As + ((kk * 4 + mb) * 64 + lane) * 16);
-#pragma unroll
-                for (int m = 0; m < NM; m++)
-#pragma unroll
-                    for (int q = 0; q < NB; q++) {
-                        acc[m][q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bf[m][q], acc[m][q][mb], 0, 0, 0);
-                        if constexpr (MIN) accm[m][q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bm[m][q], accm[m][q][mb], 0, 0, 0);
+                for (int kk = 0; kk < KST; kk++) {
+                    if (kk >= nke) break;
+                    if (S::HPS == 2 && kk == S::KA) {
+                        // second half-stage: its activations (loaded during the first) are in
+                        if (S::WDB && st + 1 < st_hi)
+                            __builtin_amdgcn_s_waitcnt(WAIT_BUT_W);
+                        else
+                            __builtin_amdgcn_s_waitcnt(0);
+                        __syncthreads();
+                        if (st + 1 < st_hi) issue_a(2 * (st + 1));
                     }
+                    issue_look(kk);
+                    const uint8_t *Ak = As + ((S::HPS == 2 ? kk / S::KA : st) & 1) * S::A_HALF + (kk % S::KA) * MF_MB * 64 * 16;
+                    f16x8 av[MBS];
+#pragma unroll
+                    for (int mb = 0; mb < MBS; mb++) av[mb] = *(const f16x8 *)(Ak + (mb * 64 + lane) * 16);
+                    if constexpr (STEP) {
+                        // a scale per K-step: move each accumulator onto it
+#pragma unroll
+                        for (int m = 0; m < NM; m++)
+#pragma unroll
+                            for (int q = 0; q < NB; q++) {
+                                const float d = MF::step_scale(rw[kk & 1][m][q]);
+                                zero[m][q] = d == 0.f;
+                                if (d != 0.f) {
+                                    const float ratio = __fdividef(rs[m][q], d);
+#pragma unroll
+                                    for (int mb = 0; mb < MBS; mb++) acc[m][q][mb] *= ratio;
+                                    rs[m][q] = d;
+                                }
+                            }
+                    }
+                    f16x8 bf[NM][NB], bm[NM][NA];
+#pragma unroll
+                    for (int m = 0; m < NM; m++)
+#pragma unroll
+                        for (int q = 0; q < NA; q++)
+                            if constexpr (MIN) bm[m][q] = as_f16x8(MF::min_frag(stg[m][q], kk, zerom[m][q]));
+#pragma unroll
+                    for (int m = 0; m < NM; m++)
+#pragma unroll
+                        for (int q = 0; q < NB; q++) {
+                            if constexpr (POW2)
+                                bf[m][q] = as_f16x8(MF::make_mx(lk[m][q], pow2_f16x2((int)rw[kk & 1][m][q].e - rb[m][q])));
+                            else
+                                bf[m][q] = as_f16x8(MF::make(rw[kk & 1][m][q], lk[m][q], stg[m][q], kk, grp, zero[m][q]));
+                        }
+                    if (kk + 2 < KST && kk + 2 < nke) issue_raw(kk + 2);  // into the buffer step kk has just used
+#pragma unroll
+                    for (int mb = 0; mb < MBS; mb++)
+#pragma unroll
+                        for (int m = 0; m < NM; m++)
+#pragma unroll
+                            for (int q = 0; q < NB; q++) {
+                                acc[m][q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[mb], bf[m][q], acc[m][q][mb], 0, 0, 0);
+                                if constexpr (MIN) accm[m][q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[mb], bm[m][q], accm[m][q][mb], 0, 0, 0);
+                            }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            };
+            switch (mbs) {
+            case 1: ksteps(Ic<1>{}); break;
+            case 2: ksteps(Ic<2>{}); break;
+            case 3: ksteps(Ic<3>{}); break;
+            case 4: ksteps(Ic<4>{}); break;
+            default: ksteps(Ic<5>{}); break;
             }
         }
-    }
 
-    // epilogue: lane holds picks 16*mb + 4*grp + i (i < 4) of weight row n (block q)
-    float fs[NM][NB];
+        // epilogue: lane holds picks 16*mb + 4*grp + i (i < 4) of weight row n (block q)
+        float fs[NB];
 #pragma unroll
-    for (int m = 0; m < NM; m++)
+        for (int q = 0; q < NB; q++) fs[q] = POW2 ? ldexpf(1.0f, rb[0][q] - 128) : rs[0][q];
+        auto value = [&](int q, int mb, int i, float sa) __attribute__((always_inline)) {
+            float v = acc[0][q][mb][i] * fs[q];
+            if constexpr (MIN) v += accm[0][q][mb][i] * rsm[0][q];
+            return v * sa;
+        };
+        if constexpr (MODE == 0) {
+            // the up waves hand their values to the gate waves through LDS (the activation
+            // buffers, free once every wave is past the last K-step)
+            float *xu = (float *)As;
+            __syncthreads();
+            if (mw == 1) {
 #pragma unroll
-        for (int q = 0; q < NB; q++) fs[m][q] = POW2 ? ldexpf(1.0f, rb[m][q] - 128) : rs[m][q];
+                for (int mb = 0; mb < MF_MB; mb++) {
+                    if (mb >= mbs) break;
 #pragma unroll
-    for (int mb = 0; mb < 4; mb++) {
-        if (mb >= mbs) break;
+                    for (int i = 0; i < 4; i++) {
+                        const int r = 16 * mb + 4 * grp + i;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int r = 16 * mb + 4 * grp + i;
-            if (r >= tile.m) continue;
-            const int pos = tile.pos0 + r;
-            const float sa = a.ascale[a.rows ? a.rows[pos] : pos];
-            const int pick = a.pile_pick ? a.pile_pick[pos] : pos;
-#pragma unroll
-            for (int q = 0; q < NB; q++) {
-                const int n = nblk * S::RPB + wave * S::RPW + 16 * q + l16;
-                if (n >= a.n) continue;
-                float v[NM];
-#pragma unroll
-                for (int m = 0; m < NM; m++) {
-                    v[m] = acc[m][q][mb][i] * fs[m][q];
-                    if constexpr (MIN) v[m] += accm[m][q][mb][i] * rsm[m][q];
-                    v[m] *= sa;
-                }
-                if constexpr (MODE == 0) {
-                    float g = v[0], u = v[NM - 1], o;
-                    if (a.act == CW_ACT_SILU) {
-                        o = g / (1.0f + expf(-g)) * u;
-                    } else {
-                        const uint32_t e = a.ids[pick];
-                        if (a.bias0) g += a.bias0[(int64_t)e * a.n + n];
-                        if (a.bias1) u += a.bias1[(int64_t)e * a.n + n];
-                        g = fminf(g, a.limit);
-                        u = fminf(fmaxf(u, -a.limit), a.limit);
-                        o = (u + 1.0f) * (g * (1.0f / (1.0f + expf(-(g * a.alpha)))));
+                        for (int q = 0; q < NB; q++) xu[r * S::RPB + wrow + 16 * q + l16] = value(q, mb, i, meta_sa[r]);
                     }
-                    a.h[(int64_t)pos * a.ldh + n] = o;
-                } else {
-                    a.dn[blockIdx.y * a.split_stride + (int64_t)pick * a.n + n] = v[0];
+                }
+            }
+            __syncthreads();
+            if (mw == 0) {
+#pragma unroll
+                for (int mb = 0; mb < MF_MB; mb++) {
+                    if (mb >= mbs) break;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int r = 16 * mb + 4 * grp + i;
+                        if (r >= tile.m) continue;
+                        const int pos = tile.pos0 + r;
+                        const int pick = meta_pick[r];
+#pragma unroll
+                        for (int q = 0; q < NB; q++) {
+                            const int n = nblk * S::RPB + wrow + 16 * q + l16;
+                            if (n >= a.n) continue;
+                            float g = value(q, mb, i, meta_sa[r]), u = xu[r * S::RPB + wrow + 16 * q + l16], o;
+                            if (a.act == CW_ACT_SILU) {
+                                o = g / (1.0f + expf(-g)) * u;
+                            } else {
+                                const uint32_t e = a.ids[pick];
+                                if (a.bias0) g += a.bias0[(int64_t)e * a.n + n];
+                                if (a.bias1) u += a.bias1[(int64_t)e * a.n + n];
+                                g = fminf(g, a.limit);
+                                u = fminf(fmaxf(u, -a.limit), a.limit);
+                                o = (u + 1.0f) * (g * (1.0f / (1.0f + expf(-(g * a.alpha)))));
+                            }
+                            a.h[(int64_t)pos * a.ldh + n] = o;
+                        }
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int mb = 0; mb < MF_MB; mb++) {
+                if (mb >= mbs) break;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int r = 16 * mb + 4 * grp + i;
+                    if (r >= tile.m) continue;
+                    const int pick = meta_pick[r];
+#pragma unroll
+                    for (int q = 0; q < NB; q++) {
+                        const int n = nblk * S::RPB + wrow + 16 * q + l16;
+                        if (n >= a.n) continue;
+                        a.dn[blockIdx.y * a.split_stride + (int64_t)pick * a.n + n] = value(q, mb, i, meta_sa[r]);
+                    }
                 }
             }
         }
@@ -779,19 +1053,39 @@ int fill_zero(float *p, int64_t n, hipStream_t s) {
     return check_launch("k_fill_zero");
 }
 
+// persistent GEMM blocks: per_cu per CU, a multiple of 8 (the XCD count)
+static int64_t resident_blocks(int per_cu = 1) {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 8) n = 256;
+        cus = n / 8 * 8;
+    }
+    return (int64_t)cus * per_cu;
+}
+
 template <class MF, int MODE>
 static int launch(const MfArgs &a, int tiles_max, int splits, hipStream_t s) {
     using S = GmShape<MF, MODE>;
     if (a.k % MF::SBK) return set_error(CW_ENOTSUP, "mfma: k %d is not a multiple of %d", a.k, MF::SBK);
+    if ((int64_t)a.n * a.row_bytes >= ((int64_t)1 << 32))
+        return set_error(CW_ENOTSUP, "mfma: a matrix of %d rows of %lld bytes is 4 GiB or more", a.n, (long long)a.row_bytes);
     const int n_nb = (a.n + S::RPB - 1) / S::RPB;
-    const int64_t blocks = (int64_t)((tiles_max + 7) / 8) * 8 * n_nb;
+    const int R = tiles_max >= 8 ? 8 : tiles_max >= 4 ? 4 : tiles_max >= 2 ? 2 : 1;
+    const int64_t items = (int64_t)((tiles_max + R - 1) / R) * R * n_nb;
+    if (items >= ((int64_t)1 << 31)) return set_error(CW_ENOTSUP, "mfma: %lld work items", (long long)items);
+    const int64_t res = resident_blocks(S::PER_CU);
+    const int64_t blocks = items < res ? (items + 7) / 8 * 8 : res;
     static bool lds_set = false;  // dynamic LDS above 64 KB is opted into once per kernel
     if (!lds_set) {
         if (hipFuncSetAttribute((const void *)k_gmm<MF, MODE>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::lds_bytes()) != hipSuccess)
             return set_error(CW_EHIP, "mfma: cannot reserve %zu bytes of LDS", S::lds_bytes());
         lds_set = true;
     }
-    hipLaunchKernelGGL((k_gmm<MF, MODE>), dim3((unsigned)blocks, (unsigned)splits), dim3(256), S::lds_bytes(), s, a);
+    MfArgs b = a;
+    b.run_tiles = R;
+    b.n_items = (int)items;
+    hipLaunchKernelGGL((k_gmm<MF, MODE>), dim3((unsigned)blocks, (unsigned)splits), dim3(S::NT), S::lds_bytes(), s, b);
     return check_launch("k_gmm");
 }
 
@@ -827,17 +1121,29 @@ __global__ void k_sum_splits(const float *part, int S, int64_t n, float *y) {
 }
 
 // the dense GEMM's N-block rows and stage size for a format (GmShape<MF, 2>)
-static void dense_shape(int dtype, int &rpb, int &kst) {
-    rpb = dtype == CW_Q4_K ? 64 : 128;
-    kst = dtype == CW_Q8_0 ? 4 : 8;
+template <class MF>
+static void shape_of(int &rpb, int &kst, int &per_cu) {
+    rpb = GmShape<MF, 2>::RPB;
+    kst = MF::KST;
+    per_cu = GmShape<MF, 2>::PER_CU;
 }
-// K splits: enough blocks to cover the chip twice, at least one stage each
+static void dense_shape(int dtype, int &rpb, int &kst, int &per_cu) {
+    switch (dtype) {
+    case CW_IQ2_XXS: return shape_of<MIQ2_XXS>(rpb, kst, per_cu);
+    case CW_IQ2_S: return shape_of<MIQ2_S>(rpb, kst, per_cu);
+    case CW_IQ3_S: return shape_of<MIQ3_S>(rpb, kst, per_cu);
+    case CW_MXFP4: return shape_of<MMXFP4>(rpb, kst, per_cu);
+    case CW_Q8_0: return shape_of<MQ8_0>(rpb, kst, per_cu);
+    default: return shape_of<MQ4_K>(rpb, kst, per_cu);
+    }
+}
+// K splits: enough work items for every resident block, at least one stage each
 static int dense_splits(int dtype, int64_t m, int64_t n, int64_t k, int &split_st) {
-    int rpb, kst;
-    dense_shape(dtype, rpb, kst);
+    int rpb, kst, per_cu;
+    dense_shape(dtype, rpb, kst, per_cu);
     const int64_t blocks = (m + MF_MT - 1) / MF_MT * ((n + rpb - 1) / rpb);
     const int n_st = (int)((k / 32 + kst - 1) / kst);
-    int S = (int)((512 + blocks - 1) / blocks);
+    int S = (int)((resident_blocks(per_cu) + blocks - 1) / blocks);
     if (S > n_st) S = n_st;
     if (S < 1) S = 1;
     split_st = (n_st + S - 1) / S;
