@@ -892,65 +892,107 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
 
 // ------------------------------------------------------------------------------ helpers
 
+// sum of the first n entries of a small LDS array
+__device__ __forceinline__ int wc_total(const int *w, int n) {
+    int t = 0;
+    for (int i = 0; i < n; i++) t += w[i];
+    return t;
+}
+
+// Inclusive prefix sum across the wave (six shuffle steps)
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int u = __shfl_up(v, d);
+        if (lane >= d) v += u;
+    }
+    return v;
+}
+
 // One block: histogram of slots, exclusive scans, scatter of picks into per-slot piles, tiles.
-// Each thread reads its (up to) PILE_PER slots of a chunk into registers before using any, so
-// the loads overlap; the order of picks inside a pile does not matter (every pick's outputs are
-// computed independently of the other rows of its tile).
-constexpr int PILE_PER = 16;
+// Each thread reads its (up to) PILE_PER slots into registers before using any, so the loads
+// overlap, and keeps them for the scatter; the order of picks inside a pile does not matter
+// (every pick's outputs are computed independently of the other rows of its tile). Up to
+// PILE_LDS picks, the scatter goes to LDS and the piles leave in coalesced stores (random 4-byte
+// stores from one CU cost a memory transaction each).
+constexpr int PILE_PER = 16, PILE_LDS = 12288;
 __global__ __launch_bounds__(1024) void k_piles(const uint32_t *slots, int TK, int K, int n_slots, int *pile_pick,
                                                  int *pile_tok, MfTile *tiles, int *n_tiles) {
-    __shared__ int cnt[1024], off[1024], toff[1024], cur[1024];
-    const int tid = threadIdx.x;
+    __shared__ int cnt[1024], off[1024], cur[1024], wtot[16], wttot[16];
+    __shared__ int staged[PILE_LDS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     cnt[tid] = 0;
     cur[tid] = 0;
+    const bool one = TK <= 1024 * PILE_PER;  // the common case: every slot read once, kept in registers
+    uint32_t v[PILE_PER];
+#pragma unroll
+    for (int q = 0; q < PILE_PER; q++) {
+        const int i = q * 1024 + tid;
+        v[q] = i < TK ? slots[i] : 0xFFFFFFFFu;
+    }
     __syncthreads();
     for (int c0 = 0; c0 < TK; c0 += 1024 * PILE_PER) {
-        uint32_t v[PILE_PER];
+        if (c0) {
 #pragma unroll
-        for (int q = 0; q < PILE_PER; q++) {
-            const int i = c0 + q * 1024 + tid;
-            v[q] = i < TK ? slots[i] : 0xFFFFFFFFu;
+            for (int q = 0; q < PILE_PER; q++) {
+                const int i = c0 + q * 1024 + tid;
+                v[q] = i < TK ? slots[i] : 0xFFFFFFFFu;
+            }
         }
 #pragma unroll
         for (int q = 0; q < PILE_PER; q++)
             if (v[q] < (uint32_t)n_slots) atomicAdd(&cnt[v[q]], 1);
     }
     __syncthreads();
-    // inclusive scans of counts and tile counts (Hillis-Steele over 1024 entries)
+    // exclusive scans of the counts and of the tile counts: per wave, then over the 16 wave totals
     const int c = tid < n_slots ? cnt[tid] : 0;
     const int tc = (c + MF_MT - 1) / MF_MT;
-    off[tid] = c;
-    toff[tid] = tc;
-    __syncthreads();
-    for (int d = 1; d < 1024; d <<= 1) {
-        const int x = tid >= d ? off[tid - d] : 0, y = tid >= d ? toff[tid - d] : 0;
-        __syncthreads();
-        off[tid] += x;
-        toff[tid] += y;
-        __syncthreads();
+    const int ic = wave_incl_scan(c, lane), itc = wave_incl_scan(tc, lane);
+    if (lane == 63) {
+        wtot[wave] = ic;
+        wttot[wave] = itc;
     }
-    const int my_off = off[tid] - c, my_toff = toff[tid] - tc;
-    if (tid == 1023) *n_tiles = toff[1023];
     __syncthreads();
+    int wc = 0, wtc = 0;
+    for (int w = 0; w < wave; w++) {
+        wc += wtot[w];
+        wtc += wttot[w];
+    }
+    const int my_off = wc + ic - c, my_toff = wtc + itc - tc;
+    if (tid == 1023) *n_tiles = my_toff + tc;
     off[tid] = my_off;
-    __syncthreads();
     if (tid < n_slots)
         for (int q = 0; q < tc; q++) tiles[my_toff + q] = MfTile{tid, my_off + q * MF_MT, min(MF_MT, c - q * MF_MT), 0};
+    __syncthreads();
     for (int c0 = 0; c0 < TK; c0 += 1024 * PILE_PER) {
-        uint32_t v[PILE_PER];
+        if (!one) {
 #pragma unroll
-        for (int q = 0; q < PILE_PER; q++) {
-            const int i = c0 + q * 1024 + tid;
-            v[q] = i < TK ? slots[i] : 0xFFFFFFFFu;
+            for (int q = 0; q < PILE_PER; q++) {
+                const int i = c0 + q * 1024 + tid;
+                v[q] = i < TK ? slots[i] : 0xFFFFFFFFu;
+            }
         }
 #pragma unroll
         for (int q = 0; q < PILE_PER; q++) {
             const int i = c0 + q * 1024 + tid;
             if (v[q] < (uint32_t)n_slots) {
                 const int pos = off[v[q]] + atomicAdd(&cur[v[q]], 1);
-                pile_pick[pos] = i;
-                pile_tok[pos] = i / K;
+                if (TK <= PILE_LDS) {
+                    staged[pos] = i;
+                } else {
+                    pile_pick[pos] = i;
+                    pile_tok[pos] = i / K;
+                }
             }
+        }
+    }
+    if (TK <= PILE_LDS) {
+        __syncthreads();
+        const int n = wtot[15] + wc_total(wtot, 15);  // picks that resolved to a slot
+        for (int p = tid; p < n; p += 1024) {
+            const int i = staged[p];
+            pile_pick[p] = i;
+            pile_tok[p] = i / K;
         }
     }
 }
