@@ -73,15 +73,17 @@ int cw_dequantize(int dtype, const void *blocks, int64_t n_elems, float *out, cw
     return dequantize(dtype, blocks, n_elems, out, (hipStream_t)stream);
 }
 
-// Rows of x from which cw_qmatmul runs as an MFMA GEMM instead of one matvec per row
-// (CWMOE_MM_MIN_ROWS overrides; the reference switches to its simdgroup-matrix kernel above 8
-// rows, vendor/candle-core/src/quantized/metal.rs:339-353).
-static int64_t mm_min_rows() {
+// Rows of x from which cw_qmatmul runs as an MFMA GEMM instead of one matvec per row, where the
+// two cross over on MI355X (graph-replayed, 2048x2048 Q8_0 and 4096x4096 Q4_K): a Q4_K matvec
+// row costs ~11 us, the GEMM ~20 us at any small M; a Q8_0 row ~4.4 us against ~14 us.
+// CWMOE_MM_MIN_ROWS overrides. (The reference switches to its simdgroup-matrix kernel above 8
+// rows, vendor/candle-core/src/quantized/metal.rs:339-353.)
+static int64_t mm_min_rows(int dtype) {
     const char *e = getenv("CWMOE_MM_MIN_ROWS");
-    return e ? atoll(e) : 32;
+    return e ? atoll(e) : dtype == CW_Q4_K ? 2 : 8;
 }
 static bool qmatmul_mfma(int dtype, int64_t k, int64_t m) {
-    return m >= mm_min_rows() && cw::mfma_supported(dtype) && k % cw_block_size(dtype) == 0 && k % 32 == 0 &&
+    return m >= mm_min_rows(dtype) && cw::mfma_supported(dtype) && k % cw_block_size(dtype) == 0 && k % 32 == 0 &&
            (dtype == CW_Q8_0 || dtype == CW_MXFP4 || k % 256 == 0);
 }
 

@@ -85,9 +85,9 @@ int cw_dequantize(int dtype, const void *blocks, int64_t n_elems, float *out, cw
  * (vendor/candle-core/src/quantized/mod.rs:1206-1345 with the Metal dispatch of
  * quantized/metal.rs:359-470, call_quantized_matmul_mv_t / _mm_t in
  * vendor/candle-metal-kernels/src/kernels/quantized.rs:32-43, 198-213).
- * From 32 rows of x (all formats) the product runs as an MFMA GEMM on fp16-rounded activations
- * (rel-L2 about 3e-4 against f64) and needs the workspace; below that it is one f32 matvec per
- * row. ws may be NULL when cw_qmatmul_workspace_size returns 0. */
+ * From 2 rows of x (Q4_K) or 8 rows (the other formats) the product runs as an MFMA GEMM on
+ * fp16-rounded activations (rel-L2 about 3e-4 against f64) and needs the workspace; below that
+ * it is one f32 matvec per row. ws may be NULL when cw_qmatmul_workspace_size returns 0. */
 size_t cw_qmatmul_workspace_size(int dtype, int64_t n, int64_t k, int64_t m);
 int cw_qmatmul(int dtype, const void *w, int64_t n, int64_t k, const float *x, int64_t m,
                float *y, void *ws, size_t ws_bytes, cw_stream_t stream);
