@@ -5,6 +5,7 @@
 #include "cw_common.h"
 #include "cw_gemv.h"
 #include "cw_mfma.h"
+#include "cw_router.h"
 #include "cw_moe_fused.h"
 #include "cw_wave.h"
 
@@ -347,6 +348,15 @@ int cw_route_topk(const float *logits, int T, int E, int K, int norm, uint32_t *
     CW_REQUIRE(K > 0 && K <= 32 && K <= E, "route: top-%d of %d experts", K, E);
     CW_REQUIRE(T == 0 || (logits && ids && w), "route: null pointer");
     return route(logits, T, E, K, norm, ids, w, (hipStream_t)stream);
+}
+
+int cw_router_logits(int wdtype, const void *w, int n_experts, int hidden, const float *bias, const float *x, int T,
+                     float *logits, cw_stream_t stream) {
+    CW_REQUIRE(T >= 0 && n_experts >= 0 && hidden > 0, "router: T %d, %d experts, hidden %d", T, n_experts, hidden);
+    CW_REQUIRE(T == 0 || n_experts == 0 || (w && x && logits), "router: null pointer");
+    CW_REQUIRE(((uintptr_t)x & 15u) == 0 && ((uintptr_t)w & 7u) == 0, "router: x must be 16-byte and w 8-byte aligned");
+    CW_REQUIRE(wdtype != CW_F32 || ((uintptr_t)w & 15u) == 0, "router: f32 weights must be 16-byte aligned");
+    return router_logits(wdtype, w, n_experts, hidden, bias, x, T, logits, (hipStream_t)stream);
 }
 
 int cw_swiglu(const float *g, const float *u, float *h, int64_t n, cw_stream_t stream) {

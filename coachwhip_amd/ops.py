@@ -104,6 +104,26 @@ class QMatMul:
     __call__ = forward
 
 
+def router_logits(w: torch.Tensor, x: torch.Tensor, bias: torch.Tensor = None) -> torch.Tensor:
+    """x (T, h) f32 times the router weight w (E, h), f32 or f16, plus bias (E,): (T, E) f32 logits.
+
+    The gate Linear of crates/engine/src/experts.rs:2428, 2577 (bias: model_gptoss.rs:168-175),
+    and its f16 decode variant cw_mv_f16 (fuse_kernel.rs:160-178)."""
+    _need(x, torch.float32, "x")
+    if not w.is_cuda or w.dtype not in (torch.float32, torch.float16) or not w.is_contiguous() or w.dim() != 2:
+        raise CwError(CW_EINVAL, "router weight must be a contiguous (E, h) f32 or f16 tensor")
+    e, h = w.shape
+    if x.shape[-1] != h:
+        raise CwError(CW_EINVAL, "x %s incompatible with a (%d, %d) router" % (tuple(x.shape), e, h))
+    if bias is not None:
+        _need(bias, torch.float32, "bias")
+    t = x.numel() // h
+    logits = torch.empty((t, e), dtype=torch.float32, device=x.device)
+    wdtype = 0 if w.dtype == torch.float32 else 1
+    check(lib().cw_router_logits(wdtype, _p(w), e, h, _p(bias), _p(x), t, _p(logits), _stream()))
+    return logits
+
+
 def route(logits: torch.Tensor, top_k: int, norm: bool):
     """(ids (T, K) u32 as int32 bits, weights (T, K) f32)."""
     _need(logits, torch.float32, "logits")

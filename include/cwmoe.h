@@ -102,6 +102,15 @@ int cw_qmatmul(int dtype, const void *w, int64_t n, int64_t k, const float *x, i
 int cw_route_topk(const float *logits, int T, int E, int K, int norm, uint32_t *ids, float *w,
                   cw_stream_t stream);
 
+/* logits[t][e] = x[t] . W[e] (+ bias[e], when bias is not NULL) for the router weight W
+ * (n_experts x hidden), f32 (CW_F32) or f16 (CW_F16) weights, f32 x and accumulation; x is
+ * T rows of hidden, 16-byte aligned, hidden a multiple of 4. Replaces the gate Linear
+ * (crates/engine/src/experts.rs:2428, 2577; gpt-oss adds the bias, model_gptoss.rs:168-175) and
+ * its f16 decode variant cw_mv_f16 (crates/engine/src/fuse_kernel.rs:160-178, 537-559). The
+ * logits then go to cw_route_topk or cw_moe_layer on the same stream. */
+int cw_router_logits(int wdtype, const void *w, int n_experts, int hidden, const float *bias,
+                     const float *x, int T, float *logits, cw_stream_t stream);
+
 /* ---- expert matvec ---------------------------------------------------------------------- */
 
 /* For each token t < T and pick j < K: out[t][j][0..n) = W[s] . x_row, with s = ids[t][j] a

@@ -205,6 +205,47 @@ def test_route_matches_the_oracle(E, K, norm):
     assert np.max(np.abs(host(w) - ww)) < 1e-5
 
 
+# ------------------------------------------------------------------------------ router logits
+
+@pytest.mark.parametrize("wdt", ["f32", "f16"])
+@pytest.mark.parametrize("E,h,T", [(256, 2048, 1), (128, 2880, 3), (512, 2048, 8), (256, 2048, 9), (130, 68, 70),
+                                   (256, 2048, 1500)])
+def test_router_logits_match_f64(wdt, E, h, T):
+    say("router logits", wdt, E, h, T)
+    rng = np.random.default_rng(E * 7 + T)
+    w = (rng.standard_normal((E, h)) * 0.05).astype(np.float32 if wdt == "f32" else np.float16)
+    x = rng.standard_normal((T, h)).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32) if T % 2 else None
+    got = host(ops.router_logits(dev(w), dev(x), None if bias is None else dev(bias)))
+    want = x.astype(np.float64) @ w.astype(np.float64).T + (0.0 if bias is None else bias.astype(np.float64))
+    # f32 accumulation of up to 2,880 products: rel-L2 near 1e-7
+    assert np.linalg.norm(got - want) <= 2e-6 * np.linalg.norm(want)
+
+
+@pytest.mark.parametrize("T", [2, 100])
+def test_router_logits_exact_on_small_integers(T):
+    # integers in [-8, 8]: every product and partial sum is an integer below 2^24, exact in f32
+    # whatever the summation order, so both kernels must return the exact dot products
+    rng = np.random.default_rng(T)
+    E, h = 96, 2048
+    w = rng.integers(-8, 9, (E, h)).astype(np.float16)
+    x = rng.integers(-8, 9, (T, h)).astype(np.float32)
+    bias = rng.integers(-4, 5, E).astype(np.float32)
+    got = host(ops.router_logits(dev(w), dev(x), dev(bias)))
+    want = (x.astype(np.int64) @ w.astype(np.int64).T + bias.astype(np.int64)).astype(np.float32)
+    assert np.array_equal(got, want)
+
+
+def test_router_logits_reject_bad_inputs():
+    x = torch.zeros((2, 64), device="cuda")
+    with pytest.raises(cw.CwError):
+        ops.router_logits(torch.zeros((8, 60), device="cuda"), x)                     # width mismatch
+    with pytest.raises(cw.CwError):
+        ops.router_logits(torch.zeros((8, 64), dtype=torch.bfloat16, device="cuda"), x)  # dtype
+    with pytest.raises(cw.CwError):
+        ops.router_logits(torch.zeros((8, 66), device="cuda"), torch.zeros((2, 66), device="cuda"))  # hidden % 4
+
+
 # ------------------------------------------------------------------------------ elementwise
 
 def test_activations_combine_and_resolve_match_the_oracle():
