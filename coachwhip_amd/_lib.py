@@ -37,6 +37,11 @@ class MoeDesc(ctypes.Structure):
                 ("slot_table", _P), ("n_slots", _I)]
 
 
+class SharedDesc(ctypes.Structure):
+    """struct cw_shared_desc (include/cwmoe.h)."""
+    _fields_ = [("hidden", _I), ("inter", _I), ("dtype", _I * 3), ("w", _P * 3), ("gate_inp", _P)]
+
+
 # every symbol include/cwmoe.h declares, with its signature
 SIGNATURES = {
     "cw_version": ([], ctypes.c_char_p),
@@ -55,6 +60,8 @@ SIGNATURES = {
     "cw_slots_resolve": ([_P, _P, _I, _P, _P, _P], _I),
     "cw_moe_workspace_size": ([ctypes.POINTER(MoeDesc), _I], ctypes.c_size_t),
     "cw_moe_layer": ([ctypes.POINTER(MoeDesc), _P, _P, _I, _P, _P, _P, _P, _P, ctypes.c_size_t, _P], _I),
+    "cw_shared_expert_workspace_size": ([ctypes.POINTER(SharedDesc), _I], ctypes.c_size_t),
+    "cw_shared_expert": ([ctypes.POINTER(SharedDesc), _P, _I, _P, _I, _P, ctypes.c_size_t, _P], _I),
     "cw_device_errors": ([], ctypes.c_uint32),
     "cw_slots_new": ([_I], _P),
     "cw_slots_free": ([_P], None),

@@ -1,6 +1,7 @@
 // Router top-k, activations, weighted combine, slot resolve and the MoE layer (gfx950).
 #include <math.h>
 #include <stdlib.h>
+#include <algorithm>
 
 #include "cw_common.h"
 #include "cw_gemv.h"
@@ -336,11 +337,71 @@ static int moe_layer(const cw_moe_desc *d, const float *x, const float *logits, 
     return moe_down(d->dtype[2], a, T, s);
 }
 
+// out[t][i] = (accumulate ? out[t][i] : 0) + y[t][i] * sigmoid(glog[t]) (glog NULL: factor 1)
+__global__ void k_gate_scale_add(const float *y, const float *glog, int T, int H, int accumulate, float *out) {
+    const int64_t n = (int64_t)T * H;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const float g = glog ? 1.0f / (1.0f + expf(-glog[i / H])) : 1.0f;
+        out[i] = (accumulate ? out[i] : 0.0f) + y[i] * g;
+    }
+}
+
+static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// workspace of the shared expert: gate and up rows (the hidden rows overwrite gate), down rows,
+// gate logits, and one region the three matmuls take in turn
+struct SharedLayout {
+    size_t g, u, y, glog, mm, total;
+};
+static SharedLayout shared_layout(const cw_shared_desc *d, int T) {
+    SharedLayout L;
+    const size_t ti = (size_t)T * d->inter * 4, th = (size_t)T * d->hidden * 4;
+    size_t mm = cw_qmatmul_workspace_size(d->dtype[0], d->inter, d->hidden, T);
+    mm = std::max(mm, cw_qmatmul_workspace_size(d->dtype[1], d->inter, d->hidden, T));
+    mm = std::max(mm, cw_qmatmul_workspace_size(d->dtype[2], d->hidden, d->inter, T));
+    L.g = 0;
+    L.u = L.g + al256(ti);
+    L.y = L.u + al256(ti);
+    L.glog = L.y + al256(th);
+    L.mm = L.glog + al256((size_t)T * 4);
+    L.total = L.mm + al256(mm);
+    return L;
+}
+
 }  // namespace cw
 
 using namespace cw;
 
 extern "C" {
+
+size_t cw_shared_expert_workspace_size(const cw_shared_desc *d, int T) {
+    if (!d || T <= 0 || d->hidden <= 0 || d->inter <= 0) return 0;
+    return shared_layout(d, T).total;
+}
+
+int cw_shared_expert(const cw_shared_desc *d, const float *x, int T, float *out, int accumulate, void *ws,
+                     size_t ws_bytes, cw_stream_t stream) {
+    CW_REQUIRE(d && d->hidden > 0 && d->inter > 0 && T >= 0, "shared expert: bad descriptor or T %d", T);
+    if (T == 0) return CW_OK;
+    CW_REQUIRE(x && out && d->w[0] && d->w[1] && d->w[2], "shared expert: null pointer");
+    const SharedLayout L = shared_layout(d, T);
+    CW_REQUIRE(ws && ws_bytes >= L.total, "shared expert: workspace of %zu bytes, %zu needed", ws_bytes, L.total);
+    hipStream_t s = (hipStream_t)stream;
+    uint8_t *base = (uint8_t *)ws;
+    float *g = (float *)(base + L.g), *u = (float *)(base + L.u), *y = (float *)(base + L.y);
+    float *glog = d->gate_inp ? (float *)(base + L.glog) : nullptr;
+    void *mm = base + L.mm;
+    const size_t mm_bytes = L.total - L.mm;
+    int rc;
+    if ((rc = cw_qmatmul(d->dtype[0], d->w[0], d->inter, d->hidden, x, T, g, mm, mm_bytes, stream))) return rc;
+    if ((rc = cw_qmatmul(d->dtype[1], d->w[1], d->inter, d->hidden, x, T, u, mm, mm_bytes, stream))) return rc;
+    if ((rc = cw_swiglu(g, u, g, (int64_t)T * d->inter, stream))) return rc;
+    if ((rc = cw_qmatmul(d->dtype[2], d->w[2], d->hidden, d->inter, g, T, y, mm, mm_bytes, stream))) return rc;
+    if (glog && (rc = router_logits(CW_F32, d->gate_inp, 1, d->hidden, nullptr, x, T, glog, s))) return rc;
+    hipLaunchKernelGGL(k_gate_scale_add, flat_grid((int64_t)T * d->hidden), dim3(256), 0, s, y, glog, T, d->hidden, accumulate,
+                       out);
+    return check_launch("k_gate_scale_add");
+}
 
 int cw_route_topk(const float *logits, int T, int E, int K, int norm, uint32_t *ids, float *w, cw_stream_t stream) {
     CW_REQUIRE(T >= 0, "route: negative token count %d", T);

@@ -22,7 +22,7 @@ import numpy as np
 import torch
 
 from . import formats as F
-from ._lib import CwError, MoeDesc, check, lib, CW_EINVAL
+from ._lib import CwError, MoeDesc, SharedDesc, check, lib, CW_EINVAL
 
 
 def _stream():
@@ -167,6 +167,52 @@ def slots_resolve(ids, table):
     missing = torch.zeros(1, dtype=torch.int32, device=ids.device)
     check(lib().cw_slots_resolve(_p(ids), _p(table), ids.numel(), _p(slots), _p(missing), _stream()))
     return slots, missing
+
+
+class SharedExpert:
+    """The expert every token uses, scaled by its own sigmoid gate (SharedExpert,
+    crates/engine/src/model_next.rs:723-742): sigmoid(x . gate_inp) * down(silu(gate x) * up x).
+
+    gate, up, down are QTensors ((inter, h), (inter, h), (h, inter)); gate_inp an (h,) f32 device
+    tensor or None."""
+
+    def __init__(self, gate: "QTensor", up: "QTensor", down: "QTensor", gate_inp: Optional[torch.Tensor] = None):
+        inter, h = gate.shape
+        if up.shape != (inter, h) or down.shape != (h, inter):
+            raise CwError(CW_EINVAL, "shared expert: gate %s, up %s, down %s" % (gate.shape, up.shape, down.shape))
+        if gate_inp is not None:
+            _need(gate_inp, torch.float32, "gate_inp")
+            if gate_inp.numel() != h:
+                raise CwError(CW_EINVAL, "shared expert: gate_inp of %d, hidden %d" % (gate_inp.numel(), h))
+        self.gate, self.up, self.down, self.gate_inp = gate, up, down, gate_inp
+        d = SharedDesc()
+        d.hidden, d.inter = h, inter
+        for i, q in enumerate((gate, up, down)):
+            d.dtype[i] = q.dtype
+            d.w[i] = q.data.data_ptr()
+        d.gate_inp = None if gate_inp is None else gate_inp.data_ptr()
+        self.desc = d
+
+    def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """The shared expert's output for each row of x; added into ``out`` when it is given."""
+        _need(x, torch.float32, "x")
+        h = self.desc.hidden
+        if x.shape[-1] != h:
+            raise CwError(CW_EINVAL, "x %s incompatible with hidden %d" % (tuple(x.shape), h))
+        t = x.numel() // h
+        acc = out is not None
+        if acc:
+            _need(out, torch.float32, "out")
+            if out.numel() != t * h:
+                raise CwError(CW_EINVAL, "out %s for %d rows of %d" % (tuple(out.shape), t, h))
+        else:
+            out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+        ws_bytes = lib().cw_shared_expert_workspace_size(ctypes.byref(self.desc), t)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+        check(lib().cw_shared_expert(ctypes.byref(self.desc), _p(x), t, _p(out), int(acc), _p(ws), ws_bytes, _stream()))
+        return out
+
+    __call__ = forward
 
 
 @dataclass

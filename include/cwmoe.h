@@ -183,6 +183,26 @@ int cw_moe_layer(const cw_moe_desc *desc, const float *x, const float *logits, i
                  uint32_t *ids_out, float *w_out, uint32_t *missing, void *ws, size_t ws_bytes,
                  cw_stream_t stream);
 
+/* The shared expert of a Qwen3.5/3.6 MoE block: every token uses it, scaled by its own sigmoid
+ * gate. Dense quantized matrices as GGUF stores ffn_{gate,up,down}_shexp: gate and up are
+ * inter x hidden, down is hidden x inter. */
+typedef struct cw_shared_desc {
+    int hidden;              /* h */
+    int inter;               /* shared FFN width */
+    int dtype[3];            /* gate, up, down */
+    const void *w[3];        /* device matrices (raw GGUF blocks) */
+    const float *gate_inp;   /* ffn_gate_inp_shexp: h floats on the device (16-byte aligned, h a
+                                multiple of 4), or NULL (factor 1) */
+} cw_shared_desc;
+
+/* out[t] = sigmoid(x[t] . gate_inp) * down(silu(gate x[t]) * (up x[t])), added to out when
+ * accumulate != 0 (the block sums routed and shared outputs). Replaces SharedExpert::forward
+ * (crates/engine/src/model_next.rs:723-742; the sum at 1430-1437). x is T rows of hidden,
+ * 16-byte aligned; ws from cw_shared_expert_workspace_size. */
+size_t cw_shared_expert_workspace_size(const cw_shared_desc *desc, int T);
+int cw_shared_expert(const cw_shared_desc *desc, const float *x, int T, float *out, int accumulate,
+                     void *ws, size_t ws_bytes, cw_stream_t stream);
+
 /* Device-side failures since the library loaded: a one-token layer runs as one persistent
  * launch whose blocks meet at a device-wide barrier; a barrier wait that times out (a block
  * could not be scheduled) makes the call's outputs NaN and is counted here. No counterpart in

@@ -246,6 +246,40 @@ def test_router_logits_reject_bad_inputs():
         ops.router_logits(torch.zeros((8, 66), device="cuda"), torch.zeros((2, 66), device="cuda"))  # hidden % 4
 
 
+# ------------------------------------------------------------------------------ shared expert
+
+@pytest.mark.parametrize("fmt,T,gated,acc", [((F.Q4_K, F.Q4_K, F.Q8_0), 1, True, False),
+                                             ((F.IQ3_S, F.IQ3_S, F.Q4_K), 3, True, True),
+                                             ((F.Q8_0, F.Q8_0, F.MXFP4), 40, False, True),
+                                             ((F.IQ2_XXS, F.IQ2_XXS, F.IQ2_S), 24, True, False)])
+def test_shared_expert_matches_the_oracle(fmt, T, gated, acc):
+    # out = sigmoid(x . gate_inp) * down(silu(gate x) * up x) (+ out), model_next.rs:733-741
+    say("shared expert", [F.NAMES[f] for f in fmt], T, gated, acc)
+    rng = np.random.default_rng(T * 31 + fmt[0])
+    h, inter = 2048, 512
+    shapes = ((inter, h), (inter, h), (h, inter))
+    raw = [synth.random_blocks(f, n * k, rng) for f, (n, k) in zip(fmt, shapes)]
+    qs = [ops.QTensor.from_blocks(r, f, shp) for r, f, shp in zip(raw, fmt, shapes)]
+    gi = (rng.standard_normal(h) * 0.02).astype(np.float32) if gated else None
+    x = rng.standard_normal((T, h)).astype(np.float32)
+    base = rng.standard_normal((T, h)).astype(np.float32)
+    se = ops.SharedExpert(*qs, None if gi is None else dev(gi))
+    out = dev(base) if acc else None
+    got = host(se.forward(dev(x), out))
+    W = [O.dequantize(f, r, n * k).reshape(n, k).astype(np.float64) for f, r, (n, k) in zip(fmt, raw, shapes)]
+    x64 = x.astype(np.float64)
+    g, u = x64 @ W[0].T, x64 @ W[1].T
+    y = (g / (1.0 + np.exp(-g)) * u) @ W[2].T
+    if gated:
+        y *= (1.0 / (1.0 + np.exp(-(x64 @ gi.astype(np.float64)))))[:, None]
+    if acc:
+        y += base
+    # the dense matmuls run on fp16 activations from 2 rows (Q4_K) or 8 rows: the 1e-3 gate;
+    # one f32 token must also meet the f32 bar
+    tol = REL_L2_F32 if T == 1 else REL_L2_GATE
+    assert np.linalg.norm(got - y) <= tol * np.linalg.norm(y)
+
+
 # ------------------------------------------------------------------------------ elementwise
 
 def test_activations_combine_and_resolve_match_the_oracle():
