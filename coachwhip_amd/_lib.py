@@ -62,6 +62,19 @@ SIGNATURES = {
     "cw_moe_layer": ([ctypes.POINTER(MoeDesc), _P, _P, _I, _P, _P, _P, _P, _P, ctypes.c_size_t, _P], _I),
     "cw_shared_expert_workspace_size": ([ctypes.POINTER(SharedDesc), _I], ctypes.c_size_t),
     "cw_shared_expert": ([ctypes.POINTER(SharedDesc), _P, _I, _P, _I, _P, ctypes.c_size_t, _P], _I),
+    "cw_gguf_open": ([ctypes.c_char_p], _P),
+    "cw_gguf_close": ([_P], None),
+    "cw_gguf_version": ([_P], _I),
+    "cw_gguf_n_tensors": ([_P], _L),
+    "cw_gguf_find": ([_P, ctypes.c_char_p], _L),
+    "cw_gguf_tensor": ([_P, _L, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_I), ctypes.POINTER(_I),
+                        ctypes.POINTER(_L), ctypes.POINTER(_L), ctypes.POINTER(_L)], _I),
+    "cw_gguf_data": ([_P, _L], _P),
+    "cw_gguf_meta_int": ([_P, ctypes.c_char_p, ctypes.POINTER(_L)], _I),
+    "cw_gguf_meta_float": ([_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)], _I),
+    "cw_gguf_meta_str": ([_P, ctypes.c_char_p], ctypes.c_char_p),
+    "cw_gguf_experts": ([_P, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_L), ctypes.POINTER(_L), ctypes.POINTER(_L),
+                         ctypes.POINTER(_L), ctypes.POINTER(_P)], _I),
     "cw_device_errors": ([], ctypes.c_uint32),
     "cw_slots_new": ([_I], _P),
     "cw_slots_free": ([_P], None),

@@ -203,6 +203,38 @@ size_t cw_shared_expert_workspace_size(const cw_shared_desc *desc, int T);
 int cw_shared_expert(const cw_shared_desc *desc, const float *x, int T, float *out, int accumulate,
                      void *ws, size_t ws_bytes, cw_stream_t stream);
 
+/* ---- GGUF files (host) -------------------------------------------------------------------- */
+
+/* A GGUF file (versions 1-3): header, metadata and tensor directory read by cw_gguf_open, the
+ * tensor data mapped read-only until cw_gguf_close. Follows candle's Content::read
+ * (vendor/candle-core/src/quantized/gguf_file.rs:469-567: caps on lengths and nesting, tensor
+ * data at the next multiple of general.alignment, default 32) and accepts IQ3_S (21) and IQ2_S
+ * (22), which the reference rejects (quantized/mod.rs:314-339). NULL on error (cw_last_error). */
+typedef struct cw_gguf cw_gguf;
+cw_gguf *cw_gguf_open(const char *path);
+void cw_gguf_close(cw_gguf *g);
+int cw_gguf_version(const cw_gguf *g);
+int64_t cw_gguf_n_tensors(const cw_gguf *g);
+/* index of the tensor called name, or -1 */
+int64_t cw_gguf_find(const cw_gguf *g, const char *name);
+/* tensor i: name, GGUF type id, dims outermost first (as candle reports them; unused entries 0),
+ * offset of its bytes from the start of the file, and their count. Pointers may be NULL. */
+int cw_gguf_tensor(const cw_gguf *g, int64_t i, const char **name, int *dtype, int *n_dims,
+                   int64_t dims[4], int64_t *file_offset, int64_t *bytes);
+/* tensor i's bytes in the mapping (host memory), or NULL */
+const void *cw_gguf_data(const cw_gguf *g, int64_t i);
+/* metadata: an integer (any integer type or bool), a float (f32/f64), a string (NULL when
+ * absent or of another type; owned by g) */
+int cw_gguf_meta_int(const cw_gguf *g, const char *key, int64_t *v);
+int cw_gguf_meta_float(const cw_gguf *g, const char *key, double *v);
+const char *cw_gguf_meta_str(const cw_gguf *g, const char *key);
+/* The experts of one layer: blk.{layer}.ffn_{gate,up,down}_exps.weight (which = 0, 1, 2) as
+ * n_experts matrices of n rows by k, expert e at data + e * expert_bytes, the layout
+ * cw_moe_desc takes as a bank once copied to the device (ExpertStore::new,
+ * crates/engine/src/experts.rs:697-718). */
+int cw_gguf_experts(const cw_gguf *g, int layer, int which, int *dtype, int64_t *n_experts,
+                    int64_t *n, int64_t *k, int64_t *expert_bytes, const void **data);
+
 /* Device-side failures since the library loaded: a one-token layer runs as one persistent
  * launch whose blocks meet at a device-wide barrier; a barrier wait that times out (a block
  * could not be scheduled) makes the call's outputs NaN and is counted here. No counterpart in
