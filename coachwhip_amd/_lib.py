@@ -9,7 +9,7 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libcwmoe.so")
 
-CW_OK, CW_ENOTSUP, CW_EINVAL, CW_EHIP = 0, 1, 2, 3
+CW_OK, CW_ENOTSUP, CW_EINVAL, CW_EHIP, CW_EFULL = 0, 1, 2, 3, 4
 NO_SLOT = 0xFFFFFFFF
 
 
@@ -40,6 +40,18 @@ class MoeDesc(ctypes.Structure):
 class SharedDesc(ctypes.Structure):
     """struct cw_shared_desc (include/cwmoe.h)."""
     _fields_ = [("hidden", _I), ("inter", _I), ("dtype", _I * 3), ("w", _P * 3), ("gate_inp", _P)]
+
+
+class BankSource(ctypes.Structure):
+    """struct cw_bank_source (include/cwmoe.h)."""
+    _fields_ = [("n_experts", _I), ("dtype", _I * 3), ("rows", _L * 3), ("cols", _L * 3), ("expert_bytes", _L * 3),
+                ("host", _P * 3)]
+
+
+class BankStats(ctypes.Structure):
+    """struct cw_bank_stats (include/cwmoe.h)."""
+    _fields_ = [(name, ctypes.c_uint64) for name in
+                ("hits", "prefetch_hits", "loads", "bytes_loaded", "prefetch_copies", "crowded")]
 
 
 # every symbol include/cwmoe.h declares, with its signature
@@ -88,6 +100,15 @@ SIGNATURES = {
     "cw_slots_lru": ([_P, _P], None),
     "cw_slots_is_prefetched": ([_P, ctypes.c_uint32], _I),
     "cw_slots_table": ([_P, _P, _I], None),
+    "cw_bank_device_bytes": ([ctypes.POINTER(BankSource), _I], ctypes.c_size_t),
+    "cw_bank_new": ([ctypes.POINTER(BankSource), _I, _P, ctypes.c_size_t], _P),
+    "cw_bank_free": ([_P], None),
+    "cw_bank_ensure": ([_P, _P, _I, _P, ctypes.POINTER(_I)], _I),
+    "cw_bank_prefetch": ([_P, _P, _I], _I),
+    "cw_bank_fill_desc": ([_P, ctypes.POINTER(MoeDesc)], _I),
+    "cw_bank_table": ([_P], _P),
+    "cw_bank_slot_of": ([_P, ctypes.c_uint32], _I),
+    "cw_bank_get_stats": ([_P, ctypes.POINTER(BankStats)], None),
 }
 
 _lib = None

@@ -1,0 +1,306 @@
+// Expert banks on the device, managed from the host: one layer's n_slots slots of each expert
+// matrix, the device expert -> slot table, the LRU bookkeeping (cw_slots) and the host memory
+// the experts are copied from.
+//
+// The reference keeps a layer's bank in Metal shared memory and reads misses from the SSD
+// straight into it (ExpertStore::ensure, crates/engine/src/experts.rs:1489-1641; make_bank
+// 1320-1378), with the GPU's copy of the table written through shared-memory atomics
+// (gpu_sync.rs:70-148, sync_table experts.rs:73-81). On a discrete GPU the slots are HBM and the
+// expert store is host memory, so here:
+//  - a miss is an H2D copy on the caller's stream, ordered before the layer's kernels;
+//  - a prefetch (experts.rs:1004-1098) copies on the bank's own stream, after the work that was
+//    on the last ensure's stream when that ensure returned (so it overwrites no slot a queued
+//    kernel still reads), and records an event per slot; ensure waits for that event on its
+//    stream (a GPU-side wait, where the reference spins on the host), and a slot still being
+//    filled is neither a victim nor listed in the device table;
+//  - the device table is patched in stream order by a small kernel whose (expert, slot) pairs
+//    travel as kernel arguments, so no host buffer has to outlive the call and nothing here is
+//    a memset (the form that stays correct when the caller captures the stream in a graph).
+#include <algorithm>
+#include <new>
+#include <unordered_set>
+#include <vector>
+
+#include "cw_common.h"
+
+namespace cw {
+namespace {
+
+constexpr int PATCH = 62;  // table entries per patch launch (500-byte argument block)
+
+struct TablePatch {
+    uint32_t n;
+    uint32_t expert[PATCH];
+    uint32_t slot[PATCH];
+};
+
+__global__ __launch_bounds__(64) void k_table_patch(uint32_t *table, TablePatch p) {
+    const uint32_t i = threadIdx.x;
+    if (i < p.n) table[p.expert[i]] = p.slot[i];
+}
+
+__global__ __launch_bounds__(256) void k_table_clear(uint32_t *table, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) table[i] = CW_NO_SLOT;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+int check_source(const cw_bank_source *src, int n_slots) {
+    CW_REQUIRE(src, "bank: no source");
+    CW_REQUIRE(n_slots > 0 && src->n_experts > 0, "bank: %d slots for %d experts", n_slots, src->n_experts);
+    for (int m = 0; m < 3; m++) {
+        const int dt = src->dtype[m];
+        CW_REQUIRE(is_weight_type(dt), "bank: matrix %d has type %d", m, dt);
+        const int64_t rows = src->rows[m], cols = src->cols[m], bs = cw_block_size(dt);
+        CW_REQUIRE(rows > 0 && cols > 0 && cols % bs == 0, "bank: matrix %d is %lld x %lld", m, (long long)rows,
+                   (long long)cols);
+        const int64_t bytes = rows * (cols / bs) * cw_type_size(dt);
+        CW_REQUIRE(src->expert_bytes[m] == bytes, "bank: matrix %d expert is %lld bytes, expected %lld", m,
+                   (long long)src->expert_bytes[m], (long long)bytes);
+        CW_REQUIRE(src->host[m], "bank: matrix %d has no host source", m);
+    }
+    return CW_OK;
+}
+
+}  // namespace
+}  // namespace cw
+
+struct cw_bank {
+    int device = -1;
+    cw_bank_source src{};
+    int n_slots = 0;
+    uint8_t *mat[3] = {};
+    uint32_t *table = nullptr;
+    cw_slots *slots = nullptr;
+    std::vector<uint32_t> dev_table;  // the device table once the patches enqueued so far ran
+    hipStream_t copy = nullptr;       // prefetch copies
+    std::vector<hipEvent_t> slot_ev;  // per slot: end of its last prefetch copy
+    std::vector<uint8_t> filling;     // per slot: that copy may still be running
+    std::vector<uint8_t> kept;        // per slot: placed by the last ensure
+    hipEvent_t fence = nullptr;       // the last ensure's stream at its return
+    bool fenced = false;
+    cw_bank_stats st{};
+
+    ~cw_bank() {  // teardown: failures here have no caller to go to
+        if (copy) (void)hipStreamSynchronize(copy);
+        for (hipEvent_t e : slot_ev)
+            if (e) (void)hipEventDestroy(e);
+        if (fence) (void)hipEventDestroy(fence);
+        if (copy) (void)hipStreamDestroy(copy);
+        cw_slots_free(slots);
+    }
+
+    int64_t expert_bytes() const { return src.expert_bytes[0] + src.expert_bytes[1] + src.expert_bytes[2]; }
+
+    int on_device() const {
+        int dev = -1;
+        if (hipGetDevice(&dev) != hipSuccess || dev != device)
+            return cw::set_error(CW_EINVAL, "bank: made on device %d, called on device %d", device, dev);
+        return CW_OK;
+    }
+
+    // slots whose prefetch copy has finished stop filling
+    int refresh() {
+        for (int s = 0; s < n_slots; s++) {
+            if (!filling[(size_t)s]) continue;
+            const hipError_t q = hipEventQuery(slot_ev[(size_t)s]);
+            if (q == hipSuccess) filling[(size_t)s] = 0;
+            else if (q != hipErrorNotReady) return cw::set_error(CW_EHIP, "bank: event query: %s", hipGetErrorString(q));
+        }
+        return CW_OK;
+    }
+
+    int copy_in(uint32_t e, uint32_t slot, hipStream_t s) {
+        for (int m = 0; m < 3; m++) {
+            const int64_t eb = src.expert_bytes[m];
+            const hipError_t r = hipMemcpyAsync(mat[m] + (int64_t)slot * eb, (const uint8_t *)src.host[m] + (int64_t)e * eb,
+                                                (size_t)eb, hipMemcpyHostToDevice, s);
+            if (r != hipSuccess) return cw::set_error(CW_EHIP, "bank: copy of expert %u: %s", e, hipGetErrorString(r));
+        }
+        return CW_OK;
+    }
+
+    // brings the device table to the bookkeeping's, leaving out slots still being filled unless
+    // the stream has waited for them (listed in waited)
+    int publish(const std::vector<uint8_t> &waited, hipStream_t s) {
+        std::vector<uint32_t> want((size_t)src.n_experts);
+        cw_slots_table(slots, want.data(), src.n_experts);
+        cw::TablePatch p{};
+        for (int e = 0; e < src.n_experts; e++) {
+            uint32_t v = want[(size_t)e];
+            if (v != CW_NO_SLOT && filling[v] && !waited[v]) v = CW_NO_SLOT;
+            if (v == dev_table[(size_t)e]) continue;
+            dev_table[(size_t)e] = v;
+            p.expert[p.n] = (uint32_t)e;
+            p.slot[p.n] = v;
+            if (++p.n == cw::PATCH) {
+                hipLaunchKernelGGL(cw::k_table_patch, dim3(1), dim3(64), 0, s, table, p);
+                p.n = 0;
+            }
+        }
+        if (p.n) hipLaunchKernelGGL(cw::k_table_patch, dim3(1), dim3(64), 0, s, table, p);
+        return cw::check_launch("k_table_patch");
+    }
+};
+
+extern "C" {
+
+size_t cw_bank_device_bytes(const cw_bank_source *src, int n_slots) {
+    if (cw::check_source(src, n_slots) != CW_OK) return 0;
+    size_t total = 0;
+    for (int m = 0; m < 3; m++) total += cw::align256((size_t)src->expert_bytes[m] * (size_t)n_slots);
+    return total + cw::align256((size_t)src->n_experts * 4);
+}
+
+cw_bank *cw_bank_new(const cw_bank_source *src, int n_slots, void *device_mem, size_t bytes) {
+    if (cw::check_source(src, n_slots) != CW_OK) return nullptr;
+    const size_t need = cw_bank_device_bytes(src, n_slots);
+    if (!device_mem || ((uintptr_t)device_mem & 255u) || bytes < need) {
+        cw::set_error(CW_EINVAL, "bank: device memory %p of %zu bytes (%zu bytes, 256-byte aligned, needed)", device_mem,
+                      bytes, need);
+        return nullptr;
+    }
+    cw_bank *b = new (std::nothrow) cw_bank();
+    if (!b) {
+        cw::set_error(CW_EINVAL, "bank: out of host memory");
+        return nullptr;
+    }
+    b->src = *src;
+    b->n_slots = n_slots;
+    b->slots = cw_slots_new(n_slots);
+    b->dev_table.assign((size_t)src->n_experts, CW_NO_SLOT);
+    b->slot_ev.assign((size_t)n_slots, nullptr);
+    b->filling.assign((size_t)n_slots, 0);
+    b->kept.assign((size_t)n_slots, 0);
+    uint8_t *p = (uint8_t *)device_mem;
+    for (int m = 0; m < 3; m++) {
+        b->mat[m] = p;
+        p += cw::align256((size_t)src->expert_bytes[m] * (size_t)n_slots);
+    }
+    b->table = (uint32_t *)p;
+    hipError_t r = hipGetDevice(&b->device);
+    // the caller's memory may still be in use by work queued before this call
+    if (r == hipSuccess) r = hipDeviceSynchronize();
+    if (r == hipSuccess) r = hipStreamCreateWithFlags(&b->copy, hipStreamNonBlocking);
+    for (int s = 0; s < n_slots && r == hipSuccess; s++) r = hipEventCreateWithFlags(&b->slot_ev[(size_t)s], hipEventDisableTiming);
+    if (r == hipSuccess) r = hipEventCreateWithFlags(&b->fence, hipEventDisableTiming);
+    if (r == hipSuccess) {
+        hipLaunchKernelGGL(cw::k_table_clear, dim3((src->n_experts + 255) / 256), dim3(256), 0, b->copy, b->table,
+                           src->n_experts);
+        r = hipGetLastError();
+    }
+    if (r == hipSuccess) r = hipStreamSynchronize(b->copy);
+    if (r != hipSuccess || !b->slots) {
+        cw::set_error(r != hipSuccess ? CW_EHIP : CW_EINVAL, "bank: set-up failed: %s", hipGetErrorString(r));
+        delete b;
+        return nullptr;
+    }
+    return b;
+}
+
+void cw_bank_free(cw_bank *b) { delete b; }
+
+int cw_bank_ensure(cw_bank *b, const uint32_t *needed, int n_needed, cw_stream_t stream, int *n_loaded) {
+    if (n_loaded) *n_loaded = 0;
+    CW_REQUIRE(b && n_needed >= 0 && (n_needed == 0 || needed), "bank ensure: bad arguments");
+    if (int rc = b->on_device()) return rc;
+    std::vector<uint32_t> want;
+    want.reserve((size_t)n_needed);
+    std::unordered_set<uint32_t> seen;
+    for (int i = 0; i < n_needed; i++) {
+        const uint32_t e = needed[i];
+        CW_REQUIRE(e < (uint32_t)b->src.n_experts, "bank ensure: expert %u of %d", e, b->src.n_experts);
+        if (seen.insert(e).second) want.push_back(e);
+    }
+    if ((int)want.size() > b->n_slots)
+        return cw::set_error(CW_EFULL, "bank: %zu experts needed, %d slots", want.size(), b->n_slots);
+    if (int rc = b->refresh()) return rc;
+    std::vector<uint8_t> ready((size_t)b->n_slots);
+    for (int s = 0; s < b->n_slots; s++) ready[(size_t)s] = b->filling[(size_t)s] ? 0 : 1;
+    const size_t n = std::max<size_t>(want.size(), 1);
+    std::vector<uint32_t> hits(2 * n), misses(2 * n);
+    int nh = 0, nm = 0;
+    uint64_t ph = 0;
+    const int r = cw_slots_assign(b->slots, want.data(), (int)want.size(), ready.data(), hits.data(), &nh,
+                                  misses.data(), &nm, &ph);
+    CW_REQUIRE(r >= 0, "bank ensure: bookkeeping refused its arguments");
+    if (r == 0) {
+        b->st.crowded++;
+        return cw::set_error(CW_EFULL, "bank: too few free slots for the %zu experts needed", want.size());
+    }
+    b->st.hits += (uint64_t)nh;
+    b->st.prefetch_hits += ph;
+    hipStream_t s = (hipStream_t)stream;
+    std::vector<uint8_t> waited((size_t)b->n_slots, 0);
+    for (int i = 0; i < nh; i++) {
+        const uint32_t slot = hits[2 * i + 1];
+        if (!b->filling[slot]) continue;
+        const hipError_t w = hipStreamWaitEvent(s, b->slot_ev[slot], 0);
+        if (w != hipSuccess) return cw::set_error(CW_EHIP, "bank: stream wait: %s", hipGetErrorString(w));
+        waited[slot] = 1;
+    }
+    for (int i = 0; i < nm; i++)
+        if (int rc = b->copy_in(misses[2 * i], misses[2 * i + 1], s)) return rc;
+    b->st.loads += (uint64_t)nm;
+    b->st.bytes_loaded += (uint64_t)nm * (uint64_t)b->expert_bytes();
+    if (int rc = b->publish(waited, s)) return rc;
+    std::fill(b->kept.begin(), b->kept.end(), 0);
+    for (int i = 0; i < nh; i++) b->kept[hits[2 * i + 1]] = 1;
+    for (int i = 0; i < nm; i++) b->kept[misses[2 * i + 1]] = 1;
+    const hipError_t f = hipEventRecord(b->fence, s);
+    if (f != hipSuccess) return cw::set_error(CW_EHIP, "bank: event record: %s", hipGetErrorString(f));
+    b->fenced = true;
+    if (n_loaded) *n_loaded = nm;
+    return CW_OK;
+}
+
+int cw_bank_prefetch(cw_bank *b, const uint32_t *predicted, int n_predicted) {
+    CW_REQUIRE(b && n_predicted >= 0 && (n_predicted == 0 || predicted), "bank prefetch: bad arguments");
+    if (int rc = b->on_device()) return -rc;
+    for (int i = 0; i < n_predicted; i++)
+        if (predicted[i] >= (uint32_t)b->src.n_experts)
+            return -cw::set_error(CW_EINVAL, "bank prefetch: expert %u of %d", predicted[i], b->src.n_experts);
+    if (n_predicted == 0) return 0;
+    if (int rc = b->refresh()) return -rc;
+    std::vector<uint8_t> ready((size_t)b->n_slots);
+    for (int s = 0; s < b->n_slots; s++) ready[(size_t)s] = !b->filling[(size_t)s] && !b->kept[(size_t)s];
+    std::vector<uint32_t> out(2 * (size_t)n_predicted);
+    const int n = cw_slots_reserve(b->slots, predicted, n_predicted, ready.data(), out.data());
+    if (n == 0) return 0;
+    if (b->fenced) {
+        const hipError_t w = hipStreamWaitEvent(b->copy, b->fence, 0);
+        if (w != hipSuccess) return -cw::set_error(CW_EHIP, "bank: stream wait: %s", hipGetErrorString(w));
+    }
+    for (int i = 0; i < n; i++) {
+        const uint32_t e = out[2 * i], slot = out[2 * i + 1];
+        if (int rc = b->copy_in(e, slot, b->copy)) return -rc;
+        const hipError_t r = hipEventRecord(b->slot_ev[slot], b->copy);
+        if (r != hipSuccess) return -cw::set_error(CW_EHIP, "bank: event record: %s", hipGetErrorString(r));
+        b->filling[slot] = 1;
+    }
+    b->st.prefetch_copies += (uint64_t)n;
+    return n;
+}
+
+int cw_bank_fill_desc(const cw_bank *b, cw_moe_desc *d) {
+    CW_REQUIRE(b && d, "bank: null argument");
+    for (int m = 0; m < 3; m++) {
+        d->dtype[m] = b->src.dtype[m];
+        d->w[m] = b->mat[m];
+        d->slot_stride[m] = b->src.expert_bytes[m];
+    }
+    d->slot_table = b->table;
+    d->n_slots = b->n_slots;
+    return CW_OK;
+}
+
+const uint32_t *cw_bank_table(const cw_bank *b) { return b ? b->table : nullptr; }
+
+int cw_bank_slot_of(const cw_bank *b, uint32_t expert) { return b ? cw_slots_slot_of(b->slots, expert) : -1; }
+
+void cw_bank_get_stats(const cw_bank *b, cw_bank_stats *out) {
+    if (b && out) *out = b->st;
+}
+
+}  // extern "C"

@@ -41,7 +41,9 @@ extern "C" {
 
 typedef void *cw_stream_t; /* hipStream_t */
 
-enum cw_status { CW_OK = 0, CW_ENOTSUP = 1, CW_EINVAL = 2, CW_EHIP = 3 };
+/* CW_EFULL: a bank cannot place the experts asked for now (more than its slots, or too few
+ * slots free); nothing changed, and the caller reads those experts another way. */
+enum cw_status { CW_OK = 0, CW_ENOTSUP = 1, CW_EINVAL = 2, CW_EHIP = 3, CW_EFULL = 4 };
 
 /* GGUF type ids of the weight formats this library reads. */
 enum cw_dtype {
@@ -271,6 +273,72 @@ int cw_slots_is_prefetched(const cw_slots *s, uint32_t expert);
 /* Writes the expert -> slot table for experts [0, n_experts) (CW_NO_SLOT when absent), the
  * host image of Bank::sync_table (crates/engine/src/experts.rs:73-81). */
 void cw_slots_table(const cw_slots *s, uint32_t *table, int n_experts);
+
+/* ---- expert banks on the device (host manager) ----------------------------------------- */
+
+/* Where a layer's experts come from: matrix m (gate, up, down) of expert e is expert_bytes[m]
+ * bytes at host[m] + e * expert_bytes[m], rows[m] x cols[m] weights of GGUF type dtype[m]
+ * (cw_gguf_experts gives these for a GGUF file). Host memory from hipHostMalloc is copied by
+ * DMA without blocking the host; other host memory is copied too, but the copy call returns
+ * only once HIP has staged the bytes. */
+typedef struct cw_bank_source {
+    int n_experts;
+    int dtype[3];
+    int64_t rows[3], cols[3];
+    int64_t expert_bytes[3];
+    const void *host[3];
+} cw_bank_source;
+
+typedef struct cw_bank_stats {
+    uint64_t hits;            /* needed experts already in a slot */
+    uint64_t prefetch_hits;   /* ... of which a prefetch brought in */
+    uint64_t loads;           /* experts copied in by cw_bank_ensure */
+    uint64_t bytes_loaded;    /* their bytes */
+    uint64_t prefetch_copies; /* experts copied in by cw_bank_prefetch */
+    uint64_t crowded;         /* ensure calls refused for too few free slots */
+} cw_bank_stats;
+
+/* One layer's expert bank on the current device: n_slots slots of each matrix (slot-major, one
+ * expert's matrix per slot), the device expert -> slot table (CW_NO_SLOT when absent), the LRU
+ * bookkeeping of cw_slots, and the host source. Replaces ExpertStore's Bank and make_bank
+ * (crates/engine/src/experts.rs:62-82, 1320-1378), GpuBank's table (gpu_sync.rs:70-148) and
+ * sync_table (experts.rs:73-81); the bytes cross PCIe from host memory instead of being read
+ * from the SSD into shared memory. Device memory comes from the caller: device_mem holds
+ * cw_bank_device_bytes(src, n_slots) bytes (256-byte aligned) for the bank's lifetime. The
+ * source's host memory must outlive the bank. A handle is used by one thread at a time, and
+ * its ensure calls, and the work that reads the bank, go on one stream. NULL on error
+ * (cw_last_error). */
+typedef struct cw_bank cw_bank;
+size_t cw_bank_device_bytes(const cw_bank_source *src, int n_slots);
+cw_bank *cw_bank_new(const cw_bank_source *src, int n_slots, void *device_mem, size_t bytes);
+/* Waits for the bank's copies, then releases its HIP stream and events. */
+void cw_bank_free(cw_bank *b);
+
+/* Places every expert in needed (duplicates ignored) in a slot before any later work on stream:
+ * the plain branch of ExpertStore::ensure (experts.rs:1489-1641). Hits stay; misses take the
+ * least recently used slots that no needed expert holds and no prefetch is filling, and their
+ * bytes are copied in on stream; a hit still being prefetched is waited for on stream (not on
+ * the host); the device table is brought up to date on stream. CW_EFULL, and nothing changed,
+ * when more experts are needed than the bank has slots or too few slots are free (the
+ * reference's Ok(None)). *n_loaded (may be NULL) receives the number of misses copied. Work
+ * that reads the bank for these experts goes on stream after this call and reads only experts
+ * placed here (a prefetch may since have taken any other slot, whose table entry the next
+ * ensure clears); the slots placed here are kept from prefetches until the next ensure. */
+int cw_bank_ensure(cw_bank *b, const uint32_t *needed, int n_needed, cw_stream_t stream, int *n_loaded);
+/* Reserves slots for predicted experts not yet held (Slots::reserve, experts.rs:273-285; the
+ * prefetch of experts.rs:1004-1098) and copies them in on the bank's own copy stream, after
+ * the work that was on the last ensure's stream when that ensure returned. Slots being filled
+ * are not taken by ensure and are waited for on the stream when needed. Returns the number of
+ * experts reserved (>= 0), or a negative status. */
+int cw_bank_prefetch(cw_bank *b, const uint32_t *predicted, int n_predicted);
+/* Fills the bank fields of a layer descriptor: dtype, w and slot_stride of the three matrices,
+ * slot_table and n_slots (cw_moe_layer then resolves picks through the table). */
+int cw_bank_fill_desc(const cw_bank *b, cw_moe_desc *d);
+/* The device expert -> slot table (n_experts u32), the slot of an expert in the host
+ * bookkeeping (-1 if none), counters. */
+const uint32_t *cw_bank_table(const cw_bank *b);
+int cw_bank_slot_of(const cw_bank *b, uint32_t expert);
+void cw_bank_get_stats(const cw_bank *b, cw_bank_stats *out);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,213 @@
+"""The device expert bank (cw_bank_*): bookkeeping, copies, the device table, prefetch, and a
+layer run through it.
+
+What pins it: the bookkeeping must follow Slots (the C++ port pinned by the reference's bank.rs
+cases in test_slots.py) call for call; every slot must hold its expert's bytes exactly as the
+host store (a GGUF file's ffn_*_exps slices) has them; the device table must equal the
+bookkeeping's expert -> slot map (the reference's sync_table, crates/engine/src/experts.rs:
+73-81); and a layer run through the bank must match the resident oracle (the experts'
+arithmetic does not depend on which slot holds them)."""
+import ctypes
+import zlib
+
+import numpy as np
+import pytest
+
+from coachwhip_amd import CwError
+from coachwhip_amd import formats as F
+from coachwhip_amd._lib import NO_SLOT, BankSource, lib
+
+SHAPES = [(256, 256), (256, 256), (256, 256)]
+DTYPES = (F.IQ2_XXS, F.IQ2_XXS, F.Q4_K)
+
+
+def _source(n_experts=40, expert_bytes=None):
+    src = BankSource()
+    src.n_experts = n_experts
+    for m in range(3):
+        src.dtype[m] = DTYPES[m]
+        src.rows[m], src.cols[m] = SHAPES[m]
+        src.expert_bytes[m] = F.matrix_bytes(DTYPES[m], *SHAPES[m]) if expert_bytes is None else expert_bytes
+        src.host[m] = 4096  # never read: these tests only size and check the source
+    return src
+
+
+def test_device_bytes_and_source_checks():
+    src = _source()
+    eb = [F.matrix_bytes(d, *s) for d, s in zip(DTYPES, SHAPES)]
+    align = lambda x: (x + 255) // 256 * 256
+    assert lib().cw_bank_device_bytes(ctypes.byref(src), 8) == sum(align(8 * b) for b in eb) + align(4 * 40)
+    assert lib().cw_bank_device_bytes(ctypes.byref(_source(expert_bytes=100)), 8) == 0       # wrong size
+    assert b"expected" in lib().cw_last_error()
+    assert lib().cw_bank_device_bytes(ctypes.byref(src), 0) == 0                              # no slots
+    bad = _source()
+    bad.cols[2] = 200                                                                          # not whole blocks
+    assert lib().cw_bank_device_bytes(ctypes.byref(bad), 8) == 0
+    bad = _source()
+    bad.host[1] = None
+    assert lib().cw_bank_device_bytes(ctypes.byref(bad), 8) == 0
+    assert not lib().cw_bank_new(ctypes.byref(src), 8, None, 1 << 20)                         # no device memory
+
+
+# ------------------------------------------------------------------------------ on the GPU
+
+def _random_store(rng, n_experts):
+    from coachwhip_amd import synth
+    return [synth.random_blocks(d, n_experts * r * c, rng) for d, (r, c) in zip(DTYPES, SHAPES)]
+
+
+def _check_bank(bank, mirror, raw, needed, skip=()):
+    import torch
+    torch.cuda.synchronize()
+    table, want = bank.table.cpu().numpy().view(np.uint32).copy(), mirror.table(bank.n_experts)
+    table[list(skip)] = want[list(skip)]
+    assert np.array_equal(table, want)
+    for e in set(int(v) for v in needed):
+        slot = mirror.slot_of[e]
+        assert bank.slot_of(e) == slot
+        for m in range(3):
+            eb = bank.expert_bytes[m]
+            got = bank.banks[m].data[slot * eb:(slot + 1) * eb].cpu().numpy()
+            assert np.array_equal(got, raw[m][e * eb:(e + 1) * eb]), (e, m, slot)
+
+
+@pytest.mark.gpu
+def test_bank_follows_slots_and_holds_the_bytes():
+    from coachwhip_amd.bank import Bank
+    from coachwhip_amd.slots import Slots
+    print("bank: 80 seeded ensure calls", flush=True)
+    rng = np.random.default_rng(5)
+    E, S = 40, 8
+    raw = _random_store(rng, E)
+    bank = Bank(raw, DTYPES, SHAPES, E, S)
+    mirror = Slots(S)
+    hot = rng.choice(E, 10, replace=False)
+    loads = hits = refused = 0
+    for step in range(80):
+        size = int(rng.integers(1, S + 2))                 # S + 1 needs more than the bank holds
+        pool = hot if rng.random() < 0.7 and size <= len(hot) else np.arange(E)
+        needed = rng.choice(pool, size, replace=False).astype(np.uint32)
+        if step % 9 == 4:
+            needed = np.concatenate([needed, needed[:2]])  # duplicates are ignored
+        got = bank.ensure(needed)
+        uniq = list(dict.fromkeys(int(v) for v in needed))
+        if len(uniq) > S:
+            assert got is None
+            refused += 1
+            continue
+        plan = mirror.assign(uniq)
+        assert plan is not None                            # nothing is being filled: always placeable
+        assert got == len(plan.misses)
+        loads += len(plan.misses)
+        hits += len(plan.hits)
+        _check_bank(bank, mirror, raw, uniq)
+    st = bank.stats()
+    assert (st["loads"], st["hits"], st["crowded"], st["prefetch_copies"]) == (loads, hits, 0, 0)
+    assert st["bytes_loaded"] == loads * sum(bank.expert_bytes)
+    assert refused > 0 and hits > 0 and loads > S
+
+
+@pytest.mark.gpu
+def test_bank_prefetch_keeps_the_placed_slots():
+    import torch
+    from coachwhip_amd.bank import Bank
+    from coachwhip_amd.slots import Slots
+    print("bank: prefetch", flush=True)
+    rng = np.random.default_rng(6)
+    E, S = 32, 8
+    raw = _random_store(rng, E)
+    bank = Bank(raw, DTYPES, SHAPES, E, S)
+    mirror = Slots(S)
+    assert bank.ensure([0, 1, 2]) == 3 and mirror.assign([0, 1, 2]) is not None
+    # 1 is held; 5, 6, 7 go to free slots without waiting for anything on the stream
+    assert bank.prefetch([5, 6, 7, 1]) == 3
+    assert mirror.reserve([5, 6, 7, 1]) == [(e, bank.slot_of(e)) for e in (5, 6, 7)]
+    assert bank.ensure([5, 6, 3]) == 1                     # 5, 6 were prefetched, 3 is a miss
+    plan = mirror.assign([5, 6, 3])
+    assert plan.prefetch_hits == 2 and len(plan.misses) == 1
+    torch.cuda.synchronize()
+    table = bank.table.cpu().numpy().view(np.uint32)
+    assert table[7] in (NO_SLOT, mirror.slot_of[7])        # listed once its copy has landed
+    _check_bank(bank, mirror, raw, [5, 6, 3], skip=[7])
+    placed = {e: bank.slot_of(e) for e in (5, 6, 3)}
+    # eight predictions, but the three slots the last ensure placed are not taken
+    n = bank.prefetch(list(range(10, 18)))
+    assert n == S - 3
+    for e, s in placed.items():
+        assert bank.slot_of(e) == s
+    ready = [0 if s in placed.values() else 1 for s in range(S)]
+    mirror.reserve(list(range(10, 18)), ready=lambda s: ready[s])
+    torch.cuda.synchronize()
+    assert bank.ensure([]) == 0                            # the copies are done: the table lists them all
+    _check_bank(bank, mirror, raw, [5, 6, 3] + list(range(10, 10 + n)))
+    st = bank.stats()
+    assert (st["prefetch_copies"], st["prefetch_hits"], st["loads"]) == (3 + n, 2, 4)
+
+
+@pytest.mark.gpu
+def test_bank_rejects_bad_calls():
+    from coachwhip_amd.bank import Bank
+    print("bank: errors", flush=True)
+    rng = np.random.default_rng(7)
+    E, S = 16, 4
+    raw = _random_store(rng, E)
+    bank = Bank(raw, DTYPES, SHAPES, E, S)
+    assert bank.ensure([0, 1, 2, 3, 4]) is None             # more than the slots
+    with pytest.raises(CwError):
+        bank.ensure([E])                                    # no such expert
+    with pytest.raises(CwError):
+        bank.prefetch([E + 3])
+    assert bank.stats()["loads"] == 0
+    with pytest.raises(CwError):
+        Bank([r[:100] for r in raw], DTYPES, SHAPES, E, S)  # host store too small
+
+
+BANK_LAYERS = [
+    # name, E, K, h, I, dtypes, slots, tokens per step
+    ("c5_shape", 128, 10, 2048, 512, (F.IQ3_S, F.IQ3_S, F.Q4_K), 24, 1),
+    ("iq2_prefill", 64, 8, 1024, 512, (F.IQ2_XXS, F.IQ2_XXS, F.IQ2_S), 48, 4),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,E,K,h,I,dts,S,T", BANK_LAYERS, ids=[c[0] for c in BANK_LAYERS])
+def test_layer_through_a_bank_matches_the_oracle(tmp_path, name, E, K, h, I, dts, S, T):
+    """Experts from a GGUF file, S slots; each step routes, ensures the picks, and runs the
+    layer through the bank's table: no pick missing, ids identical, outputs within 1e-3
+    relative L2 of the resident oracle."""
+    import torch
+    from coachwhip_amd import ops, synth
+    from coachwhip_amd.gguf import GGUFFile
+    from oracle import oracle as O
+    from tests import gguf_write as G
+    print("bank layer", name, flush=True)
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    layer = synth.moe_weights(E, K, h, I, dts, rng)
+    tensors = [("blk.0.ffn_gate_exps.weight", dts[0], (E, I, h), layer.host[0]),
+               ("blk.0.ffn_up_exps.weight", dts[1], (E, I, h), layer.host[1]),
+               ("blk.0.ffn_down_exps.weight", dts[2], (E, h, I), layer.host[2])]
+    path = tmp_path / (name + ".gguf")
+    G.write_gguf(path, [], tensors)
+    with GGUFFile(path) as g:
+        bank = g.bank(0, S)
+    moe = bank.moe_layer(K)
+    missing = torch.zeros(1, dtype=torch.int32, device="cuda")
+    loaded = 0
+    for step in range(5):
+        x = rng.standard_normal((T, h)).astype(np.float32)
+        logits = rng.standard_normal((T, E)).astype(np.float32)
+        assert not synth.near_ties_within_top_k(logits, K)
+        dl = ops.to_device(logits)
+        ids, _ = ops.route(dl, K, True)
+        n = bank.ensure(ids.cpu().numpy())
+        assert n is not None
+        loaded += n
+        out, got_ids, w = moe.forward(ops.to_device(x), dl, missing)
+        want, wids, ww, _ = O.moe_layer(layer, x, logits)
+        assert np.array_equal(got_ids.cpu().numpy().view(np.uint32), wids)
+        assert np.max(np.abs(w.cpu().numpy() - ww)) < 1e-5
+        err = O.rel_l2(out.cpu().numpy(), want)
+        print("  step", step, "loaded", n, "rel_l2", err, flush=True)
+        assert err <= 1e-3
+    assert int(missing.cpu()[0]) == 0
+    assert bank.stats()["loads"] == loaded
