@@ -34,8 +34,11 @@ class Bank:
     ``host`` holds three uint8 CPU tensors, matrix m of expert e at byte e * expert_bytes[m];
     ``shapes`` the (rows, cols) of one expert's matrix, ``dtypes`` their GGUF types."""
 
-    def __init__(self, host, dtypes, shapes, n_experts, n_slots, device="cuda"):
-        self.host = [h if isinstance(h, torch.Tensor) else pinned_copy(h) for h in host]
+    def __init__(self, host, dtypes, shapes, n_experts, n_slots, device="cuda", pin=True):
+        # numpy stores are copied to pinned memory (read by the fill kernel) unless pin is False
+        # (then they are copied by DMA from where they are)
+        as_tensor = pinned_copy if pin else (lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint8)))
+        self.host = [h if isinstance(h, torch.Tensor) else as_tensor(h) for h in host]
         self.dtypes, self.shapes = tuple(dtypes), [tuple(s) for s in shapes]
         self.n_experts, self.n_slots = n_experts, n_slots
         self.expert_bytes = [F.matrix_bytes(d, r, c) for d, (r, c) in zip(self.dtypes, self.shapes)]

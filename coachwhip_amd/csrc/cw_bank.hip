@@ -7,7 +7,11 @@
 // 1320-1378), with the GPU's copy of the table written through shared-memory atomics
 // (gpu_sync.rs:70-148, sync_table experts.rs:73-81). On a discrete GPU the slots are HBM and the
 // expert store is host memory, so here:
-//  - a miss is an H2D copy on the caller's stream, ordered before the layer's kernels;
+//  - a layer's misses are copied by one kernel on the caller's stream, ordered before the
+//    layer's kernels, that reads the host store through its device mapping (pinned memory):
+//    one launch moves every miss over PCIe at the rate of a plain DMA copy, where a DMA copy
+//    per expert matrix (27 for ten picks) reached under a third of it and cost ~4 µs of host
+//    time each. A store without a device mapping (pageable memory) is copied by DMA;
 //  - a prefetch (experts.rs:1004-1098) copies on the bank's own stream, after the work that was
 //    on the last ensure's stream when that ensure returned (so it overwrites no slot a queued
 //    kernel still reads), and records an event per slot; ensure waits for that event on its
@@ -37,6 +41,28 @@ struct TablePatch {
 __global__ __launch_bounds__(64) void k_table_patch(uint32_t *table, TablePatch p) {
     const uint32_t i = threadIdx.x;
     if (i < p.n) table[p.expert[i]] = p.slot[i];
+}
+
+constexpr int FILL = 64;  // misses per fill launch
+
+struct FillList {
+    const uint8_t *src[3];  // device view of the host store of each matrix
+    uint8_t *dst[3];        // the bank's slots of each matrix
+    int64_t bytes[3];       // one expert's matrix (a multiple of 16)
+    uint32_t n;
+    uint32_t expert[FILL], slot[FILL];
+};
+
+// block (x, y): y = miss * 3 + matrix, x strides that piece's 16-byte words
+__global__ __launch_bounds__(256) void k_bank_fill(FillList f) {
+    typedef uint32_t v4 __attribute__((ext_vector_type(4)));
+    const uint32_t i = blockIdx.y / 3, m = blockIdx.y - 3 * i;
+    if (i >= f.n) return;
+    const int64_t eb = f.bytes[m];
+    const v4 *s = (const v4 *)(f.src[m] + (int64_t)f.expert[i] * eb);
+    v4 *d = (v4 *)(f.dst[m] + (int64_t)f.slot[i] * eb);
+    const int64_t words = eb / 16;
+    for (int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x; j < words; j += (int64_t)gridDim.x * 256) d[j] = s[j];
 }
 
 __global__ __launch_bounds__(256) void k_table_clear(uint32_t *table, int n) {
@@ -71,6 +97,8 @@ struct cw_bank {
     cw_bank_source src{};
     int n_slots = 0;
     uint8_t *mat[3] = {};
+    const uint8_t *mapped[3] = {};  // device view of the host store, when it has one
+    bool by_kernel = false;         // misses copied by k_bank_fill (else by DMA)
     uint32_t *table = nullptr;
     cw_slots *slots = nullptr;
     std::vector<uint32_t> dev_table;  // the device table once the patches enqueued so far ran
@@ -111,7 +139,34 @@ struct cw_bank {
         return CW_OK;
     }
 
-    int copy_in(uint32_t e, uint32_t slot, hipStream_t s) {
+    // copies experts pairs[2i] into slots pairs[2i + 1], i < n, on stream s
+    int copy_in(const uint32_t *pairs, int n, hipStream_t s) {
+        if (!by_kernel) {
+            for (int i = 0; i < n; i++)
+                if (int rc = dma(pairs[2 * i], pairs[2 * i + 1], s)) return rc;
+            return CW_OK;
+        }
+        for (int i0 = 0; i0 < n; i0 += cw::FILL) {
+            cw::FillList f{};
+            for (int m = 0; m < 3; m++) {
+                f.src[m] = mapped[m];
+                f.dst[m] = mat[m];
+                f.bytes[m] = src.expert_bytes[m];
+            }
+            f.n = (uint32_t)std::min(cw::FILL, n - i0);
+            for (uint32_t i = 0; i < f.n; i++) {
+                f.expert[i] = pairs[2 * (i0 + i)];
+                f.slot[i] = pairs[2 * (i0 + i) + 1];
+            }
+            // about a thousand blocks in all: enough 16-byte reads in flight to cover PCIe latency
+            const int per_piece = std::max(4, std::min(64, (int)((1024 + 3 * f.n - 1) / (3 * f.n))));
+            hipLaunchKernelGGL(cw::k_bank_fill, dim3(per_piece, 3 * f.n), dim3(256), 0, s, f);
+            if (int rc = cw::check_launch("k_bank_fill")) return rc;
+        }
+        return CW_OK;
+    }
+
+    int dma(uint32_t e, uint32_t slot, hipStream_t s) {
         for (int m = 0; m < 3; m++) {
             const int64_t eb = src.expert_bytes[m];
             const hipError_t r = hipMemcpyAsync(mat[m] + (int64_t)slot * eb, (const uint8_t *)src.host[m] + (int64_t)e * eb,
@@ -185,6 +240,15 @@ cw_bank *cw_bank_new(const cw_bank_source *src, int n_slots, void *device_mem, s
     if (r == hipSuccess) r = hipStreamCreateWithFlags(&b->copy, hipStreamNonBlocking);
     for (int s = 0; s < n_slots && r == hipSuccess; s++) r = hipEventCreateWithFlags(&b->slot_ev[(size_t)s], hipEventDisableTiming);
     if (r == hipSuccess) r = hipEventCreateWithFlags(&b->fence, hipEventDisableTiming);
+    // the fill kernel needs a device view of all three stores and 16-byte pieces
+    b->by_kernel = r == hipSuccess;
+    for (int m = 0; m < 3 && b->by_kernel; m++) {
+        void *dp = nullptr;
+        b->by_kernel = hipHostGetDevicePointer(&dp, const_cast<void *>(src->host[m]), 0) == hipSuccess &&
+                       ((uintptr_t)dp & 15u) == 0 && src->expert_bytes[m] % 16 == 0;
+        b->mapped[m] = (const uint8_t *)dp;
+    }
+    (void)hipGetLastError();  // a store without a device view leaves an error behind
     if (r == hipSuccess) {
         hipLaunchKernelGGL(cw::k_table_clear, dim3((src->n_experts + 255) / 256), dim3(256), 0, b->copy, b->table,
                            src->n_experts);
@@ -240,8 +304,7 @@ int cw_bank_ensure(cw_bank *b, const uint32_t *needed, int n_needed, cw_stream_t
         if (w != hipSuccess) return cw::set_error(CW_EHIP, "bank: stream wait: %s", hipGetErrorString(w));
         waited[slot] = 1;
     }
-    for (int i = 0; i < nm; i++)
-        if (int rc = b->copy_in(misses[2 * i], misses[2 * i + 1], s)) return rc;
+    if (int rc = b->copy_in(misses.data(), nm, s)) return rc;
     b->st.loads += (uint64_t)nm;
     b->st.bytes_loaded += (uint64_t)nm * (uint64_t)b->expert_bytes();
     if (int rc = b->publish(waited, s)) return rc;
@@ -272,9 +335,9 @@ int cw_bank_prefetch(cw_bank *b, const uint32_t *predicted, int n_predicted) {
         const hipError_t w = hipStreamWaitEvent(b->copy, b->fence, 0);
         if (w != hipSuccess) return -cw::set_error(CW_EHIP, "bank: stream wait: %s", hipGetErrorString(w));
     }
-    for (int i = 0; i < n; i++) {
-        const uint32_t e = out[2 * i], slot = out[2 * i + 1];
-        if (int rc = b->copy_in(e, slot, b->copy)) return -rc;
+    if (int rc = b->copy_in(out.data(), n, b->copy)) return -rc;
+    for (int i = 0; i < n; i++) {  // one copy for them all: each slot's event marks its end
+        const uint32_t slot = out[2 * i + 1];
         const hipError_t r = hipEventRecord(b->slot_ev[slot], b->copy);
         if (r != hipSuccess) return -cw::set_error(CW_EHIP, "bank: event record: %s", hipGetErrorString(r));
         b->filling[slot] = 1;

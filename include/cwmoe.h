@@ -278,9 +278,10 @@ void cw_slots_table(const cw_slots *s, uint32_t *table, int n_experts);
 
 /* Where a layer's experts come from: matrix m (gate, up, down) of expert e is expert_bytes[m]
  * bytes at host[m] + e * expert_bytes[m], rows[m] x cols[m] weights of GGUF type dtype[m]
- * (cw_gguf_experts gives these for a GGUF file). Host memory from hipHostMalloc is copied by
- * DMA without blocking the host; other host memory is copied too, but the copy call returns
- * only once HIP has staged the bytes. */
+ * (cw_gguf_experts gives these for a GGUF file), and must hold n_experts experts of each.
+ * Host memory from hipHostMalloc (which the device can address) is read by the bank's fill
+ * kernel over PCIe without blocking the host; other host memory is copied by DMA, each copy
+ * returning once HIP has staged its bytes. */
 typedef struct cw_bank_source {
     int n_experts;
     int dtype[3];

@@ -72,14 +72,15 @@ def _check_bank(bank, mirror, raw, needed, skip=()):
 
 
 @pytest.mark.gpu
-def test_bank_follows_slots_and_holds_the_bytes():
+@pytest.mark.parametrize("pin", [True, False], ids=["pinned_fill_kernel", "pageable_dma"])
+def test_bank_follows_slots_and_holds_the_bytes(pin):
     from coachwhip_amd.bank import Bank
     from coachwhip_amd.slots import Slots
-    print("bank: 80 seeded ensure calls", flush=True)
+    print("bank: 80 seeded ensure calls, pinned", pin, flush=True)
     rng = np.random.default_rng(5)
     E, S = 40, 8
     raw = _random_store(rng, E)
-    bank = Bank(raw, DTYPES, SHAPES, E, S)
+    bank = Bank(raw, DTYPES, SHAPES, E, S, pin=pin)
     mirror = Slots(S)
     hot = rng.choice(E, 10, replace=False)
     loads = hits = refused = 0
