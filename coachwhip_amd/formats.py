@@ -6,21 +6,27 @@ type enum does not. Sizes: k_quants.rs:125-200, 631-635; quantized.metal:217-257
 """
 F32, F16 = 0, 1
 Q8_0 = 8
+Q2_K = 10
+Q3_K = 11
 Q4_K = 12
+Q5_K = 13
 Q8_K = 15
 IQ2_XXS = 16
 IQ3_S = 21
 IQ2_S = 22
 MXFP4 = 39
 
-NAMES = {F32: "f32", F16: "f16", Q8_0: "q8_0", Q4_K: "q4_K", Q8_K: "q8_K", IQ2_XXS: "iq2_xxs",
-         IQ3_S: "iq3_s", IQ2_S: "iq2_s", MXFP4: "mxfp4"}
+NAMES = {F32: "f32", F16: "f16", Q8_0: "q8_0", Q2_K: "q2_K", Q3_K: "q3_K", Q4_K: "q4_K", Q5_K: "q5_K",
+         Q8_K: "q8_K", IQ2_XXS: "iq2_xxs", IQ3_S: "iq3_s", IQ2_S: "iq2_s", MXFP4: "mxfp4"}
 BY_NAME = {v: k for k, v in NAMES.items()}
 
-_BLOCK = {F32: 1, F16: 1, Q8_0: 32, Q4_K: 256, Q8_K: 256, IQ2_XXS: 256, IQ3_S: 256, IQ2_S: 256,
-          MXFP4: 32}
-_SIZE = {F32: 4, F16: 2, Q8_0: 34, Q4_K: 144, Q8_K: 292, IQ2_XXS: 66, IQ3_S: 110, IQ2_S: 82,
-         MXFP4: 17}
+_BLOCK = {F32: 1, F16: 1, Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q8_K: 256, IQ2_XXS: 256,
+          IQ3_S: 256, IQ2_S: 256, MXFP4: 32}
+_SIZE = {F32: 4, F16: 2, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q8_K: 292, IQ2_XXS: 66,
+         IQ3_S: 110, IQ2_S: 82, MXFP4: 17}
+
+# the sources of the shrink to Q2_K (crates/engine/src/requant.rs:334-352)
+SHRINK_SOURCES = (Q3_K, Q4_K, Q5_K)
 
 # the weight formats the kernels take (Q8_K is an activation format only)
 WEIGHT_TYPES = (Q8_0, Q4_K, IQ2_XXS, IQ2_S, IQ3_S, MXFP4)

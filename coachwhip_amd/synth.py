@@ -6,6 +6,7 @@ suggested one where they give none):
 
 - Q8_0: d = f16(U[0.001, 0.02]), quants U{-127..127}.
 - Q4_K: d, dmin = f16(U[0.001, 0.02]); the 12 scale bytes and 128 quant bytes uniform.
+- Q2_K / Q3_K / Q5_K (the shrink's formats): d (and dmin) = f16(U[0.001, 0.02]); the rest uniform.
 - IQ2_XXS / IQ2_S / IQ3_S: d = f16(U[0.001, 0.02]); all other bytes uniform.
 - MXFP4: e8m0 exponent U{119..123}; nibbles uniform.
 
@@ -33,9 +34,14 @@ def random_blocks(dtype, n_weights, rng):
         d = _f16_bits(rng.uniform(0.001, 0.02, nb))
         raw[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
         raw[:, 2:34] = rng.integers(-127, 128, size=(nb, 32), dtype=np.int8).view(np.uint8)
-    elif dtype == F.Q4_K:
+    elif dtype in (F.Q4_K, F.Q5_K):
         raw[:, 0:2] = _f16_bits(rng.uniform(0.001, 0.02, nb)).view(np.uint8).reshape(nb, 2)
         raw[:, 2:4] = _f16_bits(rng.uniform(0.001, 0.02, nb)).view(np.uint8).reshape(nb, 2)
+    elif dtype == F.Q2_K:
+        raw[:, 80:82] = _f16_bits(rng.uniform(0.001, 0.02, nb)).view(np.uint8).reshape(nb, 2)
+        raw[:, 82:84] = _f16_bits(rng.uniform(0.001, 0.02, nb)).view(np.uint8).reshape(nb, 2)
+    elif dtype == F.Q3_K:
+        raw[:, 108:110] = _f16_bits(rng.uniform(0.001, 0.02, nb)).view(np.uint8).reshape(nb, 2)
     elif dtype in (F.IQ2_XXS, F.IQ2_S, F.IQ3_S):
         raw[:, 0:2] = _f16_bits(rng.uniform(0.001, 0.02, nb)).view(np.uint8).reshape(nb, 2)
     elif dtype == F.MXFP4:

@@ -17,15 +17,20 @@ int or_block_size(int dtype) {
     switch (dtype) {
     case OR_F32: case OR_F16: return 1;
     case OR_Q8_0: case OR_MXFP4: return 32;
-    case OR_Q4_K: case OR_Q8_K: case OR_IQ2_XXS: case OR_IQ2_S: case OR_IQ3_S: return QK_K;
+    case OR_Q2_K: case OR_Q3_K: case OR_Q4_K: case OR_Q5_K: case OR_Q8_K: case OR_IQ2_XXS: case OR_IQ2_S:
+    case OR_IQ3_S: return QK_K;
     default: return 0;
     }
 }
 
 int or_type_size(int dtype) {
-    /* struct sizes: k_quants.rs:125-130 (Q8_0 34), 163-170 (Q4_K 144), 195-200 (Q8_K 292),
-     * 631-635 (MXFP4 17); quantized.metal:217-257 (IQ2_XXS 66, IQ2_S 82, IQ3_S 110). */
+    /* struct sizes: k_quants.rs:125-130 (Q8_0 34), 142-148 (Q2_K 84), 152-158 (Q3_K 110),
+     * 163-170 (Q4_K 144), 173-181 (Q5_K 176), 195-200 (Q8_K 292), 631-635 (MXFP4 17);
+     * quantized.metal:217-257 (IQ2_XXS 66, IQ2_S 82, IQ3_S 110). */
     switch (dtype) {
+    case OR_Q2_K: return 84;
+    case OR_Q3_K: return 110;
+    case OR_Q5_K: return 176;
     case OR_F32: return 4;
     case OR_F16: return 2;
     case OR_Q8_0: return 34;
@@ -128,6 +133,77 @@ static void deq_q4_k(const uint8_t *b, float *y) {
     }
 }
 
+/* Q2_K {scales[16], qs[64], d, dmin}: k_quants.rs:1152-1190 */
+static void deq_q2_k(const uint8_t *b, float *y) {
+    const uint8_t *sc = b, *qs = b + 16;
+    float d = or_f16_to_f32(rd16(b + 80)), mn = or_f16_to_f32(rd16(b + 82));
+    int is = 0;
+    for (int half = 0; half < 2; half++) {
+        const uint8_t *q = qs + 32 * half;
+        float *yb = y + 128 * half;
+        int yi = 0;
+        for (int shift = 0; shift < 8; shift += 2) {
+            for (int part = 0; part < 2; part++) {
+                uint8_t s = sc[is++];
+                float dl = d * (float)(s & 0xF), ml = mn * (float)(s >> 4);
+                for (int i = 0; i < 16; i++) yb[yi++] = dl * (float)((q[16 * part + i] >> shift) & 3) - ml;
+            }
+        }
+    }
+}
+
+/* Q3_K {hmask[32], qs[64], scales[12], d}: k_quants.rs:1514-1571 */
+static void deq_q3_k(const uint8_t *b, float *y) {
+    const uint8_t *hm = b, *qs = b + 32, *sr = b + 96;
+    float d_all = or_f16_to_f32(rd16(b + 108));
+    uint32_t aux[4];
+    memcpy(aux, sr, 12);
+    uint32_t tmp = aux[2];
+    aux[2] = ((aux[0] >> 4) & 0x0f0f0f0fu) | (((tmp >> 4) & 0x03030303u) << 4);
+    aux[3] = ((aux[1] >> 4) & 0x0f0f0f0fu) | (((tmp >> 6) & 0x03030303u) << 4);
+    aux[0] = (aux[0] & 0x0f0f0f0fu) | ((tmp & 0x03030303u) << 4);
+    aux[1] = (aux[1] & 0x0f0f0f0fu) | (((tmp >> 2) & 0x03030303u) << 4);
+    int8_t scales[16];
+    memcpy(scales, aux, 16);
+    int is = 0;
+    uint8_t m = 1;
+    for (int half = 0; half < 2; half++) {
+        const uint8_t *q = qs + 32 * half;
+        for (int shift = 0; shift < 8; shift += 2) {
+            for (int part = 0; part < 2; part++) {
+                float dl = d_all * ((float)scales[is] - 32.0f);
+                for (int i = 0; i < 16; i++) {
+                    int v = (int)((q[i + 16 * part] >> shift) & 3) - ((hm[i + 16 * part] & m) ? 0 : 4);
+                    *y++ = dl * (float)v;
+                }
+                is++;
+            }
+            m <<= 1;
+        }
+    }
+}
+
+/* Q5_K {d, dmin, scales[12], qh[32], qs[128]}: k_quants.rs:2120-2152 */
+static void deq_q5_k(const uint8_t *b, float *y) {
+    float d = or_f16_to_f32(rd16(b)), mn = or_f16_to_f32(rd16(b + 2));
+    const uint8_t *sc = b + 4, *qh = b + 16, *ql = b + 48;
+    int is = 0;
+    uint8_t u1 = 1, u2 = 2;
+    for (int j = 0; j < QK_K; j += 64) {
+        uint8_t s, m;
+        scale_min_k4(is, sc, &s, &m);
+        float d1 = d * (float)s, m1 = mn * (float)m;
+        scale_min_k4(is + 1, sc, &s, &m);
+        float d2 = d * (float)s, m2 = mn * (float)m;
+        const uint8_t *q = ql + j / 2;
+        for (int l = 0; l < 32; l++) y[j + l] = d1 * ((float)(q[l] & 0xF) + ((qh[l] & u1) ? 16.0f : 0.0f)) - m1;
+        for (int l = 0; l < 32; l++) y[j + 32 + l] = d2 * ((float)(q[l] >> 4) + ((qh[l] & u2) ? 16.0f : 0.0f)) - m2;
+        is += 2;
+        u1 <<= 2;
+        u2 <<= 2;
+    }
+}
+
 /* k_quants.rs:673-691 */
 static void deq_mxfp4(const uint8_t *b, float *y) {
     float d = or_e8m0_half(b[0]);
@@ -205,13 +281,107 @@ int or_dequantize(int dtype, const void *blocks, int64_t n, float *out) {
         case OR_F32: memcpy(y, b, 4); break;
         case OR_F16: *y = or_f16_to_f32(rd16(b)); break;
         case OR_Q8_0: deq_q8_0(b, y); break;
+        case OR_Q2_K: deq_q2_k(b, y); break;
+        case OR_Q3_K: deq_q3_k(b, y); break;
         case OR_Q4_K: deq_q4_k(b, y); break;
+        case OR_Q5_K: deq_q5_k(b, y); break;
         case OR_MXFP4: deq_mxfp4(b, y); break;
         case OR_IQ2_XXS: deq_iq2_xxs(b, y); break;
         case OR_IQ2_S: deq_iq2_s(b, y); break;
         case OR_IQ3_S: deq_iq3_s(b, y); break;
         default: return -1;
         }
+    }
+    return 0;
+}
+
+/* ---- the GPU shrink to Q2_K, crates/engine/src/requant.rs:113-304 ---- */
+
+static float min_sel(float a, float b) { return b < a ? b : a; }
+static float max_sel(float a, float b) { return b > a ? b : a; }
+static int clamp03(int l) { return l < 0 ? 0 : (l > 3 ? 3 : l); }
+
+/* fit16, requant.rs:119-138 */
+static void fit16(const float *x, const float *w, float *scale, float *mn) {
+    for (int round = 0; round < 2; ++round) {
+        float sw = 0.f, swl = 0.f, swll = 0.f, swx = 0.f, swlx = 0.f;
+        for (int i = 0; i < 16; ++i) {
+            int l = 0;
+            if (*scale > 0.f) l = clamp03((int)((x[i] + *mn) / *scale + 0.5f));
+            const float wi = w[i], fl = (float)l;
+            sw += wi;
+            swl += wi * fl;
+            swll += wi * fl * fl;
+            swx += wi * x[i];
+            swlx += wi * fl * x[i];
+        }
+        const float det = sw * swll - swl * swl;
+        if (det > 1e-12f) {
+            const float a = (sw * swlx - swl * swx) / det;
+            const float b = (swl * swlx - swll * swx) / det;
+            if (a > 0.f && b >= 0.f) {
+                *scale = a;
+                *mn = b;
+            }
+        }
+    }
+}
+
+/* q2k_encode / q2k_encode_w, requant.rs:141-232 (w == NULL: every weight 1) */
+static void q2k_encode(const float *x, const float *w, uint8_t *y) {
+    float scales[16], mins[16], max_scale = 0.f, max_min = 0.f;
+    for (int j = 0; j < 16; ++j) {
+        float lo = x[16 * j], hi = x[16 * j];
+        for (int i = 1; i < 16; ++i) {
+            lo = min_sel(lo, x[16 * j + i]);
+            hi = max_sel(hi, x[16 * j + i]);
+        }
+        if (lo > 0.f) lo = 0.f;
+        float sc = (hi - lo) / 3.f, mn = -lo, wl[16];
+        for (int i = 0; i < 16; ++i) wl[i] = w ? sqrtf(max_sel(w[16 * j + i], 0.f)) + 1e-6f : 1.f;
+        fit16(x + 16 * j, wl, &sc, &mn);
+        scales[j] = sc;
+        mins[j] = mn;
+        max_scale = max_sel(max_scale, sc);
+        max_min = max_sel(max_min, mn);
+    }
+    const float inv_scale = max_scale > 0.f ? 15.f / max_scale : 0.f;
+    const float inv_min = max_min > 0.f ? 15.f / max_min : 0.f;
+    uint8_t ls[16], lm[16];
+    for (int j = 0; j < 16; ++j) {
+        int a = (int)(scales[j] * inv_scale + 0.5f), b = (int)(mins[j] * inv_min + 0.5f);
+        ls[j] = (uint8_t)(a < 15 ? a : 15);
+        lm[j] = (uint8_t)(b < 15 ? b : 15);
+        y[j] = (uint8_t)(ls[j] | (lm[j] << 4));
+    }
+    const uint16_t dh = or_f32_to_f16(max_scale / 15.f), mh = or_f32_to_f16(max_min / 15.f);
+    y[80] = (uint8_t)dh; y[81] = (uint8_t)(dh >> 8);
+    y[82] = (uint8_t)mh; y[83] = (uint8_t)(mh >> 8);
+    const float d = or_f16_to_f32(dh), dmin = or_f16_to_f32(mh);
+    uint8_t L[256];
+    for (int j = 0; j < 16; ++j) {
+        const float dj = d * (float)ls[j], mj = dmin * (float)lm[j];
+        for (int i = 0; i < 16; ++i) {
+            int l = 0;
+            if (dj > 0.f) l = clamp03((int)((x[16 * j + i] + mj) / dj + 0.5f));
+            L[16 * j + i] = (uint8_t)l;
+        }
+    }
+    for (int j = 0; j < QK_K; j += 128)
+        for (int l = 0; l < 32; ++l)
+            y[16 + j / 4 + l] = (uint8_t)(L[j + l] | (L[j + l + 32] << 2) | (L[j + l + 64] << 4) | (L[j + l + 96] << 6));
+}
+
+int or_requant_q2k(int src_dtype, const void *src, int64_t n_blocks, const float *shape,
+                   int64_t blocks_per_row, void *dst) {
+    if (src_dtype != OR_Q3_K && src_dtype != OR_Q4_K && src_dtype != OR_Q5_K) return -1;
+    if (n_blocks < 0 || (shape && blocks_per_row <= 0)) return -1;
+    const int ts = or_type_size(src_dtype);
+    #pragma omp parallel for schedule(static)
+    for (int64_t t = 0; t < n_blocks; t++) {
+        float x[QK_K];
+        or_dequantize(src_dtype, (const uint8_t *)src + t * ts, QK_K, x);
+        q2k_encode(x, shape ? shape + (t % blocks_per_row) * QK_K : NULL, (uint8_t *)dst + t * 84);
     }
     return 0;
 }

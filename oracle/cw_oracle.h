@@ -17,8 +17,8 @@ extern "C" {
 #endif
 
 /* GGUF type ids: vendor/candle-core/src/quantized/mod.rs:314-339, plus 21 (IQ3_S), 22 (IQ2_S). */
-enum { OR_F32 = 0, OR_F16 = 1, OR_Q8_0 = 8, OR_Q4_K = 12, OR_Q8_K = 15, OR_IQ2_XXS = 16,
-       OR_IQ3_S = 21, OR_IQ2_S = 22, OR_MXFP4 = 39 };
+enum { OR_F32 = 0, OR_F16 = 1, OR_Q8_0 = 8, OR_Q2_K = 10, OR_Q3_K = 11, OR_Q4_K = 12, OR_Q5_K = 13,
+       OR_Q8_K = 15, OR_IQ2_XXS = 16, OR_IQ3_S = 21, OR_IQ2_S = 22, OR_MXFP4 = 39 };
 
 int or_block_size(int dtype);   /* weights per block, 0 if unknown */
 int or_type_size(int dtype);    /* bytes per block, 0 if unknown */
@@ -30,6 +30,18 @@ float or_e8m0_half(uint8_t e);    /* k_quants.rs:642-649 */
 /* Dequantize n weights (n a multiple of the block size) into f32. 0 on success, -1 on a bad
  * dtype or size. */
 int or_dequantize(int dtype, const void *blocks, int64_t n, float *out);
+
+/* The GPU shrink, crates/engine/src/requant.rs:113-304: n_blocks super-blocks of Q3_K, Q4_K or
+ * Q5_K re-encoded as Q2_K (84 bytes each). Each block is dequantized (the values of candle's
+ * to_float, which the shader's dq_q3/dq_q4/dq_q5 equal exactly), then each sub-block of 16 is
+ * fitted by fit16 (two weighted least-squares rounds from the min/max start), the 16 scales and
+ * mins are put on 4 bits against the block's largest, and the quants rounded to 2 bits. With
+ * shape != NULL (run_shaped) the weight of value i of a block is sqrt(max(shape[col], 0)) + 1e-6
+ * for its column col = (block % blocks_per_row) * 256 + i; else every weight is 1. All
+ * arithmetic is IEEE f32 in the order the shader writes it; minimum and maximum are taken as
+ * "replace when strictly smaller / larger". 0 on success, -1 on a bad source type. */
+int or_requant_q2k(int src_dtype, const void *src, int64_t n_blocks, const float *shape,
+                   int64_t blocks_per_row, void *dst);
 
 /* y[m][n] = sum_k dequant(W)[n][k] * x[m][k] in f64 (W is n rows of k weights). */
 int or_qmatmul_f64(int dtype, const void *w, int64_t n, int64_t k, const float *x, int64_t m,

@@ -13,6 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
 F32, F16, Q8_0, Q4_K, Q8_K, IQ2_XXS, IQ3_S, IQ2_S, MXFP4 = 0, 1, 8, 12, 15, 16, 21, 22, 39
+Q2_K, Q3_K, Q5_K = 10, 11, 13
 
 _lib = None
 
@@ -73,6 +74,7 @@ def _declare(L):
     L.or_vec_dot.argtypes = [_I, _L, _P, _P]
     L.or_vec_dot.restype = ctypes.c_float
     L.or_candle_matmul.argtypes = [_I, _P, _L, _L, _P, _L, _P, _I]
+    L.or_requant_q2k.argtypes = [_I, _P, _L, _P, _L, _P]
 
 
 class MoeDesc(ctypes.Structure):
@@ -250,6 +252,16 @@ def candle_matmul(dtype, w, n, k, x, threads=0):
     y = np.empty((x.shape[0], n), dtype=np.float32)
     assert lib().or_candle_matmul(dtype, _ptr(w), n, k, _ptr(x), x.shape[0], _ptr(y), threads) == 0
     return y
+
+
+def requant_q2k(src_dtype, blocks, n_blocks, shape=None, blocks_per_row=0):
+    """The GPU shrink's Q2_K bytes (n_blocks x 84) for n_blocks source super-blocks."""
+    src = np.ascontiguousarray(blocks, dtype=np.uint8)
+    out = np.zeros(n_blocks * 84, dtype=np.uint8)
+    sh = None if shape is None else np.ascontiguousarray(shape, dtype=np.float32)
+    rc = lib().or_requant_q2k(src_dtype, _ptr(src), n_blocks, _ptr(sh), blocks_per_row, _ptr(out))
+    assert rc == 0
+    return out
 
 
 def rel_l2(got, want):
