@@ -100,6 +100,7 @@ SIGNATURES = {
     "cw_slots_lru": ([_P, _P], None),
     "cw_slots_is_prefetched": ([_P, ctypes.c_uint32], _I),
     "cw_slots_table": ([_P, _P, _I], None),
+    "cw_requant_q2k": ([_I, _P, _L, _P, _L, _P, _P], _I),
     "cw_bank_device_bytes": ([ctypes.POINTER(BankSource), _I], ctypes.c_size_t),
     "cw_bank_new": ([ctypes.POINTER(BankSource), _I, _P, ctypes.c_size_t], _P),
     "cw_bank_free": ([_P], None),

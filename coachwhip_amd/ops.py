@@ -124,6 +124,26 @@ def router_logits(w: torch.Tensor, x: torch.Tensor, bias: torch.Tensor = None) -
     return logits
 
 
+def requant_q2k(src_dtype: int, src: torch.Tensor, n_blocks: int, shape: torch.Tensor = None, blocks_per_row: int = 0,
+                out: torch.Tensor = None) -> torch.Tensor:
+    """The shrink of n_blocks Q3_K / Q4_K / Q5_K super-blocks (device uint8) to Q2_K bytes (n_blocks * 84),
+    weighted by shape (f32, blocks_per_row * 256 per row) when given (crates/engine/src/requant.rs:361-406)."""
+    if not isinstance(src, torch.Tensor) or not src.is_cuda or src.dtype != torch.uint8:
+        raise CwError(CW_EINVAL, "requant: src must be a device uint8 tensor")
+    if src_dtype in F.SHRINK_SOURCES and src.numel() < n_blocks * F.type_size(src_dtype):
+        raise CwError(CW_EINVAL, "requant: src holds %d bytes, %d blocks need more" % (src.numel(), n_blocks))
+    if shape is not None:
+        _need(shape, torch.float32, "shape")
+        if shape.numel() < blocks_per_row * 256:
+            raise CwError(CW_EINVAL, "requant: %d weights for rows of %d blocks" % (shape.numel(), blocks_per_row))
+    if out is None:
+        out = torch.empty(n_blocks * 84, dtype=torch.uint8, device=src.device)
+    elif out.numel() < n_blocks * 84:
+        raise CwError(CW_EINVAL, "requant: out holds %d bytes" % out.numel())
+    check(lib().cw_requant_q2k(src_dtype, _p(src), n_blocks, _p(shape), blocks_per_row, _p(out), _stream()))
+    return out
+
+
 def route(logits: torch.Tensor, top_k: int, norm: bool):
     """(ids (T, K) u32 as int32 bits, weights (T, K) f32)."""
     _need(logits, torch.float32, "logits")

@@ -50,7 +50,10 @@ enum cw_dtype {
     CW_F32 = 0,
     CW_F16 = 1,
     CW_Q8_0 = 8,     /* {f16 d; i8 qs[32]}: 34 B per 32 weights */
+    CW_Q2_K = 10,    /* {u8 scales[16]; u8 qs[64]; f16 d, dmin}: 84 B per 256 (the shrink's output) */
+    CW_Q3_K = 11,    /* {u8 hmask[32]; u8 qs[64]; u8 scales[12]; f16 d}: 110 B per 256 (shrink input) */
     CW_Q4_K = 12,    /* {f16 d, dmin; u8 scales[12]; u8 qs[128]}: 144 B per 256 */
+    CW_Q5_K = 13,    /* {f16 d, dmin; u8 scales[12]; u8 qh[32]; u8 qs[128]}: 176 B per 256 (shrink input) */
     CW_IQ2_XXS = 16, /* {f16 d; u16 qs[32]}: 66 B per 256 */
     CW_IQ3_S = 21,   /* {f16 d; u8 qs[64], qh[8], signs[32], scales[4]}: 110 B per 256 */
     CW_IQ2_S = 22,   /* {f16 d; u8 qs[64], qh[8], scales[8]}: 82 B per 256 */
@@ -242,6 +245,19 @@ int cw_gguf_experts(const cw_gguf *g, int layer, int which, int *dtype, int64_t 
  * could not be scheduled) makes the call's outputs NaN and is counted here. No counterpart in
  * the reference (its layer is several dispatches). Synchronizes the device. */
 uint32_t cw_device_errors(void);
+
+/* ---- the shrink to Q2_K ----------------------------------------------------------------- */
+
+/* dst (n_blocks x 84 bytes of Q2_K) = the GPU shrink of n_blocks super-blocks of src (Q3_K,
+ * Q4_K or Q5_K): each super-block dequantized, each sub-block of 16 fitted by min/max and two
+ * weighted least-squares rounds, scales and mins put on 4 bits against the block's largest,
+ * quants rounded to 2 bits. Replaces Requant::run (crates/engine/src/requant.rs:361-380,
+ * kernels 228-304) and, with shape != NULL, Requant::run_shaped (385-406): value i of block b
+ * is then weighted by sqrt(max(shape[(b % blocks_per_row) * 256 + i], 0)) + 1e-6, shape
+ * holding one f32 per column of a row of blocks_per_row super-blocks. Unlike the reference,
+ * which waits for the GPU, the call only enqueues. CW_ENOTSUP for another source type. */
+int cw_requant_q2k(int src_dtype, const void *src, int64_t n_blocks, const float *shape,
+                   int64_t blocks_per_row, void *dst, cw_stream_t stream);
 
 /* ---- host bank bookkeeping (no GPU) ----------------------------------------------------- */
 

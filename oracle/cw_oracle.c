@@ -299,7 +299,10 @@ int or_dequantize(int dtype, const void *blocks, int64_t n, float *out) {
 
 static float min_sel(float a, float b) { return b < a ? b : a; }
 static float max_sel(float a, float b) { return b > a ? b : a; }
-static int clamp03(int l) { return l < 0 ? 0 : (l > 3 ? 3 : l); }
+/* clamp((int)v, 0, 3) and min(15, (int)v) with the shader's saturating float -> int conversion
+ * (the same as the C cast wherever that is defined; NaN gives 0) */
+static int level3(float v) { return v >= 3.f ? 3 : v >= 2.f ? 2 : v >= 1.f ? 1 : 0; }
+static int level15(float v) { return v >= 15.f ? 15 : v >= 1.f ? (int)v : 0; }
 
 /* fit16, requant.rs:119-138 */
 static void fit16(const float *x, const float *w, float *scale, float *mn) {
@@ -307,7 +310,7 @@ static void fit16(const float *x, const float *w, float *scale, float *mn) {
         float sw = 0.f, swl = 0.f, swll = 0.f, swx = 0.f, swlx = 0.f;
         for (int i = 0; i < 16; ++i) {
             int l = 0;
-            if (*scale > 0.f) l = clamp03((int)((x[i] + *mn) / *scale + 0.5f));
+            if (*scale > 0.f) l = level3((x[i] + *mn) / *scale + 0.5f);
             const float wi = w[i], fl = (float)l;
             sw += wi;
             swl += wi * fl;
@@ -349,9 +352,8 @@ static void q2k_encode(const float *x, const float *w, uint8_t *y) {
     const float inv_min = max_min > 0.f ? 15.f / max_min : 0.f;
     uint8_t ls[16], lm[16];
     for (int j = 0; j < 16; ++j) {
-        int a = (int)(scales[j] * inv_scale + 0.5f), b = (int)(mins[j] * inv_min + 0.5f);
-        ls[j] = (uint8_t)(a < 15 ? a : 15);
-        lm[j] = (uint8_t)(b < 15 ? b : 15);
+        ls[j] = (uint8_t)level15(scales[j] * inv_scale + 0.5f);
+        lm[j] = (uint8_t)level15(mins[j] * inv_min + 0.5f);
         y[j] = (uint8_t)(ls[j] | (lm[j] << 4));
     }
     const uint16_t dh = or_f32_to_f16(max_scale / 15.f), mh = or_f32_to_f16(max_min / 15.f);
@@ -363,7 +365,7 @@ static void q2k_encode(const float *x, const float *w, uint8_t *y) {
         const float dj = d * (float)ls[j], mj = dmin * (float)lm[j];
         for (int i = 0; i < 16; ++i) {
             int l = 0;
-            if (dj > 0.f) l = clamp03((int)((x[16 * j + i] + mj) / dj + 0.5f));
+            if (dj > 0.f) l = level3((x[16 * j + i] + mj) / dj + 0.5f);
             L[16 * j + i] = (uint8_t)l;
         }
     }

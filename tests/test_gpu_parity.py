@@ -412,3 +412,63 @@ def test_grouped_path_repeats_to_float_atomics_precision(monkeypatch):
     a = host(moe.forward(x, lg)[0])
     b = host(moe.forward(x, lg)[0])
     assert O.rel_l2(a, b) < 1e-6
+
+
+# ------------------------------------------------------------------------------ the shrink to Q2_K
+
+@pytest.mark.parametrize("weighted", [False, True], ids=["plain", "weighted"])
+@pytest.mark.parametrize("dtype", F.SHRINK_SOURCES, ids=[F.NAMES[d] for d in F.SHRINK_SOURCES])
+def test_requant_q2k_is_bit_exact(dtype, weighted):
+    """cw_requant_q2k against the oracle's restatement of requant.rs: every output byte equal.
+    Blocks include negative, subnormal and zero scales and all-zero blocks; the count is not a
+    multiple of the 16 blocks a workgroup takes; weights include zeros and negatives."""
+    say("requant", F.NAMES[dtype], "weighted" if weighted else "plain")
+    rng = np.random.default_rng(dtype * 2 + weighted)
+    n, bpr = 4099, 8
+    raw = synth.random_blocks(dtype, 256 * n, rng).reshape(n, -1)
+    dpos = {F.Q3_K: 108, F.Q4_K: 0, F.Q5_K: 0}[dtype]
+    raw[:40, dpos + 1] |= 0x80                      # negative d
+    raw[40:80, dpos + 1] &= 0x03                    # subnormal / tiny d
+    raw[80:90, dpos:dpos + 2] = 0                   # d = 0
+    raw[90:100] = 0                                 # all-zero blocks
+    if dtype != F.Q3_K:
+        raw[100:140, 3] |= 0x80                     # negative dmin
+    raw = raw.reshape(-1)
+    shape = None
+    if weighted:
+        shape = (rng.standard_normal(bpr * 256) ** 2).astype(np.float32)
+        shape[:64] = 0.0
+        shape[64:96] = -1.0
+    got = ops.requant_q2k(dtype, dev(raw), n, None if shape is None else dev(shape), bpr if weighted else 0)
+    want = O.requant_q2k(dtype, raw, n, shape, bpr if weighted else 0)
+    g = host(got).reshape(n, 84)
+    w = want.reshape(n, 84)
+    bad = np.nonzero(np.any(g != w, axis=1))[0]
+    assert bad.size == 0, "blocks %s differ (first: got %s want %s)" % (bad[:8], g[bad[0]], w[bad[0]])
+
+
+def test_requant_q2k_full_expert_matrix_round_trip():
+    """A full config-5-sized Q4_K matrix (2048 x 512): the shrink equals the oracle's bytes, and
+    its Q2_K decodes within the bound the oracle pins (sub-block range + half grid steps)."""
+    say("requant: one 2048 x 512 Q4_K matrix")
+    rng = np.random.default_rng(77)
+    n = 2048 * 512 // 256
+    raw = synth.random_blocks(F.Q4_K, 2048 * 512, rng)
+    got = host(ops.requant_q2k(F.Q4_K, dev(raw), n))
+    assert np.array_equal(got, O.requant_q2k(F.Q4_K, raw, n))
+    x = O.dequantize(F.Q4_K, raw, 256 * n).reshape(n, 16, 16)
+    back = O.dequantize(F.Q2_K, got, 256 * n).reshape(n, 16, 16)
+    yb = got.reshape(n, 84)
+    d = np.frombuffer(yb[:, 80:82].copy().tobytes(), np.float16).astype(np.float32)[:, None]
+    dm = np.frombuffer(yb[:, 82:84].copy().tobytes(), np.float16).astype(np.float32)[:, None]
+    lo = np.minimum(x.min(axis=2), 0)
+    assert np.all(np.abs(back - x).max(axis=2) <= (x.max(axis=2) - lo) + 0.5 * d + 0.5 * dm + 1e-6)
+
+
+def test_requant_q2k_rejects_bad_calls():
+    raw = dev(np.zeros(144, np.uint8))
+    with pytest.raises(cw.CwNotSupported):
+        ops.requant_q2k(F.Q8_0, raw, 1)
+    with pytest.raises(cw.CwError):
+        ops.requant_q2k(F.Q4_K, raw, 1, dev(np.ones(256, np.float32)), 0)   # weights without a row length
+    assert ops.requant_q2k(F.Q4_K, raw, 0).numel() == 0
