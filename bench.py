@@ -231,14 +231,94 @@ def bench_c5(args, torch, np, dev):
     print(json.dumps(line), flush=True)
 
 
+def bench_shrink(args, torch, np, dev):
+    """The GPU shrink (cw_requant_q2k) on experts of config 5's shape with the reference's model-file
+    formats (gate/up Q3_K 512 x 2048, down Q5_K 2048 x 512, crates/engine/tests/gpu_shrink.rs):
+    one launch per matrix over 64 experts at once (throughput), and the three launches of a single
+    expert (the latency a bank miss sees). HBM roofline on source + output bytes."""
+    from coachwhip_amd import formats as F
+    from coachwhip_amd import ops, synth
+    from oracle import oracle as O
+    H, I, n_exp = 2048, 512, 64
+    mats = [(F.Q3_K, I, H), (F.Q3_K, I, H), (F.Q5_K, H, I)]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    srcs, outs, nbs = [], [], []
+    for dt, r, c in mats:
+        nb = n_exp * r * c // 256
+        srcs.append(synth.device_blocks(dt, nb * 256, gen, dev))
+        outs.append(torch.empty(nb * 84, dtype=torch.uint8, device=dev))
+        nbs.append(nb)
+    in_bytes = sum(nb * F.type_size(dt) for nb, (dt, _, _) in zip(nbs, mats))
+    out_bytes = sum(nb * 84 for nb in nbs)
+    log("parity of the first 4096 blocks of each matrix against the oracle")
+    parity = True
+    for (dt, _, _), src, out in zip(mats, srcs, outs):
+        ops.requant_q2k(dt, src, 4096, out=out)
+        parity &= bool(np.array_equal(out[:4096 * 84].cpu().numpy(), O.requant_q2k(dt, src[:4096 * F.type_size(dt)].cpu().numpy(), 4096)))
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def run_all(reps):
+        start.record()
+        for _ in range(reps):
+            for (dt, _, _), src, out, nb in zip(mats, srcs, outs, nbs):
+                ops.requant_q2k(dt, src, nb, out=out)
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / reps
+
+    run_all(args.warmup)
+    ms = run_all(args.steps)
+    gbs = (in_bytes + out_bytes) / (ms * 1e-3) / 1e9
+    one = [nb // n_exp for nb in nbs]
+
+    def run_one(reps):
+        start.record()
+        for _ in range(reps):
+            for (dt, _, _), src, out, nb in zip(mats, srcs, outs, one):
+                ops.requant_q2k(dt, src, nb, out=out)
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / reps
+
+    run_one(args.warmup)
+    one_us = run_one(args.steps) * 1e3
+    log("shrink: %d experts in %.3f ms (%.1f GB/s); one expert %.1f us" % (n_exp, ms, gbs, one_us))
+    line = {
+        "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (seeded Q3_K / Q5_K blocks generated on the device)",
+        "config": {"workload": "GPU shrink to Q2_K: %d config-5 experts (gate/up Q3_K %dx%d, down Q5_K %dx%d)"
+                               % (n_exp, I, H, H, I), "blocks": sum(nbs)},
+        "us_per_expert_alone": round(one_us, 2), "us_per_expert_batched": round(ms * 1e3 / n_exp, 3),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_requant_q2k",
+                     "bytes_per_step": in_bytes + out_bytes},
+        "parity": {"bytes_equal_oracle": parity}, "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        src0 = srcs[2][:nbs[2] // n_exp * F.type_size(F.Q5_K)].cpu().numpy()
+        n, t_cpu = 0, 0.0
+        while t_cpu < min(args.cpu_seconds, 5.0) and n < 200:
+            t1 = time.perf_counter()
+            O.requant_q2k(F.Q5_K, src0, nbs[2] // n_exp)
+            t_cpu += time.perf_counter() - t1
+            n += 1
+        line["cpu_baseline"] = {"value": t_cpu / n * 1e6, "unit": "us per Q5_K 2048x512 matrix", "cores": threads,
+                                "kind": "port", "sample": "%d shrinks of one down matrix by the C oracle" % n}
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--layers", type=int, default=None, help="layers per step (40 for config 3, 48 for config 5)")
-    ap.add_argument("--workload", choices=("c3", "c5"), default="c3",
-                    help="c3: the headline decode chain; c5: the bank chain (56 of 512 slots) and streaming")
+    ap.add_argument("--workload", choices=("c3", "c5", "shrink"), default="c3",
+                    help="c3: the headline decode chain; c5: the bank chain (56 of 512 slots) and streaming; "
+                         "shrink: the GPU shrink to Q2_K of config-5-shaped experts")
     ap.add_argument("--stream-tokens", type=int, default=16, help="config 5: tokens of the streaming run")
     ap.add_argument("--prefill-tokens", type=int, default=1500)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -269,6 +349,9 @@ def main():
         return
     if args.workload == "c5":
         bench_c5(args, torch, np, dev)
+        return
+    if args.workload == "shrink":
+        bench_shrink(args, torch, np, dev)
         return
     E, K, H, I = 256, 8, 2048, 512
     dts = (F.IQ2_XXS, F.IQ2_XXS, F.IQ2_S)

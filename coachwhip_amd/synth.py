@@ -134,9 +134,14 @@ def device_blocks(dtype, n_weights, gen, device="cuda"):
     if dtype == F.Q8_0:
         raw[:, 0:2] = f16_scales()
         raw[:, 2:34] = torch.randint(-127, 128, (nb, 32), dtype=torch.int8, device=device, generator=gen).view(torch.uint8)
-    elif dtype == F.Q4_K:
+    elif dtype in (F.Q4_K, F.Q5_K):
         raw[:, 0:2] = f16_scales()
         raw[:, 2:4] = f16_scales()
+    elif dtype == F.Q2_K:
+        raw[:, 80:82] = f16_scales()
+        raw[:, 82:84] = f16_scales()
+    elif dtype == F.Q3_K:
+        raw[:, 108:110] = f16_scales()
     elif dtype in (F.IQ2_XXS, F.IQ2_S, F.IQ3_S):
         raw[:, 0:2] = f16_scales()
     elif dtype == F.MXFP4:
