@@ -15,7 +15,7 @@ int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3
 int check_launch(const char *what);
 
 inline bool is_weight_type(int dtype) {
-    return dtype == CW_Q8_0 || dtype == CW_Q4_K || dtype == CW_IQ2_XXS || dtype == CW_IQ2_S ||
+    return dtype == CW_Q8_0 || dtype == CW_Q2_K || dtype == CW_Q4_K || dtype == CW_IQ2_XXS || dtype == CW_IQ2_S ||
            dtype == CW_IQ3_S || dtype == CW_MXFP4;
 }
 

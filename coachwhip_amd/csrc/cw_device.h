@@ -3,7 +3,7 @@
 // The unit every kernel works in is a 32-weight sub-block: one Q8_0 or MXFP4 block, or one
 // eighth of a Q4_K / IQ super-block. For each format, Fmt::load() reads the bytes one
 // sub-block needs straight from the raw row (gfx950 runs with unaligned access enabled, so the
-// odd GGUF block strides of 17, 34, 66, 82 and 110 bytes cost no extra instructions),
+// odd GGUF block strides of 17, 34, 66, 82, 84 and 110 bytes cost no extra instructions),
 // Fmt::dequant() writes its 32 exact f32 values and Fmt::dot() returns their dot product with
 // 32 f32 activations. Dequantization is an exact product of an f16 (or power-of-two) scale and
 // small integers in every format here, so dequant() is bit-identical to the CPU dequantizers;
@@ -11,7 +11,8 @@
 // rounding of the sum.
 //
 // Layout and arithmetic follow vendor/candle-core/src/quantized/k_quants.rs (Q8_0 766-782,
-// Q4_K 1821-1849 with get_scale_min_k4 in quantized/utils.rs:50-60, MXFP4 638-691) and the
+// Q2_K 1152-1190, Q4_K 1821-1849 with get_scale_min_k4 in quantized/utils.rs:50-60, MXFP4
+// 638-691) and the
 // Metal dequantizers in vendor/candle-metal-kernels/src/metal_src/quantized.metal
 // (IQ2_XXS 6820-6843, IQ2_S 6918-6935, IQ3_S 6893-6916).
 #pragma once
@@ -133,6 +134,60 @@ struct FQ4_K {
             xs += x[l];
         }
         return h2f(r.dd & 0xFFFF) * (float)r.sc * s - h2f(r.dd >> 16) * (float)r.mn * xs;
+    }
+};
+
+// ---------------------------------------------------------------------------------- Q2_K
+// {scales[16], qs[64], d, dmin} (k_quants.rs:1152-1190; what the shrink writes): sub-block j is
+// the 32 bytes qs[32(j/4) ..) at bit 2(j%4), its two halves of 16 weights scaled by scales[2j]
+// and scales[2j+1] (low nibble: scale, high nibble: min).
+struct FQ2_K {
+    static constexpr int BS = 256, TS = 84, LDS_BYTES = 0;
+    static __device__ __forceinline__ uint64_t table_word(int) { return 0; }
+    struct Raw { uint32_t dd; uint32_t sc; uint4 q0, q1; int sh; };
+    static __device__ __forceinline__ void fill_lds(void *, int, int) {}
+    static __device__ __forceinline__ Raw load(const uint8_t *row, int sb) {
+        const uint8_t *b = row + TS * (sb >> 3);
+        const int j = sb & 7;
+        Raw r;
+        r.dd = ld_u32(b + 80);     // d | dmin << 16
+        r.sc = ld_u16(b + 2 * j);  // scales[2j] | scales[2j+1] << 8
+        const uint8_t *qs = b + 16 + 32 * (j >> 2);
+        r.q0 = ld_u128(qs);
+        r.q1 = ld_u128(qs + 16);
+        r.sh = 2 * (j & 3);
+        return r;
+    }
+    static __device__ __forceinline__ uint32_t q(const Raw &r, int l) {
+        uint32_t w = l < 16 ? (&r.q0.x)[l >> 2] : (&r.q1.x)[(l - 16) >> 2];
+        return (w >> (8 * (l & 3) + r.sh)) & 3u;
+    }
+    static __device__ __forceinline__ void dequant(const Raw &r, const void *, float *y) {
+        // y = (d*sc)*q - dmin*m: both products exact, one rounding (k_quants.rs:1171-1185)
+        const float d = h2f(r.dd & 0xFFFF), mn = h2f(r.dd >> 16);
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t s = (r.sc >> (8 * h)) & 0xFFu;
+            const float dl = d * (float)(s & 0xF), ml = mn * (float)(s >> 4);
+#pragma unroll
+            for (int l = 0; l < 16; l++) y[16 * h + l] = dl * (float)q(r, 16 * h + l) - ml;
+        }
+    }
+    static __device__ __forceinline__ float dot(const Raw &r, const void *, const float *x) {
+        const float d = h2f(r.dd & 0xFFFF), mn = h2f(r.dd >> 16);
+        float t = 0.f;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t s = (r.sc >> (8 * h)) & 0xFFu;
+            float sq = 0.f, sx = 0.f;
+#pragma unroll
+            for (int l = 0; l < 16; l++) {
+                sq = fmaf((float)q(r, 16 * h + l), x[16 * h + l], sq);
+                sx += x[16 * h + l];
+            }
+            t += d * (float)(s & 0xF) * sq - mn * (float)(s >> 4) * sx;
+        }
+        return t;
     }
 };
 

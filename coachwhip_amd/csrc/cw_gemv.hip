@@ -113,6 +113,7 @@ static int launch_lpr(const GemvArgs &a, dim3 grid, int threads, size_t shmem, h
 static int launch_fmt(int dtype, const GemvArgs &a, dim3 grid, int threads, size_t shmem, hipStream_t s) {
     switch (dtype) {
     case CW_Q8_0: return launch_lpr<FQ8_0>(a, grid, threads, shmem, s);
+    case CW_Q2_K: return launch_lpr<FQ2_K>(a, grid, threads, shmem, s);
     case CW_Q4_K: return launch_lpr<FQ4_K>(a, grid, threads, shmem, s);
     case CW_MXFP4: return launch_lpr<FMXFP4>(a, grid, threads, shmem, s);
     case CW_IQ2_XXS: return launch_lpr<FIQ2_XXS>(a, grid, threads, shmem, s);
@@ -144,6 +145,7 @@ int dequantize(int dtype, const void *blocks, int64_t n_elems, float *out, hipSt
     const uint8_t *b = (const uint8_t *)blocks;
     switch (dtype) {
     case CW_Q8_0: hipLaunchKernelGGL(k_dequant<FQ8_0>, grid, dim3(256), 0, s, b, n_sub, out); break;
+    case CW_Q2_K: hipLaunchKernelGGL(k_dequant<FQ2_K>, grid, dim3(256), 0, s, b, n_sub, out); break;
     case CW_Q4_K: hipLaunchKernelGGL(k_dequant<FQ4_K>, grid, dim3(256), 0, s, b, n_sub, out); break;
     case CW_MXFP4: hipLaunchKernelGGL(k_dequant<FMXFP4>, grid, dim3(256), 0, s, b, n_sub, out); break;
     case CW_IQ2_XXS: hipLaunchKernelGGL(k_dequant<FIQ2_XXS>, grid, dim3(256), 0, s, b, n_sub, out); break;

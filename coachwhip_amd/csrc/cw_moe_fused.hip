@@ -527,6 +527,7 @@ template <bool DOWN>
 static int by_fmt(int dtype, const MoeArgs &a, int T, hipStream_t s) {
     switch (dtype) {
     case CW_Q8_0: return by_shape<FQ8_0, DOWN>(a, T, s);
+    case CW_Q2_K: return by_shape<FQ2_K, DOWN>(a, T, s);
     case CW_Q4_K: return by_shape<FQ4_K, DOWN>(a, T, s);
     case CW_MXFP4: return by_shape<FMXFP4, DOWN>(a, T, s);
     case CW_IQ2_XXS: return by_shape<FIQ2_XXS, DOWN>(a, T, s);

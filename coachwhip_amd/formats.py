@@ -29,7 +29,7 @@ _SIZE = {F32: 4, F16: 2, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q8
 SHRINK_SOURCES = (Q3_K, Q4_K, Q5_K)
 
 # the weight formats the kernels take (Q8_K is an activation format only)
-WEIGHT_TYPES = (Q8_0, Q4_K, IQ2_XXS, IQ2_S, IQ3_S, MXFP4)
+WEIGHT_TYPES = (Q8_0, Q2_K, Q4_K, IQ2_XXS, IQ2_S, IQ3_S, MXFP4)
 
 
 def block_size(dtype):

@@ -85,6 +85,8 @@ MM_CASES = [
     (F.MXFP4, 512, 2880, 40),
     (F.IQ2_XXS, 512, 2048, 20),
     (F.IQ3_S, 300, 1024, 65),
+    (F.Q2_K, 512, 2048, 1),
+    (F.Q2_K, 2048, 512, 9),
 ]
 
 
@@ -134,7 +136,8 @@ def test_qmatmul_rejects_bad_shapes():
 # ------------------------------------------------------------------------------ expert matvec
 
 @pytest.mark.parametrize("dtype,n,k", [(F.IQ2_XXS, 512, 2048), (F.IQ2_S, 2048, 512), (F.Q4_K, 512, 2048),
-                                       (F.IQ3_S, 512, 2048), (F.MXFP4, 256, 2880), (F.Q8_0, 128, 1024)])
+                                       (F.IQ3_S, 512, 2048), (F.MXFP4, 256, 2880), (F.Q8_0, 128, 1024),
+                                       (F.Q2_K, 2048, 512)])
 @pytest.mark.parametrize("rows_per_expert", [False, True])
 def test_matvec_id_matches_the_oracle(dtype, n, k, rows_per_expert):
     say("matvec_id", F.NAMES[dtype], n, k, rows_per_expert)
@@ -330,6 +333,8 @@ MOE_CASES = [
     ("c4_padded", 16, 4, 1024, 720, (F.MXFP4, F.MXFP4, F.Q4_K), 1, 768, 5),
     ("iq3_s_grouped", 32, 6, 1024, 512, (F.IQ3_S, F.IQ3_S, F.IQ3_S), 0, 0, 48),
     ("iq2_s_grouped_padded", 16, 4, 512, 200, (F.IQ2_S, F.IQ2_S, F.IQ2_XXS), 1, 256, 20),
+    ("c5_shrunk_q2_k", 64, 10, 2048, 512, (F.Q2_K, F.Q2_K, F.Q2_K), 0, 0, 1),
+    ("q2_k_gate_up_tokens", 32, 4, 1024, 512, (F.Q2_K, F.Q2_K, F.Q4_K), 0, 0, 24),
 ]
 
 # the grouped MFMA path rounds activations to fp16 once (2^-11 relative): its outputs are held
