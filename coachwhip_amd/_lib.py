@@ -45,7 +45,7 @@ class SharedDesc(ctypes.Structure):
 class BankSource(ctypes.Structure):
     """struct cw_bank_source (include/cwmoe.h)."""
     _fields_ = [("n_experts", _I), ("dtype", _I * 3), ("rows", _L * 3), ("cols", _L * 3), ("expert_bytes", _L * 3),
-                ("host", _P * 3)]
+                ("host", _P * 3), ("shrink", _I * 3), ("shape", _P * 3)]
 
 
 class BankStats(ctypes.Structure):

@@ -32,9 +32,13 @@ class Bank:
     """n_slots device slots of each of a layer's three expert matrices (gate, up, down).
 
     ``host`` holds three uint8 CPU tensors, matrix m of expert e at byte e * expert_bytes[m];
-    ``shapes`` the (rows, cols) of one expert's matrix, ``dtypes`` their GGUF types."""
+    ``shapes`` the (rows, cols) of one expert's matrix, ``dtypes`` their GGUF types. A matrix
+    with ``shrink[m]`` (a Q3_K, Q4_K or Q5_K store) is held as Q2_K, shrunk on arrival, weighted
+    by ``shape[m]`` (device f32, one per column) when given (ExpertStore::shrink_into,
+    crates/engine/src/experts.rs:1245-1273)."""
 
-    def __init__(self, host, dtypes, shapes, n_experts, n_slots, device="cuda", pin=True):
+    def __init__(self, host, dtypes, shapes, n_experts, n_slots, device="cuda", pin=True, shrink=(False, False, False),
+                 shape=(None, None, None)):
         # numpy stores are copied to pinned memory (read by the fill kernel) unless pin is False
         # (then they are copied by DMA from where they are)
         as_tensor = pinned_copy if pin else (lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint8)))
@@ -52,6 +56,9 @@ class Bank:
             src.rows[m], src.cols[m] = self.shapes[m]
             src.expert_bytes[m] = self.expert_bytes[m]
             src.host[m] = self.host[m].data_ptr()
+            src.shrink[m] = int(bool(shrink[m]))
+            src.shape[m] = None if shape[m] is None else shape[m].data_ptr()
+        self._shape = shape  # kept alive with the bank
         self._src = src
         need = lib().cw_bank_device_bytes(ctypes.byref(src), n_slots)
         if need == 0:
@@ -67,11 +74,11 @@ class Bank:
         self._desc = d
         root = self._mem.data_ptr()
         self.banks = []
-        for m in range(3):
+        for m in range(3):  # slot dtype and stride from the bank (Q2_K for a shrunk matrix)
             off = d.w[m] - root
-            data = self._mem[off:off + n_slots * self.expert_bytes[m]]
+            data = self._mem[off:off + n_slots * d.slot_stride[m]]
             rows, cols = self.shapes[m]
-            self.banks.append(ops.ExpertBank(data, self.dtypes[m], rows, cols, n_slots, self.expert_bytes[m]))
+            self.banks.append(ops.ExpertBank(data, d.dtype[m], rows, cols, n_slots, d.slot_stride[m]))
         off = d.slot_table - root
         self.table = self._mem[off:off + 4 * n_experts].view(torch.int32)
 

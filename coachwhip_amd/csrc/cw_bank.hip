@@ -17,6 +17,10 @@
 //    kernel still reads), and records an event per slot; ensure waits for that event on its
 //    stream (a GPU-side wait, where the reference spins on the host), and a slot still being
 //    filled is neither a victim nor listed in the device table;
+//  - a matrix the source marks for shrinking (Q3_K, Q4_K or Q5_K in the store) is held as Q2_K:
+//    its misses go into a staging area first and are shrunk from there into their slots
+//    (ExpertStore::shrink_into, experts.rs:1245-1273), in chunks of STAGE experts; ensure and
+//    prefetch each have their own staging area, as they run on different streams;
 //  - the device table is patched in stream order by a small kernel whose (expert, slot) pairs
 //    travel as kernel arguments, so no host buffer has to outlive the call and nothing here is
 //    a memset (the form that stays correct when the caller captures the stream in a graph).
@@ -26,6 +30,7 @@
 #include <vector>
 
 #include "cw_common.h"
+#include "cw_requant.h"
 
 namespace cw {
 namespace {
@@ -45,10 +50,13 @@ __global__ __launch_bounds__(64) void k_table_patch(uint32_t *table, TablePatch 
 
 constexpr int FILL = 64;  // misses per fill launch
 
+constexpr int STAGE = 8;  // experts per staging area (matrices that are shrunk on arrival)
+
 struct FillList {
     const uint8_t *src[3];  // device view of the host store of each matrix
-    uint8_t *dst[3];        // the bank's slots of each matrix
-    int64_t bytes[3];       // one expert's matrix (a multiple of 16)
+    uint8_t *dst[3];        // the bank's slots of each matrix, or its staging area
+    int64_t bytes[3];       // one expert's matrix in the store (a multiple of 16)
+    uint32_t staged;        // bit m: matrix m goes to staging position i, not to slot[i]
     uint32_t n;
     uint32_t expert[FILL], slot[FILL];
 };
@@ -60,7 +68,7 @@ __global__ __launch_bounds__(256) void k_bank_fill(FillList f) {
     if (i >= f.n) return;
     const int64_t eb = f.bytes[m];
     const v4 *s = (const v4 *)(f.src[m] + (int64_t)f.expert[i] * eb);
-    v4 *d = (v4 *)(f.dst[m] + (int64_t)f.slot[i] * eb);
+    v4 *d = (v4 *)(f.dst[m] + (int64_t)((f.staged >> m) & 1 ? i : f.slot[i]) * eb);
     const int64_t words = eb / 16;
     for (int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x; j < words; j += (int64_t)gridDim.x * 256) d[j] = s[j];
 }
@@ -72,12 +80,21 @@ __global__ __launch_bounds__(256) void k_table_clear(uint32_t *table, int n) {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// bytes of one expert's matrix m in a slot: Q2_K when it is shrunk on arrival
+int64_t slot_bytes(const cw_bank_source *src, int m) {
+    return src->shrink[m] ? src->rows[m] * (src->cols[m] / 256) * 84 : src->expert_bytes[m];
+}
+
 int check_source(const cw_bank_source *src, int n_slots) {
     CW_REQUIRE(src, "bank: no source");
     CW_REQUIRE(n_slots > 0 && src->n_experts > 0, "bank: %d slots for %d experts", n_slots, src->n_experts);
     for (int m = 0; m < 3; m++) {
         const int dt = src->dtype[m];
-        CW_REQUIRE(is_weight_type(dt), "bank: matrix %d has type %d", m, dt);
+        if (src->shrink[m])
+            CW_REQUIRE(dt == CW_Q3_K || dt == CW_Q4_K || dt == CW_Q5_K, "bank: matrix %d of type %d cannot be shrunk", m, dt);
+        else
+            CW_REQUIRE(is_weight_type(dt), "bank: matrix %d has type %d", m, dt);
+        CW_REQUIRE(src->shrink[m] || !src->shape[m], "bank: matrix %d has column weights but is not shrunk", m);
         const int64_t rows = src->rows[m], cols = src->cols[m], bs = cw_block_size(dt);
         CW_REQUIRE(rows > 0 && cols > 0 && cols % bs == 0, "bank: matrix %d is %lld x %lld", m, (long long)rows,
                    (long long)cols);
@@ -97,6 +114,9 @@ struct cw_bank {
     cw_bank_source src{};
     int n_slots = 0;
     uint8_t *mat[3] = {};
+    int64_t slot_eb[3] = {};        // one expert's matrix in a slot
+    uint8_t *stage[2][3] = {};      // staging of shrunk matrices: [0] ensure, [1] prefetch
+    bool any_shrink = false;
     const uint8_t *mapped[3] = {};  // device view of the host store, when it has one
     bool by_kernel = false;         // misses copied by k_bank_fill (else by DMA)
     uint32_t *table = nullptr;
@@ -119,7 +139,7 @@ struct cw_bank {
         cw_slots_free(slots);
     }
 
-    int64_t expert_bytes() const { return src.expert_bytes[0] + src.expert_bytes[1] + src.expert_bytes[2]; }
+    int64_t expert_bytes() const { return src.expert_bytes[0] + src.expert_bytes[1] + src.expert_bytes[2]; }  // in the store
 
     int on_device() const {
         int dev = -1;
@@ -139,38 +159,54 @@ struct cw_bank {
         return CW_OK;
     }
 
-    // copies experts pairs[2i] into slots pairs[2i + 1], i < n, on stream s
-    int copy_in(const uint32_t *pairs, int n, hipStream_t s) {
-        if (!by_kernel) {
-            for (int i = 0; i < n; i++)
-                if (int rc = dma(pairs[2 * i], pairs[2 * i + 1], s)) return rc;
-            return CW_OK;
-        }
-        for (int i0 = 0; i0 < n; i0 += cw::FILL) {
-            cw::FillList f{};
+    // copies experts pairs[2i] into slots pairs[2i + 1], i < n, on stream s; matrices that are
+    // shrunk pass through staging area `which` (0 for ensure, 1 for prefetch)
+    int copy_in(const uint32_t *pairs, int n, hipStream_t s, int which) {
+        const int chunk = any_shrink ? cw::STAGE : cw::FILL;
+        for (int i0 = 0; i0 < n; i0 += chunk) {
+            const int c = std::min(chunk, n - i0);
+            if (by_kernel) {
+                cw::FillList f{};
+                for (int m = 0; m < 3; m++) {
+                    f.src[m] = mapped[m];
+                    f.dst[m] = src.shrink[m] ? stage[which][m] : mat[m];
+                    f.bytes[m] = src.expert_bytes[m];
+                    f.staged |= src.shrink[m] ? 1u << m : 0u;
+                }
+                f.n = (uint32_t)c;
+                for (int i = 0; i < c; i++) {
+                    f.expert[i] = pairs[2 * (i0 + i)];
+                    f.slot[i] = pairs[2 * (i0 + i) + 1];
+                }
+                // about a thousand blocks in all: enough 16-byte reads in flight to cover PCIe latency
+                const int per_piece = std::max(4, std::min(64, (1024 + 3 * c - 1) / (3 * c)));
+                hipLaunchKernelGGL(cw::k_bank_fill, dim3(per_piece, 3 * c), dim3(256), 0, s, f);
+                if (int rc = cw::check_launch("k_bank_fill")) return rc;
+            } else {
+                for (int i = 0; i < c; i++)
+                    if (int rc = dma(pairs[2 * (i0 + i)], pairs[2 * (i0 + i) + 1], i, s, which)) return rc;
+            }
+            if (!any_shrink) continue;
+            cw::ShrinkIndex idx{};
+            for (int i = 0; i < c; i++) idx.i[i] = pairs[2 * (i0 + i) + 1];
             for (int m = 0; m < 3; m++) {
-                f.src[m] = mapped[m];
-                f.dst[m] = mat[m];
-                f.bytes[m] = src.expert_bytes[m];
+                if (!src.shrink[m]) continue;
+                const int64_t bpr = src.cols[m] / 256;
+                if (int rc = cw::shrink_pieces(src.dtype[m], stage[which][m], src.expert_bytes[m], idx, c, mat[m], slot_eb[m],
+                                               src.rows[m] * bpr, src.shape[m], bpr, s))
+                    return rc;
             }
-            f.n = (uint32_t)std::min(cw::FILL, n - i0);
-            for (uint32_t i = 0; i < f.n; i++) {
-                f.expert[i] = pairs[2 * (i0 + i)];
-                f.slot[i] = pairs[2 * (i0 + i) + 1];
-            }
-            // about a thousand blocks in all: enough 16-byte reads in flight to cover PCIe latency
-            const int per_piece = std::max(4, std::min(64, (int)((1024 + 3 * f.n - 1) / (3 * f.n))));
-            hipLaunchKernelGGL(cw::k_bank_fill, dim3(per_piece, 3 * f.n), dim3(256), 0, s, f);
-            if (int rc = cw::check_launch("k_bank_fill")) return rc;
         }
         return CW_OK;
     }
 
-    int dma(uint32_t e, uint32_t slot, hipStream_t s) {
+    // DMA copies of expert e: to its slot, or to staging position i for a shrunk matrix
+    int dma(uint32_t e, uint32_t slot, int i, hipStream_t s, int which) {
         for (int m = 0; m < 3; m++) {
             const int64_t eb = src.expert_bytes[m];
-            const hipError_t r = hipMemcpyAsync(mat[m] + (int64_t)slot * eb, (const uint8_t *)src.host[m] + (int64_t)e * eb,
-                                                (size_t)eb, hipMemcpyHostToDevice, s);
+            uint8_t *dst = src.shrink[m] ? stage[which][m] + (int64_t)i * eb : mat[m] + (int64_t)slot * eb;
+            const hipError_t r = hipMemcpyAsync(dst, (const uint8_t *)src.host[m] + (int64_t)e * eb, (size_t)eb,
+                                                hipMemcpyHostToDevice, s);
             if (r != hipSuccess) return cw::set_error(CW_EHIP, "bank: copy of expert %u: %s", e, hipGetErrorString(r));
         }
         return CW_OK;
@@ -204,7 +240,10 @@ extern "C" {
 size_t cw_bank_device_bytes(const cw_bank_source *src, int n_slots) {
     if (cw::check_source(src, n_slots) != CW_OK) return 0;
     size_t total = 0;
-    for (int m = 0; m < 3; m++) total += cw::align256((size_t)src->expert_bytes[m] * (size_t)n_slots);
+    for (int m = 0; m < 3; m++) {
+        total += cw::align256((size_t)cw::slot_bytes(src, m) * (size_t)n_slots);
+        if (src->shrink[m]) total += 2 * cw::align256((size_t)src->expert_bytes[m] * cw::STAGE);
+    }
     return total + cw::align256((size_t)src->n_experts * 4);
 }
 
@@ -230,8 +269,16 @@ cw_bank *cw_bank_new(const cw_bank_source *src, int n_slots, void *device_mem, s
     b->kept.assign((size_t)n_slots, 0);
     uint8_t *p = (uint8_t *)device_mem;
     for (int m = 0; m < 3; m++) {
+        b->slot_eb[m] = cw::slot_bytes(src, m);
         b->mat[m] = p;
-        p += cw::align256((size_t)src->expert_bytes[m] * (size_t)n_slots);
+        p += cw::align256((size_t)b->slot_eb[m] * (size_t)n_slots);
+        if (src->shrink[m]) {
+            b->any_shrink = true;
+            for (int w = 0; w < 2; w++) {
+                b->stage[w][m] = p;
+                p += cw::align256((size_t)src->expert_bytes[m] * cw::STAGE);
+            }
+        }
     }
     b->table = (uint32_t *)p;
     hipError_t r = hipGetDevice(&b->device);
@@ -304,7 +351,7 @@ int cw_bank_ensure(cw_bank *b, const uint32_t *needed, int n_needed, cw_stream_t
         if (w != hipSuccess) return cw::set_error(CW_EHIP, "bank: stream wait: %s", hipGetErrorString(w));
         waited[slot] = 1;
     }
-    if (int rc = b->copy_in(misses.data(), nm, s)) return rc;
+    if (int rc = b->copy_in(misses.data(), nm, s, 0)) return rc;
     b->st.loads += (uint64_t)nm;
     b->st.bytes_loaded += (uint64_t)nm * (uint64_t)b->expert_bytes();
     if (int rc = b->publish(waited, s)) return rc;
@@ -335,7 +382,7 @@ int cw_bank_prefetch(cw_bank *b, const uint32_t *predicted, int n_predicted) {
         const hipError_t w = hipStreamWaitEvent(b->copy, b->fence, 0);
         if (w != hipSuccess) return -cw::set_error(CW_EHIP, "bank: stream wait: %s", hipGetErrorString(w));
     }
-    if (int rc = b->copy_in(out.data(), n, b->copy)) return -rc;
+    if (int rc = b->copy_in(out.data(), n, b->copy, 1)) return -rc;
     for (int i = 0; i < n; i++) {  // one copy for them all: each slot's event marks its end
         const uint32_t slot = out[2 * i + 1];
         const hipError_t r = hipEventRecord(b->slot_ev[slot], b->copy);
@@ -349,9 +396,9 @@ int cw_bank_prefetch(cw_bank *b, const uint32_t *predicted, int n_predicted) {
 int cw_bank_fill_desc(const cw_bank *b, cw_moe_desc *d) {
     CW_REQUIRE(b && d, "bank: null argument");
     for (int m = 0; m < 3; m++) {
-        d->dtype[m] = b->src.dtype[m];
+        d->dtype[m] = b->src.shrink[m] ? CW_Q2_K : b->src.dtype[m];
         d->w[m] = b->mat[m];
-        d->slot_stride[m] = b->src.expert_bytes[m];
+        d->slot_stride[m] = b->slot_eb[m];
     }
     d->slot_table = b->table;
     d->n_slots = b->n_slots;

@@ -16,6 +16,7 @@
 // Arithmetic is IEEE f32 in the shader's order, with no contraction into FMAs and correctly
 // rounded division and square root, so the output bytes equal a CPU restatement's exactly.
 #include "cw_common.h"
+#include "cw_requant.h"
 
 namespace cw {
 namespace {
@@ -124,19 +125,16 @@ __device__ __forceinline__ void fit16(const float *x, const float *w, float &sca
     }
 }
 
+// One super-block per 16 lanes (g = lane % 16 = this lane's sub-block): src is the source block,
+// w the block's 256 column weights or NULL, y the 84-byte Q2_K block (stored when store is set;
+// every lane takes part in the shuffles either way).
 template <int SRC>
-__global__ __launch_bounds__(256) void k_requant_q2k(const uint8_t *src, int64_t n_blocks, const float *shape,
-                                                     int64_t blocks_per_row, uint8_t *dst) {
+__device__ __forceinline__ void shrink_block(const uint8_t *src, const float *w_row, uint8_t *y, int g, bool store) {
 #pragma clang fp contract(off)
-    constexpr int TS = SRC == CW_Q3_K ? 110 : SRC == CW_Q4_K ? 144 : 176;
-    const int g = threadIdx.x & 15;
-    const int64_t blk = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-    // every lane joins the shuffles; lanes past the end work on the last block and store nothing
-    const int64_t b = blk < n_blocks ? blk : n_blocks - 1;
     float x[16], w[16];
-    dequant16<SRC>(src + b * TS, g, x);
-    if (shape) {
-        const float *ws = shape + (b % blocks_per_row) * 256 + 16 * g;
+    dequant16<SRC>(src, g, x);
+    if (w_row) {
+        const float *ws = w_row + 16 * g;
 #pragma unroll
         for (int i = 0; i < 16; i++) w[i] = sqrtf(max_sel(ws[i], 0.f)) + 1e-6f;
     } else {
@@ -176,8 +174,7 @@ __global__ __launch_bounds__(256) void k_requant_q2k(const uint8_t *src, int64_t
         word[k] |= (uint32_t)__shfl_xor((int)word[k], 2, 64);
         word[k] |= (uint32_t)__shfl_xor((int)word[k], 4, 64);
     }
-    if (blk >= n_blocks) return;
-    uint8_t *y = dst + blk * 84;
+    if (!store) return;
     y[g] = (uint8_t)(ls | (lm << 4));
     if (shift == 0) {
         uint8_t *qs = y + 16 + 32 * (g >> 3) + 16 * (g & 1);
@@ -190,7 +187,49 @@ __global__ __launch_bounds__(256) void k_requant_q2k(const uint8_t *src, int64_t
     }
 }
 
+template <int SRC>
+constexpr int src_bytes() { return SRC == CW_Q3_K ? 110 : SRC == CW_Q4_K ? 144 : 176; }
+
+// n_blocks consecutive source blocks into n_blocks consecutive Q2_K blocks
+template <int SRC>
+__global__ __launch_bounds__(256) void k_requant_q2k(const uint8_t *src, int64_t n_blocks, const float *shape,
+                                                     int64_t blocks_per_row, uint8_t *dst) {
+    const int g = threadIdx.x & 15;
+    const int64_t blk = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    // every lane joins the shuffles; lanes past the end work on the last block and store nothing
+    const int64_t b = blk < n_blocks ? blk : n_blocks - 1;
+    shrink_block<SRC>(src + b * src_bytes<SRC>(), shape ? shape + (b % blocks_per_row) * 256 : nullptr, dst + b * 84, g,
+                      blk < n_blocks);
+}
+
+// Piece y (blockIdx.y) of a list: blocks_per_piece source blocks at src + y * src_stride into
+// dst + index[y] * dst_stride (the bank's shrink of staged experts into their slots)
+template <int SRC>
+__global__ __launch_bounds__(256) void k_shrink_pieces(const uint8_t *src, int64_t src_stride, ShrinkIndex index, uint8_t *dst,
+                                                       int64_t dst_stride, int64_t blocks_per_piece, const float *shape,
+                                                       int64_t blocks_per_row) {
+    const int g = threadIdx.x & 15;
+    const int64_t blk = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int64_t b = blk < blocks_per_piece ? blk : blocks_per_piece - 1;
+    const uint8_t *s = src + blockIdx.y * src_stride + b * src_bytes<SRC>();
+    uint8_t *y = dst + (int64_t)index.i[blockIdx.y] * dst_stride + b * 84;
+    shrink_block<SRC>(s, shape ? shape + (b % blocks_per_row) * 256 : nullptr, y, g, blk < blocks_per_piece);
+}
+
 }  // namespace
+
+int shrink_pieces(int src_dtype, const uint8_t *src, int64_t src_stride, const ShrinkIndex &index, int n, uint8_t *dst,
+                  int64_t dst_stride, int64_t blocks_per_piece, const float *shape, int64_t blocks_per_row, hipStream_t s) {
+    if (n == 0 || blocks_per_piece == 0) return CW_OK;
+    const dim3 grid((unsigned)((blocks_per_piece + 15) / 16), (unsigned)n), block(256);
+    switch (src_dtype) {
+    case CW_Q3_K: hipLaunchKernelGGL(k_shrink_pieces<CW_Q3_K>, grid, block, 0, s, src, src_stride, index, dst, dst_stride, blocks_per_piece, shape, blocks_per_row); break;
+    case CW_Q4_K: hipLaunchKernelGGL(k_shrink_pieces<CW_Q4_K>, grid, block, 0, s, src, src_stride, index, dst, dst_stride, blocks_per_piece, shape, blocks_per_row); break;
+    case CW_Q5_K: hipLaunchKernelGGL(k_shrink_pieces<CW_Q5_K>, grid, block, 0, s, src, src_stride, index, dst, dst_stride, blocks_per_piece, shape, blocks_per_row); break;
+    default: return set_error(CW_ENOTSUP, "shrink: source type %d (Q3_K, Q4_K or Q5_K)", src_dtype);
+    }
+    return check_launch("k_shrink_pieces");
+}
 
 static int requant_q2k(int src_dtype, const void *src, int64_t n_blocks, const float *shape, int64_t blocks_per_row,
                        void *dst, hipStream_t s) {

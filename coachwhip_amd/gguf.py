@@ -96,9 +96,10 @@ class GGUFFile:
         raw = np.ctypeslib.as_array((ctypes.c_uint8 * (ne.value * eb.value)).from_address(ptr.value))
         return dtype.value, ne.value, n.value, k.value, eb.value, raw
 
-    def bank(self, layer: int, n_slots: int, device="cuda"):
+    def bank(self, layer: int, n_slots: int, device="cuda", shrink=(False, False, False)):
         """A device bank of n_slots slots for the layer's experts, with the experts' bytes copied
-        once into pinned host memory as the bank's source (the host-memory expert store)."""
+        once into pinned host memory as the bank's source (the host-memory expert store); matrices
+        with shrink[m] are held as Q2_K."""
         from .bank import Bank, pinned_copy
         host, dtypes, shapes, counts = [], [], [], set()
         for which in range(3):
@@ -109,7 +110,7 @@ class GGUFFile:
             counts.add(ne)
         if len(counts) != 1:
             raise CwError(CW_EINVAL, "gguf: layer %d has differing expert counts" % layer)
-        return Bank(host, dtypes, shapes, counts.pop(), n_slots, device)
+        return Bank(host, dtypes, shapes, counts.pop(), n_slots, device, shrink=shrink)
 
     def _dense(self, name, device):
         """A F32 or F16 tensor by name as an f32 device tensor (outermost dim first), or None."""

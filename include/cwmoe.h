@@ -304,6 +304,11 @@ typedef struct cw_bank_source {
     int64_t rows[3], cols[3];
     int64_t expert_bytes[3];
     const void *host[3];
+    /* nonzero: matrix m (Q3_K, Q4_K or Q5_K in the store) is held in the slots as Q2_K, shrunk on
+     * arrival as cw_requant_q2k does (ExpertStore::shrink_into, experts.rs:1245-1273) */
+    int shrink[3];
+    /* with shrink: cols[m] f32 column weights on the device (run_shaped), or NULL */
+    const float *shape[3];
 } cw_bank_source;
 
 typedef struct cw_bank_stats {
@@ -348,8 +353,9 @@ int cw_bank_ensure(cw_bank *b, const uint32_t *needed, int n_needed, cw_stream_t
  * are not taken by ensure and are waited for on the stream when needed. Returns the number of
  * experts reserved (>= 0), or a negative status. */
 int cw_bank_prefetch(cw_bank *b, const uint32_t *predicted, int n_predicted);
-/* Fills the bank fields of a layer descriptor: dtype, w and slot_stride of the three matrices,
- * slot_table and n_slots (cw_moe_layer then resolves picks through the table). */
+/* Fills the bank fields of a layer descriptor: dtype (CW_Q2_K for a shrunk matrix), w and
+ * slot_stride of the three matrices, slot_table and n_slots (cw_moe_layer then resolves picks
+ * through the table). */
 int cw_bank_fill_desc(const cw_bank *b, cw_moe_desc *d);
 /* The device expert -> slot table (n_experts u32), the slot of an expert in the host
  * bookkeeping (-1 if none), counters. */

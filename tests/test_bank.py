@@ -212,3 +212,100 @@ def test_layer_through_a_bank_matches_the_oracle(tmp_path, name, E, K, h, I, dts
         assert err <= 1e-3
     assert int(missing.cpu()[0]) == 0
     assert bank.stats()["loads"] == loaded
+
+
+# ------------------------------------------------------------------------------ shrink on arrival
+
+SHRINK_MATS = [(F.Q3_K, 256, 512), (F.Q4_K, 256, 512), (F.Q5_K, 512, 256)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("pin", [True, False], ids=["pinned_fill_kernel", "pageable_dma"])
+def test_bank_shrinks_misses_into_q2_k_slots(pin):
+    """Gate and up (Q3_K, Q4_K) shrunk on arrival, gate with column weights; down (Q5_K) shrunk
+    too in one bank and kept as Q4_K bytes in another. Every slot equals the oracle's shrink of
+    its expert (cw_requant_q2k's bytes), through calls that miss more experts than one staging
+    chunk (8) holds, and through prefetch."""
+    import torch
+    from coachwhip_amd.bank import Bank
+    from coachwhip_amd.slots import Slots
+    from oracle import oracle as O
+    print("bank shrink, pinned", pin, flush=True)
+    rng = np.random.default_rng(21 + pin)
+    E, S = 30, 12
+    for keep_down in (False, True):
+        mats = SHRINK_MATS if not keep_down else SHRINK_MATS[:2] + [(F.Q4_K, 512, 256)]
+        raw = [synth_blocks(dt, E * r * c, rng) for dt, r, c in mats]
+        w_gate = (rng.uniform(0, 2, 512) ** 2).astype(np.float32)
+        shape = (torch.from_numpy(w_gate).cuda(), None, None)
+        shrink = (True, True, not keep_down)
+        bank = Bank(raw, [m[0] for m in mats], [(r, c) for _, r, c in mats], E, S, pin=pin, shrink=shrink, shape=shape)
+        mirror = Slots(S)
+        eb = [F.matrix_bytes(dt, r, c) for dt, r, c in mats]
+        want = []
+        for m, (dt, r, c) in enumerate(mats):
+            if shrink[m]:
+                want.append(O.requant_q2k(dt, raw[m], E * r * c // 256, w_gate if m == 0 else None, c // 256).reshape(E, -1))
+            else:
+                want.append(raw[m].reshape(E, -1))
+
+        def check(needed):
+            torch.cuda.synchronize()
+            assert np.array_equal(bank.table.cpu().numpy().view(np.uint32), mirror.table(E))
+            for e in needed:
+                slot = mirror.slot_of[int(e)]
+                for m in range(3):
+                    st = bank.banks[m].slot_stride
+                    got = bank.banks[m].data[slot * st:(slot + 1) * st].cpu().numpy()
+                    assert np.array_equal(got, want[m][e]), (keep_down, e, m)
+
+        for needed in ([0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10], [3, 11, 12, 13], list(range(14, 26)), [0, 26, 27]):
+            assert bank.ensure(needed) == len(mirror.assign(needed).misses)
+            check(needed)
+        n = bank.prefetch([28, 29, 1, 2])
+        mirror.reserve([28, 29, 1, 2], ready=lambda s, keep=[mirror.slot_of[e] for e in (0, 26, 27)]: s not in keep)
+        torch.cuda.synchronize()
+        assert n >= 2 and bank.ensure([28, 29]) == 0
+        mirror.assign([28, 29])
+        check([28, 29])
+        assert bank.banks[0].dtype == F.Q2_K and bank.banks[2].dtype == (F.Q4_K if keep_down else F.Q2_K)
+
+
+def synth_blocks(dtype, n, rng):
+    from coachwhip_amd import synth
+    return synth.random_blocks(dtype, n, rng)
+
+
+@pytest.mark.gpu
+def test_layer_through_a_shrinking_bank_matches_the_oracle():
+    """Config-5-shaped experts stored as Q3_K (gate, up) and Q5_K (down), held as Q2_K: each
+    step's picks are ensured (misses shrunk on arrival) and the layer runs through the bank; it
+    matches the oracle's layer over the oracle's shrink of every expert."""
+    import torch
+    from coachwhip_amd import ops, synth
+    from coachwhip_amd.bank import Bank
+    from oracle import oracle as O
+    print("shrinking bank layer", flush=True)
+    rng = np.random.default_rng(33)
+    E, K, H, I, S = 64, 10, 2048, 512, 24
+    mats = [(F.Q3_K, I, H), (F.Q3_K, I, H), (F.Q5_K, H, I)]
+    raw = [synth.random_blocks(dt, E * r * c, rng) for dt, r, c in mats]
+    shrunk = [O.requant_q2k(dt, raw[m], E * r * c // 256) for m, (dt, r, c) in enumerate(mats)]
+    layer = synth.MoeWeights(E, K, H, I, (F.Q2_K,) * 3, shrunk, [F.matrix_bytes(F.Q2_K, r, c) for _, r, c in mats], E)
+    bank = Bank(raw, [m[0] for m in mats], [(r, c) for _, r, c in mats], E, S, shrink=(True, True, True))
+    moe = bank.moe_layer(K)
+    missing = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for step in range(4):
+        x = rng.standard_normal((1, H)).astype(np.float32)
+        logits = rng.standard_normal((1, E)).astype(np.float32)
+        assert not synth.near_ties_within_top_k(logits, K)
+        dl = ops.to_device(logits)
+        ids, _ = ops.route(dl, K, True)
+        assert bank.ensure(ids.cpu().numpy()) is not None
+        out, got_ids, _ = moe.forward(ops.to_device(x), dl, missing)
+        want, wids, _, _ = O.moe_layer(layer, x, logits)
+        assert np.array_equal(got_ids.cpu().numpy().view(np.uint32), wids)
+        err = O.rel_l2(out.cpu().numpy(), want)
+        print("  step", step, "rel_l2", err, flush=True)
+        assert err <= 2e-5
+    assert int(missing.cpu()[0]) == 0
