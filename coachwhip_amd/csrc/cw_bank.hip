@@ -351,7 +351,11 @@ int cw_bank_ensure(cw_bank *b, const uint32_t *needed, int n_needed, cw_stream_t
         if (w != hipSuccess) return cw::set_error(CW_EHIP, "bank: stream wait: %s", hipGetErrorString(w));
         waited[slot] = 1;
     }
-    if (int rc = b->copy_in(misses.data(), nm, s, 0)) return rc;
+    if (int rc = b->copy_in(misses.data(), nm, s, 0)) {
+        // the misses' bytes may not have arrived: they must not count as held
+        for (int i = 0; i < nm; i++) cw_slots_release(b->slots, misses[2 * i]);
+        return rc;
+    }
     b->st.loads += (uint64_t)nm;
     b->st.bytes_loaded += (uint64_t)nm * (uint64_t)b->expert_bytes();
     if (int rc = b->publish(waited, s)) return rc;
@@ -382,7 +386,10 @@ int cw_bank_prefetch(cw_bank *b, const uint32_t *predicted, int n_predicted) {
         const hipError_t w = hipStreamWaitEvent(b->copy, b->fence, 0);
         if (w != hipSuccess) return -cw::set_error(CW_EHIP, "bank: stream wait: %s", hipGetErrorString(w));
     }
-    if (int rc = b->copy_in(out.data(), n, b->copy, 1)) return -rc;
+    if (int rc = b->copy_in(out.data(), n, b->copy, 1)) {
+        for (int i = 0; i < n; i++) cw_slots_release(b->slots, out[2 * i]);
+        return -rc;
+    }
     for (int i = 0; i < n; i++) {  // one copy for them all: each slot's event marks its end
         const uint32_t slot = out[2 * i + 1];
         const hipError_t r = hipEventRecord(b->slot_ev[slot], b->copy);
