@@ -427,24 +427,33 @@ def main():
     gbs = layer_bytes / (us_per_layer * 1e-6) / 1e9
     log("decode: %.2f us/layer, %.1f GB/s (wall %.3f s)" % (us_per_layer, gbs, wall))
 
-    # prefill: one layer, T tokens (the reference reads prompts in pieces; this is one piece)
+    # prefill: one layer, T tokens (the reference reads prompts in pieces; this is one piece).
+    # reps calls are captured in one graph, so the time is the GPU's and not the host's launch
+    # overhead; the replay's output is checked against an eager call.
     T = args.prefill_tokens
     xp = torch.randn((T, H), generator=gen, device=dev)
     lp = torch.randn((T, E), generator=gen, device=dev)
-    layers[1].forward(xp, lp)
+    for _ in range(2):
+        eager = layers[1].forward(xp, lp)[0]
     torch.cuda.synchronize()
-    reps = 3
+    reps = 10
+    g_pre = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_pre):
+        pre_outs = [layers[1].forward(xp, lp)[0] for _ in range(reps)]
+    torch.cuda.synchronize()
+    g_pre.replay()
+    torch.cuda.synchronize()
     start.record()
-    for _ in range(reps):
-        layers[1].forward(xp, lp)
+    g_pre.replay()
     stop.record()
     torch.cuda.synchronize()
     pre_us = start.elapsed_time(stop) * 1e3 / reps
+    pre_same = all(bool(torch.equal(o, eager)) for o in pre_outs)
     pre_flops = 2.0 * T * K * 3 * H * I
     tflops = pre_flops / (pre_us * 1e-6) / 1e12
     prefill = {"tokens": T, "us_per_layer": round(pre_us, 2), "tokens_per_s": round(T / (pre_us * 1e-6)),
                "tflops": round(tflops, 2), "mfma_util": round(tflops / MFMA_PEAK_F16_TFLOPS, 4),
-               "mfma_peak_tflops": MFMA_PEAK_F16_TFLOPS,
+               "mfma_peak_tflops": MFMA_PEAK_F16_TFLOPS, "graph_replay_equals_eager": pre_same, "calls_timed": reps,
                "path": "grouped MFMA GEMMs (fp16 integer weight codes, fp16 activations, f32 accumulate)"}
     log("prefill", prefill)
 
