@@ -12,6 +12,8 @@
 // applied to the partial sum of its K-steps. Activations are rounded to fp16 once, with a
 // power-of-two scale per row (exact) so that no row overflows: that rounding (2^-11 relative)
 // is the only approximation.
+#include <atomic>
+
 #include "cw_common.h"
 #include "cw_device.h"
 #include "cw_mfma.h"
@@ -1095,13 +1097,23 @@ int fill_zero(float *p, int64_t n, hipStream_t s) {
     return check_launch("k_fill_zero");
 }
 
-// persistent GEMM blocks: per_cu per CU, a multiple of 8 (the XCD count)
+constexpr int MAX_DEVICES = 64;
+
+static int current_device() {
+    int dev = 0;
+    return hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < MAX_DEVICES ? dev : 0;
+}
+
+// persistent GEMM blocks: per_cu per CU of the current device, a multiple of 8 (the XCD count)
 static int64_t resident_blocks(int per_cu = 1) {
-    static int cus = 0;
+    static std::atomic<int> cus_of[MAX_DEVICES];
+    const int dev = current_device();
+    int cus = cus_of[dev].load(std::memory_order_relaxed);
     if (!cus) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 8) n = 256;
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 8) n = 256;
         cus = n / 8 * 8;
+        cus_of[dev].store(cus, std::memory_order_relaxed);
     }
     return (int64_t)cus * per_cu;
 }
@@ -1118,11 +1130,12 @@ static int launch(const MfArgs &a, int tiles_max, int splits, hipStream_t s) {
     if (items >= ((int64_t)1 << 31)) return set_error(CW_ENOTSUP, "mfma: %lld work items", (long long)items);
     const int64_t res = resident_blocks(S::PER_CU);
     const int64_t blocks = items < res ? (items + 7) / 8 * 8 : res;
-    static bool lds_set = false;  // dynamic LDS above 64 KB is opted into once per kernel
-    if (!lds_set) {
+    static std::atomic<bool> lds_set[MAX_DEVICES];  // dynamic LDS above 64 KB, opted into once per kernel and device
+    const int dev = current_device();
+    if (!lds_set[dev].load(std::memory_order_acquire)) {
         if (hipFuncSetAttribute((const void *)k_gmm<MF, MODE>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::lds_bytes()) != hipSuccess)
             return set_error(CW_EHIP, "mfma: cannot reserve %zu bytes of LDS", S::lds_bytes());
-        lds_set = true;
+        lds_set[dev].store(true, std::memory_order_release);
     }
     MfArgs b = a;
     b.run_tiles = R;

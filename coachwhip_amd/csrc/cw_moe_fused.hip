@@ -10,6 +10,8 @@
 // Decode is bound by memory latency rather than bandwidth (a layer reads ~7 MB), so both kernels
 // issue all their weight loads before anything that waits: the IQ grid copy into LDS and the
 // barrier come after the loads are in flight.
+#include <mutex>
+
 #include "cw_common.h"
 #include "cw_device.h"
 #include "cw_moe_fused.h"
@@ -545,22 +547,39 @@ template <class FG, int LG, int XG, class FD, int LD, int XD, int PPW>
 static int decode_launch(const MoeArgs &a, hipStream_t s) {
     auto kern = a.E <= 256 ? k_moe_decode<FG, LG, XG, FD, LD, XD, 4, PPW> : k_moe_decode<FG, LG, XG, FD, LD, XD, 16, PPW>;
     const size_t lds = decode_hidden_lds(a);
-    // every block must be resident at once for the barrier: size the grid from the occupancy
-    // at this call's LDS size (remembered per router width for the last size asked)
-    static int per_cu[2] = {0, 0}, cus = 0;
-    static size_t per_cu_lds[2] = {0, 0};
+    // every block must be resident at once for the barrier: size the grid from the occupancy of
+    // this kernel at this call's LDS size on the current device (a few entries remembered, under
+    // a lock, so concurrent callers never size a grid from another call's entry)
+    struct Occ {
+        int dev = -1, which = -1;
+        size_t lds = 0;
+        int per_cu = 0, cus = 0;
+    };
+    static std::mutex mu;
+    static Occ cache[4];
+    static int next = 0;
     const int which = a.E <= 256 ? 0 : 1;
-    if (!per_cu[which] || per_cu_lds[which] != lds) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, 256, lds) != hipSuccess || n < 1)
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return set_error(CW_EHIP, "moe decode: no current device");
+    Occ o;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        for (const Occ &c : cache)
+            if (c.dev == dev && c.which == which && c.lds == lds) o = c;
+    }
+    if (!o.per_cu) {
+        o.dev = dev;
+        o.which = which;
+        o.lds = lds;
+        if (hipDeviceGetAttribute(&o.cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&o.per_cu, kern, 256, lds) != hipSuccess || o.per_cu < 1)
             return set_error(CW_EHIP, "moe decode: occupancy query failed");
-        per_cu[which] = n;
-        per_cu_lds[which] = lds;
+        std::lock_guard<std::mutex> lock(mu);
+        cache[next++ & 3] = o;
     }
     const int RPD = 64 / LD;
     const int want = (a.H + RPD - 1) / RPD;
-    int grid = per_cu[which] * cus;
+    int grid = o.per_cu * o.cus;
     if (grid > want) grid = want;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, s, a);
     return check_launch("k_moe_decode");
