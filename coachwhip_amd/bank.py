@@ -88,7 +88,10 @@ class Bank:
             self._h = None
 
     def __del__(self):
-        self.close()
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown: the library may already be gone
+            pass
 
     def ensure(self, needed):
         """Places the experts in ``needed`` (any int array, duplicates ignored) on the current

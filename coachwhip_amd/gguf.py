@@ -40,7 +40,10 @@ class GGUFFile:
         self.close()
 
     def __del__(self):
-        self.close()
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown: the library may already be gone
+            pass
 
     @property
     def version(self) -> int:

@@ -43,7 +43,10 @@ class Slots:
 
     def __del__(self):
         if getattr(self, "_h", None):
-            lib().cw_slots_free(self._h)
+            try:
+                lib().cw_slots_free(self._h)
+            except Exception:  # interpreter shutdown: the library may already be gone
+                pass
             self._h = None
 
     def assign(self, needed, ready=None):
