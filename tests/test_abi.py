@@ -63,3 +63,48 @@ def test_moe_descriptor_validation():
     assert L.cw_moe_workspace_size(ctypes.byref(d), 1) > 0
     d.slot_stride[2] = 100
     assert L.cw_moe_workspace_size(ctypes.byref(d), 1) == 0 and b"stride" in L.cw_last_error()
+
+
+def test_next_row_entry_points_reject_bad_arguments():
+    """The shrink, the router GEMV, the shared expert and the banks check their arguments before
+    any device work (no GPU is needed to see the status codes)."""
+    L = cw.lib()
+    F = cw.formats
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: every call below fails its checks first
+    # the shrink: Q3_K/Q4_K/Q5_K only; weights need a row length; no work, no device
+    assert L.cw_requant_q2k(F.Q8_0, fake, 4, None, 0, fake, None) == _lib.CW_ENOTSUP
+    assert b"Q3_K" in L.cw_last_error()
+    assert L.cw_requant_q2k(F.Q4_K, None, 4, None, 0, fake, None) == _lib.CW_EINVAL
+    assert L.cw_requant_q2k(F.Q4_K, fake, 4, ctypes.c_void_p(0x1000), 0, fake, None) == _lib.CW_EINVAL
+    assert L.cw_requant_q2k(F.Q4_K, fake, -1, None, 0, fake, None) == _lib.CW_EINVAL
+    assert L.cw_requant_q2k(F.Q4_K, None, 0, None, 0, None, None) == _lib.CW_OK
+    # router logits: aligned pointers, f32/f16 weights, hidden a multiple of 4
+    assert L.cw_router_logits(0, fake, 8, 64, None, ctypes.c_void_p(0x1004), 1, fake, None) == _lib.CW_EINVAL
+    assert L.cw_router_logits(0, None, 8, 64, None, fake, 1, fake, None) == _lib.CW_EINVAL
+    assert L.cw_router_logits(0, fake, 8, 64, None, fake, 0, fake, None) == _lib.CW_OK
+    # banks: a matrix that is neither readable nor shrinkable, or shrink of a readable non-K type
+    src = _lib.BankSource()
+    src.n_experts = 4
+    for m in range(3):
+        src.dtype[m] = F.Q8_0
+        src.rows[m], src.cols[m] = 32, 64
+        src.expert_bytes[m] = F.matrix_bytes(F.Q8_0, 32, 64)
+        src.host[m] = 0x1000
+    assert L.cw_bank_device_bytes(ctypes.byref(src), 2) > 0
+    src.shrink[0] = 1                                                     # Q8_0 cannot be shrunk
+    assert L.cw_bank_device_bytes(ctypes.byref(src), 2) == 0 and b"cannot be shrunk" in L.cw_last_error()
+    src.shrink[0] = 0
+    src.shape[1] = 0x2000                                                 # weights on a matrix kept as it is
+    assert L.cw_bank_device_bytes(ctypes.byref(src), 2) == 0
+    src.shape[1] = None
+    src.dtype[2], src.rows[2], src.cols[2] = F.Q5_K, 64, 256              # a shrink source must be shrunk
+    src.expert_bytes[2] = F.matrix_bytes(F.Q5_K, 64, 256)
+    assert L.cw_bank_device_bytes(ctypes.byref(src), 2) == 0
+    src.shrink[2] = 1                                                     # ... and then its slots are Q2_K
+    q2 = F.matrix_bytes(F.Q2_K, 64, 256)
+    al = lambda v: (v + 255) // 256 * 256
+    want = 2 * al(2 * src.expert_bytes[0]) + al(2 * q2) + 2 * al(8 * src.expert_bytes[2]) + al(4 * 4)
+    assert L.cw_bank_device_bytes(ctypes.byref(src), 2) == want
+    # a GGUF handle that does not exist
+    assert not L.cw_gguf_open(b"/nonexistent/model.gguf")
+    assert L.cw_gguf_n_tensors(None) == 0 and L.cw_gguf_find(None, b"x") == -1
