@@ -91,6 +91,7 @@ static dim3 flat_grid(int64_t n) {
 static int route(const float *logits, int T, int E, int K, int norm, uint32_t *ids, float *w, hipStream_t s) {
     if (T == 0) return CW_OK;
     if (E <= 256) hipLaunchKernelGGL(k_route<4>, dim3(T), dim3(64), 0, s, logits, E, K, norm, ids, w);
+    else if (E <= 512) hipLaunchKernelGGL(k_route<8>, dim3(T), dim3(64), 0, s, logits, E, K, norm, ids, w);
     else hipLaunchKernelGGL(k_route<16>, dim3(T), dim3(64), 0, s, logits, E, K, norm, ids, w);
     return check_launch("k_route");
 }

@@ -497,6 +497,7 @@ static int gateup_per(const MoeArgs &a, int T, hipStream_t s) {
     const int rows_per_block = 4 * RPW * ROWS;
     dim3 grid((a.I + rows_per_block - 1) / rows_per_block, T * a.K);
     if (a.E <= 256) hipLaunchKernelGGL((k_moe_gateup<Fmt, LPR, NX, 4, ROWS>), grid, dim3(256), 0, s, a);
+    else if (a.E <= 512) hipLaunchKernelGGL((k_moe_gateup<Fmt, LPR, NX, 8, ROWS>), grid, dim3(256), 0, s, a);
     else hipLaunchKernelGGL((k_moe_gateup<Fmt, LPR, NX, 16, ROWS>), grid, dim3(256), 0, s, a);
     return check_launch("k_moe_gateup");
 }
@@ -545,7 +546,10 @@ static constexpr size_t DECODE_MAX_HIDDEN_LDS = 64 * 1024;
 
 template <class FG, int LG, int XG, class FD, int LD, int XD, int PPW>
 static int decode_launch(const MoeArgs &a, hipStream_t s) {
-    auto kern = a.E <= 256 ? k_moe_decode<FG, LG, XG, FD, LD, XD, 4, PPW> : k_moe_decode<FG, LG, XG, FD, LD, XD, 16, PPW>;
+    // lanes hold 4, 8 or 16 router logits each (E up to 256, 512, 1024)
+    auto kern = a.E <= 256   ? k_moe_decode<FG, LG, XG, FD, LD, XD, 4, PPW>
+                : a.E <= 512 ? k_moe_decode<FG, LG, XG, FD, LD, XD, 8, PPW>
+                             : k_moe_decode<FG, LG, XG, FD, LD, XD, 16, PPW>;
     const size_t lds = decode_hidden_lds(a);
     // every block must be resident at once for the barrier: size the grid from the occupancy of
     // this kernel at this call's LDS size on the current device (a few entries remembered, under
@@ -558,7 +562,7 @@ static int decode_launch(const MoeArgs &a, hipStream_t s) {
     static std::mutex mu;
     static Occ cache[4];
     static int next = 0;
-    const int which = a.E <= 256 ? 0 : 1;
+    const int which = a.E <= 256 ? 0 : a.E <= 512 ? 1 : 2;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return set_error(CW_EHIP, "moe decode: no current device");
     Occ o;

@@ -118,40 +118,52 @@ __device__ __forceinline__ void route_keys(const float (&v)[PER], int E, RouteSt
     }
     r.m = wave_max(m);
 }
-// the K picks for PER = 4: each lane first sorts its four keys (by key, then by slot, so equal
-// keys keep index order); a round then needs only the wave maximum of the lanes' heads, the
-// lowest lane holding it, and a pop of that lane's list
-__device__ __forceinline__ void route_tournament(uint32_t (&key)[4], int K, uint32_t &mine_k, uint32_t &mine_e) {
+// the K picks for PER = 4 or 8: each lane first sorts its keys (by key, then by slot, so equal
+// keys keep index order; a bitonic network on 64-bit key|slot values); a round then needs only
+// the wave maximum of the lanes' heads, the lowest lane holding it, and a pop of that lane's list
+template <int PER>
+__device__ __forceinline__ void route_tournament(uint32_t (&key)[PER], int K, uint32_t &mine_k, uint32_t &mine_e) {
     const int lane = threadIdx.x & 63;
     // 64-bit sort keys: key above the slot's complement, so larger is better and ties go to the lower slot
-    uint64_t q[4];
+    uint64_t q[PER];
 #pragma unroll
-    for (int i = 0; i < 4; i++) q[i] = ((uint64_t)key[i] << 8) | (uint64_t)(255 - i);
-    auto cx = [&](int a, int b) {
-        const uint64_t x = q[a], y = q[b];
-        q[a] = x > y ? x : y;
-        q[b] = x > y ? y : x;
-    };
-    cx(0, 1); cx(2, 3); cx(0, 2); cx(1, 3); cx(1, 2);
-    uint32_t k[4], sl[4];
+    for (int i = 0; i < PER; i++) q[i] = ((uint64_t)key[i] << 8) | (uint64_t)(255 - i);
+    // ascending bitonic sort; the list is read from the top
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        k[i] = (uint32_t)(q[i] >> 8);
-        sl[i] = 255u - (uint32_t)(q[i] & 0xFF);
+    for (int k = 2; k <= PER; k <<= 1)
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1)
+#pragma unroll
+            for (int i = 0; i < PER; i++) {
+                const int l = i ^ j;
+                if (l > i) {
+                    const uint64_t x = q[i], y = q[l];
+                    const bool swap = (i & k) == 0 ? x > y : x < y;
+                    q[i] = swap ? y : x;
+                    q[l] = swap ? x : y;
+                }
+            }
+    uint32_t k[PER], sl[PER];
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        k[i] = (uint32_t)(q[PER - 1 - i] >> 8);
+        sl[i] = 255u - (uint32_t)(q[PER - 1 - i] & 0xFF);
     }
     for (int j = 0; j < K; j++) {
         const uint32_t best = wave_max_key(k[0]);
         const int at = __builtin_ctzll(__ballot(k[0] == best));  // the lowest lane holding it
         const uint32_t slot = __builtin_amdgcn_readlane((int)sl[0], at);
         if (lane == at) {
-            k[0] = k[1]; sl[0] = sl[1];
-            k[1] = k[2]; sl[1] = sl[2];
-            k[2] = k[3]; sl[2] = sl[3];
-            k[3] = 0u;
+#pragma unroll
+            for (int i = 0; i + 1 < PER; i++) {
+                k[i] = k[i + 1];
+                sl[i] = sl[i + 1];
+            }
+            k[PER - 1] = 0u;
         }
         if (lane == j) {
             mine_k = best;
-            mine_e = 4u * (uint32_t)at + slot;
+            mine_e = (uint32_t)PER * (uint32_t)at + slot;
         }
     }
 }
@@ -161,7 +173,7 @@ __device__ __forceinline__ void route_pick(const float (&v)[PER], RouteState<PER
                                            float *w) {
     const int lane = threadIdx.x & 63;
     uint32_t mine_k = 0, mine_e = 0xFFFFFFFFu;
-    if constexpr (PER == 4) route_tournament(r.key, K, mine_k, mine_e);
+    if constexpr (PER <= 8) route_tournament<PER>(r.key, K, mine_k, mine_e);
     else for (int j = 0; j < K; j++) {
         uint32_t best = r.key[0];
 #pragma unroll

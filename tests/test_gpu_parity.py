@@ -194,6 +194,16 @@ def test_route_ties_across_signed_zero_and_slots():
     lg[:, ::57] = 1.0
     ids, _ = ops.route(dev(lg), 8, False)
     assert host(ids).tolist() == [list(range(0, 57 * 8, 57))] * 2
+    # eight logits per lane (E in 257..512, last lanes partly empty): equal maxima inside one
+    # lane's sorted list (9, 13, 15) and across lanes (300), and -0 / +0 in one lane (16, 17)
+    lg = np.full((1, 400), -2.0, np.float32)
+    lg[0, [15, 13, 9, 300, 301]] = 3.0
+    lg[0, [17, 16]] = [-0.0, 0.0]
+    ids, w = ops.route(dev(lg), 7, True)
+    wids, ww = O.route(lg, 7, True)
+    assert wids.tolist() == [[9, 13, 15, 300, 301, 16, 17]]
+    assert np.array_equal(host(ids).view(np.uint32), wids)
+    assert np.max(np.abs(host(w) - ww)) < 1e-6
 
 
 @pytest.mark.parametrize("E,K,norm", [(256, 8, True), (128, 4, True), (512, 10, True), (1024, 32, False), (20, 20, True)])
