@@ -270,17 +270,24 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoeArgs a) {
     constexpr int RPG = 64 / LG, RPD = 64 / LD;
     __shared__ float part[32 * RPD];
     __shared__ float pick_w[32];
-    __shared__ uint32_t pick_e[32];
+    __shared__ uint32_t pick_e[32], pick_slot[32];
     extern __shared__ __align__(16) float hs[];  // hidden rows, sub-blocks of 32 floats 36 apart
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int K = a.K;
     // the logits alone first: every wave of the grid starts at once, and the table and x loads
     // of 2048 waves queued in front of them in L2 (~2.5 us to the first logit). Those loads are
-    // issued once the logits are in and complete during the top-k.
+    // issued once the logits are in and complete during the top-k. With 8 logits per lane or
+    // more, wave 0 alone routes (the other waves would only repeat it on the same SIMDs: 0.5 us
+    // of a 512-expert layer) and hands the picks to the block through LDS behind a barrier; with
+    // fewer, every wave routes for itself, which is faster than waiting at the barrier.
+    constexpr bool ONE_ROUTER = PER >= 8;
+    const bool routes = !ONE_ROUTER || wave == 0;
     float lv[PER];
-    route_load<PER>(a.logits, a.E, lv);
     RouteState<PER> rst;
-    route_keys<PER>(lv, a.E, rst);
+    if (routes) {
+        route_load<PER>(a.logits, a.E, lv);
+        route_keys<PER>(lv, a.E, rst);
+    }
     TableRegs<FG> tg;
     TableRegs<FD> td;
     tg.load(threadIdx.x);
@@ -289,25 +296,32 @@ __global__ __launch_bounds__(256) void k_moe_decode(const MoeArgs a) {
     float xr[XG][32];
     load_xs<XG>(xr, a.x, subg, LG, nsbg);
 
-    uint32_t rid;
-    float rw;
-    route_pick<PER>(lv, rst, a.E, K, a.norm, &rid, &rw);
-    uint32_t my_slot = 0xFFFFFFFFu;  // lane j < K: slot of pick j
-    bool absent = false;
-    if (lane < K) {
-        my_slot = a.table ? a.table[rid] : rid;
-        absent = my_slot == CW_NO_SLOT;
-        if (absent) my_slot = 0;
-        if (my_slot >= (uint32_t)a.n_slots) my_slot = 0xFFFFFFFFu;
-    }
-    if (wave == 0 && lane < K) {
-        pick_w[lane] = rw;
-        pick_e[lane] = rid;
-        if (blockIdx.x == 0) {
-            a.ids[lane] = rid;
-            a.w[lane] = rw;
-            if (absent && a.missing) atomicAdd(a.missing, 1u);
+    uint32_t rid = 0xFFFFFFFFu;      // lane j < K: pick j's expert
+    uint32_t my_slot = 0xFFFFFFFFu;  // ... and its slot
+    if (routes) {
+        float rw;
+        route_pick<PER>(lv, rst, a.E, K, a.norm, &rid, &rw);
+        if (lane < K) {
+            my_slot = a.table ? a.table[rid] : rid;
+            const bool absent = my_slot == CW_NO_SLOT;
+            if (absent) my_slot = 0;
+            if (my_slot >= (uint32_t)a.n_slots) my_slot = 0xFFFFFFFFu;
+            if (wave == 0) {
+                pick_w[lane] = rw;
+                pick_e[lane] = rid;
+                pick_slot[lane] = my_slot;
+                if (blockIdx.x == 0) {
+                    a.ids[lane] = rid;
+                    a.w[lane] = rw;
+                    if (absent && a.missing) atomicAdd(a.missing, 1u);
+                }
+            }
         }
+    }
+    if (ONE_ROUTER) {
+        __syncthreads();
+        rid = lane < K ? pick_e[lane] : 0xFFFFFFFFu;
+        my_slot = lane < K ? pick_slot[lane] : 0xFFFFFFFFu;
     }
 
     // gate / up items (pick j, 2*RPG rows) spread over every wave of the grid; the first
