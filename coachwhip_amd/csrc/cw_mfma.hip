@@ -402,10 +402,53 @@ struct MQ4_K {
         return fma4(x, splat_f16f((float)sc), splat_f16f(-1024.0f * (float)sc));
     }
     // codes -m for all 8 weights (the minimum term)
-    static __device__ __forceinline__ uint4 min_frag(const Stage &stg, int kk, bool zero) {
+    static __device__ __forceinline__ uint4 min_frag(const Stage &stg, int kk, int, bool zero) {
         uint32_t sc, m;
         sc_m(stg, kk, sc, m);
         const uint32_t v = zero ? 0u : splat_f16f(-(float)m);
+        return make_uint4(v, v, v, v);
+    }
+};
+
+// Q2_K (what the shrink writes): y = d*(sc&15)*q - dmin*(sc>>4) per 16 weights (k_quants.rs:1152-1190).
+// K-step kk is sub-block kk of 32 weights: bits 2(kk&3) of qs[32(kk>>2) ..), so lane group grp
+// reads the 8 bytes qs[32(kk>>2) + 8grp ..) and its 8 weights share scale byte 2kk + (grp>>1).
+// Codes sc*q (<= 45) with d as the running scale; the minimum term as for Q4_K, codes -m (<= 15).
+struct MQ2_K {
+    static constexpr int TS = 84, SBK = 256, LDS = 16;
+    static constexpr int KST = 8, SCALE = 0, ORG = 16;
+    static constexpr bool HAS_MIN = true;
+    static __device__ void fill(uint8_t *, int, int) {}
+    // the 16 scale bytes (0..15) of the super-block, read once per stage
+    struct Stage {
+        uint32_t b[4];
+        __device__ __forceinline__ void load(const WinRef &w, int) {
+            const uint2 lo = w.u64(-16), hi = w.u64(-8);
+            b[0] = lo.x;
+            b[1] = lo.y;
+            b[2] = hi.x;
+            b[3] = hi.y;
+        }
+        // scale byte 2kk + (grp >> 1)
+        __device__ __forceinline__ uint32_t byte(int kk, int grp) const {
+            return (b[kk >> 1] >> (16 * (kk & 1) + 8 * (grp >> 1))) & 0xFF;
+        }
+    };
+    static __device__ __forceinline__ float scale(const uint8_t *win) { return h2f(lds_u16(win + 80)); }
+    static __device__ __forceinline__ float dmin(const uint8_t *win) { return h2f(lds_u16(win + 82)); }
+    struct Raw { uint2 q; };
+    struct Look {};
+    static __device__ __forceinline__ Raw raw(const WinRef &w, const Stage &, int kk, int grp) { return Raw{w.u64(32 * (kk >> 2) + 8 * grp)}; }
+    static __device__ __forceinline__ Look look(const Raw &, const Stage &, int, int, const uint8_t *, bool) { return Look{}; }
+    static __device__ __forceinline__ uint4 make(const Raw &r, const Look &, const Stage &stg, int kk, int grp, bool zero) {
+        const uint32_t sc = zero ? 0u : stg.byte(kk, grp) & 0xF;
+        const int sh = 2 * (kk & 3);
+        const uint4 x = bytes_plus_1024((r.q.x >> sh) & 0x03030303u, (r.q.y >> sh) & 0x03030303u);
+        return fma4(x, splat_f16f((float)sc), splat_f16f(-1024.0f * (float)sc));
+    }
+    // codes -m for the lane's 8 weights (the minimum term)
+    static __device__ __forceinline__ uint4 min_frag(const Stage &stg, int kk, int grp, bool zero) {
+        const uint32_t v = zero ? 0u : splat_f16f(-(float)(stg.byte(kk, grp) >> 4));
         return make_uint4(v, v, v, v);
     }
 };
@@ -417,7 +460,7 @@ __device__ __forceinline__ uint32_t pow2_f16x2(int x) {
 }
 
 // A stage is KST K-steps (8: 256 weights of k; 4 for Q8_0). The window of a row for a stage
-// holds the stage's bytes (an IQ or Q4_K super-block, or KST MXFP4 / Q8_0 blocks) from the
+// holds the stage's bytes (an IQ, Q2_K or Q4_K super-block, or KST MXFP4 / Q8_0 blocks) from the
 // 16-byte boundary at or below their start, in PCS pieces of 16 bytes.
 template <class MF>
 struct Win {
@@ -557,10 +600,10 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
 
         const int n_ks = a.k / 32, n_st = (n_ks + KST - 1) / KST;
         f32x4 acc[NM][NB][MF_MB];
-        f32x4 accm[NM][NA][MF_MB];  // minimum term (Q4_K)
+        f32x4 accm[NM][NA][MF_MB];  // minimum term (Q4_K, Q2_K)
         float rs[NM][NB];     // running scale (f16 scales) ...
         int rb[NM][NB];       // ... or running base exponent (MXFP4)
-        float rsm[NM][NA];    // running dmin (Q4_K)
+        float rsm[NM][NA];    // running dmin (Q4_K, Q2_K)
 #pragma unroll
         for (int m = 0; m < NM; m++)
 #pragma unroll
@@ -782,7 +825,7 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
                     for (int m = 0; m < NM; m++)
 #pragma unroll
                         for (int q = 0; q < NA; q++)
-                            if constexpr (MIN) bm[m][q] = as_f16x8(MF::min_frag(stg[m][q], kk, zerom[m][q]));
+                            if constexpr (MIN) bm[m][q] = as_f16x8(MF::min_frag(stg[m][q], kk, grp, zerom[m][q]));
 #pragma unroll
                     for (int m = 0; m < NM; m++)
 #pragma unroll
@@ -1058,7 +1101,8 @@ __global__ void k_fill_zero(float *p, int64_t n) {
 // ------------------------------------------------------------------------------ launchers
 
 bool mfma_supported(int dtype) {
-    return dtype == CW_IQ2_XXS || dtype == CW_IQ2_S || dtype == CW_IQ3_S || dtype == CW_MXFP4 || dtype == CW_Q4_K || dtype == CW_Q8_0;
+    return dtype == CW_IQ2_XXS || dtype == CW_IQ2_S || dtype == CW_IQ3_S || dtype == CW_MXFP4 || dtype == CW_Q4_K || dtype == CW_Q8_0 ||
+           dtype == CW_Q2_K;
 }
 
 int max_tiles(int TK, int n_slots) { return (TK + MF_MT - 1) / MF_MT + (n_slots < TK ? n_slots : TK); }
@@ -1153,6 +1197,7 @@ static int by_fmt(int dtype, const MfArgs &a, int tiles_max, int splits, hipStre
     case CW_MXFP4: return launch<MMXFP4, MODE>(a, tiles_max, splits, s);
     case CW_Q4_K: return launch<MQ4_K, MODE>(a, tiles_max, splits, s);
     case CW_Q8_0: return launch<MQ8_0, MODE>(a, tiles_max, splits, s);
+    case CW_Q2_K: return launch<MQ2_K, MODE>(a, tiles_max, splits, s);
     default: return set_error(CW_ENOTSUP, "mfma: dtype %d has no MFMA path", dtype);
     }
 }
@@ -1189,6 +1234,7 @@ static void dense_shape(int dtype, int &rpb, int &kst, int &per_cu) {
     case CW_IQ3_S: return shape_of<MIQ3_S>(rpb, kst, per_cu);
     case CW_MXFP4: return shape_of<MMXFP4>(rpb, kst, per_cu);
     case CW_Q8_0: return shape_of<MQ8_0>(rpb, kst, per_cu);
+    case CW_Q2_K: return shape_of<MQ2_K>(rpb, kst, per_cu);
     default: return shape_of<MQ4_K>(rpb, kst, per_cu);
     }
 }

@@ -277,10 +277,11 @@ def synth_blocks(dtype, n, rng):
 
 
 @pytest.mark.gpu
-def test_layer_through_a_shrinking_bank_matches_the_oracle():
+def test_layer_through_a_shrinking_bank_matches_the_oracle(monkeypatch):
     """Config-5-shaped experts stored as Q3_K (gate, up) and Q5_K (down), held as Q2_K: each
     step's picks are ensured (misses shrunk on arrival) and the layer runs through the bank; it
-    matches the oracle's layer over the oracle's shrink of every expert."""
+    matches the oracle's layer over the oracle's shrink of every expert. Then a 40-token batch
+    over 20 resident experts takes the grouped MFMA path over the same Q2_K slots."""
     import torch
     from coachwhip_amd import ops, synth
     from coachwhip_amd.bank import Bank
@@ -308,4 +309,22 @@ def test_layer_through_a_shrinking_bank_matches_the_oracle():
         err = O.rel_l2(out.cpu().numpy(), want)
         print("  step", step, "rel_l2", err, flush=True)
         assert err <= 2e-5
+    assert int(missing.cpu()[0]) == 0
+
+    # prefill: the grouped path rounds activations to fp16 once, so the 1e-3 gate
+    monkeypatch.setenv("CWMOE_PREFILL_MIN_TOKENS", "1")
+    live = rng.choice(E, 20, replace=False)
+    assert bank.ensure(live) is not None
+    mask = np.full(E, -1e30, np.float32)
+    mask[live] = 0.0
+    T = 40
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    logits = rng.standard_normal((T, E)).astype(np.float32) + mask
+    assert not synth.near_ties_within_top_k(logits, K)
+    out, got_ids, _ = moe.forward(ops.to_device(x), ops.to_device(logits), missing)
+    want, wids, _, _ = O.moe_layer(layer, x, logits)
+    assert np.array_equal(got_ids.cpu().numpy().view(np.uint32), wids)
+    err = O.rel_l2(out.cpu().numpy(), want)
+    print("  prefill rel_l2", err, flush=True)
+    assert err <= 1e-3
     assert int(missing.cpu()[0]) == 0

@@ -18,7 +18,7 @@ pytestmark = pytest.mark.gpu
 
 REL_L2_GATE = 1e-3      # north-star tolerance for matmul / MoE outputs
 REL_L2_F32 = 2e-5       # what an f32-activation path must reach
-MFMA_TYPES = (F.IQ2_XXS, F.IQ2_S, F.IQ3_S, F.MXFP4, F.Q4_K, F.Q8_0)  # formats of the grouped / dense GEMM
+MFMA_TYPES = (F.IQ2_XXS, F.IQ2_S, F.IQ3_S, F.MXFP4, F.Q4_K, F.Q8_0, F.Q2_K)  # formats of the grouped / dense GEMM
 
 
 def dev(a):
@@ -87,6 +87,7 @@ MM_CASES = [
     (F.IQ3_S, 300, 1024, 65),
     (F.Q2_K, 512, 2048, 1),
     (F.Q2_K, 2048, 512, 9),
+    (F.Q2_K, 200, 768, 70),       # three super-blocks per row, N-blocks past the last row
 ]
 
 
@@ -112,12 +113,12 @@ def test_qmatmul_edge_scales(path, monkeypatch):
     # zero and subnormal f16 scales (and a zero dmin) take the kernels' zero-scale branches
     monkeypatch.setenv("CWMOE_MM_MIN_ROWS", MM_PATHS[path])
     rng = np.random.default_rng(77)
-    for dtype, n, k in ((F.Q4_K, 64, 1024), (F.Q8_0, 64, 512)):
+    for dtype, n, k, d_at in ((F.Q4_K, 64, 1024, 0), (F.Q8_0, 64, 512, 0), (F.Q2_K, 64, 1024, 80)):
         raw = synth.random_blocks(dtype, n * k, rng).reshape(-1, F.type_size(dtype)).copy()
-        raw[::3, 0:2] = 0                    # d = 0
-        raw[1::5, 0:2] = [0x01, 0x00]        # smallest subnormal d
-        if dtype == F.Q4_K:
-            raw[2::7, 2:4] = 0               # dmin = 0
+        raw[::3, d_at:d_at + 2] = 0                  # d = 0
+        raw[1::5, d_at:d_at + 2] = [0x01, 0x00]      # smallest subnormal d
+        if dtype != F.Q8_0:
+            raw[2::7, d_at + 2:d_at + 4] = 0         # dmin = 0
         raw = raw.reshape(-1)
         x = rng.standard_normal((48, k)).astype(np.float32)
         y = host(ops.QMatMul(ops.QTensor.from_blocks(raw, dtype, (n, k))).forward(dev(x)))
@@ -345,6 +346,7 @@ MOE_CASES = [
     ("iq2_s_grouped_padded", 16, 4, 512, 200, (F.IQ2_S, F.IQ2_S, F.IQ2_XXS), 1, 256, 20),
     ("c5_shrunk_q2_k", 64, 10, 2048, 512, (F.Q2_K, F.Q2_K, F.Q2_K), 0, 0, 1),
     ("q2_k_gate_up_tokens", 32, 4, 1024, 512, (F.Q2_K, F.Q2_K, F.Q4_K), 0, 0, 24),
+    ("q2_k_grouped", 32, 4, 1024, 512, (F.Q2_K, F.Q2_K, F.Q2_K), 0, 0, 56),
 ]
 
 # the grouped MFMA path rounds activations to fp16 once (2^-11 relative): its outputs are held
