@@ -13,6 +13,7 @@
 // power-of-two scale per row (exact) so that no row overflows: that rounding (2^-11 relative)
 // is the only approximation.
 #include <atomic>
+#include <type_traits>
 
 #include "cw_common.h"
 #include "cw_device.h"
@@ -88,26 +89,7 @@ constexpr Tab<256> make_iq3s_f16() {  // two 4-value entries per U4: entry 2i in
     }
     return t;
 }
-// IQ2_XXS sign-and-scale multipliers: entry (s << 7) | s7 holds the 8 fp16 values +-8(2s+1),
-// negative where bit j of s7 | parity(s7) << 7 is set (ksigns_iq2xs: the 8th sign is the even
-// parity of the other 7); entry 2048 is all zeros (a super-block whose scale is 0).
-constexpr Tab<2049> make_iq2xxs_sm() {
-    Tab<2049> t{};
-    for (int s = 0; s < 16; s++)
-        for (uint32_t s7 = 0; s7 < 128; s7++) {
-            uint32_t p = s7 ^ (s7 >> 4);
-            p ^= p >> 2;
-            p ^= p >> 1;
-            const uint32_t b = s7 | ((p & 1u) << 7), m = f16_int(8 * (2 * s + 1));
-            uint32_t w[4] = {};
-            for (int i = 0; i < 4; i++)
-                w[i] = (m | (((b >> (2 * i)) & 1u) << 15)) | ((m | (((b >> (2 * i + 1)) & 1u) << 15)) << 16);
-            t.v[(s << 7) | s7] = U4{w[0], w[1], w[2], w[3]};
-        }
-    return t;
-}
 static __constant__ Tab<256> c_iq2xxs_f16 = make_iq2xxs_f16();
-static __constant__ Tab<2049> c_iq2xxs_sm = make_iq2xxs_sm();
 static __constant__ Tab<1024> c_iq2s_f16 = make_iq2s_f16();
 static __constant__ Tab<256> c_iq3s_f16 = make_iq3s_f16();
 
@@ -166,29 +148,28 @@ struct WinRef {
 // (read by scale()), 1 = MXFP4's power-of-two block scales, 2 = one f16 scale per 32-weight block
 // (read by step_scale()); HAS_MIN = an f16 dmin per super-block and a 6-bit m per sub-block.
 struct MIQ2_XXS {
-    static constexpr int TS = 66, SBK = 256, LDS = 256 * 16 + 2049 * 16;
+    static constexpr int TS = 66, SBK = 256, LDS = 256 * 16;
     static constexpr int KST = 8, SCALE = 0, ORG = 2;
     static constexpr bool HAS_MIN = false;
-    static __device__ void fill(uint8_t *lds, int tid, int nt) {
-        copy_tab(lds, c_iq2xxs_f16, tid, nt);
-        copy_tab(lds + 256 * 16, c_iq2xxs_sm, tid, nt);
-    }
+    static __device__ void fill(uint8_t *lds, int tid, int nt) { copy_tab(lds, c_iq2xxs_f16, tid, nt); }
     struct Stage {
         __device__ __forceinline__ void load(const WinRef &, int) {}
     };
-    // A fragment is the grid entry times a sign-and-scale entry (two lookups and 4 packed
-    // multiplies). The multiplier is 8*(2s+1), exact in fp16 with the grid values (at most
+    // A fragment is the grid entry (one lookup) with the signs applied arithmetically: the 7 sign
+    // bits of the lane's 8 weights plus their even parity as the 8th (ksigns_iq2xs), and the
+    // multiplier 8*(2s+1) as one packed multiply, exact in fp16 with the grid values (at most
     // 43*248 = 1333*8); scale() takes the 8 back out. zero: the super-block scale is 0, so the
-    // codes must not contribute (the all-zero entry).
+    // codes must not contribute (multiplier 0).
     struct Raw { uint2 q; };
-    struct Look { uint4 g, m; };
+    struct Look { uint4 g; };
     static __device__ __forceinline__ Raw raw(const WinRef &w, const Stage &, int kk, int) { return Raw{w.u64(8 * kk)}; }
-    static __device__ __forceinline__ Look look(const Raw &r, const Stage &, int, int grp, const uint8_t *lds, bool zero) {
-        const uint32_t sm = zero ? 2048u : ((r.q.y >> 28) << 7) | ((r.q.y >> (7 * grp)) & 127);
-        return Look{((const uint4 *)lds)[(r.q.x >> (8 * grp)) & 0xFF], ((const uint4 *)(lds + 256 * 16))[sm]};
+    static __device__ __forceinline__ Look look(const Raw &r, const Stage &, int, int grp, const uint8_t *lds, bool) {
+        return Look{((const uint4 *)lds)[(r.q.x >> (8 * grp)) & 0xFF]};
     }
-    static __device__ __forceinline__ uint4 make(const Raw &, const Look &l, const Stage &, int, int, bool) {
-        return make_uint4(pk_mul_u(l.g.x, l.m.x), pk_mul_u(l.g.y, l.m.y), pk_mul_u(l.g.z, l.m.z), pk_mul_u(l.g.w, l.m.w));
+    static __device__ __forceinline__ uint4 make(const Raw &r, const Look &l, const Stage &, int, int grp, bool zero) {
+        const uint32_t s7 = (r.q.y >> (7 * grp)) & 127;
+        const uint32_t b = s7 | ((__builtin_popcount(s7) & 1u) << 7);
+        return scale4(apply_signs(l.g, b), splat_mult(zero ? 0u : ((r.q.y >> 28) << 4) | 8));
     }
     static __device__ __forceinline__ float scale(const uint8_t *win) { return h2f(lds_u16(win)) * (0.125f / 8); }
 };
@@ -476,9 +457,28 @@ template <int V> struct Ic { static constexpr int value = V; };
 __device__ __forceinline__ f16x8 as_f16x8(uint4 v) { return __builtin_bit_cast(f16x8, v); }
 
 // 16 bytes from global memory to LDS without passing through registers: lane l of the wave
-// writes lds_base + 16*l (lds_base is the same for the whole wave)
+// writes lds_base + 16*l (lds_base is the same for the whole wave).
+// ASM: issued as inline asm instead of through __builtin_amdgcn_global_load_lds. The compiler
+// counts the builtin as an LDS store that any later LDS read at a dynamic address (a table
+// lookup) may alias, and puts an s_waitcnt vmcnt(0) before that read, so every prefetch is
+// waited for right after it is issued. The kernel orders these loads itself: an explicit
+// s_waitcnt on the issuing wave, then a barrier, before any wave reads the bytes, and a barrier
+// between the last read of a buffer and the loads that overwrite it. Loads return in order, so
+// the compiler's own vmcnt waits stay correct with these in flight (they only wait longer: a
+// register spill's reload then waits for the prefetches before it, which is why the formats
+// that spill keep the builtin).
+template <bool ASM>
 __device__ __forceinline__ void dma16(const void *g, uint8_t *lds_base) {
-    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)lds_base, 16, 0, 0);
+    if constexpr (ASM) {
+        const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)lds_base);
+        // M0 (the LDS base of the load) is reserved to the compiler, which may keep a value in it:
+        // saved and restored around the load
+        uint32_t keep;
+        asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                     : "=&s"(keep) : "v"(g), "s"(m) : "memory");
+    } else {
+        __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)lds_base, 16, 0, 0);
+    }
 }
 
 // Tile shape of the grouped GEMM: a block of NW = 16 waves (one block per CU, four waves per
@@ -493,6 +493,13 @@ struct GmShape {
     static constexpr int LDS_MAX = 160 * 1024;
     static constexpr int NM = MODE == 0 ? 2 : 1;
     static constexpr int NB = 1;
+    // PF: K-step table lookups and activation fragments read one step ahead (two register sets).
+    // ADMA: the stage loads issued as inline asm (dma16). Both for the formats where they measured
+    // faster: not for the formats with a minimum term (Q4_K, Q2_K), whose second accumulator set
+    // leaves no registers for the second fragment set and which spill, nor for MXFP4 (equal or
+    // slower with either).
+    static constexpr bool FAST = !MF::HAS_MIN && !std::is_same<MF, MMXFP4>::value;
+    static constexpr bool PF = FAST, ADMA = FAST;
     static constexpr int KA = 4, HPS = MF::KST / KA;                // K-steps per activation buffer, buffers per stage
     static constexpr int A_HALF = KA * MF_MB * 64 * 16, A_BYTES = 2 * A_HALF;  // two activation buffers
     static constexpr int META_BYTES = MF_MT * 8;                     // scale and pick of each row of the tile
@@ -649,7 +656,7 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
                 const uint32_t o = row_off(r, m) + (uint32_t)(W::SEG * st_w);  // the row's stage bytes
                 const uint32_t mis = ((uint32_t)(uintptr_t)mb + o) & 15;      // ... from a 16-byte boundary
                 const uint32_t pc = min((uint32_t)p, (mis + seg_w - 1) >> 4);
-                dma16(mb + (o - mis + 16 * pc), wbuf + (i - (tido & 63)) * 16);
+                dma16<S::ADMA>(mb + (o - mis + 16 * pc), wbuf + (i - (tido & 63)) * 16);
             }
         };
         // Activations of half-stage h (K-steps h*KA .. h*KA+KA-1, clamped to the row: a clamped load
@@ -658,7 +665,7 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
             if (stager) {
 #pragma unroll
                 for (int kk = 0; kk < S::KA; kk++)
-                    dma16(asrc + min(h * S::KA + kk, n_ks - 1) * 32, As + (h & 1) * S::A_HALF + ((kk * MF_MB + wave) * 64) * 16);
+                    dma16<S::ADMA>(asrc + min(h * S::KA + kk, n_ks - 1) * 32, As + (h & 1) * S::A_HALF + ((kk * MF_MB + wave) * 64) * 16);
             }
         };
         // vmcnt(NTW) alone: every load but this wave's last NTW (the next stage's windows) is done
@@ -764,15 +771,18 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
             }
 
             // The K-steps, with the tile's count of 16-pick MFMA blocks as a constant, software
-            // pipelined: the window bytes of a step are requested two steps ahead (step kk asks for
-            // those of kk+2 once its own are decoded), so only the table lookups and activation loads
-            // of a step wait on LDS within it. A scheduling fence closes each step (without it the
-            // compiler interleaves all eight steps and runs out of registers).
+            // pipelined so that no step waits on an LDS read it issued itself: the window bytes of a
+            // step are requested two steps ahead, its table lookups and activation fragments one step
+            // ahead (step kk issues those of kk+1 once its own fragment is decoded, and they arrive
+            // while its MFMAs run). The first step of the second half-stage reads its activations
+            // after the barrier that publishes them. A scheduling fence closes each step (without
+            // it the compiler interleaves all eight steps and runs out of registers).
             auto ksteps = [&](auto mbs_c) __attribute__((always_inline)) {
                 constexpr int MBS = decltype(mbs_c)::value;
                 const int nke = MF::SBK == 32 ? nk : KST;  // super-block formats: every stage is whole
                 typename MF::Raw rw[2][NM][NB];
-                typename MF::Look lk[NM][NB];
+                typename MF::Look lk[2][NM][NB];
+                f16x8 av[2][MBS];
                 auto issue_raw = [&](int kk) __attribute__((always_inline)) {
 #pragma unroll
                     for (int m = 0; m < NM; m++)
@@ -783,10 +793,19 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
 #pragma unroll
                     for (int m = 0; m < NM; m++)
 #pragma unroll
-                        for (int q = 0; q < NB; q++) lk[m][q] = MF::look(rw[kk & 1][m][q], stg[m][q], kk, grp, tab, zero[m][q]);
+                        for (int q = 0; q < NB; q++) lk[kk & 1][m][q] = MF::look(rw[kk & 1][m][q], stg[m][q], kk, grp, tab, zero[m][q]);
+                };
+                auto issue_av = [&](int kk) __attribute__((always_inline)) {
+                    const uint8_t *Ak = As + ((S::HPS == 2 ? kk / S::KA : st) & 1) * S::A_HALF + (kk % S::KA) * MF_MB * 64 * 16;
+#pragma unroll
+                    for (int mb = 0; mb < MBS; mb++) av[kk & 1][mb] = *(const f16x8 *)(Ak + (mb * 64 + lane) * 16);
                 };
                 issue_raw(0);
                 if (1 < nke) issue_raw(1);
+                if constexpr (S::PF) {
+                    issue_look(0);
+                    issue_av(0);
+                }
 #pragma unroll
                 for (int kk = 0; kk < KST; kk++) {
                     if (kk >= nke) break;
@@ -798,12 +817,12 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
                             __builtin_amdgcn_s_waitcnt(0);
                         __syncthreads();
                         if (st + 1 < st_hi) issue_a(2 * (st + 1));
+                        if constexpr (S::PF) issue_av(kk);
                     }
-                    issue_look(kk);
-                    const uint8_t *Ak = As + ((S::HPS == 2 ? kk / S::KA : st) & 1) * S::A_HALF + (kk % S::KA) * MF_MB * 64 * 16;
-                    f16x8 av[MBS];
-#pragma unroll
-                    for (int mb = 0; mb < MBS; mb++) av[mb] = *(const f16x8 *)(Ak + (mb * 64 + lane) * 16);
+                    if constexpr (!S::PF) {
+                        issue_look(kk);
+                        issue_av(kk);
+                    }
                     if constexpr (STEP) {
                         // a scale per K-step: move each accumulator onto it
 #pragma unroll
@@ -831,19 +850,23 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
 #pragma unroll
                         for (int q = 0; q < NB; q++) {
                             if constexpr (POW2)
-                                bf[m][q] = as_f16x8(MF::make_mx(lk[m][q], pow2_f16x2((int)rw[kk & 1][m][q].e - rb[m][q])));
+                                bf[m][q] = as_f16x8(MF::make_mx(lk[kk & 1][m][q], pow2_f16x2((int)rw[kk & 1][m][q].e - rb[m][q])));
                             else
-                                bf[m][q] = as_f16x8(MF::make(rw[kk & 1][m][q], lk[m][q], stg[m][q], kk, grp, zero[m][q]));
+                                bf[m][q] = as_f16x8(MF::make(rw[kk & 1][m][q], lk[kk & 1][m][q], stg[m][q], kk, grp, zero[m][q]));
                         }
                     if (kk + 2 < KST && kk + 2 < nke) issue_raw(kk + 2);  // into the buffer step kk has just used
+                    if (S::PF && kk + 1 < KST && kk + 1 < nke) {
+                        issue_look(kk + 1);
+                        if (!(S::HPS == 2 && kk + 1 == S::KA)) issue_av(kk + 1);
+                    }
 #pragma unroll
                     for (int mb = 0; mb < MBS; mb++)
 #pragma unroll
                         for (int m = 0; m < NM; m++)
 #pragma unroll
                             for (int q = 0; q < NB; q++) {
-                                acc[m][q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[mb], bf[m][q], acc[m][q][mb], 0, 0, 0);
-                                if constexpr (MIN) accm[m][q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[mb], bm[m][q], accm[m][q][mb], 0, 0, 0);
+                                acc[m][q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[kk & 1][mb], bf[m][q], acc[m][q][mb], 0, 0, 0);
+                                if constexpr (MIN) accm[m][q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[kk & 1][mb], bm[m][q], accm[m][q][mb], 0, 0, 0);
                             }
                     __builtin_amdgcn_sched_barrier(0);
                 }
