@@ -721,6 +721,7 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
                 }
 
             bool zero[NM][NB], zerom[NM][NA];
+            float ratio[NM][NB], ratiom[NM][NA];  // running-scale moves of this stage (scale per super-block)
             if constexpr (STEP) {
 #pragma unroll
                 for (int m = 0; m < NM; m++)
@@ -749,23 +750,17 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
                 for (int m = 0; m < NM; m++)
 #pragma unroll
                     for (int q = 0; q < NB; q++) {
+                        // the accumulators move onto the new scale at the start of the K-steps (only
+                        // the tile's pick blocks); a zero scale keeps the old one (its codes do not count)
                         const float d = MF::scale(win[m][q]);
                         zero[m][q] = d == 0.f;
-                        if (d != 0.f) {
-                            const float ratio = __fdividef(rs[m][q], d);
-#pragma unroll
-                            for (int mb = 0; mb < MF_MB; mb++) acc[m][q][mb] *= ratio;
-                            rs[m][q] = d;
-                        }
+                        ratio[m][q] = d != 0.f ? rs[m][q] * __builtin_amdgcn_rcpf(d) : 1.f;
+                        rs[m][q] = d != 0.f ? d : rs[m][q];
                         if constexpr (MIN) {
                             const float dm = MF::dmin(win[m][q]);
                             zerom[m][q] = dm == 0.f;
-                            if (dm != 0.f) {
-                                const float ratio = __fdividef(rsm[m][q], dm);
-#pragma unroll
-                                for (int mb = 0; mb < MF_MB; mb++) accm[m][q][mb] *= ratio;
-                                rsm[m][q] = dm;
-                            }
+                            ratiom[m][q] = dm != 0.f ? rsm[m][q] * __builtin_amdgcn_rcpf(dm) : 1.f;
+                            rsm[m][q] = dm != 0.f ? dm : rsm[m][q];
                         }
                     }
             }
@@ -800,6 +795,19 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
 #pragma unroll
                     for (int mb = 0; mb < MBS; mb++) av[kk & 1][mb] = *(const f16x8 *)(Ak + (mb * 64 + lane) * 16);
                 };
+                if constexpr (!STEP && !POW2) {
+#pragma unroll
+                    for (int m = 0; m < NM; m++)
+#pragma unroll
+                        for (int q = 0; q < NB; q++) {
+#pragma unroll
+                            for (int mb = 0; mb < MBS; mb++) acc[m][q][mb] *= ratio[m][q];
+                            if constexpr (MIN) {
+#pragma unroll
+                                for (int mb = 0; mb < MBS; mb++) accm[m][q][mb] *= ratiom[m][q];
+                            }
+                        }
+                }
                 issue_raw(0);
                 if (1 < nke) issue_raw(1);
                 if constexpr (S::PF) {
