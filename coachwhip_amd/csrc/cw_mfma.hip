@@ -247,49 +247,44 @@ struct MIQ3_S {
 // 2^(e - base) relative to the largest exponent of the row's stage, and the accumulator is
 // rescaled when that base changes; in fp16 the product code * 2^(e - base) is exact down to
 // 2^-24 of the stage's largest block scale (smaller contributions round).
-constexpr Tab<64> make_mxfp4_pairs() {  // fp16 pair of the doubled-E2M1 codes (lo, hi), index lo | hi << 4
-    Tab<64> t{};
-    const int kv[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
-    uint32_t w[256] = {};
-    for (int i = 0; i < 256; i++) {
-        uint32_t h[2] = {};
-        for (int q = 0; q < 2; q++) {
-            const int v = kv[(i >> (4 * q)) & 15];
-            h[q] = f16_int((uint32_t)(v < 0 ? -v : v)) | (v < 0 ? 0x8000u : 0u);
-        }
-        w[i] = h[0] | (h[1] << 16);
-    }
-    for (int i = 0; i < 64; i++) t.v[i] = U4{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]};
-    return t;
-}
-static __constant__ Tab<64> c_mxfp4_pairs = make_mxfp4_pairs();
 
 struct MMXFP4 {
-    static constexpr int TS = 17, SBK = 32, LDS = 1024;
+    static constexpr int TS = 17, SBK = 32, LDS = 0;
     static constexpr int KST = 8, SCALE = 1, ORG = 1;
     static constexpr bool HAS_MIN = false;
-    static __device__ void fill(uint8_t *lds, int tid, int nt) { copy_tab(lds, c_mxfp4_pairs, tid, nt); }
+    static __device__ void fill(uint8_t *, int, int) {}
     struct Stage {
         __device__ __forceinline__ void load(const WinRef &, int) {}
     };
     static __device__ __forceinline__ uint32_t expo(const uint8_t *win, int kk) { return lds_u8(win + TS * kk); }
-    static __device__ __forceinline__ uint32_t pair(const uint32_t *tab, uint32_t w) {
-        return tab[(w & 0xF) | ((w >> 4) & 0xF0)];
-    }
-    // lane group grp takes the low (grp < 2) or high nibbles of bytes 8*(grp&1)..+8; the
-    // multiplier is the splatted fp16 2^(e - base)
+    // lane group grp takes the low (grp < 2) or high nibbles of bytes 8*(grp&1)..+8 (weights j and
+    // j+16 of a block are the low and high nibbles of byte j)
     struct Raw { uint2 q; uint32_t e; };
-    struct Look { uint4 p; };
+    struct Look {};
     static __device__ __forceinline__ Raw raw(const WinRef &w, const Stage &, int kk, int grp) {
         return Raw{w.u64x(TS * kk + 8 * (grp & 1)), expo(w.p, kk)};
     }
-    static __device__ __forceinline__ Look look(const Raw &r, const Stage &, int, int grp, const uint8_t *lds, bool) {
-        const uint32_t *tab = (const uint32_t *)lds;
-        const int sh = 4 * (grp >> 1);
-        const uint32_t a = (r.q.x >> sh) & 0x0F0F0F0F, b = (r.q.y >> sh) & 0x0F0F0F0F;
-        return Look{make_uint4(pair(tab, a), pair(tab, a >> 16), pair(tab, b), pair(tab, b >> 16))};
+    static __device__ __forceinline__ Look look(const Raw &, const Stage &, int, int, const uint8_t *, bool) { return Look{}; }
+    // The fragment by gfx950's scaled FP4 conversion (v_cvt_scalef32_pk_f16_fp4: the two E2M1
+    // values of one byte, low nibble first, times an f32 scale, to fp16): the lane's 8 nibbles are
+    // packed two to a byte (bytes 0 and 2 of each dword), and the scale 2^(de+1) gives the doubled
+    // E2M1 codes times 2^de, de = e - base <= 0 the block's exponent against the stage's largest.
+    // Every product is exact in fp16 down to 2^-24 of that largest block scale; below it, it rounds.
+    static __device__ __forceinline__ uint32_t cvt2(uint32_t v, float sc, int sel) {
+        f16x2 h;
+        if (sel == 0)
+            h = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, sc, 0);
+        else
+            h = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, sc, 2);
+        return __builtin_bit_cast(uint32_t, h);
     }
-    static __device__ __forceinline__ uint4 make_mx(const Look &l, uint32_t mult) { return scale4(l.p, mult); }
+    static __device__ __forceinline__ uint4 make_mx(const Raw &r, int grp, int de) {
+        const float sc = de >= -127 ? __uint_as_float((uint32_t)(de + 128) << 23) : 0.f;
+        const int sh = 4 * (grp >> 1);
+        const uint32_t a = (r.q.x >> sh) & 0x0F0F0F0Fu, b = (r.q.y >> sh) & 0x0F0F0F0Fu;
+        const uint32_t pa = a | (a >> 4), pb = b | (b >> 4);
+        return make_uint4(cvt2(pa, sc, 0), cvt2(pa, sc, 2), cvt2(pb, sc, 0), cvt2(pb, sc, 2));
+    }
 };
 
 // 8 small unsigned byte values (v < 1024) of two dwords -> fp16 (1024 + v), by placing each byte
@@ -434,11 +429,6 @@ struct MQ2_K {
     }
 };
 
-// fp16 bits of 2^x for x <= 0 (0 below the subnormal range), splatted to both halves
-__device__ __forceinline__ uint32_t pow2_f16x2(int x) {
-    const uint32_t h = x >= -14 ? (uint32_t)(x + 15) << 10 : (x >= -24 ? 1u << (x + 24) : 0u);
-    return h | (h << 16);
-}
 
 // A stage is KST K-steps (8: 256 weights of k; 4 for Q8_0). The window of a row for a stage
 // holds the stage's bytes (an IQ, Q2_K or Q4_K super-block, or KST MXFP4 / Q8_0 blocks) from the
@@ -858,7 +848,7 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
 #pragma unroll
                         for (int q = 0; q < NB; q++) {
                             if constexpr (POW2)
-                                bf[m][q] = as_f16x8(MF::make_mx(lk[kk & 1][m][q], pow2_f16x2((int)rw[kk & 1][m][q].e - rb[m][q])));
+                                bf[m][q] = as_f16x8(MF::make_mx(rw[kk & 1][m][q], grp, (int)rw[kk & 1][m][q].e - rb[m][q]));
                             else
                                 bf[m][q] = as_f16x8(MF::make(rw[kk & 1][m][q], lk[kk & 1][m][q], stg[m][q], kk, grp, zero[m][q]));
                         }
