@@ -231,6 +231,118 @@ def bench_c5(args, torch, np, dev):
     print(json.dumps(line), flush=True)
 
 
+def bench_c4(args, torch, np, dev):
+    """Config 4: gpt-oss-style MoE layers: 128 experts, top-4, hidden and expert FFN 2880, MXFP4
+    gate/up/down, clamped SwiGLU (alpha 1.702, limit 7) with per-expert biases N(0, 0.02^2),
+    activations N(0,1) rounded to bf16 values (passed as f32). Decode b=1 through a chain of
+    --layers layers (12 by default: 20 GB of experts, so a step's 635 MB of picked experts cannot
+    come from the 256 MB Infinity Cache), captured in a graph and timed like config 3; prefill:
+    2,048 tokens, ten layer calls over the chain's layers captured in one graph (each call reads
+    another layer's 1.69 GB of experts from HBM)."""
+    from coachwhip_amd import formats as F
+    from coachwhip_amd import ops, synth
+    from oracle import oracle as O
+    E, K, H, I, T = 128, 4, 2880, 2880, 2048
+    dts = (F.MXFP4,) * 3
+    shapes = [(I, H), (I, H), (H, I)]
+    L = args.layers or 12
+    eb = [F.matrix_bytes(d, *sh) for d, sh in zip(dts, shapes)]
+    expert_bytes = sum(eb)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    log("building %d layers of %d MXFP4 experts (%.1f GB) on the device" % (L, E, L * E * expert_bytes / 1e9))
+    layers, biases = [], []
+    for l in range(L):
+        banks = [ops.ExpertBank(synth.device_blocks(dts[m], E * shapes[m][0] * shapes[m][1], gen, dev), dts[m],
+                                shapes[m][0], shapes[m][1], E, eb[m]) for m in range(3)]
+        bias = [torch.randn((E, I), generator=gen, device=dev) * 0.02, torch.randn((E, I), generator=gen, device=dev) * 0.02,
+                torch.randn((E, H), generator=gen, device=dev) * 0.02]
+        layers.append(ops.MoeLayer(*banks, n_experts=E, top_k=K, norm_topk_prob=True,
+                                   act=ops.ExpertAct.clamped_swiglu(1.702, 7.0, *bias)))
+        biases.append(bias)
+    total = args.warmup + args.steps
+    x_all = torch.randn((total, 1, H), generator=gen, device=dev).to(torch.bfloat16).float()
+    logits_all = torch.randn((total, L, 1, E), generator=gen, device=dev)
+    torch.cuda.synchronize()
+
+    log("parity of layer 0 against the CPU oracle")
+    out0, ids0, w0 = layers[0].forward(x_all[0], logits_all[0, 0])
+    host_layer = synth.MoeWeights(E, K, H, I, dts, [b.data.cpu().numpy() for b in layers[0].banks],
+                                  [b.slot_stride for b in layers[0].banks], E, act=1,
+                                  bias=[b.cpu().numpy() for b in biases[0]])
+    x0, lg0 = x_all[0].cpu().numpy(), logits_all[0, 0].cpu().numpy()
+    want, wids, ww, _ = O.moe_layer(host_layer, x0, lg0)
+    parity = {"rel_l2": O.rel_l2(out0.cpu().numpy(), want),
+              "ids_equal": bool(np.array_equal(ids0.cpu().numpy().view(np.uint32), wids)),
+              "max_weight_err": float(np.max(np.abs(w0.cpu().numpy() - ww)))}
+    log("parity", parity)
+
+    log("timing the decode chain: %d steps x %d layers" % (args.steps, L))
+    ms = time_graph(torch, layers, x_all, logits_all, args.warmup, args.steps)
+    us_per_layer = ms * 1e3 / (args.steps * L)
+    layer_bytes = K * expert_bytes + K * 3 * I * 4 + H * 4 + E * 4 + H * 4  # picked experts, their biases, x, logits, out
+    gbs = layer_bytes / (us_per_layer * 1e-6) / 1e9
+    log("decode: %.2f us/layer, %.1f GB/s" % (us_per_layer, gbs))
+
+    xp = torch.randn((T, H), generator=gen, device=dev).to(torch.bfloat16).float()
+    lp = torch.randn((T, E), generator=gen, device=dev)
+    eager = [layers[l].forward(xp, lp)[0].clone() for l in range(min(L, 2))]
+    torch.cuda.synchronize()
+    reps = 10
+    g_pre = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_pre):
+        pre_outs = [layers[r % L].forward(xp, lp)[0] for r in range(reps)]
+    torch.cuda.synchronize()
+    g_pre.replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    g_pre.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    pre_us = start.elapsed_time(stop) * 1e3 / reps
+    pre_same = all(bool(torch.equal(pre_outs[r], eager[r % L])) for r in range(reps) if r % L < len(eager))
+    pre_flops = 2.0 * T * K * 3 * H * I
+    tflops = pre_flops / (pre_us * 1e-6) / 1e12
+    # every expert is picked at 2,048 tokens: the layer reads all its experts once
+    pre_bytes = E * expert_bytes + 3 * E * I * 4 + T * H * 4 + T * E * 4 + T * H * 4
+    prefill = {"tokens": T, "us_per_layer": round(pre_us, 2), "tokens_per_s": round(T / (pre_us * 1e-6)),
+               "tflops": round(tflops, 2), "mfma_util": round(tflops / MFMA_PEAK_F16_TFLOPS, 4),
+               "mfma_peak_tflops": MFMA_PEAK_F16_TFLOPS, "hbm_gbs": round(pre_bytes / (pre_us * 1e-6) / 1e9, 1),
+               "hbm_frac": round(pre_bytes / (pre_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+               "graph_replay_equals_eager": pre_same, "calls_timed": reps,
+               "path": "grouped MFMA GEMMs (MXFP4 codes by the scaled FP4 conversion, fp16 activations, f32 accumulate)"}
+    log("prefill", prefill)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        n, t_cpu = 0, 0.0
+        while t_cpu < min(args.cpu_seconds, 5.0) and n < 1000:
+            lg = logits_all[n % total, 0].cpu().numpy()
+            t1 = time.perf_counter()
+            O.moe_layer(host_layer, x0, lg)
+            t_cpu += time.perf_counter() - t1
+            n += 1
+        cpu = {"value": t_cpu / n * 1e6, "unit": "us/layer", "cores": threads, "kind": "port",
+               "sample": "%d decode calls (T=1) of the C oracle MoE layer (MXFP4 dequantize, f64 dots) on layer 0; "
+                         "candle's own MXFP4 CPU path quantizes x to Q8_0 and is not restated" % n}
+    line = {
+        "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms / args.steps, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded MXFP4 blocks, biases and bf16-valued N(0,1) activations, generated on the device)",
+        "config": {"workload": "config 4 decode: gpt-oss-style MoE layer chain, b=1", "experts": E, "top_k": K,
+                   "hidden": H, "expert_ffn": I, "weights": "mxfp4", "act": "clamped swiglu", "layers": L, "tokens": 1},
+        "us_per_layer": round(us_per_layer, 3),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "MoE decode layer (MXFP4, clamped SwiGLU)", "bytes_per_launch": layer_bytes},
+        "prefill": prefill, "parity": parity, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def bench_shrink(args, torch, np, dev):
     """The GPU shrink (cw_requant_q2k) on experts of config 5's shape with the reference's model-file
     formats (gate/up Q3_K 512 x 2048, down Q5_K 2048 x 512, crates/engine/tests/gpu_shrink.rs):
@@ -316,8 +428,9 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--layers", type=int, default=None, help="layers per step (40 for config 3, 48 for config 5)")
-    ap.add_argument("--workload", choices=("c3", "c5", "shrink"), default="c3",
-                    help="c3: the headline decode chain; c5: the bank chain (56 of 512 slots) and streaming; "
+    ap.add_argument("--workload", choices=("c3", "c4", "c5", "shrink"), default="c3",
+                    help="c3: the headline decode chain; c4: the gpt-oss-style MXFP4 chain and its 2,048-token "
+                         "prefill; c5: the bank chain (56 of 512 slots) and streaming; "
                          "shrink: the GPU shrink to Q2_K of config-5-shaped experts")
     ap.add_argument("--stream-tokens", type=int, default=16, help="config 5: tokens of the streaming run")
     ap.add_argument("--prefill-tokens", type=int, default=1500)
@@ -346,6 +459,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.copy_calibration:
         copy_calibration(torch, dev)
+        return
+    if args.workload == "c4":
+        bench_c4(args, torch, np, dev)
         return
     if args.workload == "c5":
         bench_c5(args, torch, np, dev)

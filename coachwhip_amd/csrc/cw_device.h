@@ -50,7 +50,6 @@ __device__ __forceinline__ uint32_t ksign(uint32_t i7) { return i7 | ((__popc(i7
 __device__ __forceinline__ float e8m0_half(uint32_t e) {
     return __uint_as_float(e < 2 ? (0x00200000u << e) : ((e - 1) << 23));
 }
-// doubled E2M1 value of a 4-bit code (k_quants.rs:639): magnitudes {0,1,2,3,4,6,8,12}
 __device__ __forceinline__ float kv_mxfp4(uint32_t c) {
     uint32_t m = c & 7u;
     int mag = (int)(m < 4 ? m : ((2u | (m & 1u)) << ((m >> 1) - 1)));  // 4, 6, 8, 12 for 4..7
@@ -204,21 +203,38 @@ struct FMXFP4 {
         r.q = ld_u128(b + 1);
         return r;
     }
-    static __device__ __forceinline__ uint32_t byte(const Raw &r, int j) { return ((&r.q.x)[j >> 2] >> (8 * (j & 3))) & 0xFFu; }
+    // The doubled E2M1 values of byte j's two codes (low nibble first) by gfx950's scaled FP4
+    // conversion (v_cvt_scalef32_pk_f32_fp4) with scale 2: exact, one instruction for two weights.
+    // Code 8 gives -0 where the reference's i8 table has +0: dequant adds +0 to turn it into +0;
+    // in dot it cannot show (the sum starts at +0, so no fma of a -0 product leaves a -0).
+    static __device__ __forceinline__ float2 kv2(const Raw &r, int j) {
+        const uint32_t w = (&r.q.x)[j >> 2];
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        f32x2 v;
+        switch (j & 3) {
+        case 0: v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 2.0f, 0); break;
+        case 1: v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 2.0f, 1); break;
+        case 2: v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 2.0f, 2); break;
+        default: v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 2.0f, 3); break;
+        }
+        return make_float2(v.x, v.y);
+    }
     static __device__ __forceinline__ void dequant(const Raw &r, const void *, float *y) {
         float d = e8m0_half(r.e);
 #pragma unroll
         for (int j = 0; j < 16; j++) {
-            y[j] = kv_mxfp4(byte(r, j) & 0xF) * d;
-            y[j + 16] = kv_mxfp4(byte(r, j) >> 4) * d;
+            const float2 v = kv2(r, j);
+            y[j] = (v.x + 0.0f) * d;
+            y[j + 16] = (v.y + 0.0f) * d;
         }
     }
     static __device__ __forceinline__ float dot(const Raw &r, const void *, const float *x) {
         float s = 0.f;
 #pragma unroll
         for (int j = 0; j < 16; j++) {
-            s = fmaf(kv_mxfp4(byte(r, j) & 0xF), x[j], s);
-            s = fmaf(kv_mxfp4(byte(r, j) >> 4), x[j + 16], s);
+            const float2 v = kv2(r, j);
+            s = fmaf(v.x, x[j], s);
+            s = fmaf(v.y, x[j + 16], s);
         }
         return s * e8m0_half(r.e);
     }
