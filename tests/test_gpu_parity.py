@@ -113,11 +113,12 @@ def test_qmatmul_edge_scales(path, monkeypatch):
     # zero and subnormal f16 scales (and a zero dmin) take the kernels' zero-scale branches
     monkeypatch.setenv("CWMOE_MM_MIN_ROWS", MM_PATHS[path])
     rng = np.random.default_rng(77)
-    for dtype, n, k, d_at in ((F.Q4_K, 64, 1024, 0), (F.Q8_0, 64, 512, 0), (F.Q2_K, 64, 1024, 80)):
+    for dtype, n, k, d_at in ((F.Q4_K, 64, 1024, 0), (F.Q8_0, 64, 512, 0), (F.Q2_K, 64, 1024, 80),
+                              (F.IQ2_XXS, 64, 1024, 0), (F.IQ2_S, 64, 1024, 0), (F.IQ3_S, 64, 1024, 0)):
         raw = synth.random_blocks(dtype, n * k, rng).reshape(-1, F.type_size(dtype)).copy()
         raw[::3, d_at:d_at + 2] = 0                  # d = 0
         raw[1::5, d_at:d_at + 2] = [0x01, 0x00]      # smallest subnormal d
-        if dtype != F.Q8_0:
+        if dtype in (F.Q4_K, F.Q2_K):
             raw[2::7, d_at + 2:d_at + 4] = 0         # dmin = 0
         raw = raw.reshape(-1)
         x = rng.standard_normal((48, k)).astype(np.float32)
@@ -126,6 +127,31 @@ def test_qmatmul_edge_scales(path, monkeypatch):
         err = O.rel_l2(y, want)
         say("edge scales", F.NAMES[dtype], path, err)
         assert err <= REL_L2_GATE
+
+
+@pytest.mark.parametrize("path", sorted(MM_PATHS))
+def test_qmatmul_mxfp4_exponents(path, monkeypatch):
+    # e8m0 block scales from subnormal (e = 0, 1: 2^-128, 2^-127) to 2^23, mixed within rows: the
+    # matvec path's scaled FP4 conversion and the MFMA path's exponents against the stage's largest
+    # (a block 2^150 below it contributes nothing); the f64 oracle decodes with k_quants.rs:638-691
+    monkeypatch.setenv("CWMOE_MM_MIN_ROWS", MM_PATHS[path])
+    rng = np.random.default_rng(78)
+    n, k = 64, 2880
+    raw = synth.random_blocks(F.MXFP4, n * k, rng).reshape(-1, F.type_size(F.MXFP4)).copy()
+    exps = np.array([0, 1, 2, 90, 120, 127, 140, 150], np.uint8)
+    raw[:, 0] = exps[rng.integers(0, len(exps), raw.shape[0])]
+    raw[::11, 1:] = 0x88                             # codes 8 (the i8 table's +0) in both nibbles
+    raw = raw.reshape(-1)
+    for m in (1, 40):
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        y = host(ops.QMatMul(ops.QTensor.from_blocks(raw, F.MXFP4, (n, k))).forward(dev(x)))
+        want = O.qmatmul_f64(F.MXFP4, raw, n, k, x)
+        err = O.rel_l2(y, want)
+        say("mxfp4 exponents", path, m, err)
+        assert np.all(np.isfinite(y))
+        assert err <= REL_L2_GATE
+        if path == "matvec":
+            assert err <= REL_L2_F32
 
 
 def test_qmatmul_rejects_bad_shapes():
