@@ -32,13 +32,14 @@ COPY_BYTES = 1 << 30
 
 
 TRAFFIC_PROFILE = "profiles/moe_c3_hbm_traffic.md"
+TRAFFIC_PROFILE_C4 = "profiles/moe_c4_kernels.md"
 
 
-def measured_traffic(root):
-    """HBM bytes per decode-layer launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+def measured_traffic(root, profile=TRAFFIC_PROFILE):
+    """HBM bytes per decode-layer launch from a committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
     (counters scaled by a copy kernel of known size), or None when the summary is absent."""
     try:
-        with open(os.path.join(root, TRAFFIC_PROFILE)) as f:
+        with open(os.path.join(root, profile)) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_launch:"):
                     return int(line.split(":")[1])
@@ -336,7 +337,9 @@ def bench_c4(args, torch, np, dev):
                    "hidden": H, "expert_ffn": I, "weights": "mxfp4", "act": "clamped swiglu", "layers": L, "tokens": 1},
         "us_per_layer": round(us_per_layer, 3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(os.path.dirname(os.path.abspath(__file__)), TRAFFIC_PROFILE_C4),
+                     "traffic_source": TRAFFIC_PROFILE_C4,
                      "kernel": "MoE decode layer (MXFP4, clamped SwiGLU)", "bytes_per_launch": layer_bytes},
         "prefill": prefill, "parity": parity, "cpu_baseline": cpu,
     }
