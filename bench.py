@@ -346,6 +346,84 @@ def bench_c4(args, torch, np, dev):
     print(json.dumps(line), flush=True)
 
 
+def bench_dense(args, torch, np, dev):
+    """Configs 1 and 2: one quantized matrix, y = x . W^T (QMatMul): Q8_0 2048 x 2048 at M = 1, and
+    Q4_K 4096 x 4096 at M in {1, 16, 128, 512}. Each case captures one call per copy of the matrix
+    (copies past ~600 MB, so the Infinity Cache cannot serve them) in a graph and times its replay;
+    achieved rates use the algorithmic bytes (matrix + x + y) and flops (2 M n k), against HBM
+    (8 TB/s) or fp16 MFMA (2.5 PFLOP/s), whichever bounds the case. Parity of each case against
+    the f64 oracle; the CPU baseline is the oracle's restatement of candle's x86 path (activations
+    quantized to Q8_K / Q8_0, integer block dots) on the host's threads."""
+    from coachwhip_amd import formats as F
+    from coachwhip_amd import ops, synth
+    from oracle import oracle as O
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    rng = np.random.default_rng(args.seed)
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    cases = []
+    for name, dt, n, k, ms in (("config 1: Q8_0 GEMV", F.Q8_0, 2048, 2048, (1,)),
+                               ("config 2: Q4_K matmul", F.Q4_K, 4096, 4096, (1, 16, 128, 512))):
+        wb = F.matrix_bytes(dt, n, k)
+        copies = max(8, -(-600_000_000 // wb))
+        mats = [ops.QMatMul(ops.QTensor(synth.device_blocks(dt, n * k, gen, dev), dt, (n, k))) for _ in range(copies)]
+        host_w = mats[0].w.data.cpu().numpy()
+        for m in ms:
+            x = torch.randn((m, k), generator=gen, device=dev)
+            y0 = mats[0].forward(x)
+            torch.cuda.synchronize()
+            xh = x.cpu().numpy()
+            err = O.rel_l2(y0.cpu().numpy(), O.qmatmul_f64(dt, host_w, n, k, xh))
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for c in range(copies):
+                    mats[c].forward(x)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            g.replay()
+            stop.record()
+            torch.cuda.synchronize()
+            us = start.elapsed_time(stop) * 1e3 / copies
+            nbytes = wb + 4 * m * k + 4 * m * n
+            flops = 2.0 * m * n * k
+            t_hbm, t_mfma = nbytes / (HBM_PEAK_GBS * 1e9), flops / (MFMA_PEAK_F16_TFLOPS * 1e12)
+            bound = "hbm" if t_hbm >= t_mfma else "mfma"
+            case = {"case": name, "m": m, "n": n, "k": k, "us": round(us, 3),
+                    "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "tflops": round(flops / (us * 1e-6) / 1e12, 2),
+                    "bound": bound, "roofline_frac": round(max(t_hbm, t_mfma) / (us * 1e-6), 4), "rel_l2": err}
+            if not args.no_cpu_baseline:
+                O.candle_matmul(dt, host_w, n, k, xh)
+                reps, t_cpu = 0, 0.0
+                while t_cpu < 2.0 and reps < 200:
+                    t1 = time.perf_counter()
+                    O.candle_matmul(dt, host_w, n, k, xh)
+                    t_cpu += time.perf_counter() - t1
+                    reps += 1
+                case["cpu_us"] = round(t_cpu / reps * 1e6, 1)
+            log(case)
+            cases.append(case)
+        del mats
+        torch.cuda.empty_cache()
+    head = cases[0]
+    line = {
+        "metric": METRIC, "value": head["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": 1, "warmup": 1,
+        "ms_per_step": head["us"] / 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (seeded Q8_0 / Q4_K blocks generated on the device, x ~ N(0,1))",
+        "config": {"workload": "configs 1 and 2: dense QMatMul (Q8_0 2048x2048 M=1; Q4_K 4096x4096 M=1,16,128,512)"},
+        "roofline": {"bound": head["bound"], "achieved": head["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": head["roofline_frac"], "traffic": None, "kernel": "QMatMul, config 1"},
+        "cases": cases,
+        "cpu_baseline": None if args.no_cpu_baseline else {
+            "value": head["cpu_us"], "unit": "us per call (config 1)", "cores": threads, "kind": "port",
+            "sample": "the oracle's restatement of candle's x86 quantized matmul (activations to Q8_K/Q8_0, integer "
+                      "block dots) per case, ~2 s each; cpu_us in each case"},
+    }
+    print(json.dumps(line), flush=True)
+
+
 def bench_shrink(args, torch, np, dev):
     """The GPU shrink (cw_requant_q2k) on experts of config 5's shape with the reference's model-file
     formats (gate/up Q3_K 512 x 2048, down Q5_K 2048 x 512, crates/engine/tests/gpu_shrink.rs):
@@ -431,9 +509,9 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--layers", type=int, default=None, help="layers per step (40 for config 3, 48 for config 5)")
-    ap.add_argument("--workload", choices=("c3", "c4", "c5", "shrink"), default="c3",
+    ap.add_argument("--workload", choices=("c3", "c4", "c5", "shrink", "dense"), default="c3",
                     help="c3: the headline decode chain; c4: the gpt-oss-style MXFP4 chain and its 2,048-token "
-                         "prefill; c5: the bank chain (56 of 512 slots) and streaming; "
+                         "prefill; c5: the bank chain (56 of 512 slots) and streaming; dense: configs 1-2 QMatMul; "
                          "shrink: the GPU shrink to Q2_K of config-5-shaped experts")
     ap.add_argument("--stream-tokens", type=int, default=16, help="config 5: tokens of the streaming run")
     ap.add_argument("--prefill-tokens", type=int, default=1500)
@@ -465,6 +543,9 @@ def main():
         return
     if args.workload == "c4":
         bench_c4(args, torch, np, dev)
+        return
+    if args.workload == "dense":
+        bench_dense(args, torch, np, dev)
         return
     if args.workload == "c5":
         bench_c5(args, torch, np, dev)
