@@ -12,11 +12,13 @@
 //    one launch moves every miss over PCIe at the rate of a plain DMA copy, where a DMA copy
 //    per expert matrix (27 for ten picks) reached under a third of it and cost ~4 µs of host
 //    time each. A store without a device mapping (pageable memory) is copied by DMA;
-//  - a prefetch (experts.rs:1004-1098) copies on the bank's own stream, after the work that was
-//    on the last ensure's stream when that ensure returned (so it overwrites no slot a queued
-//    kernel still reads), and records an event per slot; ensure waits for that event on its
-//    stream (a GPU-side wait, where the reference spins on the host), and a slot still being
-//    filled is neither a victim nor listed in the device table;
+//  - a prefetch (experts.rs:1004-1098) first takes its victims out of the device table on the
+//    last ensure's stream (the reference marks the slot not ready and syncs the GPU table before
+//    it copies, experts.rs:1052-1058), then copies on the bank's own stream after the work queued
+//    on that stream up to the prefetch call (so it overwrites no slot a queued kernel may read),
+//    and records an event per slot; ensure waits for that event on its stream (a GPU-side wait,
+//    where the reference spins on the host), and a slot still being filled is neither a victim
+//    nor listed in the device table;
 //  - a matrix the source marks for shrinking (Q3_K, Q4_K or Q5_K in the store) is held as Q2_K:
 //    its misses go into a staging area first and are shrunk from there into their slots
 //    (ExpertStore::shrink_into, experts.rs:1245-1273), in chunks of STAGE experts; ensure and
@@ -126,8 +128,9 @@ struct cw_bank {
     std::vector<hipEvent_t> slot_ev;  // per slot: end of its last prefetch copy
     std::vector<uint8_t> filling;     // per slot: that copy may still be running
     std::vector<uint8_t> kept;        // per slot: placed by the last ensure
-    hipEvent_t fence = nullptr;       // the last ensure's stream at its return
-    bool fenced = false;
+    hipEvent_t fence = nullptr;       // the last ensure's stream, when a prefetch was last called
+    hipStream_t last = nullptr;       // the stream of the last ensure
+    bool fenced = false;              // an ensure has run (last is set)
     cw_bank_stats st{};
 
     ~cw_bank() {  // teardown: failures here have no caller to go to
@@ -362,8 +365,7 @@ int cw_bank_ensure(cw_bank *b, const uint32_t *needed, int n_needed, cw_stream_t
     std::fill(b->kept.begin(), b->kept.end(), 0);
     for (int i = 0; i < nh; i++) b->kept[hits[2 * i + 1]] = 1;
     for (int i = 0; i < nm; i++) b->kept[misses[2 * i + 1]] = 1;
-    const hipError_t f = hipEventRecord(b->fence, s);
-    if (f != hipSuccess) return cw::set_error(CW_EHIP, "bank: event record: %s", hipGetErrorString(f));
+    b->last = s;
     b->fenced = true;
     if (n_loaded) *n_loaded = nm;
     return CW_OK;
@@ -383,8 +385,33 @@ int cw_bank_prefetch(cw_bank *b, const uint32_t *predicted, int n_predicted) {
     const int n = cw_slots_reserve(b->slots, predicted, n_predicted, ready.data(), out.data());
     if (n == 0) return 0;
     if (b->fenced) {
-        const hipError_t w = hipStreamWaitEvent(b->copy, b->fence, 0);
-        if (w != hipSuccess) return -cw::set_error(CW_EHIP, "bank: stream wait: %s", hipGetErrorString(w));
+        // everything queued on the ensure stream so far may read the victims' slots: the copies
+        // wait for it, and what is queued there later finds the victims absent from the table
+        hipError_t w = hipEventRecord(b->fence, b->last);
+        if (w == hipSuccess) w = hipStreamWaitEvent(b->copy, b->fence, 0);
+        if (w != hipSuccess) {
+            for (int i = 0; i < n; i++) cw_slots_release(b->slots, out[2 * i]);
+            return -cw::set_error(CW_EHIP, "bank: stream wait: %s", hipGetErrorString(w));
+        }
+        std::vector<uint8_t> taken((size_t)b->n_slots, 0);
+        for (int i = 0; i < n; i++) taken[out[2 * i + 1]] = 1;
+        cw::TablePatch p{};
+        for (int e = 0; e < b->src.n_experts; e++) {
+            const uint32_t v = b->dev_table[(size_t)e];
+            if (v == CW_NO_SLOT || !taken[v]) continue;
+            b->dev_table[(size_t)e] = CW_NO_SLOT;
+            p.expert[p.n] = (uint32_t)e;
+            p.slot[p.n] = CW_NO_SLOT;
+            if (++p.n == cw::PATCH) {
+                hipLaunchKernelGGL(cw::k_table_patch, dim3(1), dim3(64), 0, b->last, b->table, p);
+                p.n = 0;
+            }
+        }
+        if (p.n) hipLaunchKernelGGL(cw::k_table_patch, dim3(1), dim3(64), 0, b->last, b->table, p);
+        if (int rc = cw::check_launch("k_table_patch")) {
+            for (int i = 0; i < n; i++) cw_slots_release(b->slots, out[2 * i]);
+            return -rc;
+        }
     }
     if (int rc = b->copy_in(out.data(), n, b->copy, 1)) {
         for (int i = 0; i < n; i++) cw_slots_release(b->slots, out[2 * i]);

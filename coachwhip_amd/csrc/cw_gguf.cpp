@@ -272,6 +272,10 @@ cw_gguf *cw_gguf_open(const char *path) {
             elems *= d;
         }
         if (elems % ts.block) return fail_open(g, CW_EINVAL, path, "tensor '" + t.name + "' is not whole blocks");
+        // a tensor bigger than the file is refused before its size is formed, so the product
+        // cannot wrap (8-byte types with more than 2^61 elements would)
+        if ((uint64_t)(elems / ts.block) > (uint64_t)g->size / (uint64_t)ts.bytes)
+            return fail_open(g, CW_EINVAL, path, "tensor '" + t.name + "' is larger than the file");
         t.bytes = (uint64_t)(elems / ts.block) * (uint64_t)ts.bytes;
         g->index[t.name] = (int64_t)g->tensors.size();
         g->tensors.push_back(std::move(t));

@@ -59,8 +59,9 @@ int mfma_down(int dtype, const MfArgs &a, int tiles_max, hipStream_t s);
 size_t mfma_dense_workspace(int dtype, int64_t m, int64_t n, int64_t k);
 int mfma_dense(int dtype, const uint8_t *w, int64_t row_bytes, int n, int k, const float *x, int m, float *y, void *ws,
                size_t ws_bytes, hipStream_t s);
-// out[t] = sum_j w[t*K+j] * (dn[t*K+j] + bias[ids[t*K+j]]), picks in order (H a multiple of 4)
-int combine_picks(const float *dn, const float *w, const float *bias, const uint32_t *ids, int T, int K, int H, float *out,
-                  hipStream_t s);
+// out[t] = sum_j w[t*K+j] * (dn[t*K+j] + bias[ids[t*K+j]]), picks in order (H a multiple of 4); a
+// pick with slots[t*K+j] >= n_slots contributes NaN (it has no row)
+int combine_picks(const float *dn, const float *w, const float *bias, const uint32_t *ids, const uint32_t *slots, int n_slots,
+                  int T, int K, int H, float *out, hipStream_t s);
 
 }  // namespace cw

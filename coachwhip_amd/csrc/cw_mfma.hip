@@ -1096,15 +1096,18 @@ __global__ __launch_bounds__(256) void k_pack_f16(const float *x, int rows, int 
     if (lane == 0) ascale[row] = ldexpf(1.0f, -ex);
 }
 
-// one thread per 4 outputs of a token: the weighted sum of its K picks' rows, bias added per pick
-__global__ __launch_bounds__(256) void k_combine(const float *dn, const float *w, const float *bias, const uint32_t *ids, int K,
-                                                 int H, float *out) {
+// one thread per 4 outputs of a token: the weighted sum of its K picks' rows, bias added per pick.
+// A pick whose slot is out of range is in no pile and has no row: it contributes NaN, as it does
+// on the matvec and decode paths.
+__global__ __launch_bounds__(256) void k_combine(const float *dn, const float *w, const float *bias, const uint32_t *ids,
+                                                 const uint32_t *slots, uint32_t n_slots, int K, int H, float *out) {
     const int t = blockIdx.y, j = 4 * (blockIdx.x * 256 + threadIdx.x);
     if (j >= H) return;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int e = 0; e < K; e++) {
         const int64_t pick = (int64_t)t * K + e;
-        float4 d = *(const float4 *)(dn + pick * H + j);
+        const float nan = __int_as_float(0x7fc00000);
+        float4 d = slots[pick] < n_slots ? *(const float4 *)(dn + pick * H + j) : make_float4(nan, nan, nan, nan);
         if (bias) {
             const float4 b = *(const float4 *)(bias + (int64_t)ids[pick] * H + j);
             d.x += b.x; d.y += b.y; d.z += b.z; d.w += b.w;
@@ -1147,11 +1150,12 @@ int pack_rows_f16(const float *x, int rows, int k, int ldx, uint16_t *a16, float
     return set_error(CW_ENOTSUP, "pack: rows of %d above 8192", k);
 }
 
-int combine_picks(const float *dn, const float *w, const float *bias, const uint32_t *ids, int T, int K, int H, float *out,
-                  hipStream_t s) {
+int combine_picks(const float *dn, const float *w, const float *bias, const uint32_t *ids, const uint32_t *slots, int n_slots,
+                  int T, int K, int H, float *out, hipStream_t s) {
     if (T == 0) return CW_OK;
     if (H % 4) return set_error(CW_ENOTSUP, "combine: width %d is not a multiple of 4", H);
-    hipLaunchKernelGGL(k_combine, dim3((H / 4 + 255) / 256, T), dim3(256), 0, s, dn, w, bias, ids, K, H, out);
+    hipLaunchKernelGGL(k_combine, dim3((H / 4 + 255) / 256, T), dim3(256), 0, s, dn, w, bias, ids, slots, (uint32_t)n_slots, K, H,
+                       out);
     return check_launch("k_combine");
 }
 

@@ -99,7 +99,7 @@ static int route(const float *logits, int T, int E, int K, int norm, uint32_t *i
 // ------------------------------------------------------------------------------ MoE layer
 
 struct MoeLayout {
-    size_t ids, w, slots, g, u, h, total;
+    size_t state, ids, w, slots, g, u, h, total;
     // grouped (MFMA) path
     bool grouped;
     size_t pile_pick, pile_tok, tiles, n_tiles, x16, xscale, h16, hscale, dn;
@@ -118,6 +118,13 @@ static int prefill_min_tokens() {
 static bool decode_single_launch() {
     const char *e = getenv("CWMOE_DECODE_KERNELS");
     return !(e && atoi(e) == 2);
+}
+
+// Polls of the one-launch decode's device-wide barrier before a block gives up (outputs NaN, the
+// error counted): CWMOE_BARRIER_POLLS overrides, for tests of the give-up path.
+static uint32_t decode_polls() {
+    const char *e = getenv("CWMOE_BARRIER_POLLS");
+    return e ? (uint32_t)strtoul(e, nullptr, 10) : (1u << 17);
 }
 
 static bool grouped_path(const cw_moe_desc *d, int T) {
@@ -160,6 +167,9 @@ static MoeLayout layout(const cw_moe_desc *d, int T) {
     const int P = d->pad > d->inter ? d->pad : d->inter;
     MoeLayout L;
     size_t off = 0;
+    // the decode's sync state first, at the same offset for every token count, so that a workspace
+    // reused across calls of any size keeps it (zero between calls)
+    L.state = off; off = align256(off + DECODE_STATE_BYTES);
     L.ids = off; off = align256(off + TK * 4);
     L.w = off; off = align256(off + TK * 4);
     L.slots = off; off = align256(off + TK * 4);
@@ -247,7 +257,7 @@ static int moe_grouped(const cw_moe_desc *d, const MoeArgs &a, const MoeLayout &
     dn.K = K;
     dn.dn = (float *)(base + L.dn);
     if ((rc = mfma_down(d->dtype[2], dn, tmax, s))) return rc;
-    return combine_picks(dn.dn, a.w, a.bd, a.ids, T, K, a.H, a.out, s);
+    return combine_picks(dn.dn, a.w, a.bd, a.ids, slots, a.n_slots, T, K, a.H, a.out, s);
 }
 
 static int moe_layer(const cw_moe_desc *d, const float *x, const float *logits, int T, float *out, uint32_t *ids_out,
@@ -292,6 +302,8 @@ static int moe_layer(const cw_moe_desc *d, const float *x, const float *logits, 
     a.slots = (uint32_t *)(base + L.slots);
     a.h = (float *)(base + L.h);
     a.out = out;
+    a.state = base + L.state;
+    a.polls = decode_polls();
 
     if (L.grouped) return moe_grouped(d, a, L, base, T, s);
     if (T == 1 && d->dtype[0] == d->dtype[1] && decode_single_launch()) {
@@ -336,6 +348,52 @@ static int moe_layer(const cw_moe_desc *d, const float *x, const float *logits, 
         if ((rc = check_launch("k_clamped_swiglu"))) return rc;
     }
     return moe_down(d->dtype[2], a, T, s);
+}
+
+// ------------------------------------------------------------------------------ grouped expert matmul
+
+// rows of picks whose slot is past the bank: NaN (they are in no pile, so the GEMM writes nothing)
+__global__ void k_nan_rows(const uint32_t *ids, int n_picks, uint32_t n_slots, int n, float *out) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n_picks; i += gridDim.x * blockDim.x)
+        if (ids[i] >= n_slots)
+            for (int r = 0; r < n; r++) out[(int64_t)i * n + r] = __int_as_float(0x7fc00000);
+}
+
+struct GroupedLayout {
+    size_t pile_pick, pile_tok, tiles, n_tiles, x16, xscale, total;
+};
+static GroupedLayout grouped_layout(int64_t k, int64_t n_slots, int x_per_pick, int K, int T) {
+    const size_t TK = (size_t)T * K, rows = x_per_pick ? TK : (size_t)T;
+    GroupedLayout L;
+    size_t off = 0;
+    L.pile_pick = off; off = align256(off + TK * 4);
+    L.pile_tok = off; off = align256(off + TK * 4);
+    L.tiles = off; off = align256(off + (size_t)max_tiles((int)TK, (int)n_slots) * sizeof(MfTile));
+    L.n_tiles = off; off = align256(off + 4);
+    L.x16 = off; off = align256(off + rows * (size_t)k * 2);
+    L.xscale = off; off = align256(off + rows * 4);
+    L.total = off;
+    return L;
+}
+
+// CW_OK when the grouped GEMM takes this call, else the status to return (CW_ENOTSUP: use cw_matvec_id)
+static int grouped_check(int dtype, int64_t n, int64_t k, int64_t n_slots, int64_t slot_stride, int K, int T) {
+    if (!is_weight_type(dtype)) return set_error(CW_ENOTSUP, "matmul_id_grouped: dtype %d is not supported", dtype);
+    if (!mfma_supported(dtype)) return set_error(CW_ENOTSUP, "matmul_id_grouped: dtype %d has no grouped kernel", dtype);
+    const int bs = cw_block_size(dtype);
+    CW_REQUIRE(n > 0 && k > 0 && n < (1ll << 31), "matmul_id_grouped: n %lld, k %lld", (long long)n, (long long)k);
+    CW_REQUIRE(k % bs == 0, "matmul_id_grouped: k %lld is not whole %d-weight blocks", (long long)k, bs);
+    CW_REQUIRE(K > 0 && K <= 32 && T >= 0, "matmul_id_grouped: K %d, T %d", K, T);
+    CW_REQUIRE(n_slots > 0, "matmul_id_grouped: %lld slots", (long long)n_slots);
+    CW_REQUIRE((int64_t)T * K < (1ll << 30), "matmul_id_grouped: %lld picks", (long long)T * K);
+    const int64_t row_bytes = k / bs * cw_type_size(dtype);
+    CW_REQUIRE(slot_stride >= n * row_bytes, "matmul_id_grouped: slot stride %lld below the %lld-byte matrix",
+               (long long)slot_stride, (long long)(n * row_bytes));
+    if (n_slots > 1024) return set_error(CW_ENOTSUP, "matmul_id_grouped: %lld slots (1024 max)", (long long)n_slots);
+    if (k % 256 && dtype != CW_Q8_0 && dtype != CW_MXFP4)
+        return set_error(CW_ENOTSUP, "matmul_id_grouped: k %lld is not whole super-blocks", (long long)k);
+    if (k > 8192) return set_error(CW_ENOTSUP, "matmul_id_grouped: k %lld above 8192", (long long)k);
+    return CW_OK;
 }
 
 // out[t][i] = (accumulate ? out[t][i] : 0) + y[t][i] * sigmoid(glog[t]) (glog NULL: factor 1)
@@ -402,6 +460,52 @@ int cw_shared_expert(const cw_shared_desc *d, const float *x, int T, float *out,
     hipLaunchKernelGGL(k_gate_scale_add, flat_grid((int64_t)T * d->hidden), dim3(256), 0, s, y, glog, T, d->hidden, accumulate,
                        out);
     return check_launch("k_gate_scale_add");
+}
+
+size_t cw_matmul_id_grouped_workspace_size(int dtype, int64_t n, int64_t k, int64_t n_slots, int64_t slot_stride,
+                                           int x_rows_per_expert, int K, int T) {
+    if (grouped_check(dtype, n, k, n_slots, slot_stride, K, T) != CW_OK) return 0;
+    return grouped_layout(k, n_slots, x_rows_per_expert ? 1 : 0, K, T).total;
+}
+
+int cw_matmul_id_grouped(int dtype, int64_t n, int64_t k, int64_t n_slots, int64_t slot_stride, const void *bank,
+                         const float *x, int x_rows_per_expert, const uint32_t *ids, int K, int T, float *out, void *ws,
+                         size_t ws_bytes, cw_stream_t stream) {
+    int rc = grouped_check(dtype, n, k, n_slots, slot_stride, K, T);
+    if (rc) return rc;
+    if (T == 0) return CW_OK;
+    CW_REQUIRE(bank && x && ids && out, "matmul_id_grouped: null pointer");
+    CW_REQUIRE(((uintptr_t)x & 15u) == 0 && k % 4 == 0, "matmul_id_grouped: x must be 16-byte aligned rows of whole float4s");
+    const int xpp = x_rows_per_expert ? 1 : 0;
+    const GroupedLayout L = grouped_layout(k, n_slots, xpp, K, T);
+    CW_REQUIRE(ws && ws_bytes >= L.total, "matmul_id_grouped: workspace of %zu bytes, %zu needed", ws_bytes, L.total);
+    hipStream_t s = (hipStream_t)stream;
+    uint8_t *base = (uint8_t *)ws;
+    const int TK = T * K;
+    int *pile_pick = (int *)(base + L.pile_pick), *pile_tok = (int *)(base + L.pile_tok), *n_tiles = (int *)(base + L.n_tiles);
+    MfTile *tiles = (MfTile *)(base + L.tiles);
+    uint16_t *x16 = (uint16_t *)(base + L.x16);
+    float *xscale = (float *)(base + L.xscale);
+    if ((rc = mfma_piles(ids, TK, K, (int)n_slots, pile_pick, pile_tok, tiles, n_tiles, s))) return rc;
+    if ((rc = pack_rows_f16(x, xpp ? TK : T, (int)k, (int)k, x16, xscale, s))) return rc;
+    MfArgs a = {};
+    a.w0 = (const uint8_t *)bank;
+    a.s0 = slot_stride;
+    a.row_bytes = k / cw_block_size(dtype) * cw_type_size(dtype);
+    a.n = (int)n;
+    a.k = (int)k;
+    a.a16 = x16;
+    a.ascale = xscale;
+    a.lda = (int)k;
+    a.rows = xpp ? pile_pick : pile_tok;  // the activation row of each pile position
+    a.tiles = tiles;
+    a.n_tiles = n_tiles;
+    a.pile_pick = pile_pick;
+    a.K = K;
+    a.dn = out;
+    if ((rc = mfma_down(dtype, a, max_tiles(TK, (int)n_slots), s))) return rc;
+    hipLaunchKernelGGL(k_nan_rows, flat_grid(TK), dim3(256), 0, s, ids, TK, (uint32_t)n_slots, (int)n, out);
+    return check_launch("k_nan_rows");
 }
 
 int cw_route_topk(const float *logits, int T, int E, int K, int norm, uint32_t *ids, float *w, cw_stream_t stream) {

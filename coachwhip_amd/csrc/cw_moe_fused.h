@@ -23,7 +23,13 @@ struct MoeArgs {
     uint32_t *slots;               // T x K slots
     float *h;                      // T*K x P hidden rows
     float *out;                    // T x H
+    void *state;                   // the one-launch decode's sync state (DECODE_STATE_BYTES, zero
+                                   // before and after each call)
+    uint32_t polls;                // its bounded waits give up after this many polls
 };
+
+// workspace bytes of the decode's sync state, at the start of every MoE-layer workspace
+constexpr size_t DECODE_STATE_BYTES = 4096;
 
 int moe_gateup(int dtype, const MoeArgs &a, int T, hipStream_t s);
 // the whole layer for one token in one launch (CW_ENOTSUP for shapes it does not cover)

@@ -188,24 +188,26 @@ __global__ __launch_bounds__(256) void k_moe_down(const MoeArgs a) {
 
 // ------------------------------------------------------------------------------ one-kernel decode
 
-// Device-wide barrier of the persistent decode kernel. The state lives in the library (zero
-// at load) and resets itself. Blocks first arrive on a counter of their XCD (blocks go to the
-// 8 XCDs round-robin, blockIdx % 8); the last of each XCD arrives on a top counter, and the
-// last of those clears it and bumps the generation every block waits on. Splitting the
-// arrivals over 9 counters, 128 bytes apart, keeps them from serializing on one address (one
-// counter for 512 blocks measured ~15 us, this ~2.3 us). Everything the blocks exchange
-// through memory inside the kernel is written and read with agent-scope atomics, which go to
-// the coherence point, so the counters need no fences: an agent-scope release / acquire pair
-// here (L2 write-back and invalidate in every block) measured 3x slower, and so did polling
-// all 8 XCD counters from every block. A wait gives up after a bounded number of polls and
-// counts an error instead of hanging. One persistent decode call runs at a time per device.
+// Device-wide barrier of the persistent decode kernel. Its state (DecodeBarrier) lives in the
+// caller's workspace, which the caller zero-fills once, and every call leaves it at zero again, so
+// calls with distinct workspaces are independent. Blocks first arrive on a counter of their XCD
+// (blocks go to the 8 XCDs round-robin, blockIdx % 8); the last of each XCD clears that counter and
+// arrives on a top counter, and the last of those clears it and bumps the generation every block
+// waits on. Splitting the arrivals over 9 counters, 128 bytes apart, keeps them from serializing on
+// one address (one counter for 512 blocks measured ~15 us, this ~2.3 us). Everything the blocks
+// exchange through memory inside the kernel is written and read with agent-scope atomics, which go
+// to the coherence point, so the counters need no fences: an agent-scope release / acquire pair
+// here (L2 write-back and invalidate in every block) measured 3x slower, and so did polling all 8
+// XCD counters from every block. A wait gives up after `polls` polls and counts an error
+// (g_decode_errors) instead of hanging; every block still arrives exactly once, so the state is
+// back at zero (and the generation one further) when the kernel ends, timed out or not.
 struct DecodeBarrier {
     uint32_t sub[8][32];
     uint32_t top[32];
     uint32_t gen[32];
-    uint32_t errors;
 };
-static __device__ DecodeBarrier g_decode_barrier;
+static_assert(sizeof(DecodeBarrier) <= DECODE_STATE_BYTES, "the decode state does not fit its workspace region");
+static __device__ uint32_t g_decode_errors;
 
 #define CW_AGENT __HIP_MEMORY_SCOPE_AGENT
 // buffer descriptor word 3 for raw byte-addressed buffers on gfx9, and the cache policy bit of
@@ -213,12 +215,11 @@ static __device__ DecodeBarrier g_decode_barrier;
 #define CW_BUFFER_DWORD3 0x00020000
 #define CW_CPOL_SC1 16
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-__device__ bool grid_barrier(uint32_t nblocks) {
+__device__ bool grid_barrier(DecodeBarrier *b, uint32_t nblocks, uint32_t polls) {
     __builtin_amdgcn_s_waitcnt(0);  // this thread's coherent stores have landed
     __syncthreads();
     __shared__ int ok;
     if (threadIdx.x == 0) {
-        DecodeBarrier *b = &g_decode_barrier;
         const uint32_t gen = __hip_atomic_load(&b->gen[0], __ATOMIC_RELAXED, CW_AGENT);
         const uint32_t x = blockIdx.x & 7;
         const uint32_t nsub = (nblocks - x + 7) / 8, nx = nblocks < 8 ? nblocks : 8;
@@ -233,14 +234,14 @@ __device__ bool grid_barrier(uint32_t nblocks) {
         if (last) {
             __hip_atomic_fetch_add(&b->gen[0], 1u, __ATOMIC_RELAXED, CW_AGENT);
         } else {
-            uint32_t polls = 0;
+            uint32_t n = 0;
             while (__hip_atomic_load(&b->gen[0], __ATOMIC_RELAXED, CW_AGENT) == gen) {
-                __builtin_amdgcn_s_sleep(1);
-                if (++polls > (1u << 17)) {
+                if (n++ >= polls) {
                     good = 0;
-                    __hip_atomic_fetch_add(&b->errors, 1u, __ATOMIC_RELAXED, CW_AGENT);
+                    __hip_atomic_fetch_add(&g_decode_errors, 1u, __ATOMIC_RELAXED, CW_AGENT);
                     break;
                 }
+                __builtin_amdgcn_s_sleep(1);
             }
         }
         ok = good;
@@ -418,7 +419,7 @@ __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
         store_coherent(a.h + (int64_t)j * a.P + a.I + (c - j * (a.P - a.I)), 0.f);
     }
 
-    const bool ok = grid_barrier(gridDim.x);
+    const bool ok = grid_barrier((DecodeBarrier *)a.state, gridDim.x, a.polls);
 
     // every hidden row into LDS once per block, read at the coherence point (16-byte buffer
     // loads with the sc1 policy, the form of an agent-scope atomic load, 8 in flight per thread),
@@ -630,9 +631,9 @@ int moe_decode(int dtg, int dtd, const MoeArgs &a, hipStream_t s) {
 }
 
 uint32_t decode_barrier_errors() {
-    DecodeBarrier b = {};
-    if (hipMemcpyFromSymbol(&b, HIP_SYMBOL(g_decode_barrier), sizeof b) != hipSuccess) return 0xFFFFFFFFu;
-    return b.errors;
+    uint32_t n = 0;
+    if (hipMemcpyFromSymbol(&n, HIP_SYMBOL(g_decode_errors), sizeof n) != hipSuccess) return 0xFFFFFFFFu;
+    return n;
 }
 
 int moe_gateup(int dtype, const MoeArgs &a, int T, hipStream_t s) { return T ? by_fmt<false>(dtype, a, T, s) : CW_OK; }

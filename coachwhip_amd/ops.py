@@ -22,7 +22,7 @@ import numpy as np
 import torch
 
 from . import formats as F
-from ._lib import CwError, MoeDesc, SharedDesc, check, lib, CW_EINVAL
+from ._lib import CwError, MoeDesc, SharedDesc, check, lib, CW_EINVAL, CW_ENOTSUP
 
 
 def _stream():
@@ -255,10 +255,33 @@ class ExpertBank:
 
 
 class MoeMatvec:
-    """out[t][j] = W[ids[t][j]] . x_row, x_row = x[t] or x[t*nei0 + j] (rows_per_expert)."""
+    """out[t][j] = W[ids[t][j]] . x_row, x_row = x[t] or x[t*nei0 + j] (rows_per_expert).
 
-    def __init__(self, bank: ExpertBank, nei0: int, rows_per_expert: bool):
+    Above ``grouped_above`` tokens (8, the reference's switch, crates/engine/src/experts.rs:2225)
+    the call runs as grouped GEMMs on the matrix cores (cw_matmul_id_grouped), and falls back to
+    the per-pick matvec (cw_matvec_id) when that reports the shape unsupported; ``grouped_above``
+    None keeps every call on the matvec."""
+
+    def __init__(self, bank: ExpertBank, nei0: int, rows_per_expert: bool, grouped_above: Optional[int] = 8):
         self.bank, self.nei0, self.rows_per_expert = bank, nei0, rows_per_expert
+        self.grouped_above = grouped_above
+        self._ws = None
+
+    def _grouped(self, x, ids, out, tokens):
+        b = self.bank
+        need = lib().cw_matmul_id_grouped_workspace_size(b.dtype, b.n, b.k, b.n_slots, b.slot_stride,
+                                                         int(self.rows_per_expert), self.nei0, tokens)
+        if need == 0:
+            return False
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(need, dtype=torch.uint8, device=x.device)
+        rc = lib().cw_matmul_id_grouped(b.dtype, b.n, b.k, b.n_slots, b.slot_stride, _p(b.data), _p(x),
+                                        int(self.rows_per_expert), _p(ids), self.nei0, tokens, _p(out), _p(self._ws),
+                                        need, _stream())
+        if rc == CW_ENOTSUP:
+            return False
+        check(rc)
+        return True
 
     def forward(self, x: torch.Tensor, ids: torch.Tensor) -> torch.Tensor:
         _need(x, torch.float32, "x")
@@ -272,6 +295,8 @@ class MoeMatvec:
             raise CwError(CW_EINVAL, "x is %dx%d, expected k=%d for %d tokens" % (rows, k, self.bank.k, tokens))
         b = self.bank
         out = torch.empty((tokens, nei0, b.n), dtype=torch.float32, device=x.device)
+        if self.grouped_above is not None and tokens > self.grouped_above and self._grouped(x, ids, out, tokens):
+            return out
         check(lib().cw_matvec_id(b.dtype, b.n, b.k, b.n_slots, b.slot_stride, _p(b.data), _p(x), int(self.rows_per_expert),
                                  _p(ids), nei0, tokens, _p(out), _stream()))
         return out
@@ -330,7 +355,8 @@ class MoeLayer:
         if need == 0 and tokens > 0:
             raise CwError(CW_EINVAL, lib().cw_last_error().decode(errors="replace"))
         if self._ws is None or self._ws.numel() < need:
-            self._ws = torch.empty(need, dtype=torch.uint8, device=device)
+            # zero-filled once: the one-token layer keeps its sync state there, at zero between calls
+            self._ws = torch.zeros(need, dtype=torch.uint8, device=device)
         return self._ws, need
 
     def forward(self, xs: torch.Tensor, logits: torch.Tensor, missing: torch.Tensor = None):

@@ -23,11 +23,9 @@
  *    caller may fall back, as mv_id.rs:156-179 does with Ok(false)), CW_EINVAL (shape, stride
  *    or argument error, as candle::bail! in crates/engine/src/experts.rs:2204-2217), CW_EHIP
  *    (the HIP runtime failed). cw_last_error() describes the last failure on this thread.
- *  - Calls on distinct streams may run concurrently, with one exception: a one-token
- *    cw_moe_layer call runs as a single persistent launch whose blocks meet at a device-wide
- *    barrier kept in library state, so two such calls must not overlap on one device (issue
- *    them on one stream). Set CWMOE_DECODE_KERNELS=2 in the environment to use the two-kernel
- *    form instead, which has no such state.
+ *  - Calls on distinct streams may run concurrently when they use distinct workspaces: a call
+ *    keeps all its scratch, including the one-token MoE layer's device-wide barrier, in the
+ *    workspace it is given.
  */
 #ifndef CWMOE_H
 #define CWMOE_H
@@ -128,6 +126,25 @@ int cw_matvec_id(int dtype, int64_t n, int64_t k, int64_t n_slots, int64_t slot_
                  const void *bank, const float *x, int x_rows_per_expert, const uint32_t *ids,
                  int K, int T, float *out, cw_stream_t stream);
 
+/* The cw_matvec_id contract for a batch of tokens, as grouped GEMMs on the matrix cores: picks are
+ * grouped by slot, and each slot's picks multiply its matrix as one small matrix product (the
+ * activations rounded to fp16 with a power-of-two scale per row: rel-L2 about 3e-4 against f64,
+ * where cw_matvec_id's f32 path is about 1e-7). Ids >= n_slots give NaN rows, as in
+ * cw_matvec_id. x is 16-byte aligned, k a multiple of 4. The workspace is sized by
+ * cw_matmul_id_grouped_workspace_size (0 when the call is not supported).
+ * CW_ENOTSUP (the caller falls back to cw_matvec_id) for a dtype without a grouped kernel, more
+ * than 1024 slots, k above 8192, or rows that are not whole 256-weight super-blocks (Q8_0 and
+ * MXFP4 need only whole blocks).
+ * Replaces mv_id::matmul_id_grouped / matmul_id_piles (crates/engine/src/mv_id.rs:213-227,
+ * 282-297), which MoeMatvec takes above 8 tokens (crates/engine/src/experts.rs:2225-2239), and
+ * their Ok(false) probe. */
+size_t cw_matmul_id_grouped_workspace_size(int dtype, int64_t n, int64_t k, int64_t n_slots,
+                                           int64_t slot_stride, int x_rows_per_expert, int K, int T);
+int cw_matmul_id_grouped(int dtype, int64_t n, int64_t k, int64_t n_slots, int64_t slot_stride,
+                         const void *bank, const float *x, int x_rows_per_expert,
+                         const uint32_t *ids, int K, int T, float *out, void *ws, size_t ws_bytes,
+                         cw_stream_t stream);
+
 /* ---- activations and combine ------------------------------------------------------------ */
 
 /* h = silu(g) * u elementwise (cw_silu_mul, crates/engine/src/fuse_kernel.rs:77-85). */
@@ -182,7 +199,12 @@ typedef struct cw_moe_desc {
  * Replaces StreamedMoe::forward's resident branch (crates/engine/src/experts.rs:2562-2614)
  * and its bank branch with a slot map (3003-3015, with coachwhip_resolve). When slot_table is
  * set, picks whose expert has no slot read slot 0 and are counted in *missing (device u32,
- * may be NULL). ids_out / w_out (T x K, device, may be NULL) receive the routing. */
+ * may be NULL). ids_out / w_out (T x K, device, may be NULL) receive the routing.
+ * The workspace (256-byte aligned) must be zero-filled once before its first use, for example
+ * when it is allocated: its first CW_MOE_STATE_BYTES bytes hold the one-token layer's sync state,
+ * which every call leaves at zero again, at the same offset for every T (so one workspace serves
+ * calls of any size). Calls that overlap in time need distinct workspaces. */
+#define CW_MOE_STATE_BYTES 4096
 size_t cw_moe_workspace_size(const cw_moe_desc *desc, int T);
 int cw_moe_layer(const cw_moe_desc *desc, const float *x, const float *logits, int T, float *out,
                  uint32_t *ids_out, float *w_out, uint32_t *missing, void *ws, size_t ws_bytes,
@@ -240,10 +262,11 @@ const char *cw_gguf_meta_str(const cw_gguf *g, const char *key);
 int cw_gguf_experts(const cw_gguf *g, int layer, int which, int *dtype, int64_t *n_experts,
                     int64_t *n, int64_t *k, int64_t *expert_bytes, const void **data);
 
-/* Device-side failures since the library loaded: a one-token layer runs as one persistent
- * launch whose blocks meet at a device-wide barrier; a barrier wait that times out (a block
- * could not be scheduled) makes the call's outputs NaN and is counted here. No counterpart in
- * the reference (its layer is several dispatches). Synchronizes the device. */
+/* Device-side failures on the current device since the library loaded: a one-token layer runs as
+ * one persistent launch whose blocks meet at a device-wide barrier; a barrier wait that gives up
+ * (a block could not be scheduled; CWMOE_BARRIER_POLLS in the environment sets the polls, 131072
+ * by default) makes the call's outputs NaN and is counted here. No counterpart in the reference
+ * (its layer is several dispatches). Synchronizes the device. */
 uint32_t cw_device_errors(void);
 
 /* ---- the shrink to Q2_K ----------------------------------------------------------------- */
@@ -344,14 +367,17 @@ void cw_bank_free(cw_bank *b);
  * when more experts are needed than the bank has slots or too few slots are free (the
  * reference's Ok(None)). *n_loaded (may be NULL) receives the number of misses copied. Work
  * that reads the bank for these experts goes on stream after this call and reads only experts
- * placed here (a prefetch may since have taken any other slot, whose table entry the next
- * ensure clears); the slots placed here are kept from prefetches until the next ensure. */
+ * placed here (a prefetch may since have taken any other slot, and takes its expert out of the
+ * table first); the slots placed here are kept from prefetches until the next ensure. */
 int cw_bank_ensure(cw_bank *b, const uint32_t *needed, int n_needed, cw_stream_t stream, int *n_loaded);
 /* Reserves slots for predicted experts not yet held (Slots::reserve, experts.rs:273-285; the
  * prefetch of experts.rs:1004-1098) and copies them in on the bank's own copy stream, after
- * the work that was on the last ensure's stream when that ensure returned. Slots being filled
- * are not taken by ensure and are waited for on the stream when needed. Returns the number of
- * experts reserved (>= 0), or a negative status. */
+ * the work queued on the last ensure's stream up to this call. The experts whose slots are
+ * taken leave the device table first, in that stream's order (experts.rs:1052-1058: the slot is
+ * marked not ready and the GPU table synced before the copy), so later work there counts them
+ * missing instead of reading a slot being overwritten; that stream must still exist. Slots being
+ * filled are not taken by ensure and are waited for on the stream when needed. Returns the number
+ * of experts reserved (>= 0), or a negative status. */
 int cw_bank_prefetch(cw_bank *b, const uint32_t *predicted, int n_predicted);
 /* Fills the bank fields of a layer descriptor: dtype (CW_Q2_K for a shrunk matrix), w and
  * slot_stride of the three matrices, slot_table and n_slots (cw_moe_layer then resolves picks

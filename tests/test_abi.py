@@ -61,8 +61,31 @@ def test_moe_descriptor_validation():
     d.slot_stride[0] = d.slot_stride[1] = 512 * 8 * 66
     d.slot_stride[2] = 2048 * 2 * 82
     assert L.cw_moe_workspace_size(ctypes.byref(d), 1) > 0
+    # the decode's sync state leads every layout, so one workspace serves calls of any size
+    assert L.cw_moe_workspace_size(ctypes.byref(d), 1) < L.cw_moe_workspace_size(ctypes.byref(d), 1500)
     d.slot_stride[2] = 100
     assert L.cw_moe_workspace_size(ctypes.byref(d), 1) == 0 and b"stride" in L.cw_last_error()
+
+
+def test_matmul_id_grouped_probe_and_checks():
+    """cw_matmul_id_grouped answers "not supported" (the reference's Ok(false), mv_id.rs:298-307) for
+    shapes without a grouped kernel, so the caller falls back to cw_matvec_id; shape errors are
+    CW_EINVAL; no GPU is needed to see either."""
+    L = cw.lib()
+    F = cw.formats
+    stride = F.matrix_bytes(F.IQ2_XXS, 512, 2048)
+    ws = L.cw_matmul_id_grouped_workspace_size(F.IQ2_XXS, 512, 2048, 256, stride, 0, 8, 1500)
+    # piles and tiles for 12,000 picks, the x rows in fp16 and their scales
+    assert ws >= 12000 * 8 + 1500 * 2048 * 2 + 1500 * 4
+    assert L.cw_matmul_id_grouped_workspace_size(F.IQ2_XXS, 512, 2048, 256, stride, 1, 8, 1500) > ws
+    assert L.cw_matmul_id_grouped_workspace_size(F.IQ2_XXS, 512, 2048, 2048, stride, 0, 8, 20) == 0  # > 1024 slots
+    assert b"1024" in L.cw_last_error()
+    assert L.cw_matmul_id_grouped(F.F16, 512, 2048, 8, stride, None, None, 0, None, 8, 20, None, None, 0,
+                                  None) == _lib.CW_ENOTSUP
+    assert L.cw_matmul_id_grouped(F.IQ2_XXS, 512, 2048, 8, 100, None, None, 0, None, 8, 20, None, None, 0,
+                                  None) == _lib.CW_EINVAL                 # slot stride below the matrix
+    assert L.cw_matmul_id_grouped(F.IQ2_XXS, 512, 2048, 8, stride, None, None, 0, None, 8, 0, None, None, 0,
+                                  None) == _lib.CW_OK                     # no tokens, no work
 
 
 def test_next_row_entry_points_reject_bad_arguments():

@@ -146,6 +146,42 @@ def test_bank_prefetch_keeps_the_placed_slots():
 
 
 @pytest.mark.gpu
+def test_bank_prefetch_unlists_its_victims():
+    """A prefetch that takes the slots of held experts takes those experts out of the device table
+    in the ensure stream's order before it copies (the reference's not-ready mark and table sync,
+    crates/engine/src/experts.rs:1052-1058): work queued after it counts them missing instead of
+    reading a slot being overwritten. The prefetched experts are listed by the next ensure."""
+    import torch
+    from coachwhip_amd.bank import Bank
+    from coachwhip_amd.slots import Slots
+    print("bank: prefetch victims", flush=True)
+    rng = np.random.default_rng(7)
+    E, S = 32, 8
+    raw = _random_store(rng, E)
+    bank = Bank(raw, DTYPES, SHAPES, E, S)
+    mirror = Slots(S)
+    assert bank.ensure(list(range(S))) == S and mirror.assign(list(range(S))) is not None
+    assert bank.ensure([0, 1]) == 0 and mirror.assign([0, 1]) is not None
+    held = {e: bank.slot_of(e) for e in range(S)}
+    ready = [0 if s in (held[0], held[1]) else 1 for s in range(S)]
+    want = mirror.reserve([20, 21, 22], ready=lambda s: ready[s])
+    assert bank.prefetch([20, 21, 22]) == 3
+    assert want == [(e, bank.slot_of(e)) for e in (20, 21, 22)]
+    taken = {s for _, s in want}
+    victims = [e for e in range(S) if held[e] in taken]
+    assert len(victims) == 3 and not {0, 1} & set(victims)
+    torch.cuda.synchronize()
+    table = bank.table.cpu().numpy().view(np.uint32)
+    for e in range(S):
+        assert table[e] == (NO_SLOT if e in victims else held[e]), e
+    for e in (20, 21, 22):
+        assert table[e] == NO_SLOT                         # listed by the next ensure
+    assert bank.ensure([20, 21, 22]) == 0                  # all three were prefetched
+    assert mirror.assign([20, 21, 22]).prefetch_hits == 3
+    _check_bank(bank, mirror, raw, [20, 21, 22])
+
+
+@pytest.mark.gpu
 def test_bank_rejects_bad_calls():
     from coachwhip_amd.bank import Bank
     print("bank: errors", flush=True)

@@ -128,6 +128,9 @@ def test_rejects_malformed_files(tmp_path):
     _bad(tmp_path, G.gguf_bytes([], unknown)[0], "unknown type 99")
     ragged = [("t", F.Q8_0, (1, 48), np.zeros(34, np.uint8))]
     _bad(tmp_path, G.gguf_bytes([], ragged)[0], "not whole blocks")
+    # 2^62 f32 elements: 2^64 bytes, which a 64-bit product would wrap to 0 and pass the end check
+    huge = [("t", F.F32, (1 << 31, 1 << 31), np.zeros(4, np.uint8))]
+    _bad(tmp_path, G.gguf_bytes([], huge)[0], "larger than the file")
     _bad(tmp_path, _header(0, 1) + (1 << 40).to_bytes(8, "little") + b"k" * 64, "string length exceeds")
     arr = _header(0, 1) + (1).to_bytes(8, "little") + b"k" + (G.ARRAY).to_bytes(4, "little") + \
         (G.U32).to_bytes(4, "little") + (1 << 35).to_bytes(8, "little") + bytes(64)

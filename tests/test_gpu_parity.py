@@ -181,6 +181,40 @@ def test_matvec_id_matches_the_oracle(dtype, n, k, rows_per_expert):
     assert err <= REL_L2_F32
 
 
+@pytest.mark.parametrize("dtype,n,k", [(F.IQ2_XXS, 512, 2048), (F.IQ2_S, 2048, 512), (F.Q4_K, 512, 2048),
+                                       (F.IQ3_S, 512, 2048), (F.MXFP4, 256, 2880), (F.Q8_0, 128, 1056),
+                                       (F.Q2_K, 2048, 512)])
+@pytest.mark.parametrize("rows_per_expert", [False, True])
+def test_matmul_id_grouped_matches_the_oracle(dtype, n, k, rows_per_expert):
+    """cw_matmul_id_grouped (the reference's matmul_id_piles, which MoeMatvec takes above 8 tokens):
+    160 picks over 24 slots (one unused, one with a single pick, ragged piles), shared or per-pick
+    activation rows, against the oracle's matvec_id at the fp16-activation bar; an id past the bank
+    gives a NaN row and leaves the others alone."""
+    say("matmul_id_grouped", F.NAMES[dtype], n, k, rows_per_expert)
+    rng = np.random.default_rng(dtype * 37 + n)
+    slots, T, K = 24, 40, 4
+    raw = synth.random_blocks(dtype, slots * n * k, rng)
+    bank = ops.ExpertBank.from_blocks(raw, dtype, n, k, slots)
+    ids = rng.integers(0, slots - 2, size=(T, K), dtype=np.uint32)
+    ids[7, 2] = slots - 1                                   # a pile of one
+    x = rng.standard_normal((T * K if rows_per_expert else T, k)).astype(np.float32)
+    mv = ops.MoeMatvec(bank, K, rows_per_expert)
+    assert mv.grouped_above == 8
+    out = host(mv.forward(dev(x), dev(ids)))
+    want = O.matvec_id(dtype, n, k, raw, bank.slot_stride, x, ids, rows_per_expert)
+    err = O.rel_l2(out, want)
+    say("  rel_l2", err)
+    assert err <= REL_L2_GATE
+    assert err > REL_L2_F32 / 100          # the fp16-activation GEMM ran, not the f32 matvec
+    bad = ids.copy()
+    bad[3, 1] = slots + 5
+    out2 = host(mv.forward(dev(x), dev(bad)))
+    assert np.all(np.isnan(out2[3, 1]))
+    keep = np.ones((T, K), bool)
+    keep[3, 1] = False
+    assert np.array_equal(out2[keep].view(np.uint32), out[keep].view(np.uint32))
+
+
 def test_matvec_id_marks_out_of_range_slots():
     rng = np.random.default_rng(2)
     raw = synth.random_blocks(F.Q8_0, 2 * 8 * 64, rng)
@@ -432,6 +466,105 @@ def test_moe_layer_through_a_slot_table():
     assert O.rel_l2(host(out2), want2) <= REL_L2_F32
 
 
+@pytest.mark.parametrize("E", [512, 400])
+def test_moe_decode_through_a_slot_table(E):
+    """Config 5's one-token layer: the persistent decode kernel with 8 router logits per lane, where
+    one wave per block routes and hands the picks to the block (E = 512; E = 400 leaves the top
+    lanes partly filled). Top-10, 56 resident slots, IQ3_S gate/up and Q4_K down. Masked logits:
+    ids, weights and output equal the oracle's, nothing missing; unmasked logits: absent experts
+    read slot 0 and are counted, as the oracle does."""
+    say("moe decode bank", E)
+    rng = np.random.default_rng(500 + E)
+    K, slots = 10, 56
+    layer = synth.moe_weights(E, K, 2048, 512, (F.IQ3_S, F.IQ3_S, F.Q4_K), rng, n_slots=slots)
+    table = np.full(E, 0xFFFFFFFF, dtype=np.uint32)
+    resident = rng.choice(E, size=slots, replace=False)
+    table[resident] = rng.permutation(slots).astype(np.uint32)
+    mask = np.full(E, -1e30, dtype=np.float32)
+    mask[resident] = 0.0
+    moe = upload_layer(layer, slot_table=table)
+    missing = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for trial in range(3):
+        x = rng.standard_normal((1, 2048)).astype(np.float32)
+        logits = rng.standard_normal((1, E)).astype(np.float32) + mask
+        assert not synth.near_ties_within_top_k(logits, K)
+        missing.zero_()
+        out, ids, w = moe.forward(dev(x), dev(logits), missing=missing)
+        want, wids, ww, wmiss = O.moe_layer(layer, x, logits, slot_table=table, n_slots=slots)
+        assert wmiss == 0 and int(host(missing)[0]) == 0
+        assert np.array_equal(host(ids).view(np.uint32), wids)
+        assert np.max(np.abs(host(w) - ww)) < 1e-5
+        err = O.rel_l2(host(out), want)
+        say("  masked", trial, err)
+        assert err <= REL_L2_F32
+    x = rng.standard_normal((1, 2048)).astype(np.float32)
+    logits = rng.standard_normal((1, E)).astype(np.float32)
+    assert not synth.near_ties_within_top_k(logits, K)
+    missing.zero_()
+    out, ids, w = moe.forward(dev(x), dev(logits), missing=missing)
+    want, wids, ww, wmiss = O.moe_layer(layer, x, logits, slot_table=table, n_slots=slots)
+    assert int(host(missing)[0]) == wmiss > 0
+    assert np.array_equal(host(ids).view(np.uint32), wids)
+    err = O.rel_l2(host(out), want)
+    say("  unmasked, missing", wmiss, err)
+    assert err <= REL_L2_F32
+
+
+def test_moe_decode_barrier_gives_up_without_hanging(monkeypatch):
+    """The one-token layer's device-wide barrier waits a bounded number of polls. With the bound
+    forced to 0 from the host, every block that does not arrive last gives up at once: the call
+    completes, its outputs are NaN where a block gave up, and the device error count grows. Every
+    block still arrives, so the sync state in the workspace is back at zero: the next call on the
+    same workspace, with the default bound, matches the oracle."""
+    say("moe decode barrier give-up")
+    rng = np.random.default_rng(91)
+    E, K = 256, 8
+    layer = synth.moe_weights(E, K, 2048, 512, (F.IQ2_XXS, F.IQ2_XXS, F.IQ2_S), rng)
+    moe = upload_layer(layer)
+    x = rng.standard_normal((1, 2048)).astype(np.float32)
+    logits = rng.standard_normal((1, E)).astype(np.float32)
+    want, _, _, _ = O.moe_layer(layer, x, logits)
+    out, _, _ = moe.forward(dev(x), dev(logits))
+    assert O.rel_l2(host(out), want) <= REL_L2_F32
+    before = cw.lib().cw_device_errors()
+    monkeypatch.setenv("CWMOE_BARRIER_POLLS", "0")
+    out, _, _ = moe.forward(dev(x), dev(logits))
+    got = host(out)
+    after = cw.lib().cw_device_errors()
+    monkeypatch.delenv("CWMOE_BARRIER_POLLS")
+    say("  errors", before, "->", after, "NaN outputs", int(np.isnan(got).sum()))
+    assert after > before
+    assert np.isnan(got).any()
+    out, _, _ = moe.forward(dev(x), dev(logits))
+    assert O.rel_l2(host(out), want) <= REL_L2_F32
+    assert cw.lib().cw_device_errors() == after
+
+
+@pytest.mark.parametrize("path,T", [("gemv", 1), ("gemv", 40), ("grouped", 40)])
+def test_moe_layer_marks_out_of_range_slots(path, T, monkeypatch):
+    """A slot table entry past the bank (a corrupt table) is rejected on the device on every path:
+    the tokens that pick that expert get NaN outputs (the one-token decode, the two-kernel matvec
+    path, and the grouped path, where such a pick is in no pile), the other tokens match the
+    oracle run on the intact table."""
+    monkeypatch.setenv("CWMOE_PREFILL_MIN_TOKENS", PATHS[path])
+    say("moe out-of-range slot", path, T)
+    rng = np.random.default_rng(93 + T)
+    E, K = 64, 4
+    layer = synth.moe_weights(E, K, 2048, 512, (F.IQ2_XXS, F.IQ2_XXS, F.IQ2_S), rng)
+    table = np.arange(E, dtype=np.uint32)
+    x = rng.standard_normal((T, 2048)).astype(np.float32)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    want, wids, _, _ = O.moe_layer(layer, x, logits, slot_table=table, n_slots=E)
+    table[wids[0, 1]] = E + 3
+    moe = upload_layer(layer, slot_table=table)
+    got = host(moe.forward(dev(x), dev(logits))[0])
+    hit = np.any(wids == wids[0, 1], axis=1)
+    assert hit[0] and np.all(np.isnan(got[hit]))
+    assert np.all(np.isfinite(got[~hit]))
+    if (~hit).any():
+        assert O.rel_l2(got[~hit], want[~hit]) <= REL_L2_GATE
+
+
 def test_moe_layer_output_is_deterministic():
     rng = np.random.default_rng(77)
     layer = synth.moe_weights(64, 8, 2048, 512, (F.IQ2_XXS, F.IQ2_XXS, F.IQ2_S), rng)
@@ -443,9 +576,9 @@ def test_moe_layer_output_is_deterministic():
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
-def test_grouped_path_repeats_to_float_atomics_precision(monkeypatch):
-    # the grouped path adds each pick's weighted down row into its token's output with f32
-    # atomics, so two runs agree to rounding order only
+def test_grouped_path_output_is_deterministic(monkeypatch):
+    # the grouped path writes one down row per pick and sums each token's rows in pick order
+    # (k_combine), so two runs agree bit for bit
     monkeypatch.setenv("CWMOE_PREFILL_MIN_TOKENS", "1")
     rng = np.random.default_rng(78)
     layer = synth.moe_weights(64, 8, 2048, 512, (F.IQ2_XXS, F.IQ2_XXS, F.IQ2_S), rng)
@@ -454,7 +587,7 @@ def test_grouped_path_repeats_to_float_atomics_precision(monkeypatch):
     lg = dev(rng.standard_normal((40, 64)).astype(np.float32))
     a = host(moe.forward(x, lg)[0])
     b = host(moe.forward(x, lg)[0])
-    assert O.rel_l2(a, b) < 1e-6
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
 # ------------------------------------------------------------------------------ the shrink to Q2_K
