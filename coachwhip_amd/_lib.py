@@ -74,6 +74,7 @@ SIGNATURES = {
     "cw_slots_resolve": ([_P, _P, _I, _P, _P, _P], _I),
     "cw_moe_workspace_size": ([ctypes.POINTER(MoeDesc), _I], ctypes.c_size_t),
     "cw_moe_layer": ([ctypes.POINTER(MoeDesc), _P, _P, _I, _P, _P, _P, _P, _P, ctypes.c_size_t, _P], _I),
+    "cw_moe_layer_noalloc": ([ctypes.POINTER(MoeDesc), _P, _P, _I, _P, _P, _P, _P, _P], _I),
     "cw_shared_expert_workspace_size": ([ctypes.POINTER(SharedDesc), _I], ctypes.c_size_t),
     "cw_shared_expert": ([ctypes.POINTER(SharedDesc), _P, _I, _P, _I, _P, ctypes.c_size_t, _P], _I),
     "cw_gguf_open": ([ctypes.c_char_p], _P),

@@ -2,6 +2,7 @@
 #include <math.h>
 #include <stdlib.h>
 #include <algorithm>
+#include <mutex>
 
 #include "cw_common.h"
 #include "cw_gemv.h"
@@ -396,6 +397,36 @@ static int grouped_check(int dtype, int64_t n, int64_t k, int64_t n_slots, int64
     return CW_OK;
 }
 
+// ------------------------------------------------------------------------------ the layer without a workspace
+
+// Scratch of cw_moe_layer_noalloc, for callers that cannot allocate: one array per device, loaded
+// with the library (zero-filled, as the decode's sync state at its start must be) and kept until the
+// process ends. Every call on a device shares it: the layer's regions are rewritten by each call
+// before they are read, and the sync state is back at zero when each call's kernels end, so a call
+// needs nothing cleared; calls that overlap in time on one device race on it.
+constexpr size_t NOALLOC_SCRATCH_BYTES = CW_MOE_NOALLOC_BYTES;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+// The device address of this device's copy of `scratch`, looked up once per device (host code
+// must not use the array's name as an address: that is a host-side stand-in).
+static int noalloc_scratch(void **out) {
+    constexpr int MAX_DEV = 64;
+    static std::mutex mu;
+    static void *ptr[MAX_DEV];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV)
+        return set_error(CW_EHIP, "moe noalloc: no current device (or device %d past %d)", dev, MAX_DEV);
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return set_error(CW_EHIP, "moe noalloc: scratch address: %s", hipGetErrorString(e));
+        ptr[dev] = p;
+    }
+    *out = ptr[dev];
+    return CW_OK;
+}
+
 // out[t][i] = (accumulate ? out[t][i] : 0) + y[t][i] * sigmoid(glog[t]) (glog NULL: factor 1)
 __global__ void k_gate_scale_add(const float *y, const float *glog, int T, int H, int accumulate, float *out) {
     const int64_t n = (int64_t)T * H;
@@ -569,6 +600,20 @@ int cw_slots_resolve(const uint32_t *ids, const uint32_t *table, int n, uint32_t
 uint32_t cw_device_errors(void) {
     (void)hipDeviceSynchronize();
     return decode_barrier_errors();
+}
+
+int cw_moe_layer_noalloc(const cw_moe_desc *desc, const float *x, const float *logits, int T, float *out, uint32_t *ids_out,
+                         float *w_out, uint32_t *missing, cw_stream_t stream) {
+    int rc = check_desc(desc, T);
+    if (rc) return rc;
+    if (T == 0) return CW_OK;
+    const size_t need = layout(desc, T).total;
+    if (need > NOALLOC_SCRATCH_BYTES)
+        return set_error(CW_EINVAL, "moe noalloc: %d tokens need %zu bytes of scratch, above the %zu the library holds", T, need,
+                         NOALLOC_SCRATCH_BYTES);
+    void *ws = nullptr;
+    if ((rc = noalloc_scratch(&ws))) return rc;
+    return moe_layer(desc, x, logits, T, out, ids_out, w_out, missing, ws, NOALLOC_SCRATCH_BYTES, (hipStream_t)stream);
 }
 
 size_t cw_moe_workspace_size(const cw_moe_desc *desc, int T) {

@@ -210,6 +210,19 @@ int cw_moe_layer(const cw_moe_desc *desc, const float *x, const float *logits, i
                  uint32_t *ids_out, float *w_out, uint32_t *missing, void *ws, size_t ws_bytes,
                  cw_stream_t stream);
 
+/* cw_moe_layer without a workspace, for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation). No counterpart in the
+ * reference. Its scratch is one static array per device in the library (CW_MOE_NOALLOC_BYTES,
+ * held from the library's load until the process ends); a call whose cw_moe_workspace_size is
+ * larger is refused with CW_EINVAL (config 3's shape fits about 90 tokens). The call allocates
+ * nothing. Every call on a device shares that device's array: calls that overlap in time on one
+ * device (on different streams, or from different threads) race and must not be made. Outputs
+ * equal cw_moe_layer's bit for bit (the same kernels). */
+#define CW_MOE_NOALLOC_BYTES ((size_t)8 << 20)
+int cw_moe_layer_noalloc(const cw_moe_desc *desc, const float *x, const float *logits, int T,
+                         float *out, uint32_t *ids_out, float *w_out, uint32_t *missing,
+                         cw_stream_t stream);
+
 /* The shared expert of a Qwen3.5/3.6 MoE block: every token uses it, scaled by its own sigmoid
  * gate. Dense quantized matrices as GGUF stores ffn_{gate,up,down}_shexp: gate and up are
  * inter x hidden, down is hidden x inter. */
