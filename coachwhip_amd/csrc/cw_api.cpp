@@ -123,7 +123,7 @@ int cw_qmatmul(int dtype, const void *w, int64_t n, int64_t k, const float *x, i
     a.K = 1;
     a.out = y;
     a.out_width = (int)n;
-    return gemv_plain(dtype, a, (int)m, (hipStream_t)stream);
+    return gemv_dense(dtype, a, (int)m, (hipStream_t)stream);
 }
 
 int cw_matvec_id(int dtype, int64_t n, int64_t k, int64_t n_slots, int64_t slot_stride, const void *bank, const float *x,

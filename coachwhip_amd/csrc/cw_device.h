@@ -57,6 +57,19 @@ __device__ __forceinline__ float kv_mxfp4(uint32_t c) {
     return (float)((c & 8u) ? -mag : mag);
 }
 
+// Sums of the two halves (16 values each) of a lane's 32 activations: computed once per lane and
+// passed to the dots of formats with a minimum term (Q4_K, Q2_K), which subtract dmin * m * sum.
+__device__ __forceinline__ void half_sums(const float *x, float *xs) {
+    float a = 0.f, b = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        a += x[i];
+        b += x[16 + i];
+    }
+    xs[0] = a;
+    xs[1] = b;
+}
+
 // ---------------------------------------------------------------------------------- Q8_0
 struct FQ8_0 {
     static constexpr int BS = 32, TS = 34, LDS_BYTES = 0;
@@ -92,47 +105,71 @@ struct FQ8_0 {
 struct FQ4_K {
     static constexpr int BS = 256, TS = 144, LDS_BYTES = 0;
     static __device__ __forceinline__ uint64_t table_word(int) { return 0; }
-    struct Raw { uint32_t dd; uint32_t sc; uint32_t mn; uint4 q0, q1; int hi; };
+    // hd: d, dmin and the 12 scale bytes (the super-block's first 16 bytes, one load); sub-blocks
+    // 2c and 2c+1 share the 32 bytes qs[32c..32c+32) (low and high nibbles). The 6-bit scale and
+    // min are unpacked where they are used, so that load() only issues loads.
+    struct Raw { uint4 hd; uint4 q0, q1; int j; };
     static __device__ __forceinline__ void fill_lds(void *, int, int) {}
     static __device__ __forceinline__ Raw load(const uint8_t *row, int sb) {
         const uint8_t *b = row + TS * (sb >> 3);
         const int j = sb & 7;
         Raw r;
-        r.dd = ld_u32(b);
-        // get_scale_min_k4 (quantized/utils.rs:50-60) for sub-block j
-        const uint8_t *q = b + 4;
-        if (j < 4) {
-            r.sc = q[j] & 63;
-            r.mn = q[j + 4] & 63;
-        } else {
-            r.sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
-            r.mn = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
-        }
-        // sub-blocks 2c and 2c+1 share the 32 bytes qs[32c..32c+32): low and high nibbles
+        r.hd = ld_u128(b);
         const uint8_t *qs = b + 16 + 32 * (j >> 1);
         r.q0 = ld_u128(qs);
         r.q1 = ld_u128(qs + 16);
-        r.hi = j & 1;
+        r.j = j;
         return r;
+    }
+    static __device__ __forceinline__ uint32_t sbyte(const Raw &r, int i) {  // scale byte i (0..11)
+        return ((&r.hd.x)[1 + (i >> 2)] >> (8 * (i & 3))) & 0xFF;
+    }
+    // get_scale_min_k4 (quantized/utils.rs:50-60) for sub-block j
+    static __device__ __forceinline__ void sc_mn(const Raw &r, uint32_t &sc, uint32_t &mn) {
+        const int j = r.j;
+        if (j < 4) {
+            sc = sbyte(r, j) & 63;
+            mn = sbyte(r, j + 4) & 63;
+        } else {
+            sc = (sbyte(r, j + 4) & 0xF) | ((sbyte(r, j - 4) >> 6) << 4);
+            mn = (sbyte(r, j + 4) >> 4) | ((sbyte(r, j) >> 6) << 4);
+        }
     }
     static __device__ __forceinline__ uint32_t nib(const Raw &r, int l) {
         uint32_t w = l < 16 ? (&r.q0.x)[l >> 2] : (&r.q1.x)[(l - 16) >> 2];
-        return (w >> (8 * (l & 3) + 4 * r.hi)) & 0xFu;
+        return (w >> (8 * (l & 3) + 4 * (r.j & 1))) & 0xFu;
     }
     static __device__ __forceinline__ void dequant(const Raw &r, const void *, float *y) {
         // y = (d*sc)*q - dmin*m: both products exact, one rounding (k_quants.rs:1834-1843)
-        float d1 = h2f(r.dd & 0xFFFF) * (float)r.sc, m1 = h2f(r.dd >> 16) * (float)r.mn;
+        uint32_t sc, mn;
+        sc_mn(r, sc, mn);
+        float d1 = h2f(r.hd.x & 0xFFFF) * (float)sc, m1 = h2f(r.hd.x >> 16) * (float)mn;
 #pragma unroll
         for (int l = 0; l < 32; l++) y[l] = d1 * (float)nib(r, l) - m1;
     }
-    static __device__ __forceinline__ float dot(const Raw &r, const void *, const float *x) {
-        float s = 0.f, xs = 0.f;
+    // sum of q * x: the 32 nibbles masked to bytes 4 at a time, each byte converted to f32 directly
+    static __device__ __forceinline__ float qdot(const Raw &r, const float *x) {
+        const uint32_t sh = 4 * (r.j & 1);
+        float s = 0.f;
 #pragma unroll
-        for (int l = 0; l < 32; l++) {
-            s = fmaf((float)nib(r, l), x[l], s);
-            xs += x[l];
+        for (int k = 0; k < 8; k++) {
+            const uint32_t w = ((k < 4 ? (&r.q0.x)[k] : (&r.q1.x)[k - 4]) >> sh) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int i = 0; i < 4; i++) s = fmaf(ubyte(w, i), x[4 * k + i], s);
         }
-        return h2f(r.dd & 0xFFFF) * (float)r.sc * s - h2f(r.dd >> 16) * (float)r.mn * xs;
+        return s;
+    }
+    static constexpr bool HAS_MIN = true;
+    // xs: the half sums of x (half_sums)
+    static __device__ __forceinline__ float dot_s(const Raw &r, const void *, const float *x, const float *xs) {
+        uint32_t sc, mn;
+        sc_mn(r, sc, mn);
+        return h2f(r.hd.x & 0xFFFF) * (float)sc * qdot(r, x) - h2f(r.hd.x >> 16) * (float)mn * (xs[0] + xs[1]);
+    }
+    static __device__ __forceinline__ float dot(const Raw &r, const void *lds, const float *x) {
+        float xs[2];
+        half_sums(x, xs);
+        return dot_s(r, lds, x, xs);
     }
 };
 
@@ -172,21 +209,29 @@ struct FQ2_K {
             for (int l = 0; l < 16; l++) y[16 * h + l] = dl * (float)q(r, 16 * h + l) - ml;
         }
     }
-    static __device__ __forceinline__ float dot(const Raw &r, const void *, const float *x) {
+    static constexpr bool HAS_MIN = true;
+    // xs: the half sums of x (half_sums); the 2-bit fields masked to bytes 4 at a time
+    static __device__ __forceinline__ float dot_s(const Raw &r, const void *, const float *x, const float *xs) {
         const float d = h2f(r.dd & 0xFFFF), mn = h2f(r.dd >> 16);
         float t = 0.f;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const uint32_t s = (r.sc >> (8 * h)) & 0xFFu;
-            float sq = 0.f, sx = 0.f;
+            float sq = 0.f;
 #pragma unroll
-            for (int l = 0; l < 16; l++) {
-                sq = fmaf((float)q(r, 16 * h + l), x[16 * h + l], sq);
-                sx += x[16 * h + l];
+            for (int k = 0; k < 4; k++) {
+                const uint32_t w = ((h == 0 ? (&r.q0.x)[k] : (&r.q1.x)[k]) >> r.sh) & 0x03030303u;
+#pragma unroll
+                for (int i = 0; i < 4; i++) sq = fmaf(ubyte(w, i), x[16 * h + 4 * k + i], sq);
             }
-            t += d * (float)(s & 0xF) * sq - mn * (float)(s >> 4) * sx;
+            t += d * (float)(s & 0xF) * sq - mn * (float)(s >> 4) * xs[h];
         }
         return t;
+    }
+    static __device__ __forceinline__ float dot(const Raw &r, const void *lds, const float *x) {
+        float xs[2];
+        half_sums(x, xs);
+        return dot_s(r, lds, x, xs);
     }
 };
 
@@ -352,7 +397,9 @@ struct FIQ3_S {
     static __device__ __forceinline__ uint64_t table_word(int i) {
         return (uint64_t)c_iq3s_grid[2 * i] | ((uint64_t)c_iq3s_grid[2 * i + 1] << 32);
     }
-    struct Raw { uint32_t d; uint2 qs; uint32_t qh; uint32_t sg; uint32_t sc; };
+    // sc: the scales byte holding this sub-block's nibble at bit `sh` (unpacked where used, so that
+    // load() only issues loads)
+    struct Raw { uint32_t d; uint2 qs; uint32_t qh; uint32_t sg; uint32_t sc; uint32_t sh; };
     static __device__ __forceinline__ void fill_lds(void *lds, int tid, int nt) {
         uint32_t *t = (uint32_t *)lds;
         for (int i = tid; i < 512; i += nt) t[i] = c_iq3s_grid[i];
@@ -365,7 +412,8 @@ struct FIQ3_S {
         r.qs = ld_u64(b + 2 + 8 * ib);            // low 8 bits of eight grid indices
         r.qh = b[66 + ib];                        // their 9th bits
         r.sg = ld_u32(b + 74 + 4 * ib);           // one sign bit per weight
-        r.sc = (b[106 + (ib >> 1)] >> (4 * (ib & 1))) & 0xF;
+        r.sc = b[106 + (ib >> 1)];
+        r.sh = 4 * (ib & 1);
         return r;
     }
     static __device__ __forceinline__ uint32_t gidx(const Raw &r, int g) {
@@ -374,7 +422,7 @@ struct FIQ3_S {
     }
     static __device__ __forceinline__ void dequant(const Raw &r, const void *lds, float *y) {
         const uint32_t *grid = (const uint32_t *)lds;
-        float dl = h2f(r.d) * (float)(1 + 2 * (int)r.sc);
+        float dl = h2f(r.d) * (float)(1 + 2 * (int)((r.sc >> r.sh) & 0xF));
 #pragma unroll
         for (int g = 0; g < 8; g++) {
             uint32_t gw = grid[gidx(r, g)];
@@ -394,7 +442,7 @@ struct FIQ3_S {
 #pragma unroll
             for (int i = 0; i < 4; i++) s = fmaf(ubyte(gw, i), flip(x[4 * g + i], r.sg, 4 * g + i), s);
         }
-        return s * (h2f(r.d) * (float)(1 + 2 * (int)r.sc));
+        return s * (h2f(r.d) * (float)(1 + 2 * (int)((r.sc >> r.sh) & 0xF)));
     }
 };
 
@@ -420,5 +468,16 @@ struct TableRegs {
         }
     }
 };
+
+// a format's dot with the lane's half sums of x precomputed (used only by formats with a minimum term)
+template <class F, class = void>
+struct HasMin { static constexpr bool value = false; };
+template <class F>
+struct HasMin<F, decltype((void)F::HAS_MIN)> { static constexpr bool value = F::HAS_MIN; };
+template <class F>
+__device__ __forceinline__ float dot_xs(const typename F::Raw &r, const void *lds, const float *x, const float *xs) {
+    if constexpr (HasMin<F>::value) return F::dot_s(r, lds, x, xs);
+    else return F::dot(r, lds, x);
+}
 
 }  // namespace cw

@@ -20,6 +20,8 @@ struct GemvArgs {
 };
 
 int gemv_plain(int dtype, const GemvArgs &a, int picks, hipStream_t s);
+// y[t] = W x[t] for t < m rows of x and one matrix (QMatMul at small m): x staged once per block
+int gemv_dense(int dtype, const GemvArgs &a, int m, hipStream_t s);
 int dequantize(int dtype, const void *blocks, int64_t n_elems, float *out, hipStream_t s);
 int max_gemv_k();
 

@@ -73,6 +73,67 @@ __global__ __launch_bounds__(256) void k_gemv(const GemvArgs a) {
     }
 }
 
+// Dense matvec (one matrix, blockIdx.y = row t of x). Each wave takes P consecutive passes of
+// 64/LPR rows and requests all of their weight bytes at once; the block stages x[t] in LDS once
+// (every lane needs its slice of x for every row it visits: one copy per block instead of one per
+// wave) with the x loads issued behind the weight loads, so a wave waits for its memory once. Every
+// load is unconditional, from a clamped address: a load under a branch makes the compiler wait
+// for it at the branch's end, which serializes the round trips.
+template <class Fmt, int LPR, int NX, int P>
+__global__ __launch_bounds__(256) void k_gemv_dense(const GemvArgs a) {
+    __shared__ __align__(16) uint8_t lds[Fmt::LDS_BYTES > 0 ? Fmt::LDS_BYTES : 16];
+    extern __shared__ __align__(16) float xs[];
+    constexpr int RPW = 64 / LPR, XV = (NX * LPR * 8 + 255) / 256;  // float4 pieces of x per thread
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane % LPR, rsub = lane / LPR;
+    const int t = blockIdx.y;
+    const int r0 = (blockIdx.x * 4 + wave) * P * RPW + rsub;
+    typename Fmt::Raw raw[P][NX];
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+        const int r = min(r0 + p * RPW, a.n - 1);  // rows past the matrix: unused
+#pragma unroll
+        for (int i = 0; i < NX; i++) {
+            const int sb = sub + i * LPR;
+            raw[p][i] = Fmt::load(a.w0 + (int64_t)r * a.row_bytes, sb < a.nsb ? sb : a.nsb - 1);
+        }
+    }
+    const float4 *xg = (const float4 *)(a.x + (int64_t)t * a.k);
+    const int nx4 = a.k / 4;
+    float4 xv[XV];
+#pragma unroll
+    for (int v = 0; v < XV; v++) {
+        const int i = threadIdx.x + 256 * v;
+        xv[v] = xg[i < nx4 ? i : nx4 - 1];
+    }
+    // unconditional stores: xs holds 256 * XV pieces, those past x are never read
+#pragma unroll
+    for (int v = 0; v < XV; v++) ((float4 *)xs)[threadIdx.x + 256 * v] = xv[v];
+    Fmt::fill_lds(lds, threadIdx.x, blockDim.x);
+    __syncthreads();
+    float xr[NX][32], xsum[NX][2];
+#pragma unroll
+    for (int i = 0; i < NX; i++) {
+        const int sb = sub + i * LPR;
+        const float4 *src = (const float4 *)(xs + 32 * (sb < a.nsb ? sb : 0));
+#pragma unroll
+        for (int v = 0; v < 8; v++) *(float4 *)(xr[i] + 4 * v) = src[v];
+        half_sums(xr[i], xsum[i]);
+    }
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+        const int r = r0 + p * RPW;
+        float g = 0.f;
+#pragma unroll
+        for (int i = 0; i < NX; i++) {
+            const int sb = sub + i * LPR;
+            if (r < a.n && sb < a.nsb) g += dot_xs<Fmt>(raw[p][i], lds, xr[i], xsum[i]);
+        }
+        g = group_sum<LPR>(g);
+        if (sub == 0 && r < a.n) a.out[(int64_t)t * a.out_width + r] = g;
+    }
+}
+
 template <class Fmt>
 __global__ __launch_bounds__(256) void k_dequant(const uint8_t *blocks, int64_t n_sub, float *out) {
     __shared__ __align__(16) uint8_t lds[Fmt::LDS_BYTES > 0 ? Fmt::LDS_BYTES : 16];
@@ -135,6 +196,49 @@ static dim3 rows_grid(const GemvArgs &a, int picks) {
 int gemv_plain(int dtype, const GemvArgs &a, int picks, hipStream_t s) {
     if (picks == 0 || a.n == 0) return CW_OK;
     return launch_fmt(dtype, a, rows_grid(a, picks), 256, 0, s);
+}
+
+template <class Fmt, int LPR, int NX>
+static int dense_launch(const GemvArgs &a, int m, hipStream_t s) {
+    constexpr int RPW = 64 / LPR;
+    // about 2048 waves (two 4-wave blocks per CU) of 1, 2 or 4 passes each
+    const int64_t passes_all = (a.n + RPW - 1) / RPW;
+    const int64_t want = (passes_all + 2047) / 2048;
+    const int P = want <= 1 ? 1 : want <= 2 ? 2 : 4;
+    const int64_t waves = (passes_all + P - 1) / P;
+    const dim3 grid((unsigned)((waves + 3) / 4), (unsigned)m);
+    const size_t shmem = (size_t)256 * 16 * ((NX * LPR * 8 + 255) / 256);  // x staging, padded (k_gemv_dense)
+    if (P == 1) hipLaunchKernelGGL((k_gemv_dense<Fmt, LPR, NX, 1>), grid, dim3(256), shmem, s, a);
+    else if (P == 2) hipLaunchKernelGGL((k_gemv_dense<Fmt, LPR, NX, 2>), grid, dim3(256), shmem, s, a);
+    else hipLaunchKernelGGL((k_gemv_dense<Fmt, LPR, NX, 4>), grid, dim3(256), shmem, s, a);
+    return check_launch("k_gemv_dense");
+}
+
+template <class Fmt>
+static int dense_lpr(const GemvArgs &a, int m, hipStream_t s) {
+    const int lpr = pick_lpr(a.nsb);
+    const int nx = (a.nsb + lpr - 1) / lpr;
+#define CW_DENSE_CASE(L, X) \
+    if (lpr == L && nx == X) return dense_launch<Fmt, L, X>(a, m, s);
+    CW_DENSE_CASE(8, 1) CW_DENSE_CASE(16, 1) CW_DENSE_CASE(32, 1) CW_DENSE_CASE(64, 1)
+    CW_DENSE_CASE(64, 2) CW_DENSE_CASE(64, 3) CW_DENSE_CASE(64, 4)
+#undef CW_DENSE_CASE
+    return set_error(CW_ENOTSUP, "gemv: rows of %d weights exceed the %d-weight limit", a.k, 64 * 4 * 32);
+}
+
+int gemv_dense(int dtype, const GemvArgs &a, int m, hipStream_t s) {
+    if (m == 0 || a.n == 0) return CW_OK;
+    if (a.k % 4) return set_error(CW_ENOTSUP, "gemv: row of %d weights is not whole float4s", a.k);
+    switch (dtype) {
+    case CW_Q8_0: return dense_lpr<FQ8_0>(a, m, s);
+    case CW_Q2_K: return dense_lpr<FQ2_K>(a, m, s);
+    case CW_Q4_K: return dense_lpr<FQ4_K>(a, m, s);
+    case CW_MXFP4: return dense_lpr<FMXFP4>(a, m, s);
+    case CW_IQ2_XXS: return dense_lpr<FIQ2_XXS>(a, m, s);
+    case CW_IQ2_S: return dense_lpr<FIQ2_S>(a, m, s);
+    case CW_IQ3_S: return dense_lpr<FIQ3_S>(a, m, s);
+    default: return set_error(CW_ENOTSUP, "gemv: dtype %d is not supported", dtype);
+    }
 }
 
 int dequantize(int dtype, const void *blocks, int64_t n_elems, float *out, hipStream_t s) {

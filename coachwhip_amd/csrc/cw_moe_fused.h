@@ -29,7 +29,7 @@ struct MoeArgs {
 };
 
 // workspace bytes of the decode's sync state, at the start of every MoE-layer workspace
-constexpr size_t DECODE_STATE_BYTES = 4096;
+constexpr size_t DECODE_STATE_BYTES = 8192;
 
 int moe_gateup(int dtype, const MoeArgs &a, int T, hipStream_t s);
 // the whole layer for one token in one launch (CW_ENOTSUP for shapes it does not cover)

@@ -190,11 +190,12 @@ __global__ __launch_bounds__(256) void k_moe_down(const MoeArgs a) {
 
 // Device-wide barrier of the persistent decode kernel. Its state (DecodeBarrier) lives in the
 // caller's workspace, which the caller zero-fills once, and every call leaves it at zero again, so
-// calls with distinct workspaces are independent. Blocks first arrive on a counter of their XCD
-// (blocks go to the 8 XCDs round-robin, blockIdx % 8); the last of each XCD clears that counter and
-// arrives on a top counter, and the last of those clears it and bumps the generation every block
-// waits on. Splitting the arrivals over 9 counters, 128 bytes apart, keeps them from serializing on
-// one address (one counter for 512 blocks measured ~15 us, this ~2.3 us). Everything the blocks
+// calls with distinct workspaces are independent. Blocks first arrive on one of 32 counters
+// (blockIdx % 32: blocks go to the 8 XCDs round-robin, so each counter's blocks share an XCD); the
+// last of each clears it and arrives on a top counter, and the last of those clears it and bumps
+// the generation every block waits on. Splitting the arrivals over 33 counters, 128 bytes apart,
+// keeps them from serializing on one address (a microbenchmark of 512 blocks: one counter 6.1 us
+// above an empty launch, 8 counters 1.4 us, 32 counters 1.0 us). Everything the blocks
 // exchange through memory inside the kernel is written and read with agent-scope atomics, which go
 // to the coherence point, so the counters need no fences: an agent-scope release / acquire pair
 // here (L2 write-back and invalidate in every block) measured 3x slower, and so did polling all 8
@@ -202,7 +203,7 @@ __global__ __launch_bounds__(256) void k_moe_down(const MoeArgs a) {
 // (g_decode_errors) instead of hanging; every block still arrives exactly once, so the state is
 // back at zero (and the generation one further) when the kernel ends, timed out or not.
 struct DecodeBarrier {
-    uint32_t sub[8][32];
+    uint32_t sub[32][32];
     uint32_t top[32];
     uint32_t gen[32];
 };
@@ -221,8 +222,8 @@ __device__ bool grid_barrier(DecodeBarrier *b, uint32_t nblocks, uint32_t polls)
     __shared__ int ok;
     if (threadIdx.x == 0) {
         const uint32_t gen = __hip_atomic_load(&b->gen[0], __ATOMIC_RELAXED, CW_AGENT);
-        const uint32_t x = blockIdx.x & 7;
-        const uint32_t nsub = (nblocks - x + 7) / 8, nx = nblocks < 8 ? nblocks : 8;
+        const uint32_t x = blockIdx.x & 31;
+        const uint32_t nsub = (nblocks - x + 31) / 32, nx = nblocks < 32 ? nblocks : 32;
         bool last = false;
         if (__hip_atomic_fetch_add(&b->sub[x][0], 1u, __ATOMIC_RELAXED, CW_AGENT) == nsub - 1) {
             // the reset only has to land before the next call, which the kernel's end ensures
@@ -295,7 +296,6 @@ __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
     TableRegs<FG> tg;
     TableRegs<FD> td;
     tg.load(threadIdx.x);
-    td.load(threadIdx.x);
     const int subg = lane % LG, rsg = lane / LG, nsbg = a.H / 32;
     float xr[XG][32];
     load_xs<XG>(xr, a.x, subg, LG, nsbg);
@@ -374,8 +374,10 @@ __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
             }
         }
     }
+    // down's table is needed only after the barrier: its loads go out behind the weights', and
+    // it is stored to LDS once the gate/up items are done
+    td.load(threadIdx.x);
     tg.store(ldsg, threadIdx.x);
-    td.store(ldsd, threadIdx.x);
     __syncthreads();
 
     for (int it = gwave; it < n_items; it += total_waves) {
@@ -419,6 +421,7 @@ __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
         store_coherent(a.h + (int64_t)j * a.P + a.I + (c - j * (a.P - a.I)), 0.f);
     }
 
+    td.store(ldsd, threadIdx.x);
     const bool ok = grid_barrier((DecodeBarrier *)a.state, gridDim.x, a.polls);
 
     // every hidden row into LDS once per block, read at the coherence point (16-byte buffer

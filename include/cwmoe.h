@@ -204,7 +204,7 @@ typedef struct cw_moe_desc {
  * when it is allocated: its first CW_MOE_STATE_BYTES bytes hold the one-token layer's sync state,
  * which every call leaves at zero again, at the same offset for every T (so one workspace serves
  * calls of any size). Calls that overlap in time need distinct workspaces. */
-#define CW_MOE_STATE_BYTES 4096
+#define CW_MOE_STATE_BYTES 8192
 size_t cw_moe_workspace_size(const cw_moe_desc *desc, int T);
 int cw_moe_layer(const cw_moe_desc *desc, const float *x, const float *logits, int T, float *out,
                  uint32_t *ids_out, float *w_out, uint32_t *missing, void *ws, size_t ws_bytes,
