@@ -270,6 +270,7 @@ __device__ __forceinline__ void store_coherent(float *p, float v) {
 // spilled registers); the other instances fit already.
 template <class FG, int LG, int XG, class FD, int LD, int XD, int PER, int PPW>
 __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
+    constexpr int RI = 2;  // rows (of RPG) per gate/up item: 4 measured slower (config 4 spills, config 5 too)
     __shared__ __align__(16) uint8_t ldsg[FG::LDS_BYTES > 0 ? FG::LDS_BYTES : 16];
     __shared__ __align__(16) uint8_t ldsd[FD::LDS_BYTES > 0 ? FD::LDS_BYTES : 16];
     constexpr int RPG = 64 / LG, RPD = 64 / LD;
@@ -328,27 +329,37 @@ __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
         my_slot = lane < K ? pick_slot[lane] : 0xFFFFFFFFu;
     }
 
-    // gate / up items (pick j, 2*RPG rows) spread over every wave of the grid; the first
-    // item's weights and the block's first down rows are requested right after routing
-    const int row_items = (a.I + 2 * RPG - 1) / (2 * RPG);
+    // gate / up items (pick j, RI*RPG rows) spread over every wave of the grid; the first item's
+    // weights and the block's first down rows are requested right after routing. With one sub-block
+    // per lane the loads are unconditional, from a clamped row and sub-block: a load under a
+    // per-lane branch is waited for at the branch's end (config 3 layer 13.15 -> 12.92 us, config 5
+    // 17.97 -> 17.08). Rows of more than 64 sub-blocks keep the conditional form: most lanes have no
+    // second sub-block, and the unconditional form measured 2.6-4 us slower for config 4.
+    const int row_items = (a.I + RI * RPG - 1) / (RI * RPG);
     const int n_items = K * row_items;
     const int gwave = blockIdx.x * 4 + wave, total_waves = gridDim.x * 4;
-    typename FG::Raw rg[2][XG], ru[2][XG];
+    typename FG::Raw rg[RI][XG], ru[RI][XG];
     auto load_item = [&](int it) {
-        const int j = it / row_items, r0 = (it - j * row_items) * 2 * RPG + rsg;
+        const int j = it / row_items, r0 = (it - j * row_items) * RI * RPG + rsg;
         const uint32_t slot = __shfl(my_slot, j);
         const uint32_t sl = slot == 0xFFFFFFFFu ? 0 : slot;
         const uint8_t *bg = a.wg + (int64_t)sl * a.sg;
         const uint8_t *bu = a.wu + (int64_t)sl * a.su;
 #pragma unroll
-        for (int q = 0; q < 2; q++) {
-            const int r = r0 + q * RPG;
+        for (int q = 0; q < RI; q++) {
+            if constexpr (XG == 1) {
+                const int r = min(r0 + q * RPG, a.I - 1), sb = min(subg, nsbg - 1);
+                rg[q][0] = FG::load(bg + (int64_t)r * a.rbg, sb);
+                ru[q][0] = FG::load(bu + (int64_t)r * a.rbg, sb);
+            } else {
+                const int r = r0 + q * RPG;
 #pragma unroll
-            for (int i = 0; i < XG; i++) {
-                const int sb = subg + i * LG;
-                if (r < a.I && sb < nsbg) {
-                    rg[q][i] = FG::load(bg + (int64_t)r * a.rbg, sb);
-                    ru[q][i] = FG::load(bu + (int64_t)r * a.rbg, sb);
+                for (int i = 0; i < XG; i++) {
+                    const int sb = subg + i * LG;
+                    if (r < a.I && sb < nsbg) {
+                        rg[q][i] = FG::load(bg + (int64_t)r * a.rbg, sb);
+                        ru[q][i] = FG::load(bu + (int64_t)r * a.rbg, sb);
+                    }
                 }
             }
         }
@@ -364,7 +375,10 @@ __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
         for (int q = 0; q < PPW; q++) {
             const int j = wave + 4 * q;
             dslot[q] = __shfl(my_slot, j < K ? j : 0);
-            if (j < K && dslot[q] != 0xFFFFFFFFu && r < a.H) {
+            if constexpr (XD == 1) {  // unconditional (unused past K)
+                const uint8_t *base = a.wd + (int64_t)(dslot[q] == 0xFFFFFFFFu ? 0 : dslot[q]) * a.sd + (int64_t)min(r, a.H - 1) * a.rbd;
+                draw[q][0] = FD::load(base, min(subd, nsbd - 1));
+            } else if (j < K && dslot[q] != 0xFFFFFFFFu && r < a.H) {
                 const uint8_t *base = a.wd + (int64_t)dslot[q] * a.sd + (int64_t)r * a.rbd;
 #pragma unroll
                 for (int i = 0; i < XD; i++) {
@@ -382,12 +396,12 @@ __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
 
     for (int it = gwave; it < n_items; it += total_waves) {
         if (it != gwave) load_item(it);
-        const int j = it / row_items, r0 = (it - j * row_items) * 2 * RPG + rsg;
+        const int j = it / row_items, r0 = (it - j * row_items) * RI * RPG + rsg;
         const uint32_t slot = __shfl(my_slot, j);
         const uint32_t expert = __shfl(rid, j);
         const bool bad = slot == 0xFFFFFFFFu;
 #pragma unroll
-        for (int q = 0; q < 2; q++) {
+        for (int q = 0; q < RI; q++) {
             const int r = r0 + q * RPG;
             float g = 0.f, u = 0.f;
 #pragma unroll
@@ -565,27 +579,22 @@ static int by_fmt(int dtype, const MoeArgs &a, int T, hipStream_t s) {
 static size_t decode_hidden_lds(const MoeArgs &a) { return (size_t)a.K * (a.P / 32) * 36 * sizeof(float); }
 static constexpr size_t DECODE_MAX_HIDDEN_LDS = 64 * 1024;
 
-template <class FG, int LG, int XG, class FD, int LD, int XD, int PPW>
-static int decode_launch(const MoeArgs &a, hipStream_t s) {
-    // lanes hold 4, 8 or 16 router logits each (E up to 256, 512, 1024)
-    auto kern = a.E <= 256   ? k_moe_decode<FG, LG, XG, FD, LD, XD, 4, PPW>
-                : a.E <= 512 ? k_moe_decode<FG, LG, XG, FD, LD, XD, 8, PPW>
-                             : k_moe_decode<FG, LG, XG, FD, LD, XD, 16, PPW>;
-    const size_t lds = decode_hidden_lds(a);
-    // every block must be resident at once for the barrier: size the grid from the occupancy of
-    // this kernel at this call's LDS size on the current device (a few entries remembered, under
-    // a lock, so concurrent callers never size a grid from another call's entry)
+// Grid of the persistent decode kernel: every block must be resident at once for the barrier, so
+// the grid is sized from the occupancy of this kernel at this call's LDS size on the current
+// device (a few entries remembered, under a lock, so concurrent callers never size a grid from
+// another call's entry). 0 on failure.
+template <class Kern>
+static int decode_grid(Kern kern, int which, const MoeArgs &a, size_t lds, int want) {
     struct Occ {
         int dev = -1, which = -1;
         size_t lds = 0;
         int per_cu = 0, cus = 0;
     };
     static std::mutex mu;
-    static Occ cache[4];
+    static Occ cache[8];
     static int next = 0;
-    const int which = a.E <= 256 ? 0 : a.E <= 512 ? 1 : 2;
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return set_error(CW_EHIP, "moe decode: no current device");
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
     Occ o;
     {
         std::lock_guard<std::mutex> lock(mu);
@@ -598,16 +607,31 @@ static int decode_launch(const MoeArgs &a, hipStream_t s) {
         o.lds = lds;
         if (hipDeviceGetAttribute(&o.cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
             hipOccupancyMaxActiveBlocksPerMultiprocessor(&o.per_cu, kern, 256, lds) != hipSuccess || o.per_cu < 1)
-            return set_error(CW_EHIP, "moe decode: occupancy query failed");
+            return 0;
         std::lock_guard<std::mutex> lock(mu);
-        cache[next++ & 3] = o;
+        cache[next++ & 7] = o;
     }
+    const int grid = o.per_cu * o.cus;
+    return grid < want ? grid : want;
+}
+
+template <class FG, int LG, int XG, class FD, int LD, int XD, int PER, int PPW>
+static int decode_launch_per(const MoeArgs &a, int which, hipStream_t s) {
+    const size_t lds = decode_hidden_lds(a);
     const int RPD = 64 / LD;
-    const int want = (a.H + RPD - 1) / RPD;
-    int grid = o.per_cu * o.cus;
-    if (grid > want) grid = want;
+    auto kern = k_moe_decode<FG, LG, XG, FD, LD, XD, PER, PPW>;
+    const int grid = decode_grid(kern, which, a, lds, (a.H + RPD - 1) / RPD);
+    if (!grid) return set_error(CW_EHIP, "moe decode: occupancy query failed");
     hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, s, a);
     return check_launch("k_moe_decode");
+}
+
+template <class FG, int LG, int XG, class FD, int LD, int XD, int PPW>
+static int decode_launch(const MoeArgs &a, hipStream_t s) {
+    // lanes hold 4, 8 or 16 router logits each (E up to 256, 512, 1024)
+    if (a.E <= 256) return decode_launch_per<FG, LG, XG, FD, LD, XD, 4, PPW>(a, 0, s);
+    if (a.E <= 512) return decode_launch_per<FG, LG, XG, FD, LD, XD, 8, PPW>(a, 1, s);
+    return decode_launch_per<FG, LG, XG, FD, LD, XD, 16, PPW>(a, 2, s);
 }
 
 template <class FG, int LG, int XG, class FD, int LD, int XD>
