@@ -29,10 +29,46 @@ def log(*a):
 
 
 COPY_BYTES = 1 << 30
+SPIN_CYCLES = 20_000_000      # torch.cuda._sleep: ~10 ms of one wave's spin at the shader clock
+
+
+def host_cpu():
+    """The host the CPU baseline runs on: CPU model, logical CPUs and physical cores in this process's
+    affinity mask, and the x86 vector tiers candle's CPU path selects among
+    (vendor/candle-core/src/quantized/repack_x86.rs: AVX512-VNNI, else AVX-VNNI, else AVX2; AMX for
+    Q4_K from 32 rows). Candle's default thread count is the physical cores
+    (vendor/candle-core/src/utils.rs:382-421)."""
+    allowed = sorted(os.sched_getaffinity(0))
+    model, flags, cores, cur = "unknown", set(), {}, {}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f.read().splitlines() + [""]:
+                if not line.strip():
+                    if "processor" in cur:
+                        cores[int(cur["processor"])] = (cur.get("physical id", "0"), cur.get("core id", cur["processor"]))
+                    cur = {}
+                    continue
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                cur[k] = v
+                if k == "model name":
+                    model = v
+                elif k == "flags" and not flags:
+                    flags = set(v.split())
+    except OSError:
+        pass
+    physical = len({cores.get(c, (0, c)) for c in allowed}) or len(allowed)
+    isa = [f for f in ("avx2", "fma", "avx512f", "avx512_vnni", "avx512bw", "avx_vnni", "amx_tile", "amx_int8") if f in flags]
+    tier = ("avx512_vnni" if {"avx512f", "avx512_vnni"} <= flags else "avx_vnni" if "avx_vnni" in flags
+            else "avx2" if "avx2" in flags else "scalar")
+    return {"model": model, "logical": len(allowed), "physical": physical, "isa": isa, "tier": tier,
+            "amx": {"amx_tile", "amx_int8"} <= flags}
 
 
 TRAFFIC_PROFILE = "profiles/moe_c3_hbm_traffic.md"
 TRAFFIC_PROFILE_C4 = "profiles/moe_c4_kernels.md"
+TRAFFIC_PROFILE_C5 = "profiles/bank_c5_kernels.md"
+TRAFFIC_PROFILE_DENSE = "profiles/dense_qmatmul_kernels.md"
 
 
 def measured_traffic(root, profile=TRAFFIC_PROFILE):
@@ -205,7 +241,9 @@ def bench_c5(args, torch, np, dev):
 
     cpu = None
     if not args.no_cpu_baseline:
-        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        host = host_cpu()
+        O.set_threads(host["physical"])
+        threads = O.get_threads()
         n, t_cpu = 0, 0.0
         while t_cpu < min(args.cpu_seconds, 5.0) and n < 1000:
             lg = logits_all[n % total, 0].cpu().numpy()
@@ -213,7 +251,7 @@ def bench_c5(args, torch, np, dev):
             O.moe_layer(host_layer, x0, lg)
             t_cpu += time.perf_counter() - t1
             n += 1
-        cpu = {"value": t_cpu / n * 1e6, "unit": "us/layer", "cores": threads, "kind": "port",
+        cpu = {"value": t_cpu / n * 1e6, "unit": "us/layer", "cores": threads, "host": host, "kind": "port",
                "sample": "%d decode calls (T=1) of the C oracle MoE layer on layer 0's host store" % n}
     line = {
         "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -225,7 +263,9 @@ def bench_c5(args, torch, np, dev):
                    "slots": S, "tokens": 1},
         "us_per_layer": round(us_per_layer, 3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(os.path.dirname(os.path.abspath(__file__)), TRAFFIC_PROFILE_C5),
+                     "traffic_source": TRAFFIC_PROFILE_C5,
                      "kernel": "MoE decode layer through the bank's slot table", "bytes_per_launch": layer_bytes},
         "streaming": streaming, "parity": parity, "cpu_baseline": cpu,
     }
@@ -317,7 +357,9 @@ def bench_c4(args, torch, np, dev):
 
     cpu = None
     if not args.no_cpu_baseline:
-        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        host = host_cpu()
+        O.set_threads(host["physical"])
+        threads = O.get_threads()
         n, t_cpu = 0, 0.0
         while t_cpu < min(args.cpu_seconds, 5.0) and n < 1000:
             lg = logits_all[n % total, 0].cpu().numpy()
@@ -325,7 +367,7 @@ def bench_c4(args, torch, np, dev):
             O.moe_layer(host_layer, x0, lg)
             t_cpu += time.perf_counter() - t1
             n += 1
-        cpu = {"value": t_cpu / n * 1e6, "unit": "us/layer", "cores": threads, "kind": "port",
+        cpu = {"value": t_cpu / n * 1e6, "unit": "us/layer", "cores": threads, "host": host, "kind": "port",
                "sample": "%d decode calls (T=1) of the C oracle MoE layer (MXFP4 dequantize, f64 dots) on layer 0; "
                          "candle's own MXFP4 CPU path quantizes x to Q8_0 and is not restated" % n}
     line = {
@@ -349,8 +391,10 @@ def bench_c4(args, torch, np, dev):
 def bench_dense(args, torch, np, dev):
     """Configs 1 and 2: one quantized matrix, y = x . W^T (QMatMul): Q8_0 2048 x 2048 at M = 1, and
     Q4_K 4096 x 4096 at M in {1, 16, 128, 512}. Each case captures one call per copy of the matrix
-    (copies past ~600 MB, so the Infinity Cache cannot serve them) in a graph and times its replay;
-    achieved rates use the algorithmic bytes (matrix + x + y) and flops (2 M n k), against HBM
+    (copies past ~600 MB, so the Infinity Cache cannot serve them) in a graph and times its replay
+    behind a bounded GPU spin, so the calls run back to back on the device (us); us_host_fed is the
+    same replay started on an idle device, where a call of a few µs waits for the host to submit
+    the next one. Achieved rates use the algorithmic bytes (matrix + x + y) and flops (2 M n k), against HBM
     (8 TB/s) or fp16 MFMA (2.5 PFLOP/s), whichever bounds the case. Parity of each case against
     the f64 oracle; the CPU baseline is the oracle's restatement of candle's x86 path (activations
     quantized to Q8_K / Q8_0, integer block dots) on the host's threads."""
@@ -360,7 +404,9 @@ def bench_dense(args, torch, np, dev):
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed)
     rng = np.random.default_rng(args.seed)
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    host = host_cpu()
+    O.set_threads(host["physical"])
+    threads = O.get_threads()
     cases = []
     for name, dt, n, k, ms in (("config 1: Q8_0 GEMV", F.Q8_0, 2048, 2048, (1,)),
                                ("config 2: Q4_K matmul", F.Q4_K, 4096, 4096, (1, 16, 128, 512))):
@@ -386,14 +432,32 @@ def bench_dense(args, torch, np, dev):
             g.replay()
             stop.record()
             torch.cuda.synchronize()
+            us_fed = start.elapsed_time(stop) * 1e3 / copies
+            # A call of a few µs finishes before the host has submitted the next node of the
+            # replayed graph, so the replay above measures the host's submission rate. Timed
+            # again behind a bounded GPU spin that outlasts the submission, the calls run back to
+            # back and the events measure the device.
+            spin0 = torch.cuda.Event(enable_timing=True)
+            spin0.record()
+            torch.cuda._sleep(SPIN_CYCLES)
+            start.record()
+            t_host = time.perf_counter()
+            g.replay()
+            t_host = time.perf_counter() - t_host
+            stop.record()
+            torch.cuda.synchronize()
             us = start.elapsed_time(stop) * 1e3 / copies
+            spin_us = spin0.elapsed_time(start) * 1e3
+            if t_host * 1e6 >= spin_us:
+                log("warning: the graph's submission (%.0f us) outlasted the spin (%.0f us)" % (t_host * 1e6, spin_us))
             nbytes = wb + 4 * m * k + 4 * m * n
             flops = 2.0 * m * n * k
             t_hbm, t_mfma = nbytes / (HBM_PEAK_GBS * 1e9), flops / (MFMA_PEAK_F16_TFLOPS * 1e12)
             bound = "hbm" if t_hbm >= t_mfma else "mfma"
             case = {"case": name, "m": m, "n": n, "k": k, "us": round(us, 3),
                     "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "tflops": round(flops / (us * 1e-6) / 1e12, 2),
-                    "bound": bound, "roofline_frac": round(max(t_hbm, t_mfma) / (us * 1e-6), 4), "rel_l2": err}
+                    "bound": bound, "roofline_frac": round(max(t_hbm, t_mfma) / (us * 1e-6), 4), "rel_l2": err,
+                    "us_host_fed": round(us_fed, 3)}
             if not args.no_cpu_baseline:
                 O.candle_matmul(dt, host_w, n, k, xh)
                 reps, t_cpu = 0, 0.0
@@ -414,10 +478,12 @@ def bench_dense(args, torch, np, dev):
         "dtype": "f32", "data": "synthetic (seeded Q8_0 / Q4_K blocks generated on the device, x ~ N(0,1))",
         "config": {"workload": "configs 1 and 2: dense QMatMul (Q8_0 2048x2048 M=1; Q4_K 4096x4096 M=1,16,128,512)"},
         "roofline": {"bound": head["bound"], "achieved": head["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": head["roofline_frac"], "traffic": None, "kernel": "QMatMul, config 1"},
+                     "frac": head["roofline_frac"],
+                     "traffic": measured_traffic(os.path.dirname(os.path.abspath(__file__)), TRAFFIC_PROFILE_DENSE),
+                     "traffic_source": TRAFFIC_PROFILE_DENSE, "kernel": "QMatMul, config 1"},
         "cases": cases,
         "cpu_baseline": None if args.no_cpu_baseline else {
-            "value": head["cpu_us"], "unit": "us per call (config 1)", "cores": threads, "kind": "port",
+            "value": head["cpu_us"], "unit": "us per call (config 1)", "cores": threads, "host": host, "kind": "port",
             "sample": "the oracle's restatement of candle's x86 quantized matmul (activations to Q8_K/Q8_0, integer "
                       "block dots) per case, ~2 s each; cpu_us in each case"},
     }
@@ -490,7 +556,9 @@ def bench_shrink(args, torch, np, dev):
         "parity": {"bytes_equal_oracle": parity}, "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
-        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        host = host_cpu()
+        O.set_threads(host["physical"])
+        threads = O.get_threads()
         src0 = srcs[2][:nbs[2] // n_exp * F.type_size(F.Q5_K)].cpu().numpy()
         n, t_cpu = 0, 0.0
         while t_cpu < min(args.cpu_seconds, 5.0) and n < 200:
@@ -498,7 +566,7 @@ def bench_shrink(args, torch, np, dev):
             O.requant_q2k(F.Q5_K, src0, nbs[2] // n_exp)
             t_cpu += time.perf_counter() - t1
             n += 1
-        line["cpu_baseline"] = {"value": t_cpu / n * 1e6, "unit": "us per Q5_K 2048x512 matrix", "cores": threads,
+        line["cpu_baseline"] = {"value": t_cpu / n * 1e6, "unit": "us per Q5_K 2048x512 matrix", "cores": threads, "host": host,
                                 "kind": "port", "sample": "%d shrinks of one down matrix by the C oracle" % n}
     print(json.dumps(line), flush=True)
 
@@ -633,13 +701,15 @@ def main():
     T = args.prefill_tokens
     xp = torch.randn((T, H), generator=gen, device=dev)
     lp = torch.randn((T, E), generator=gen, device=dev)
-    for _ in range(2):
-        eager = layers[1].forward(xp, lp)[0]
+    # the calls rotate over ROT layers (ROT x 224 MB of experts, past the 256 MB Infinity Cache), so
+    # each call reads its experts from HBM
+    ROT = min(3, L)
+    eager = [layers[1 + r % (L - 1) if L > 1 else 0].forward(xp, lp)[0].clone() for r in range(ROT)]
     torch.cuda.synchronize()
-    reps = 10
+    reps = 12
     g_pre = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g_pre):
-        pre_outs = [layers[1].forward(xp, lp)[0] for _ in range(reps)]
+        pre_outs = [layers[1 + (r % ROT) % (L - 1) if L > 1 else 0].forward(xp, lp)[0] for r in range(reps)]
     torch.cuda.synchronize()
     g_pre.replay()
     torch.cuda.synchronize()
@@ -648,18 +718,21 @@ def main():
     stop.record()
     torch.cuda.synchronize()
     pre_us = start.elapsed_time(stop) * 1e3 / reps
-    pre_same = all(bool(torch.equal(o, eager)) for o in pre_outs)
+    pre_same = all(bool(torch.equal(o, eager[r % ROT])) for r, o in enumerate(pre_outs))
     pre_flops = 2.0 * T * K * 3 * H * I
     tflops = pre_flops / (pre_us * 1e-6) / 1e12
     prefill = {"tokens": T, "us_per_layer": round(pre_us, 2), "tokens_per_s": round(T / (pre_us * 1e-6)),
                "tflops": round(tflops, 2), "mfma_util": round(tflops / MFMA_PEAK_F16_TFLOPS, 4),
                "mfma_peak_tflops": MFMA_PEAK_F16_TFLOPS, "graph_replay_equals_eager": pre_same, "calls_timed": reps,
+               "layers_rotated": ROT,
                "path": "grouped MFMA GEMMs (fp16 integer weight codes, fp16 activations, f32 accumulate)"}
     log("prefill", prefill)
 
     cpu = None
     if not args.no_cpu_baseline:
-        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        host = host_cpu()
+        O.set_threads(host["physical"])
+        threads = O.get_threads()
         log("cpu baseline: oracle MoE layer, %d threads, ~%.0f s" % (threads, args.cpu_seconds))
         rng = np.random.default_rng(args.seed)
         n, t_cpu = 0, 0.0
@@ -669,7 +742,7 @@ def main():
             O.moe_layer(host_layer, x0, lg)
             t_cpu += time.perf_counter() - t1
             n += 1
-        cpu = {"value": t_cpu / n * 1e6, "unit": "us/layer", "cores": threads, "kind": "port",
+        cpu = {"value": t_cpu / n * 1e6, "unit": "us/layer", "cores": threads, "host": host, "kind": "port",
                "sample": "%d decode calls (T=1) of the C oracle MoE layer (dequantize the picked experts, f64 dots) "
                          "on layer 0 of the same bank; IQ formats have no candle CPU path" % n}
         log("cpu", cpu)

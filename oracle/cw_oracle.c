@@ -629,6 +629,13 @@ int or_moe_layer(const or_moe_desc *d, const float *x, const float *logits, int 
     return bad ? -1 : missing;
 }
 
+/* ---- threads ---- */
+
+/* the OpenMP thread count of the parallel loops below (the CPU baseline sets it to the host's
+ * physical cores, candle's default: vendor/candle-core/src/utils.rs:382-421) */
+void or_set_threads(int n) { if (n > 0) omp_set_num_threads(n); }
+int or_get_threads(void) { return omp_get_max_threads(); }
+
 /* ---- candle's CPU quantized path (baseline numerics) ---- */
 
 void or_quantize_q8_0(const float *x, int64_t n, void *blocks) {

@@ -107,6 +107,9 @@ float or_vec_dot(int dtype, int64_t k, const void *wrow, const void *xq);
 int or_candle_matmul(int dtype, const void *w, int64_t n, int64_t k, const float *x, int64_t m,
                      float *y, int threads);
 
+void or_set_threads(int n);
+int or_get_threads(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -71,6 +71,10 @@ def _declare(L):
     L.or_quantize_q8_0.restype = None
     L.or_quantize_q8_k.argtypes = [_P, _L, _P]
     L.or_quantize_q8_k.restype = None
+    L.or_set_threads.argtypes = [_I]
+    L.or_set_threads.restype = None
+    L.or_get_threads.argtypes = []
+    L.or_get_threads.restype = _I
     L.or_vec_dot.argtypes = [_I, _L, _P, _P]
     L.or_vec_dot.restype = ctypes.c_float
     L.or_candle_matmul.argtypes = [_I, _P, _L, _L, _P, _L, _P, _I]
@@ -238,6 +242,15 @@ def quantize_q8_k(x):
     out = np.empty(x.size // 256 * 292, dtype=np.uint8)
     lib().or_quantize_q8_k(_ptr(x), x.size, _ptr(out))
     return out
+
+
+def set_threads(n):
+    """OpenMP threads of the oracle's parallel loops."""
+    lib().or_set_threads(int(n))
+
+
+def get_threads():
+    return lib().or_get_threads()
 
 
 def vec_dot(dtype, k, wrow, xq):
