@@ -396,8 +396,9 @@ def bench_dense(args, torch, np, dev):
     same replay started on an idle device, where a call of a few µs waits for the host to submit
     the next one. Achieved rates use the algorithmic bytes (matrix + x + y) and flops (2 M n k), against HBM
     (8 TB/s) or fp16 MFMA (2.5 PFLOP/s), whichever bounds the case. Parity of each case against
-    the f64 oracle; the CPU baseline is the oracle's restatement of candle's x86 path (activations
-    quantized to Q8_K / Q8_0, integer block dots) on the host's threads."""
+    the f64 oracle; the CPU baseline is the restatement of candle's x86 QMatMul (the repacked
+    AVX-512 VNNI tiles of repack_x86.rs where candle takes them, else the generic vec_dot driver)
+    on the host's physical cores."""
     from coachwhip_amd import formats as F
     from coachwhip_amd import ops, synth
     from oracle import oracle as O
@@ -407,7 +408,7 @@ def bench_dense(args, torch, np, dev):
     host = host_cpu()
     O.set_threads(host["physical"])
     threads = O.get_threads()
-    cases = []
+    cases, packs = [], {}
     for name, dt, n, k, ms in (("config 1: Q8_0 GEMV", F.Q8_0, 2048, 2048, (1,)),
                                ("config 2: Q4_K matmul", F.Q4_K, 4096, 4096, (1, 16, 128, 512))):
         wb = F.matrix_bytes(dt, n, k)
@@ -459,11 +460,22 @@ def bench_dense(args, torch, np, dev):
                     "bound": bound, "roofline_frac": round(max(t_hbm, t_mfma) / (us * 1e-6), 4), "rel_l2": err,
                     "us_host_fed": round(us_fed, 3)}
             if not args.no_cpu_baseline:
-                O.candle_matmul(dt, host_w, n, k, xh)
+                # candle's CPU QMatMul on this host: the repacked x86 tiles where it takes them
+                # (weights packed once, as candle caches them), else the generic vec_dot driver
+                if O.x86_select(dt, m, n, k):
+                    if dt not in packs:
+                        packs[dt] = O.x86_pack(dt, host_w, n, k)
+                    run = lambda: O.x86_matmul(dt, packs[dt], n, k, xh)  # noqa: E731
+                    case["cpu_path"] = "x86 tiles, tier %d" % O.x86_level()
+                else:
+                    run = lambda: O.candle_matmul(dt, host_w, n, k, xh)  # noqa: E731
+                    case["cpu_path"] = "generic vec_dot"
+                yc = run()
+                case["cpu_rel_l2"] = O.rel_l2(yc, O.qmatmul_f64(dt, host_w, n, k, xh))
                 reps, t_cpu = 0, 0.0
                 while t_cpu < 2.0 and reps < 200:
                     t1 = time.perf_counter()
-                    O.candle_matmul(dt, host_w, n, k, xh)
+                    run()
                     t_cpu += time.perf_counter() - t1
                     reps += 1
                 case["cpu_us"] = round(t_cpu / reps * 1e6, 1)
@@ -484,8 +496,10 @@ def bench_dense(args, torch, np, dev):
         "cases": cases,
         "cpu_baseline": None if args.no_cpu_baseline else {
             "value": head["cpu_us"], "unit": "us per call (config 1)", "cores": threads, "host": host, "kind": "port",
-            "sample": "the oracle's restatement of candle's x86 quantized matmul (activations to Q8_K/Q8_0, integer "
-                      "block dots) per case, ~2 s each; cpu_us in each case"},
+            "sample": "candle's CPU QMatMul restated (repack_x86.rs: weights in 16-row tiles packed once, "
+                      "activations to Q8_K, AVX-512 VNNI units over the physical cores; the generic vec_dot "
+                      "driver where candle does not take the tiles), ~2 s per case; cpu_us, cpu_path and "
+                      "cpu_rel_l2 (against the f64 product) in each case"},
     }
     print(json.dumps(line), flush=True)
 

@@ -2,7 +2,7 @@
 
 Type ids are GGUF's (vendor/candle-core/src/quantized/mod.rs:314-339), plus 21 (IQ3_S) and
 22 (IQ2_S), which the reference's Metal shaders implement (quantized.metal:232-257) but its
-type enum does not. Sizes: k_quants.rs:125-200, 631-635; quantized.metal:217-257.
+type enum does not. Sizes: k_quants.rs:125-200, 631-635, 2959-2968; quantized.metal:217-296.
 """
 F32, F16 = 0, 1
 Q8_0 = 8
@@ -10,20 +10,27 @@ Q2_K = 10
 Q3_K = 11
 Q4_K = 12
 Q5_K = 13
+Q6_K = 14
 Q8_K = 15
 IQ2_XXS = 16
+IQ3_XXS = 18
 IQ3_S = 21
 IQ2_S = 22
+IQ4_XS = 23
 MXFP4 = 39
 
 NAMES = {F32: "f32", F16: "f16", Q8_0: "q8_0", Q2_K: "q2_K", Q3_K: "q3_K", Q4_K: "q4_K", Q5_K: "q5_K",
-         Q8_K: "q8_K", IQ2_XXS: "iq2_xxs", IQ3_S: "iq3_s", IQ2_S: "iq2_s", MXFP4: "mxfp4"}
+         Q6_K: "q6_K", Q8_K: "q8_K", IQ2_XXS: "iq2_xxs", IQ3_XXS: "iq3_xxs", IQ3_S: "iq3_s", IQ2_S: "iq2_s",
+         IQ4_XS: "iq4_xs", MXFP4: "mxfp4"}
 BY_NAME = {v: k for k, v in NAMES.items()}
 
-_BLOCK = {F32: 1, F16: 1, Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q8_K: 256, IQ2_XXS: 256,
-          IQ3_S: 256, IQ2_S: 256, MXFP4: 32}
-_SIZE = {F32: 4, F16: 2, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q8_K: 292, IQ2_XXS: 66,
-         IQ3_S: 110, IQ2_S: 82, MXFP4: 17}
+_BLOCK = {F32: 1, F16: 1, Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_K: 256,
+          IQ2_XXS: 256, IQ3_XXS: 256, IQ3_S: 256, IQ2_S: 256, IQ4_XS: 256, MXFP4: 32}
+_SIZE = {F32: 4, F16: 2, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292,
+         IQ2_XXS: 66, IQ3_XXS: 98, IQ3_S: 110, IQ2_S: 82, IQ4_XS: 136, MXFP4: 17}
+# byte offset of the f16 super-block (or block) scale d
+D_OFFSET = {Q8_0: 0, Q2_K: 80, Q3_K: 108, Q4_K: 0, Q5_K: 0, Q6_K: 208, IQ2_XXS: 0, IQ3_XXS: 0, IQ3_S: 0,
+            IQ2_S: 0, IQ4_XS: 0}
 
 # the sources of the shrink to Q2_K (crates/engine/src/requant.rs:334-352)
 SHRINK_SOURCES = (Q3_K, Q4_K, Q5_K)

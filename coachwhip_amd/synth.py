@@ -42,7 +42,9 @@ def random_blocks(dtype, n_weights, rng):
         raw[:, 82:84] = _f16_bits(rng.uniform(0.001, 0.02, nb)).view(np.uint8).reshape(nb, 2)
     elif dtype == F.Q3_K:
         raw[:, 108:110] = _f16_bits(rng.uniform(0.001, 0.02, nb)).view(np.uint8).reshape(nb, 2)
-    elif dtype in (F.IQ2_XXS, F.IQ2_S, F.IQ3_S):
+    elif dtype == F.Q6_K:
+        raw[:, 208:210] = _f16_bits(rng.uniform(0.001, 0.02, nb)).view(np.uint8).reshape(nb, 2)
+    elif dtype in (F.IQ2_XXS, F.IQ2_S, F.IQ3_S, F.IQ3_XXS, F.IQ4_XS):
         raw[:, 0:2] = _f16_bits(rng.uniform(0.001, 0.02, nb)).view(np.uint8).reshape(nb, 2)
     elif dtype == F.MXFP4:
         raw[:, 0] = rng.integers(119, 124, size=nb, dtype=np.uint8)
@@ -142,7 +144,9 @@ def device_blocks(dtype, n_weights, gen, device="cuda"):
         raw[:, 82:84] = f16_scales()
     elif dtype == F.Q3_K:
         raw[:, 108:110] = f16_scales()
-    elif dtype in (F.IQ2_XXS, F.IQ2_S, F.IQ3_S):
+    elif dtype == F.Q6_K:
+        raw[:, 208:210] = f16_scales()
+    elif dtype in (F.IQ2_XXS, F.IQ2_S, F.IQ3_S, F.IQ3_XXS, F.IQ4_XS):
         raw[:, 0:2] = f16_scales()
     elif dtype == F.MXFP4:
         raw[:, 0] = torch.randint(119, 124, (nb,), dtype=torch.uint8, device=device, generator=gen)

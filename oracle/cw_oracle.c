@@ -17,20 +17,24 @@ int or_block_size(int dtype) {
     switch (dtype) {
     case OR_F32: case OR_F16: return 1;
     case OR_Q8_0: case OR_MXFP4: return 32;
-    case OR_Q2_K: case OR_Q3_K: case OR_Q4_K: case OR_Q5_K: case OR_Q8_K: case OR_IQ2_XXS: case OR_IQ2_S:
-    case OR_IQ3_S: return QK_K;
+    case OR_Q2_K: case OR_Q3_K: case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_Q8_K: case OR_IQ2_XXS:
+    case OR_IQ2_S: case OR_IQ3_XXS: case OR_IQ3_S: case OR_IQ4_XS: return QK_K;
     default: return 0;
     }
 }
 
 int or_type_size(int dtype) {
     /* struct sizes: k_quants.rs:125-130 (Q8_0 34), 142-148 (Q2_K 84), 152-158 (Q3_K 110),
-     * 163-170 (Q4_K 144), 173-181 (Q5_K 176), 195-200 (Q8_K 292), 631-635 (MXFP4 17);
-     * quantized.metal:217-257 (IQ2_XXS 66, IQ2_S 82, IQ3_S 110). */
+     * 163-170 (Q4_K 144), 173-181 (Q5_K 176), 185-191 (Q6_K 210), 195-200 (Q8_K 292), 631-635
+     * (MXFP4 17), 2959-2968 (IQ2_XXS 66, IQ3_XXS 98, IQ4_XS 136); quantized.metal:217-257 (IQ2_S 82,
+     * IQ3_S 110). */
     switch (dtype) {
     case OR_Q2_K: return 84;
     case OR_Q3_K: return 110;
     case OR_Q5_K: return 176;
+    case OR_Q6_K: return 210;
+    case OR_IQ3_XXS: return 98;
+    case OR_IQ4_XS: return 136;
     case OR_F32: return 4;
     case OR_F16: return 2;
     case OR_Q8_0: return 34;
@@ -270,6 +274,71 @@ static void deq_iq3_s(const uint8_t *b, float *y) {
     }
 }
 
+/* Q6_K {ql[128], qh[64], scales[16] (i8), d}: k_quants.rs:2420-2451, y = (d * sc) * (q - 32) */
+static void deq_q6_k(const uint8_t *b, float *y) {
+    float d = or_f16_to_f32(rd16(b + 208));
+    for (int h = 0; h < 2; h++) {
+        const uint8_t *ql = b + 64 * h, *qh = b + 128 + 32 * h;
+        const int8_t *sc = (const int8_t *)(b + 192 + 8 * h);
+        float *yy = y + 128 * h;
+        for (int l = 0; l < 32; l++) {
+            int is = l / 16;
+            int q1 = (int)((ql[l] & 0xF) | ((qh[l] & 3) << 4)) - 32;
+            int q2 = (int)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+            int q3 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+            int q4 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+            yy[l] = d * (float)sc[is] * (float)q1;
+            yy[l + 32] = d * (float)sc[is + 2] * (float)q2;
+            yy[l + 64] = d * (float)sc[is + 4] * (float)q3;
+            yy[l + 96] = d * (float)sc[is + 6] * (float)q4;
+        }
+    }
+}
+
+/* dequantize_iq3_xxs, quantized.metal:6866-6891 (GGUF type 18; the reference has no CPU path).
+ * Sub-block ib: 8 grid indices qs[8ib..8ib+8) of 4 values each, and the little-endian word at
+ * qs[64 + 4ib]: four 7-bit sign indices and the 4-bit scale s on top; dl = d * (s + 0.5) * 0.5.
+ * Weights 8h'..8h'+7 (h' = 0..3) take sign index h' and grid indices 2h', 2h'+1. */
+static void deq_iq3_xxs(const uint8_t *b, float *y) {
+    float d = or_f16_to_f32(rd16(b));
+    for (int ib = 0; ib < 8; ib++) {
+        const uint8_t *q3 = b + 2 + 8 * ib, *gs = b + 2 + 64 + 4 * ib;
+        uint32_t aux = (uint32_t)gs[0] | ((uint32_t)gs[1] << 8) | ((uint32_t)gs[2] << 16) | ((uint32_t)gs[3] << 24);
+        float dl = d * (0.5f + (float)(aux >> 28)) * 0.5f;
+        for (int h = 0; h < 4; h++) {
+            uint8_t signs = ksign((aux >> (7 * h)) & 127);
+            for (int t = 0; t < 2; t++) {
+                uint32_t grid = cw_iq3xxs_grid[q3[2 * h + t]];
+                for (int i = 0; i < 4; i++) {
+                    float gv = (float)((grid >> (8 * i)) & 0xFF);
+                    y[32 * ib + 8 * h + 4 * t + i] = dl * gv * ((signs >> (4 * t + i)) & 1 ? -1.f : 1.f);
+                }
+            }
+        }
+    }
+}
+
+/* kvalues_iq4nl_f, quantized.metal:4561-4563: the 16 non-linear IQ4 levels (format data) */
+static const float KV_IQ4NL[16] = {-127.f, -104.f, -83.f, -65.f, -49.f, -35.f, -22.f, -10.f,
+                                   1.f, 13.f, 25.f, 38.f, 53.f, 69.f, 89.f, 113.f};
+
+/* dequantize_iq4_xs, quantized.metal:7000-7016 (GGUF type 23): {d, scales_h (u16), scales_l[4],
+ * qs[128]}; sub-block ib has the 6-bit scale ls = scales_l nibble | 2 bits of scales_h << 4,
+ * d_ib = d * (ls - 32), and its 32 weights are the low then the high nibbles of qs[16ib..16ib+16). */
+static void deq_iq4_xs(const uint8_t *b, float *y) {
+    float d0 = or_f16_to_f32(rd16(b));
+    uint32_t sh = rd16(b + 2);
+    const uint8_t *sl = b + 4, *qs = b + 8;
+    for (int ib = 0; ib < 8; ib++) {
+        int ls = ((sl[ib / 2] >> (4 * (ib % 2))) & 0xF) | (int)(((sh >> (2 * ib)) & 3) << 4);
+        float d = d0 * (float)(ls - 32);
+        for (int j = 0; j < 16; j++) {
+            y[32 * ib + j] = d * KV_IQ4NL[qs[16 * ib + j] & 0xF];
+            y[32 * ib + 16 + j] = d * KV_IQ4NL[qs[16 * ib + j] >> 4];
+        }
+    }
+}
+
 int or_dequantize(int dtype, const void *blocks, int64_t n, float *out) {
     int bs = or_block_size(dtype), ts = or_type_size(dtype);
     if (bs == 0 || n < 0 || n % bs) return -1;
@@ -285,6 +354,9 @@ int or_dequantize(int dtype, const void *blocks, int64_t n, float *out) {
         case OR_Q3_K: deq_q3_k(b, y); break;
         case OR_Q4_K: deq_q4_k(b, y); break;
         case OR_Q5_K: deq_q5_k(b, y); break;
+        case OR_Q6_K: deq_q6_k(b, y); break;
+        case OR_IQ3_XXS: deq_iq3_xxs(b, y); break;
+        case OR_IQ4_XS: deq_iq4_xs(b, y); break;
         case OR_MXFP4: deq_mxfp4(b, y); break;
         case OR_IQ2_XXS: deq_iq2_xxs(b, y); break;
         case OR_IQ2_S: deq_iq2_s(b, y); break;

@@ -18,7 +18,8 @@ extern "C" {
 
 /* GGUF type ids: vendor/candle-core/src/quantized/mod.rs:314-339, plus 21 (IQ3_S), 22 (IQ2_S). */
 enum { OR_F32 = 0, OR_F16 = 1, OR_Q8_0 = 8, OR_Q2_K = 10, OR_Q3_K = 11, OR_Q4_K = 12, OR_Q5_K = 13,
-       OR_Q8_K = 15, OR_IQ2_XXS = 16, OR_IQ3_S = 21, OR_IQ2_S = 22, OR_MXFP4 = 39 };
+       OR_Q6_K = 14, OR_Q8_K = 15, OR_IQ2_XXS = 16, OR_IQ3_XXS = 18, OR_IQ3_S = 21, OR_IQ2_S = 22,
+       OR_IQ4_XS = 23, OR_MXFP4 = 39 };
 
 int or_block_size(int dtype);   /* weights per block, 0 if unknown */
 int or_type_size(int dtype);    /* bytes per block, 0 if unknown */
@@ -109,6 +110,19 @@ int or_candle_matmul(int dtype, const void *w, int64_t n, int64_t k, const float
 
 void or_set_threads(int n);
 int or_get_threads(void);
+
+/* candle's x86 repacked QMatMul (repack.rs:219-283, repack_x86.rs), in cw_candle_x86.c: the
+ * weights packed once into tiles of 16 rows, activations quantized to Q8_K per call, units of
+ * 16 rows x up to 4 activation rows over the threads. */
+int or_x86_level(void);   /* 2 AVX-512 VNNI, 1 AVX-VNNI, 0 AVX2 + FMA, -1 none (repack_x86.rs:905-928) */
+/* whether candle takes this path for (dtype, m, n, k) on this host (repack_x86.rs:43-60) */
+int or_x86_select(int dtype, int64_t m, int64_t n, int64_t k);
+int64_t or_x86_packed_bytes(int dtype, int64_t n, int64_t k);  /* 0: not a packed case */
+int or_x86_pack(int dtype, const void *w, int64_t n, int64_t k, void *packed);
+/* y[m][n]; simd 1 = AVX-512 VNNI unit when the host has it, 0 = the plain-C unit (same bits);
+ * threads 0 = all available */
+int or_x86_matmul(int dtype, const void *packed, int64_t n, int64_t k, const float *x, int64_t m,
+                  float *y, int simd, int threads);
 
 #ifdef __cplusplus
 }

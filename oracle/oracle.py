@@ -78,6 +78,14 @@ def _declare(L):
     L.or_vec_dot.argtypes = [_I, _L, _P, _P]
     L.or_vec_dot.restype = ctypes.c_float
     L.or_candle_matmul.argtypes = [_I, _P, _L, _L, _P, _L, _P, _I]
+    L.or_x86_level.argtypes = []
+    L.or_x86_level.restype = _I
+    L.or_x86_select.argtypes = [_I, _L, _L, _L]
+    L.or_x86_select.restype = _I
+    L.or_x86_packed_bytes.argtypes = [_I, _L, _L]
+    L.or_x86_packed_bytes.restype = _L
+    L.or_x86_pack.argtypes = [_I, _P, _L, _L, _P]
+    L.or_x86_matmul.argtypes = [_I, _P, _L, _L, _P, _L, _P, _I, _I]
     L.or_requant_q2k.argtypes = [_I, _P, _L, _P, _L, _P]
 
 
@@ -264,6 +272,34 @@ def candle_matmul(dtype, w, n, k, x, threads=0):
     x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, k)
     y = np.empty((x.shape[0], n), dtype=np.float32)
     assert lib().or_candle_matmul(dtype, _ptr(w), n, k, _ptr(x), x.shape[0], _ptr(y), threads) == 0
+    return y
+
+
+def x86_level():
+    """candle's x86 tier on this host: 2 AVX-512 VNNI, 1 AVX-VNNI, 0 AVX2, -1 none."""
+    return lib().or_x86_level()
+
+
+def x86_select(dtype, m, n, k):
+    """Whether candle's repacked x86 path takes (dtype, m, n, k) on this host."""
+    return bool(lib().or_x86_select(dtype, m, n, k))
+
+
+def x86_pack(dtype, w, n, k):
+    """The weight tiles of candle's x86 path (packed once per matrix, as candle caches them)."""
+    nb = lib().or_x86_packed_bytes(dtype, n, k)
+    assert nb > 0
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    out = np.empty(nb, dtype=np.uint8)
+    assert lib().or_x86_pack(dtype, _ptr(w), n, k, _ptr(out)) == 0
+    return out
+
+
+def x86_matmul(dtype, packed, n, k, x, simd=True, threads=0):
+    """candle's x86 QMatMul over packed tiles: x rows to Q8_K, then the tile units."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, k)
+    y = np.empty((x.shape[0], n), dtype=np.float32)
+    assert lib().or_x86_matmul(dtype, _ptr(packed), n, k, _ptr(x), x.shape[0], _ptr(y), int(simd), threads) == 0
     return y
 
 

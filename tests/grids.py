@@ -43,3 +43,12 @@ def reference_table(name):
     text = open(REF_METAL).read()
     m = re.search(r"GGML_TABLE_BEGIN\(\w+,\s*%s,\s*\w+\)(.*?)GGML_TABLE_END\(\)" % name, text, re.S)
     return [int(v, 0) for v in re.findall(r"0x[0-9a-fA-F]+|\b\d+\b", m.group(1))]
+
+
+def reference_kvalues_iq4nl():
+    """kvalues_iq4nl_f (quantized.metal:4561-4563) as written in the shader text, or None."""
+    if not os.path.exists(REF_METAL):
+        return None
+    text = open(REF_METAL).read()
+    m = re.search(r"kvalues_iq4nl_f\[16\]\s*=\s*\{(.*?)\}", text, re.S)
+    return [float(v) for v in re.findall(r"-?\d+(?:\.\d*)?", m.group(1))]

@@ -1,7 +1,8 @@
 """Pins of the oracle's restatement of candle's CPU quantized path: the activation quantizers
 (Q8_0 and Q8_K from_float) byte for byte against numpy closed forms of
-vendor/candle-core/src/quantized/k_quants.rs:784-821 and 2495-2534, and the generic matmul driver
-(k_quants.rs:2551-2670) against its pieces.
+vendor/candle-core/src/quantized/k_quants.rs:784-821 and 2495-2534, the generic matmul driver
+(k_quants.rs:2551-2670) against its pieces, and the x86 repacked tile path (repack_x86.rs)
+against the f64 product it computes and against its own plain-C unit.
 
 The closed forms are written from the Rust text, not from the C: f32 arithmetic throughout,
 Rust's f32::round (half away from zero, which numpy's round is not), the saturating `as i8`, the
@@ -142,3 +143,56 @@ def test_candle_matmul_is_quantize_then_vec_dot(dtype):
         xd = (qb[:, :, 2:34].view(np.int8).astype(np.float64) * d[..., None]).reshape(m, k)
     assert O.rel_l2(y, xd @ wd.T) < 1e-6
     assert O.rel_l2(y, x.astype(np.float64) @ wd.T) > 1e-4
+
+
+# ---------------------------------------------------------------- candle's x86 repacked path
+
+def _q8k_dequantized(x):
+    qb = np.stack([O.quantize_q8_k(r).reshape(-1, 292) for r in x])
+    d = qb[:, :, 0:4].copy().view(np.float32)[..., 0].astype(np.float64)
+    return (qb[:, :, 4:260].view(np.int8).astype(np.float64) * d[..., None]).reshape(x.shape[0], -1)
+
+
+@pytest.mark.parametrize("dtype", [F.Q4_K, F.Q6_K, F.Q8_0])
+def test_x86_tiles_compute_the_q8k_product(dtype):
+    """repack_x86.rs: the tile units give W . Q8_K(x) (weights dequantized, activations quantized
+    to Q8_K as quantize_lhs does) up to f32 accumulation; the +128 (Q8_0) and +32 (Q6_K) code
+    offsets and the Q4_K mins, taken out through the bsums, would leave errors of order 1 if
+    wrong. The AVX-512 VNNI unit and the plain-C unit give the same bits, for row counts on and
+    off the 4-row unit."""
+    rng = np.random.default_rng(50 + dtype)
+    n, k = 48, 512
+    w = synth.random_blocks(dtype, n * k, rng)
+    packed = O.x86_pack(dtype, w, n, k)
+    wd = O.dequantize(dtype, w, n * k).reshape(n, k).astype(np.float64)
+    for m in (1, 3, 4, 5, 9):
+        x = rng.standard_normal((m, k)).astype(np.float32) * 2
+        y = O.x86_matmul(dtype, packed, n, k, x, simd=False)
+        want = _q8k_dequantized(x) @ wd.T
+        assert O.rel_l2(y, want) < 2e-6, (m, O.rel_l2(y, want))
+        if O.x86_level() == 2:
+            assert np.array_equal(O.x86_matmul(dtype, packed, n, k, x, simd=True), y), m
+
+
+def test_x86_q4k_agrees_with_the_generic_driver():
+    """Both quantize x to Q8_K; the tiles and k_quants' vec_dot differ only in f32 summation order."""
+    rng = np.random.default_rng(60)
+    n, k, m = 32, 1024, 6
+    w = synth.random_blocks(F.Q4_K, n * k, rng)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    y = O.x86_matmul(F.Q4_K, O.x86_pack(F.Q4_K, w, n, k), n, k, x)
+    assert O.rel_l2(y, O.candle_matmul(F.Q4_K, w, n, k, x)) < 1e-6
+
+
+def test_x86_path_selection():
+    """repack_x86.rs:43-60: n a multiple of 16 and k of 256; Q6_K only for m > 1; Q8_0 not on the
+    AVX2-only tier."""
+    lv = O.x86_level()
+    if lv < 0:
+        assert not O.x86_select(F.Q4_K, 1, 64, 256)
+        return
+    assert O.x86_select(F.Q4_K, 1, 64, 256) and not O.x86_select(F.Q4_K, 1, 72, 256)
+    assert not O.x86_select(F.Q4_K, 1, 64, 288) and not O.x86_select(F.Q4_K, 1, 64, 0)
+    assert not O.x86_select(F.Q6_K, 1, 64, 256) and O.x86_select(F.Q6_K, 2, 64, 256)
+    assert O.x86_select(F.Q8_0, 1, 64, 256) == (lv != 0)
+    assert not O.x86_select(F.MXFP4, 1, 64, 256)

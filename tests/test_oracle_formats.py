@@ -134,6 +134,61 @@ def test_iq3_s_hand_block():
         assert y[32 + v] == 15.0 * float(g[idx][v % 4]) * (-1 if neg else 1), v
 
 
+def test_q6_k_hand_block():
+    # k_quants.rs:2420-2451: value l of half h is ql/qh bits, minus 32, times d * scales[8h + l//16 + 2r]
+    ql = [0] * 128
+    qh = [0] * 64
+    ql[0] = 0x21          # l = 0: low nibble 1 (r = 0), high nibble 2 (r = 2)
+    ql[32] = 0x43         # l = 0: low nibble 3 (r = 1), high nibble 4 (r = 3)
+    qh[0] = 0b11100100    # l = 0: 2-bit highs 0, 1, 2, 3 for r = 0..3
+    ql[64 + 17] = 0xFF    # half 1, l = 17: codes 15 | 16 * qh bits
+    qh[32 + 17] = 0xFF
+    scales = [2, -3, 4, -5, 6, -7, 8, -9] + [1, 10, 1, 1, 1, 1, 1, 1]
+    blk = np.array(ql + qh + [v & 0xFF for v in scales] + le16(0x3800), dtype=np.uint8)  # d = 0.5
+    y = O.dequantize(F.Q6_K, blk, 256)
+    assert y[0] == 0.5 * 2 * (1 - 32)                # r = 0 uses scale 0
+    assert y[32] == 0.5 * 4 * (3 + 16 - 32)          # r = 1: scale 2, qh bits 2-3 = 1
+    assert y[64] == 0.5 * 6 * (2 + 32 - 32)          # r = 2: scale 4, qh bits 4-5 = 2
+    assert y[96] == 0.5 * 8 * (4 + 48 - 32)          # r = 3: scale 6, qh bits 6-7 = 3
+    assert y[1] == 0.5 * 2 * -32 and y[16] == 0.5 * -3 * -32   # l >= 16 takes the next scale
+    assert y[128 + 17] == 0.5 * 10 * (63 - 32)       # half 1, l = 17: scale 8 + 1
+    assert y[128 + 17 + 64] == 0.5 * 1 * (63 - 32)   # high nibble, qh bits 4-5: scale 8 + 1 + 4
+
+
+def test_iq3_xxs_hand_block():
+    g = G.grid_bytes("iq3xxs_grid")
+    # sub-block 1: grid indices 0..7, sign indices (1, 0, 127, 2) and scale nibble 5 in its word
+    qs = [0] * 8 + list(range(8)) + [0] * 48
+    aux = 1 | (0 << 7) | (127 << 14) | (2 << 21) | (5 << 28)
+    gas = [0, 0, 0, 0] + [(aux >> (8 * i)) & 0xFF for i in range(4)] + [0] * 24
+    blk = np.array(le16(0x3C00) + qs + gas, dtype=np.uint8)
+    y = O.dequantize(F.IQ3_XXS, blk, 256)
+    assert list(y[:32]) == [0.25 * float(g[0][i % 4]) for i in range(32)]  # dl = (0 + 0.5) * 0.5
+    dl = (5 + 0.5) * 0.5
+    ks = {1: 0b10000001, 0: 0, 127: 0xFF, 2: 0b10000010}   # 7 sign bits + even parity
+    for h, si in enumerate((1, 0, 127, 2)):
+        for t in range(2):
+            for i in range(4):
+                v = 8 * h + 4 * t + i
+                neg = (ks[si] >> (4 * t + i)) & 1
+                assert y[32 + v] == dl * float(g[2 * h + t][i]) * (-1 if neg else 1), v
+
+
+def test_iq4_xs_hand_block():
+    kv = [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]
+    # sub-block scales ls_ib = (scales_l nibble) | (2 bits of scales_h) << 4
+    ls = [32, 33, 0, 63, 31, 40, 17, 48]
+    sl = [(ls[2 * i] & 0xF) | ((ls[2 * i + 1] & 0xF) << 4) for i in range(4)]
+    sh = sum(((v >> 4) & 3) << (2 * i) for i, v in enumerate(ls))
+    qs = [(j % 16) | ((15 - j % 16) << 4) for j in range(128)]
+    blk = np.array(le16(0x3800) + le16(sh) + sl + qs, dtype=np.uint8)  # d = 0.5
+    y = O.dequantize(F.IQ4_XS, blk, 256)
+    for ib in range(8):
+        d = 0.5 * (ls[ib] - 32)
+        for j in range(16):
+            assert y[32 * ib + j] == d * kv[j % 16] and y[32 * ib + 16 + j] == d * kv[15 - j % 16], (ib, j)
+
+
 # ---------------------------------------------------------------- second formulations
 
 def _utmp_scales(sc12):
@@ -198,6 +253,78 @@ def test_candle_vec_dot_agrees_with_dequantize_then_dot(dtype):
         want = float(np.dot(O.dequantize(dtype, w, k).astype(np.float64), xd))
         got = O.vec_dot(dtype, k, w, xq)
         assert abs(got - want) <= 1e-5 * max(1.0, abs(want)), (got, want)
+
+
+def _q8k_rows(x):
+    """x quantized to Q8_K: (codes, d, bsums) per super-block."""
+    qb = O.quantize_q8_k(x).reshape(-1, 292)
+    d = qb[:, 0:4].copy().view(np.float32)[:, 0].astype(np.float64)
+    return qb[:, 4:260].view(np.int8).astype(np.int64), d, qb[:, 260:292].copy().view(np.int16).astype(np.int64)
+
+
+def _vd_q6_k(blk, q8, yd):
+    """candle's Q6_K x Q8_K vec_dot_unopt (k_quants.rs:2208-2262) for one row, in f64."""
+    tot = 0.0
+    for ibl in range(len(blk) // 210):
+        b = blk[210 * ibl:210 * ibl + 210].astype(np.int64)
+        ql, qh = b[0:128], b[128:192]
+        sc = blk[210 * ibl + 192:210 * ibl + 208].view(np.int8).astype(np.int64)
+        d = float(blk[210 * ibl + 208:210 * ibl + 210].view(np.float16)[0])
+        aux8 = np.zeros(256, dtype=np.int64)
+        for j in range(0, 256, 128):
+            q4, h = ql[j // 2:], qh[j // 4:]
+            for l in range(32):
+                aux8[j + l] = ((q4[l] & 0xF) | ((h[l] & 3) << 4)) - 32
+                aux8[j + l + 32] = ((q4[l + 32] & 0xF) | (((h[l] >> 2) & 3) << 4)) - 32
+                aux8[j + l + 64] = ((q4[l] >> 4) | (((h[l] >> 4) & 3) << 4)) - 32
+                aux8[j + l + 96] = ((q4[l + 32] >> 4) | (((h[l] >> 6) & 3) << 4)) - 32
+        isum = sum(float(sc[j]) * float(np.dot(q8[ibl, 16 * j:16 * j + 16], aux8[16 * j:16 * j + 16])) for j in range(16))
+        tot += d * yd[ibl] * isum
+    return tot
+
+
+def _vd_q5_k(blk, q8, yd, bsums):
+    """candle's Q5_K x Q8_K vec_dot_unopt (k_quants.rs:1870-1956) for one row, in f64, with the
+    scales and mins unpacked through the utmp word shuffle."""
+    tot = 0.0
+    for ibl in range(len(blk) // 176):
+        b = blk[176 * ibl:176 * ibl + 176].astype(np.int64)
+        d = float(blk[176 * ibl:176 * ibl + 2].view(np.float16)[0])
+        dmin = float(blk[176 * ibl + 2:176 * ibl + 4].view(np.float16)[0])
+        scales, mins = _utmp_scales(blk[176 * ibl + 4:176 * ibl + 16])
+        hm, q5 = b[16:48], b[48:176]
+        aux8 = np.zeros(256, dtype=np.int64)
+        m, pos = 1, 0
+        for c in range(4):
+            for half in range(2):
+                for l in range(32):
+                    v = (q5[32 * c + l] & 0xF) if half == 0 else (q5[32 * c + l] >> 4)
+                    aux8[pos + l] = v + (16 if hm[l] & m else 0)
+                pos += 32
+                m <<= 1
+        isum = sum(scales[j] * float(np.dot(q8[ibl, 32 * j:32 * j + 32], aux8[32 * j:32 * j + 32])) for j in range(8))
+        sumi = sum(int(bsums[ibl, j]) * mins[j // 2] for j in range(16))
+        tot += d * yd[ibl] * isum - dmin * yd[ibl] * sumi
+    return tot
+
+
+@pytest.mark.parametrize("dtype", [F.Q5_K, F.Q6_K])
+def test_k_quant_dequantize_agrees_with_candle_vec_dot_layout(dtype):
+    """The oracle's Q5_K / Q6_K dequantizers against candle's vec_dot_unopt arithmetic (a second
+    reading of the same bytes): both in f64 against the same Q8_K activation codes, equal up to the
+    f32 rounding of the dequantized weights (a misplaced bit or scale is off by far more)."""
+    rng = np.random.default_rng(40 + dtype)
+    k, rows = 512, 5
+    w = synth.random_blocks(dtype, rows * k, rng).reshape(rows, -1)
+    x = rng.standard_normal(k).astype(np.float32)
+    q8, yd, bsums = _q8k_rows(x)
+    xd = (q8 * yd[:, None]).reshape(-1)
+    got = O.qmatmul_f64(dtype, w, rows, k, xd.astype(np.float32))[0]
+    if dtype == F.Q6_K:
+        want = np.array([_vd_q6_k(w[r], q8, yd) for r in range(rows)])
+    else:
+        want = np.array([_vd_q5_k(w[r], q8, yd, bsums) for r in range(rows)])
+    assert np.allclose(got, want, rtol=1e-6, atol=1e-6)
 
 
 def test_mxfp4_matches_the_metal_table_for_every_exponent_and_code():
@@ -290,7 +417,54 @@ def _mv_iq3_s(blk, x):
     return tot
 
 
-@pytest.mark.parametrize("dtype,mv", [(F.IQ2_XXS, _mv_iq2_xxs), (F.IQ2_S, _mv_iq2_s), (F.IQ3_S, _mv_iq3_s)])
+def _mv_iq3_xxs(blk, x):
+    """kernel_mul_mv_iq3_xxs_f32_impl (quantized.metal:5700-5786) for one row, in f64."""
+    g, ks = G.grid_bytes("iq3xxs_grid"), G.ksigns_closed_form()
+    tot = 0.0
+    for ibl in range(len(blk) // 98):
+        b = blk[98 * ibl:98 * ibl + 98].astype(np.int64)
+        db = float(blk[98 * ibl:98 * ibl + 2].view(np.float16)[0])
+        for ib in range(8):
+            yl = x[256 * ibl + 32 * ib:256 * ibl + 32 * ib + 32]
+            q3 = b[2 + 8 * ib:]
+            gas = b[2 + 64 + 4 * ib:]
+            aux32 = int(gas[0]) | (int(gas[1]) << 8) | (int(gas[2]) << 16) | (int(gas[3]) << 24)
+            d = db * (0.5 + (aux32 >> 28))
+            s0 = s1 = 0.0
+            for l in range(4):
+                g1, g2 = g[int(q3[2 * l])], g[int(q3[2 * l + 1])]
+                signs = ks[(aux32 >> 7 * l) & 127]
+                for j in range(4):
+                    s0 += yl[8 * l + j] * float(g1[j]) * (-1.0 if signs & (1 << j) else 1.0)
+                    s1 += yl[8 * l + j + 4] * float(g2[j]) * (-1.0 if signs & (1 << (j + 4)) else 1.0)
+            tot += d * (s0 + s1)
+    return tot * 0.5
+
+
+def _mv_iq4_xs(blk, x):
+    """kernel_mul_mv_iq4_xs_f32_impl (quantized.metal:6384-6460) for one row, in f64: lane
+    (ib, il) pairs the low nibbles of bytes 8il..8il+8 of the sub-block with x[32ib + 8il ..) and
+    the high nibbles with x[32ib + 16 + 8il ..)."""
+    kv = G.reference_kvalues_iq4nl() or [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]
+    tot = 0.0
+    for ibl in range(len(blk) // 136):
+        b = blk[136 * ibl:136 * ibl + 136].astype(np.int64)
+        db = float(blk[136 * ibl:136 * ibl + 2].view(np.float16)[0])
+        sh = int(b[2]) | (int(b[3]) << 8)
+        for ib in range(8):
+            ls = (((int(b[4 + ib // 2]) >> 4 * (ib % 2)) & 0xF) | (((sh >> 2 * ib) & 3) << 4)) - 32
+            acc = 0.0
+            for il in range(2):
+                yb = x[256 * ibl + 32 * ib + 8 * il:]
+                q4 = b[8 + 16 * ib + 8 * il:]
+                for j in range(8):
+                    acc += yb[j] * kv[int(q4[j]) & 0xF] + yb[16 + j] * kv[int(q4[j]) >> 4]
+            tot += db * ls * acc
+    return tot
+
+
+@pytest.mark.parametrize("dtype,mv", [(F.IQ2_XXS, _mv_iq2_xxs), (F.IQ2_S, _mv_iq2_s), (F.IQ3_S, _mv_iq3_s),
+                                      (F.IQ3_XXS, _mv_iq3_xxs), (F.IQ4_XS, _mv_iq4_xs)])
 def test_iq_dequantize_agrees_with_the_metal_matvec_formulation(dtype, mv):
     rng = np.random.default_rng(dtype)
     k, rows = 512, 6
@@ -325,18 +499,27 @@ def test_dequantized_values_are_exact_products(dtype):
 
 def test_grid_table_invariants():
     assert G.GRIDS["iq2xxs_grid"].size == 256 and G.GRIDS["iq2s_grid"].size == 1024
-    assert G.GRIDS["iq3s_grid"].size == 512
+    assert G.GRIDS["iq3s_grid"].size == 512 and G.GRIDS["iq3xxs_grid"].size == 256
     assert set(np.unique(G.grid_bytes("iq2xxs_grid"))) == {8, 25, 43}
     assert set(np.unique(G.grid_bytes("iq2s_grid"))) == {8, 25, 43}
     assert set(np.unique(G.grid_bytes("iq3s_grid"))) == set(range(1, 16, 2))
+    assert set(np.unique(G.grid_bytes("iq3xxs_grid"))) == {4, 12, 20, 28, 36, 44, 52, 62}
     # lattice points are distinct within each table
-    for name in ("iq2xxs_grid", "iq2s_grid", "iq3s_grid"):
+    for name in ("iq2xxs_grid", "iq2s_grid", "iq3s_grid", "iq3xxs_grid"):
         assert len(np.unique(G.GRIDS[name])) == G.GRIDS[name].size
 
 
 @pytest.mark.skipif(G.reference_table("iq2xxs_grid") is None, reason="reference checkout absent")
 def test_tables_equal_the_reference_shader_text():
-    for name in ("iq2xxs_grid", "iq2s_grid", "iq3s_grid"):
+    for name in ("iq2xxs_grid", "iq2s_grid", "iq3s_grid", "iq3xxs_grid"):
         assert [int(v) for v in G.GRIDS[name]] == G.reference_table(name), name
+    # the oracle's IQ4 levels: one code per sub-block position with d = 1 and scale 33 (d_ib = 1)
+    blk = np.zeros(136, dtype=np.uint8)
+    blk[0:2] = np.array([np.float16(1.0)]).view(np.uint8)
+    blk[2:4] = [0xAA, 0xAA]                              # scales_h: bits 10 per sub-block -> 32
+    blk[4:8] = 0x11                                      # scales_l nibbles 1 -> ls = 1 + 32 = 33
+    blk[8:24] = np.arange(16, dtype=np.uint8)            # sub-block 0: codes 0..15 (low nibbles)
+    y = O.dequantize(F.IQ4_XS, blk, 256)
+    assert list(y[:16]) == G.reference_kvalues_iq4nl()
     assert list(G.ksigns_closed_form()) == G.reference_table("ksigns_iq2xs")
     assert G.reference_table("kmask_iq2xs") == [1 << i for i in range(8)]
