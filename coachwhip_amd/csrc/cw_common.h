@@ -15,8 +15,9 @@ int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3
 int check_launch(const char *what);
 
 inline bool is_weight_type(int dtype) {
-    return dtype == CW_Q8_0 || dtype == CW_Q2_K || dtype == CW_Q4_K || dtype == CW_IQ2_XXS || dtype == CW_IQ2_S ||
-           dtype == CW_IQ3_S || dtype == CW_MXFP4;
+    return dtype == CW_Q8_0 || dtype == CW_Q2_K || dtype == CW_Q4_K || dtype == CW_Q5_K || dtype == CW_Q6_K ||
+           dtype == CW_IQ2_XXS || dtype == CW_IQ2_S || dtype == CW_IQ3_XXS || dtype == CW_IQ3_S || dtype == CW_IQ4_XS ||
+           dtype == CW_MXFP4;
 }
 
 }  // namespace cw

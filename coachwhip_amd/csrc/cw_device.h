@@ -11,10 +11,10 @@
 // rounding of the sum.
 //
 // Layout and arithmetic follow vendor/candle-core/src/quantized/k_quants.rs (Q8_0 766-782,
-// Q2_K 1152-1190, Q4_K 1821-1849 with get_scale_min_k4 in quantized/utils.rs:50-60, MXFP4
-// 638-691) and the
-// Metal dequantizers in vendor/candle-metal-kernels/src/metal_src/quantized.metal
-// (IQ2_XXS 6820-6843, IQ2_S 6918-6935, IQ3_S 6893-6916).
+// Q2_K 1152-1190, Q4_K 1821-1849 with get_scale_min_k4 in quantized/utils.rs:50-60, Q5_K
+// 2120-2152, Q6_K 2420-2451, MXFP4 638-691) and the Metal dequantizers in
+// vendor/candle-metal-kernels/src/metal_src/quantized.metal (IQ2_XXS 6820-6843, IQ2_S 6918-6935,
+// IQ3_XXS 6866-6891, IQ3_S 6893-6916, IQ4_XS 7000-7016).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
@@ -31,6 +31,10 @@ struct TableRegs;
 static __constant__ uint64_t c_iq2xxs_grid[256] = {CW_IQ2XXS_GRID_VALUES};
 static __constant__ uint64_t c_iq2s_grid[1024] = {CW_IQ2S_GRID_VALUES};
 static __constant__ uint32_t c_iq3s_grid[512] = {CW_IQ3S_GRID_VALUES};
+static __constant__ uint32_t c_iq3xxs_grid[256] = {CW_IQ3XXS_GRID_VALUES};
+// kvalues_iq4nl_f (quantized.metal:4561-4563): the 16 non-linear levels of IQ4_XS
+static __constant__ float c_kv_iq4nl[16] = {-127.f, -104.f, -83.f, -65.f, -49.f, -35.f, -22.f, -10.f,
+                                            1.f,    13.f,   25.f,  38.f,  53.f,  69.f,  89.f,  113.f};
 
 __device__ __forceinline__ uint32_t ld_u32(const uint8_t *p) { uint32_t v; __builtin_memcpy(&v, p, 4); return v; }
 __device__ __forceinline__ uint32_t ld_u16(const uint8_t *p) { uint16_t v; __builtin_memcpy(&v, p, 2); return v; }
@@ -101,6 +105,19 @@ struct FQ8_0 {
     }
 };
 
+// get_scale_min_k4 (quantized/utils.rs:50-60) for sub-block j of a Q4_K / Q5_K super-block whose
+// first 16 bytes (d, dmin, the 12 scale bytes) are hd
+__device__ __forceinline__ uint32_t k4_sbyte(const uint4 &hd, int i) { return ((&hd.x)[1 + (i >> 2)] >> (8 * (i & 3))) & 0xFF; }
+__device__ __forceinline__ void k4_sc_mn(const uint4 &hd, int j, uint32_t &sc, uint32_t &mn) {
+    if (j < 4) {
+        sc = k4_sbyte(hd, j) & 63;
+        mn = k4_sbyte(hd, j + 4) & 63;
+    } else {
+        sc = (k4_sbyte(hd, j + 4) & 0xF) | ((k4_sbyte(hd, j - 4) >> 6) << 4);
+        mn = (k4_sbyte(hd, j + 4) >> 4) | ((k4_sbyte(hd, j) >> 6) << 4);
+    }
+}
+
 // ---------------------------------------------------------------------------------- Q4_K
 struct FQ4_K {
     static constexpr int BS = 256, TS = 144, LDS_BYTES = 0;
@@ -121,20 +138,7 @@ struct FQ4_K {
         r.j = j;
         return r;
     }
-    static __device__ __forceinline__ uint32_t sbyte(const Raw &r, int i) {  // scale byte i (0..11)
-        return ((&r.hd.x)[1 + (i >> 2)] >> (8 * (i & 3))) & 0xFF;
-    }
-    // get_scale_min_k4 (quantized/utils.rs:50-60) for sub-block j
-    static __device__ __forceinline__ void sc_mn(const Raw &r, uint32_t &sc, uint32_t &mn) {
-        const int j = r.j;
-        if (j < 4) {
-            sc = sbyte(r, j) & 63;
-            mn = sbyte(r, j + 4) & 63;
-        } else {
-            sc = (sbyte(r, j + 4) & 0xF) | ((sbyte(r, j - 4) >> 6) << 4);
-            mn = (sbyte(r, j + 4) >> 4) | ((sbyte(r, j) >> 6) << 4);
-        }
-    }
+    static __device__ __forceinline__ void sc_mn(const Raw &r, uint32_t &sc, uint32_t &mn) { k4_sc_mn(r.hd, r.j, sc, mn); }
     static __device__ __forceinline__ uint32_t nib(const Raw &r, int l) {
         uint32_t w = l < 16 ? (&r.q0.x)[l >> 2] : (&r.q1.x)[(l - 16) >> 2];
         return (w >> (8 * (l & 3) + 4 * (r.j & 1))) & 0xFu;
@@ -227,6 +231,125 @@ struct FQ2_K {
             t += d * (float)(s & 0xF) * sq - mn * (float)(s >> 4) * xs[h];
         }
         return t;
+    }
+    static __device__ __forceinline__ float dot(const Raw &r, const void *lds, const float *x) {
+        float xs[2];
+        half_sums(x, xs);
+        return dot_s(r, lds, x, xs);
+    }
+};
+
+// ---------------------------------------------------------------------------------- Q5_K
+// {d, dmin, scales[12], qh[32], qs[128]} (k_quants.rs:2120-2152): sub-block j is the low (j even)
+// or high (j odd) nibbles of qs[32(j/2) ..) plus 16 times bit j of qh[l], scaled as Q4_K:
+// y = (d*sc)*q - dmin*m, the product exact (q < 32), one rounding.
+struct FQ5_K {
+    static constexpr int BS = 256, TS = 176, LDS_BYTES = 0;
+    static __device__ __forceinline__ uint64_t table_word(int) { return 0; }
+    struct Raw { uint4 hd; uint4 q0, q1; uint4 h0, h1; int j; };
+    static __device__ __forceinline__ void fill_lds(void *, int, int) {}
+    static __device__ __forceinline__ Raw load(const uint8_t *row, int sb) {
+        const uint8_t *b = row + TS * (sb >> 3);
+        const int j = sb & 7;
+        Raw r;
+        r.hd = ld_u128(b);
+        r.h0 = ld_u128(b + 16);
+        r.h1 = ld_u128(b + 32);
+        const uint8_t *qs = b + 48 + 32 * (j >> 1);
+        r.q0 = ld_u128(qs);
+        r.q1 = ld_u128(qs + 16);
+        r.j = j;
+        return r;
+    }
+    // the 5-bit codes of weights 4k..4k+3 as bytes
+    static __device__ __forceinline__ uint32_t codes4(const Raw &r, int k) {
+        const uint32_t w = k < 4 ? (&r.q0.x)[k] : (&r.q1.x)[k - 4];
+        const uint32_t h = k < 4 ? (&r.h0.x)[k] : (&r.h1.x)[k - 4];
+        return ((w >> (4 * (r.j & 1))) & 0x0F0F0F0Fu) | (((h >> r.j) & 0x01010101u) << 4);
+    }
+    static __device__ __forceinline__ void dequant(const Raw &r, const void *, float *y) {
+        uint32_t sc, mn;
+        k4_sc_mn(r.hd, r.j, sc, mn);
+        const float d1 = h2f(r.hd.x & 0xFFFF) * (float)sc, m1 = h2f(r.hd.x >> 16) * (float)mn;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t c = codes4(r, k);
+#pragma unroll
+            for (int i = 0; i < 4; i++) y[4 * k + i] = d1 * ubyte(c, i) - m1;
+        }
+    }
+    static constexpr bool HAS_MIN = true;
+    static __device__ __forceinline__ float dot_s(const Raw &r, const void *, const float *x, const float *xs) {
+        uint32_t sc, mn;
+        k4_sc_mn(r.hd, r.j, sc, mn);
+        float s = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t c = codes4(r, k);
+#pragma unroll
+            for (int i = 0; i < 4; i++) s = fmaf(ubyte(c, i), x[4 * k + i], s);
+        }
+        return h2f(r.hd.x & 0xFFFF) * (float)sc * s - h2f(r.hd.x >> 16) * (float)mn * (xs[0] + xs[1]);
+    }
+    static __device__ __forceinline__ float dot(const Raw &r, const void *lds, const float *x) {
+        float xs[2];
+        half_sums(x, xs);
+        return dot_s(r, lds, x, xs);
+    }
+};
+
+// ---------------------------------------------------------------------------------- Q6_K
+// {ql[128], qh[64], scales[16] (i8), d} (k_quants.rs:2420-2451): sub-block j = 4h + r (half h,
+// quadrant r) is the low (r < 2) or high nibbles of ql[64h + 32(r&1) ..) plus 16 times bits
+// 2r, 2r+1 of qh[32h + l], minus 32; its halves of 16 are scaled by d * scales[8h + 2r (+1)].
+// y = (d*sc)*(q-32) is exact in f32.
+struct FQ6_K {
+    static constexpr int BS = 256, TS = 210, LDS_BYTES = 0;
+    static __device__ __forceinline__ uint64_t table_word(int) { return 0; }
+    struct Raw { uint4 q0, q1; uint4 h0, h1; uint32_t sc; uint32_t d; int r; };
+    static __device__ __forceinline__ void fill_lds(void *, int, int) {}
+    static __device__ __forceinline__ Raw load(const uint8_t *row, int sb) {
+        const uint8_t *b = row + TS * (sb >> 3);
+        const int j = sb & 7, h = j >> 2, q = j & 3;
+        Raw r;
+        const uint8_t *ql = b + 64 * h + 32 * (q & 1), *qh = b + 128 + 32 * h;
+        r.q0 = ld_u128(ql);
+        r.q1 = ld_u128(ql + 16);
+        r.h0 = ld_u128(qh);
+        r.h1 = ld_u128(qh + 16);
+        r.sc = ld_u16(b + 192 + 8 * h + 2 * q);  // the scales of the two halves
+        r.d = ld_u16(b + 208);
+        r.r = q;
+        return r;
+    }
+    // the 6-bit codes (before the -32) of weights 4k..4k+3 as bytes
+    static __device__ __forceinline__ uint32_t codes4(const Raw &r, int k) {
+        const uint32_t w = k < 4 ? (&r.q0.x)[k] : (&r.q1.x)[k - 4];
+        const uint32_t h = k < 4 ? (&r.h0.x)[k] : (&r.h1.x)[k - 4];
+        return ((w >> (4 * (r.r >> 1))) & 0x0F0F0F0Fu) | (((h >> (2 * r.r)) & 0x03030303u) << 4);
+    }
+    static __device__ __forceinline__ float scale(const Raw &r, int half) { return (float)(int8_t)(r.sc >> (8 * half)); }
+    static __device__ __forceinline__ void dequant(const Raw &r, const void *, float *y) {
+        const float d = h2f(r.d);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t c = codes4(r, k);
+            const float ds = d * scale(r, k >> 2);
+#pragma unroll
+            for (int i = 0; i < 4; i++) y[4 * k + i] = ds * (float)((int)((c >> (8 * i)) & 0xFF) - 32);
+        }
+    }
+    static constexpr bool HAS_MIN = true;
+    // sum over each half of code * x, less 32 times the half's sum of x
+    static __device__ __forceinline__ float dot_s(const Raw &r, const void *, const float *x, const float *xs) {
+        float s[2] = {0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t c = codes4(r, k);
+#pragma unroll
+            for (int i = 0; i < 4; i++) s[k >> 2] = fmaf(ubyte(c, i), x[4 * k + i], s[k >> 2]);
+        }
+        return h2f(r.d) * (scale(r, 0) * (s[0] - 32.f * xs[0]) + scale(r, 1) * (s[1] - 32.f * xs[1]));
     }
     static __device__ __forceinline__ float dot(const Raw &r, const void *lds, const float *x) {
         float xs[2];
@@ -443,6 +566,113 @@ struct FIQ3_S {
             for (int i = 0; i < 4; i++) s = fmaf(ubyte(gw, i), flip(x[4 * g + i], r.sg, 4 * g + i), s);
         }
         return s * (h2f(r.d) * (float)(1 + 2 * (int)((r.sc >> r.sh) & 0xF)));
+    }
+};
+
+// ---------------------------------------------------------------------------------- IQ3_XXS
+// {d, qs[64] grid indices, then one word per sub-block: four 7-bit sign indices and the 4-bit
+// scale s on top} (quantized.metal:6866-6891): weights 8h..8h+7 of sub-block ib take grid entries
+// qs[8ib + 2h], qs[8ib + 2h + 1] (4 values each) and the signs of index (word >> 7h) & 127;
+// dl = d * (s + 0.5) * 0.5.
+struct FIQ3_XXS {
+    static constexpr int BS = 256, TS = 98, LDS_BYTES = 256 * 4;
+    static __device__ __forceinline__ uint64_t table_word(int i) {
+        return (uint64_t)c_iq3xxs_grid[2 * i] | ((uint64_t)c_iq3xxs_grid[2 * i + 1] << 32);
+    }
+    struct Raw { uint32_t d; uint2 q; uint32_t s; };
+    static __device__ __forceinline__ void fill_lds(void *lds, int tid, int nt) {
+        uint32_t *t = (uint32_t *)lds;
+        for (int i = tid; i < 256; i += nt) t[i] = c_iq3xxs_grid[i];
+    }
+    static __device__ __forceinline__ Raw load(const uint8_t *row, int sb) {
+        const uint8_t *b = row + TS * (sb >> 3);
+        const int ib = sb & 7;
+        Raw r;
+        r.d = ld_u16(b);
+        r.q = ld_u64(b + 2 + 8 * ib);
+        r.s = ld_u32(b + 66 + 4 * ib);
+        return r;
+    }
+    static __device__ __forceinline__ uint32_t gidx(const Raw &r, int g) { return ((g < 4 ? r.q.x : r.q.y) >> (8 * (g & 3))) & 0xFF; }
+    static __device__ __forceinline__ float dl(const Raw &r) { return h2f(r.d) * (0.5f + (float)(r.s >> 28)) * 0.5f; }
+    static __device__ __forceinline__ void dequant(const Raw &r, const void *lds, float *y) {
+        const uint32_t *grid = (const uint32_t *)lds;
+        const float d = dl(r);
+#pragma unroll
+        for (int h = 0; h < 4; h++) {
+            const uint32_t sg = ksign((r.s >> (7 * h)) & 127);
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const uint32_t gw = grid[gidx(r, 2 * h + t)];
+#pragma unroll
+                for (int i = 0; i < 4; i++) y[8 * h + 4 * t + i] = d * ubyte(gw, i) * ((sg >> (4 * t + i)) & 1 ? -1.f : 1.f);
+            }
+        }
+    }
+    static __device__ __forceinline__ float dot(const Raw &r, const void *lds, const float *x) {
+        const uint32_t *grid = (const uint32_t *)lds;
+        float s = 0.f;
+#pragma unroll
+        for (int h = 0; h < 4; h++) {
+            const uint32_t sg = ksign((r.s >> (7 * h)) & 127);
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const uint32_t gw = grid[gidx(r, 2 * h + t)];
+#pragma unroll
+                for (int i = 0; i < 4; i++) s = fmaf(ubyte(gw, i), flip(x[8 * h + 4 * t + i], sg, 4 * t + i), s);
+            }
+        }
+        return s * dl(r);
+    }
+};
+
+// ---------------------------------------------------------------------------------- IQ4_XS
+// {d, scales_h (u16), scales_l[4], qs[128]} (quantized.metal:7000-7016): sub-block ib has the
+// 6-bit scale ls (a scales_l nibble, 2 bits of scales_h on top), d_ib = d * (ls - 32), and its 32
+// weights are the levels kvalues[nibble] of the low, then the high nibbles of qs[16ib ..). The
+// 16 levels sit in LDS.
+struct FIQ4_XS {
+    static constexpr int BS = 256, TS = 136, LDS_BYTES = 16 * 4;
+    static __device__ __forceinline__ uint64_t table_word(int i) {
+        return (uint64_t)__float_as_uint(c_kv_iq4nl[2 * i]) | ((uint64_t)__float_as_uint(c_kv_iq4nl[2 * i + 1]) << 32);
+    }
+    struct Raw { uint2 hd; uint4 q; int ib; };
+    static __device__ __forceinline__ void fill_lds(void *lds, int tid, int nt) {
+        float *t = (float *)lds;
+        for (int i = tid; i < 16; i += nt) t[i] = c_kv_iq4nl[i];
+    }
+    static __device__ __forceinline__ Raw load(const uint8_t *row, int sb) {
+        const uint8_t *b = row + TS * (sb >> 3);
+        Raw r;
+        r.hd = ld_u64(b);  // d | scales_h << 16, scales_l[4]
+        r.ib = sb & 7;
+        r.q = ld_u128(b + 8 + 16 * r.ib);
+        return r;
+    }
+    static __device__ __forceinline__ float dib(const Raw &r) {
+        const uint32_t ls = ((r.hd.y >> (4 * r.ib)) & 0xF) | (((r.hd.x >> (16 + 2 * r.ib)) & 3) << 4);
+        return h2f(r.hd.x & 0xFFFF) * (float)((int)ls - 32);
+    }
+    static __device__ __forceinline__ void dequant(const Raw &r, const void *lds, float *y) {
+        const float *kv = (const float *)lds;
+        const float d = dib(r);
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const uint32_t b = ((&r.q.x)[j >> 2] >> (8 * (j & 3))) & 0xFF;
+            y[j] = d * kv[b & 0xF];
+            y[16 + j] = d * kv[b >> 4];
+        }
+    }
+    static __device__ __forceinline__ float dot(const Raw &r, const void *lds, const float *x) {
+        const float *kv = (const float *)lds;
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const uint32_t b = ((&r.q.x)[j >> 2] >> (8 * (j & 3))) & 0xFF;
+            s = fmaf(kv[b & 0xF], x[j], s);
+            s = fmaf(kv[b >> 4], x[16 + j], s);
+        }
+        return s * dib(r);
     }
 };
 

@@ -180,6 +180,10 @@ static int launch_fmt(int dtype, const GemvArgs &a, dim3 grid, int threads, size
     case CW_IQ2_XXS: return launch_lpr<FIQ2_XXS>(a, grid, threads, shmem, s);
     case CW_IQ2_S: return launch_lpr<FIQ2_S>(a, grid, threads, shmem, s);
     case CW_IQ3_S: return launch_lpr<FIQ3_S>(a, grid, threads, shmem, s);
+    case CW_Q5_K: return launch_lpr<FQ5_K>(a, grid, threads, shmem, s);
+    case CW_Q6_K: return launch_lpr<FQ6_K>(a, grid, threads, shmem, s);
+    case CW_IQ3_XXS: return launch_lpr<FIQ3_XXS>(a, grid, threads, shmem, s);
+    case CW_IQ4_XS: return launch_lpr<FIQ4_XS>(a, grid, threads, shmem, s);
     default: return set_error(CW_ENOTSUP, "gemv: dtype %d is not supported", dtype);
     }
 }
@@ -237,6 +241,10 @@ int gemv_dense(int dtype, const GemvArgs &a, int m, hipStream_t s) {
     case CW_IQ2_XXS: return dense_lpr<FIQ2_XXS>(a, m, s);
     case CW_IQ2_S: return dense_lpr<FIQ2_S>(a, m, s);
     case CW_IQ3_S: return dense_lpr<FIQ3_S>(a, m, s);
+    case CW_Q5_K: return dense_lpr<FQ5_K>(a, m, s);
+    case CW_Q6_K: return dense_lpr<FQ6_K>(a, m, s);
+    case CW_IQ3_XXS: return dense_lpr<FIQ3_XXS>(a, m, s);
+    case CW_IQ4_XS: return dense_lpr<FIQ4_XS>(a, m, s);
     default: return set_error(CW_ENOTSUP, "gemv: dtype %d is not supported", dtype);
     }
 }
@@ -255,6 +263,10 @@ int dequantize(int dtype, const void *blocks, int64_t n_elems, float *out, hipSt
     case CW_IQ2_XXS: hipLaunchKernelGGL(k_dequant<FIQ2_XXS>, grid, dim3(256), 0, s, b, n_sub, out); break;
     case CW_IQ2_S: hipLaunchKernelGGL(k_dequant<FIQ2_S>, grid, dim3(256), 0, s, b, n_sub, out); break;
     case CW_IQ3_S: hipLaunchKernelGGL(k_dequant<FIQ3_S>, grid, dim3(256), 0, s, b, n_sub, out); break;
+    case CW_Q5_K: hipLaunchKernelGGL(k_dequant<FQ5_K>, grid, dim3(256), 0, s, b, n_sub, out); break;
+    case CW_Q6_K: hipLaunchKernelGGL(k_dequant<FQ6_K>, grid, dim3(256), 0, s, b, n_sub, out); break;
+    case CW_IQ3_XXS: hipLaunchKernelGGL(k_dequant<FIQ3_XXS>, grid, dim3(256), 0, s, b, n_sub, out); break;
+    case CW_IQ4_XS: hipLaunchKernelGGL(k_dequant<FIQ4_XS>, grid, dim3(256), 0, s, b, n_sub, out); break;
     default: return set_error(CW_ENOTSUP, "dequantize: dtype %d is not supported", dtype);
     }
     return check_launch("k_dequant");

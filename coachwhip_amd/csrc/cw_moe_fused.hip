@@ -571,6 +571,10 @@ static int by_fmt(int dtype, const MoeArgs &a, int T, hipStream_t s) {
     case CW_IQ2_XXS: return by_shape<FIQ2_XXS, DOWN>(a, T, s);
     case CW_IQ2_S: return by_shape<FIQ2_S, DOWN>(a, T, s);
     case CW_IQ3_S: return by_shape<FIQ3_S, DOWN>(a, T, s);
+    case CW_Q5_K: return by_shape<FQ5_K, DOWN>(a, T, s);
+    case CW_Q6_K: return by_shape<FQ6_K, DOWN>(a, T, s);
+    case CW_IQ3_XXS: return by_shape<FIQ3_XXS, DOWN>(a, T, s);
+    case CW_IQ4_XS: return by_shape<FIQ4_XS, DOWN>(a, T, s);
     default: return set_error(CW_ENOTSUP, "moe: dtype %d is not supported", dtype);
     }
 }

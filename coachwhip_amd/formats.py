@@ -36,7 +36,7 @@ D_OFFSET = {Q8_0: 0, Q2_K: 80, Q3_K: 108, Q4_K: 0, Q5_K: 0, Q6_K: 208, IQ2_XXS: 
 SHRINK_SOURCES = (Q3_K, Q4_K, Q5_K)
 
 # the weight formats the kernels take (Q8_K is an activation format only)
-WEIGHT_TYPES = (Q8_0, Q2_K, Q4_K, IQ2_XXS, IQ2_S, IQ3_S, MXFP4)
+WEIGHT_TYPES = (Q8_0, Q2_K, Q4_K, Q5_K, Q6_K, IQ2_XXS, IQ2_S, IQ3_XXS, IQ3_S, IQ4_XS, MXFP4)
 
 
 def block_size(dtype):

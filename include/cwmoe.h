@@ -51,10 +51,13 @@ enum cw_dtype {
     CW_Q2_K = 10,    /* {u8 scales[16]; u8 qs[64]; f16 d, dmin}: 84 B per 256 (the shrink's output) */
     CW_Q3_K = 11,    /* {u8 hmask[32]; u8 qs[64]; u8 scales[12]; f16 d}: 110 B per 256 (shrink input) */
     CW_Q4_K = 12,    /* {f16 d, dmin; u8 scales[12]; u8 qs[128]}: 144 B per 256 */
-    CW_Q5_K = 13,    /* {f16 d, dmin; u8 scales[12]; u8 qh[32]; u8 qs[128]}: 176 B per 256 (shrink input) */
+    CW_Q5_K = 13,    /* {f16 d, dmin; u8 scales[12]; u8 qh[32]; u8 qs[128]}: 176 B per 256 */
+    CW_Q6_K = 14,    /* {u8 ql[128]; u8 qh[64]; i8 scales[16]; f16 d}: 210 B per 256 */
     CW_IQ2_XXS = 16, /* {f16 d; u16 qs[32]}: 66 B per 256 */
+    CW_IQ3_XXS = 18, /* {f16 d; u8 qs[64]; u32 scales_and_signs[8]}: 98 B per 256 */
     CW_IQ3_S = 21,   /* {f16 d; u8 qs[64], qh[8], signs[32], scales[4]}: 110 B per 256 */
     CW_IQ2_S = 22,   /* {f16 d; u8 qs[64], qh[8], scales[8]}: 82 B per 256 */
+    CW_IQ4_XS = 23,  /* {f16 d; u16 scales_h; u8 scales_l[4]; u8 qs[128]}: 136 B per 256 */
     CW_MXFP4 = 39    /* {u8 e8m0; u8 qs[16]}: 17 B per 32 */
 };
 

@@ -120,8 +120,8 @@ def test_next_row_entry_points_reject_bad_arguments():
     src.shape[1] = 0x2000                                                 # weights on a matrix kept as it is
     assert L.cw_bank_device_bytes(ctypes.byref(src), 2) == 0
     src.shape[1] = None
-    src.dtype[2], src.rows[2], src.cols[2] = F.Q5_K, 64, 256              # a shrink source must be shrunk
-    src.expert_bytes[2] = F.matrix_bytes(F.Q5_K, 64, 256)
+    src.dtype[2], src.rows[2], src.cols[2] = F.Q3_K, 64, 256              # Q3_K is read only through the shrink
+    src.expert_bytes[2] = F.matrix_bytes(F.Q3_K, 64, 256)
     assert L.cw_bank_device_bytes(ctypes.byref(src), 2) == 0
     src.shrink[2] = 1                                                     # ... and then its slots are Q2_K
     q2 = F.matrix_bytes(F.Q2_K, 64, 256)

@@ -49,7 +49,8 @@ def test_dequantize_is_bit_exact(dtype):
         ts = F.type_size(dtype)
         nb = n // F.block_size(dtype)
         edge = np.array([0x8001, 0x0001, 0x03FF, 0xBC00, 0x7BFF, 0x0000], dtype=np.uint16).view(np.uint8).reshape(-1, 2)
-        raw.reshape(nb, ts)[:len(edge), 0:2] = edge
+        o = F.D_OFFSET[dtype]
+        raw.reshape(nb, ts)[:len(edge), o:o + 2] = edge
     got = host(ops.dequantize(dtype, dev(raw), n))
     want = O.dequantize(dtype, raw, n)
     if dtype == F.MXFP4:
@@ -70,6 +71,11 @@ QMM_CASES = [
     (F.IQ3_S, 512, 2048, 2),
     (F.Q8_0, 96, 64, 5),          # short rows: 2 blocks, 8 lanes per row
     (F.Q4_K, 33, 256, 1),         # one super-block per row, ragged row count
+    (F.Q5_K, 512, 2048, 1),
+    (F.Q6_K, 1024, 1024, 3),
+    (F.Q6_K, 77, 256, 1),
+    (F.IQ3_XXS, 512, 2048, 2),
+    (F.IQ4_XS, 300, 1024, 4),
 ]
 
 
@@ -164,7 +170,8 @@ def test_qmatmul_rejects_bad_shapes():
 
 @pytest.mark.parametrize("dtype,n,k", [(F.IQ2_XXS, 512, 2048), (F.IQ2_S, 2048, 512), (F.Q4_K, 512, 2048),
                                        (F.IQ3_S, 512, 2048), (F.MXFP4, 256, 2880), (F.Q8_0, 128, 1024),
-                                       (F.Q2_K, 2048, 512)])
+                                       (F.Q2_K, 2048, 512), (F.Q5_K, 512, 2048), (F.Q6_K, 2048, 512),
+                                       (F.IQ3_XXS, 512, 2048), (F.IQ4_XS, 2048, 512)])
 @pytest.mark.parametrize("rows_per_expert", [False, True])
 def test_matvec_id_matches_the_oracle(dtype, n, k, rows_per_expert):
     say("matvec_id", F.NAMES[dtype], n, k, rows_per_expert)
@@ -407,6 +414,10 @@ MOE_CASES = [
     ("c5_shrunk_q2_k", 64, 10, 2048, 512, (F.Q2_K, F.Q2_K, F.Q2_K), 0, 0, 1),
     ("q2_k_gate_up_tokens", 32, 4, 1024, 512, (F.Q2_K, F.Q2_K, F.Q4_K), 0, 0, 24),
     ("q2_k_grouped", 32, 4, 1024, 512, (F.Q2_K, F.Q2_K, F.Q2_K), 0, 0, 56),
+    ("iq3_xxs_iq4_xs", 32, 6, 1024, 512, (F.IQ3_XXS, F.IQ3_XXS, F.IQ4_XS), 0, 0, 3),
+    ("iq3_xxs_iq4_xs_tokens", 32, 6, 1024, 512, (F.IQ3_XXS, F.IQ3_XXS, F.IQ4_XS), 0, 0, 40),
+    ("q5_k_q6_k", 16, 4, 1024, 512, (F.Q5_K, F.Q5_K, F.Q6_K), 0, 0, 2),
+    ("q6_k_q5_k_tokens", 16, 4, 1024, 512, (F.Q6_K, F.Q6_K, F.Q5_K), 0, 0, 24),
 ]
 
 # the grouped MFMA path rounds activations to fp16 once (2^-11 relative): its outputs are held
