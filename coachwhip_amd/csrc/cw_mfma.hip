@@ -89,9 +89,16 @@ constexpr Tab<256> make_iq3s_f16() {  // two 4-value entries per U4: entry 2i in
     }
     return t;
 }
+constexpr Tab<128> make_iq3xxs_f16() {  // two 4-value entries per U4: entry 2i in x,y and 2i+1 in z,w
+    constexpr uint32_t g[256] = {CW_IQ3XXS_GRID_VALUES};
+    Tab<128> t{};
+    for (int i = 0; i < 128; i++) t.v[i] = pack8((uint64_t)g[2 * i] | ((uint64_t)g[2 * i + 1] << 32));
+    return t;
+}
 static __constant__ Tab<256> c_iq2xxs_f16 = make_iq2xxs_f16();
 static __constant__ Tab<1024> c_iq2s_f16 = make_iq2s_f16();
 static __constant__ Tab<256> c_iq3s_f16 = make_iq3s_f16();
+static __constant__ Tab<128> c_iq3xxs_f16 = make_iq3xxs_f16();
 
 template <int N>
 __device__ __forceinline__ void copy_tab(uint8_t *lds, const Tab<N> &t, int tid, int nt) {
@@ -134,6 +141,11 @@ struct WinRef {
         const uint32_t *q = qa + off / 4;
         const uint32_t d0 = q[0], d1 = q[1], d2 = q[2];
         return make_uint2(__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh));
+    }
+    // 4 bytes at p + ORG + off, off a multiple of 4
+    __device__ __forceinline__ uint32_t u32(int off) const {
+        const uint32_t *q = qa + off / 4;
+        return __builtin_amdgcn_alignbyte(q[1], q[0], sh);
     }
     // 8 bytes at p + ORG + off, any off
     __device__ __forceinline__ uint2 u64x(int off) const {
@@ -429,6 +441,77 @@ struct MQ2_K {
     }
 };
 
+
+// IQ3_XXS: weights 8grp..8grp+7 of K-step kk are the grid entries qs[8kk + 2grp], qs[8kk + 2grp + 1]
+// (4 values each) with the signs of index (w >> 7grp) & 127, w the sub-block's word at byte
+// 66 + 4kk (scale nibble s on top). The multiplier 8*(2s+1), as (s << 4) | 8, keeps the codes
+// (at most 8*31*62) exact in fp16; scale() takes the 8 and the 1/4 of dl = d*(2s+1)/4 back out.
+struct MIQ3_XXS {
+    static constexpr int TS = 98, SBK = 256, LDS = 256 * 8;
+    static constexpr int KST = 8, SCALE = 0, ORG = 66;
+    static constexpr bool HAS_MIN = false;
+    static __device__ void fill(uint8_t *lds, int tid, int nt) { copy_tab(lds, c_iq3xxs_f16, tid, nt); }  // entry i: 4 halves at byte 8*i
+    struct Stage {
+        __device__ __forceinline__ void load(const WinRef &, int) {}
+    };
+    struct Raw { uint32_t qs, w; };
+    struct Look { uint2 x, y; };
+    static __device__ __forceinline__ Raw raw(const WinRef &w, const Stage &, int kk, int grp) {
+        return Raw{lds_u16(w.p + 2 + 8 * kk + 2 * grp), w.u32(4 * kk)};
+    }
+    static __device__ __forceinline__ Look look(const Raw &r, const Stage &, int, int, const uint8_t *lds, bool) {
+        const uint2 *g = (const uint2 *)lds;
+        return Look{g[r.qs & 0xFF], g[(r.qs >> 8) & 0xFF]};
+    }
+    static __device__ __forceinline__ uint4 make(const Raw &r, const Look &l, const Stage &, int, int grp, bool zero) {
+        const uint32_t s7 = (r.w >> (7 * grp)) & 127;
+        const uint32_t b = s7 | ((__builtin_popcount(s7) & 1u) << 7);
+        return scale4(apply_signs(make_uint4(l.x.x, l.x.y, l.y.x, l.y.y), b), splat_mult(zero ? 0u : ((r.w >> 28) << 4) | 8));
+    }
+    static __device__ __forceinline__ float scale(const uint8_t *win) { return h2f(lds_u16(win)) * (0.25f / 8); }
+};
+
+// IQ4_XS: K-step kk is sub-block kk, with its own scale d*(ls - 32) (per K-step, as Q8_0). Lane
+// group grp takes the low (grp < 2) or high nibbles of qs[16kk + 8(grp&1) ..); a nibble's level
+// kvalues[n] (exact in fp16) comes from a byte table of kvalues + 128 by two byte permutes and a
+// select on the nibble's top bit, then through the fp16 1024 + byte pattern less 1152.
+struct MIQ4_XS {
+    static constexpr int TS = 136, SBK = 256, LDS = 16;
+    static constexpr int KST = 8, SCALE = 2, ORG = 0;
+    static constexpr bool HAS_MIN = false;
+    static __device__ void fill(uint8_t *, int, int) {}
+    // d | scales_h << 16 and scales_l[4]: the super-block's first 8 bytes, read once per stage
+    struct Stage {
+        uint32_t h0, h1;
+        __device__ __forceinline__ void load(const WinRef &w, int) {
+            const uint2 h = w.u64(0);
+            h0 = h.x;
+            h1 = h.y;
+        }
+    };
+    struct Raw { uint2 q; float d; };
+    struct Look {};
+    static __device__ __forceinline__ Raw raw(const WinRef &w, const Stage &st, int kk, int grp) {
+        const uint32_t ls = ((st.h1 >> (4 * kk)) & 0xF) | (((st.h0 >> (16 + 2 * kk)) & 3) << 4);
+        return Raw{w.u64(8 + 16 * kk + 8 * (grp & 1)), h2f(st.h0 & 0xFFFF) * (float)((int)ls - 32)};
+    }
+    static __device__ __forceinline__ Look look(const Raw &, const Stage &, int, int, const uint8_t *, bool) { return Look{}; }
+    static __device__ __forceinline__ float step_scale(const Raw &r) { return r.d; }
+    // kvalues_iq4nl + 128 as bytes, entries 0..15 over four dwords
+    static constexpr uint32_t T0 = 0x3F2D1801u, T1 = 0x766A5D4Fu, T2 = 0xA6998D81u, T3 = 0xF1D9C5B5u;
+    static __device__ __forceinline__ uint32_t levels4(uint32_t n) {  // 4 nibbles (one per byte) -> 4 table bytes
+        const uint32_t lo = __builtin_amdgcn_perm(T1, T0, n & 0x07070707u);
+        const uint32_t hi = __builtin_amdgcn_perm(T3, T2, n & 0x07070707u);
+        const uint32_t top = ((n >> 3) & 0x01010101u) * 0xFFu;
+        return (hi & top) | (lo & ~top);
+    }
+    static __device__ __forceinline__ uint4 make(const Raw &r, const Look &, const Stage &, int, int grp, bool zero) {
+        const int sh = 4 * (grp >> 1);
+        const uint4 x = bytes_plus_1024(levels4((r.q.x >> sh) & 0x0F0F0F0Fu), levels4((r.q.y >> sh) & 0x0F0F0F0Fu));
+        const uint32_t one = zero ? 0u : 0x3C003C00u, off = zero ? 0u : 0xE480E480u;  // 1.0, -1152.0
+        return fma4(x, one, off);
+    }
+};
 
 // A stage is KST K-steps (8: 256 weights of k; 4 for Q8_0). The window of a row for a stage
 // holds the stage's bytes (an IQ, Q2_K or Q4_K super-block, or KST MXFP4 / Q8_0 blocks) from the
@@ -1126,7 +1209,7 @@ __global__ void k_fill_zero(float *p, int64_t n) {
 
 bool mfma_supported(int dtype) {
     return dtype == CW_IQ2_XXS || dtype == CW_IQ2_S || dtype == CW_IQ3_S || dtype == CW_MXFP4 || dtype == CW_Q4_K || dtype == CW_Q8_0 ||
-           dtype == CW_Q2_K;
+           dtype == CW_Q2_K || dtype == CW_IQ3_XXS || dtype == CW_IQ4_XS;
 }
 
 int max_tiles(int TK, int n_slots) { return (TK + MF_MT - 1) / MF_MT + (n_slots < TK ? n_slots : TK); }
@@ -1223,6 +1306,8 @@ static int by_fmt(int dtype, const MfArgs &a, int tiles_max, int splits, hipStre
     case CW_Q4_K: return launch<MQ4_K, MODE>(a, tiles_max, splits, s);
     case CW_Q8_0: return launch<MQ8_0, MODE>(a, tiles_max, splits, s);
     case CW_Q2_K: return launch<MQ2_K, MODE>(a, tiles_max, splits, s);
+    case CW_IQ3_XXS: return launch<MIQ3_XXS, MODE>(a, tiles_max, splits, s);
+    case CW_IQ4_XS: return launch<MIQ4_XS, MODE>(a, tiles_max, splits, s);
     default: return set_error(CW_ENOTSUP, "mfma: dtype %d has no MFMA path", dtype);
     }
 }
@@ -1260,6 +1345,8 @@ static void dense_shape(int dtype, int &rpb, int &kst, int &per_cu) {
     case CW_MXFP4: return shape_of<MMXFP4>(rpb, kst, per_cu);
     case CW_Q8_0: return shape_of<MQ8_0>(rpb, kst, per_cu);
     case CW_Q2_K: return shape_of<MQ2_K>(rpb, kst, per_cu);
+    case CW_IQ3_XXS: return shape_of<MIQ3_XXS>(rpb, kst, per_cu);
+    case CW_IQ4_XS: return shape_of<MIQ4_XS>(rpb, kst, per_cu);
     default: return shape_of<MQ4_K>(rpb, kst, per_cu);
     }
 }

@@ -18,7 +18,7 @@ pytestmark = pytest.mark.gpu
 
 REL_L2_GATE = 1e-3      # north-star tolerance for matmul / MoE outputs
 REL_L2_F32 = 2e-5       # what an f32-activation path must reach
-MFMA_TYPES = (F.IQ2_XXS, F.IQ2_S, F.IQ3_S, F.MXFP4, F.Q4_K, F.Q8_0, F.Q2_K)  # formats of the grouped / dense GEMM
+MFMA_TYPES = (F.IQ2_XXS, F.IQ2_S, F.IQ3_S, F.MXFP4, F.Q4_K, F.Q8_0, F.Q2_K, F.IQ3_XXS, F.IQ4_XS)  # formats of the grouped / dense GEMM
 
 
 def dev(a):
@@ -94,6 +94,9 @@ MM_CASES = [
     (F.Q2_K, 512, 2048, 1),
     (F.Q2_K, 2048, 512, 9),
     (F.Q2_K, 200, 768, 70),       # three super-blocks per row, N-blocks past the last row
+    (F.IQ3_XXS, 512, 2048, 24),
+    (F.IQ4_XS, 300, 1024, 65),
+    (F.IQ4_XS, 2048, 512, 9),
 ]
 
 
@@ -190,7 +193,7 @@ def test_matvec_id_matches_the_oracle(dtype, n, k, rows_per_expert):
 
 @pytest.mark.parametrize("dtype,n,k", [(F.IQ2_XXS, 512, 2048), (F.IQ2_S, 2048, 512), (F.Q4_K, 512, 2048),
                                        (F.IQ3_S, 512, 2048), (F.MXFP4, 256, 2880), (F.Q8_0, 128, 1056),
-                                       (F.Q2_K, 2048, 512)])
+                                       (F.Q2_K, 2048, 512), (F.IQ3_XXS, 512, 2048), (F.IQ4_XS, 2048, 512)])
 @pytest.mark.parametrize("rows_per_expert", [False, True])
 def test_matmul_id_grouped_matches_the_oracle(dtype, n, k, rows_per_expert):
     """cw_matmul_id_grouped (the reference's matmul_id_piles, which MoeMatvec takes above 8 tokens):
