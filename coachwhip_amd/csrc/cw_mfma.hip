@@ -1,13 +1,15 @@
 // Grouped expert GEMMs on MFMA (gfx950, v_mfma_f32_16x16x32_f16) for the MoE layer's prefill.
 //
-// Picks are grouped by the slot they read (mfma_piles); a tile is up to 64 picks of one slot by
-// 128 or 256 weight rows. Each of the 8 waves of a block owns 16 or 32 weight rows and all 64
-// picks (4 MFMA blocks).
+// Picks are grouped by the slot they read (mfma_piles); a tile is up to MF_MT = 80 picks of one
+// slot (5 MFMA blocks of 16) by RPB weight rows per matrix. A block has 16 waves for gate/up
+// (8 on gate, 8 on up) and 8 for down and dense matmuls; each wave owns 16 weight rows and every
+// pick block of the tile.
 //
 // Exactness: a weight is (f16 super-block scale) x (small integer code). The codes go through
 // MFMA as fp16 integers, which they represent exactly: IQ2_XXS / IQ2_S codes (2s+1)*grid*sign
-// are at most 31*43 = 1333, IQ3_S codes (1+2s)*grid*sign at most 31*15 = 465, MXFP4 codes the
-// doubled E2M1 values up to 12. Products with fp16 activations are exact in the f32
+// are at most 31*43 = 1333, IQ3_XXS codes 8*(2s+1)*grid*sign multiples of 8 up to 8*31*62, IQ3_S
+// codes (1+2s)*grid*sign at most 31*15 = 465, MXFP4 codes the doubled E2M1 values up to 12,
+// IQ4_XS codes the non-linear levels (|v| <= 127, scaled per K-step like Q8_0). Products with fp16 activations are exact in the f32
 // accumulators; the f32 scale of each super-block (d/8, d, or MXFP4's 2^(e-128) per 32) is
 // applied to the partial sum of its K-steps. Activations are rounded to fp16 once, with a
 // power-of-two scale per row (exact) so that no row overflows: that rounding (2^-11 relative)
@@ -554,13 +556,12 @@ __device__ __forceinline__ void dma16(const void *g, uint8_t *lds_base) {
     }
 }
 
-// Tile shape of the grouped GEMM: a block of NW = 16 waves (one block per CU, four waves per
-// SIMD at 128 registers) owns one M-tile (up to 64 picks of a slot, in 16-row pick blocks) and
-// RPB weight rows per matrix. Each wave takes NB blocks of 16 rows in each of its NM matrices
-// (gate and up together for MODE 0, so the activation sees both) and every pick block: per
-// K-step it reads one activation fragment per pick block, decodes NM*NB weight fragments and
-// issues up to 4*NM*NB MFMAs. The decode is VALU-bound, so the block keeps the whole LDS for
-// code tables that take work off the VALU, with the activations shared by all 16 waves.
+// Tile shape of the grouped GEMM: a block owns one M-tile (up to MF_MT = 80 picks of a slot, in
+// 16-row pick blocks) and RPB weight rows per matrix. Each wave takes NB blocks of 16 rows of one
+// matrix and every pick block: per K-step it reads one activation fragment per pick block,
+// decodes NB weight fragments and issues up to MF_MB*NB MFMAs. The decode is the VALU's work, so
+// the LDS holds code tables that take work off the VALU, and the activations are shared by all
+// waves of the block.
 template <class MF, int MODE>
 struct GmShape {
     static constexpr int LDS_MAX = 160 * 1024;
@@ -717,18 +718,42 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
         // stage's wait can leave exactly the next stage's loads in flight. RPB*PCS is a multiple of
         // 64: a wave's pieces lie in one matrix and the matrix base stays scalar.
         constexpr int NP = S::NM * S::RPB * W::PCS, NTW = (NP + S::NT - 1) / S::NT;
+        // A piece's row offset and its place in the row's window are the same in every stage: for
+        // the formats with registers to spare (S::FAST) they are worked out once per tile (the
+        // division by the window's piece count and the row's 32-bit multiply were most of the
+        // stage's address arithmetic), the others recompute them per stage.
+        uint32_t wp_off[NTW], wp_p[NTW];
+        if constexpr (S::FAST) {
+#pragma unroll
+            for (int t = 0; t < NTW; t++) {
+                const int i0 = tid + S::NT * t, i = i0 < NP ? i0 : i0 - NP;
+                const int r = i / W::PCS;
+                wp_p[t] = (uint32_t)(i - r * W::PCS);
+                wp_off[t] = row_off(r, __builtin_amdgcn_readfirstlane(r / S::RPB));
+            }
+        }
         auto issue_w = [&](int st_w, uint8_t *wbuf, int tido) __attribute__((always_inline)) {
             const int nk_w = min(KST, n_ks - st_w * KST);
             const uint32_t seg_w = MF::SBK == 32 ? MF::TS * nk_w : MF::TS;  // bytes of a row in this stage
 #pragma unroll
             for (int t = 0; t < NTW; t++) {
                 const int i0 = tido + S::NT * t, i = i0 < NP ? i0 : i0 - NP;  // the wrap is uniform across the wave
-                const int r = i / W::PCS, p = i - r * W::PCS;
-                const int m = __builtin_amdgcn_readfirstlane(r / S::RPB);
+                int m;
+                uint32_t o, p;
+                if constexpr (S::FAST) {
+                    m = S::NM > 1 ? __builtin_amdgcn_readfirstlane(i / (S::RPB * W::PCS)) : 0;
+                    o = wp_off[t];
+                    p = wp_p[t];
+                } else {
+                    const int r = i / W::PCS;
+                    p = (uint32_t)(i - r * W::PCS);
+                    m = __builtin_amdgcn_readfirstlane(r / S::RPB);
+                    o = row_off(r, m);
+                }
                 const uint8_t *mb = m == 0 ? wb0 : wb1;
-                const uint32_t o = row_off(r, m) + (uint32_t)(W::SEG * st_w);  // the row's stage bytes
+                o += (uint32_t)(W::SEG * st_w);                                // the row's stage bytes
                 const uint32_t mis = ((uint32_t)(uintptr_t)mb + o) & 15;      // ... from a 16-byte boundary
-                const uint32_t pc = min((uint32_t)p, (mis + seg_w - 1) >> 4);
+                const uint32_t pc = min(p, (mis + seg_w - 1) >> 4);
                 dma16<S::ADMA>(mb + (o - mis + 16 * pc), wbuf + (i - (tido & 63)) * 16);
             }
         };
