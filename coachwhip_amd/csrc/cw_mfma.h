@@ -40,9 +40,22 @@ struct MfArgs {
     int ldh;
     float *dn;                    // down: one row of n per pick, in pick order (t*K + j)
     // split-K (dense matmul): block row blockIdx.y takes stages [y*split_st, (y+1)*split_st) and
-    // writes its partial rows at dn + y*split_stride; 0 = no split
+    // writes its partial rows at dn + y*split_stride; 0 = no split. The last split of a work item
+    // to finish (split_cnt[item], zero at launch) adds the partial rows in split order into y.
     int split_st;
     int64_t split_stride;
+    int *split_cnt;
+    float *y;
+};
+
+// Work a pack launch also does for the dense matmul that follows it: the tile list of m rows, and
+// the split counters zeroed.
+struct PackExtra {
+    MfTile *tiles;
+    int *n_tiles;
+    int m;
+    int *zero;
+    int n_zero;
 };
 
 bool mfma_supported(int dtype);
@@ -51,7 +64,8 @@ int mfma_piles(const uint32_t *slots, int TK, int K, int n_slots, int *pile_pick
                int *n_tiles, hipStream_t s);
 int max_tiles(int TK, int n_slots);
 // rows x k f32 -> fp16 rows (ld = k) with per-row power-of-two scales
-int pack_rows_f16(const float *x, int rows, int k, int ldx, uint16_t *a16, float *ascale, hipStream_t s);
+int pack_rows_f16(const float *x, int rows, int k, int ldx, uint16_t *a16, float *ascale, hipStream_t s,
+                  const PackExtra *extra = nullptr);
 int fill_zero(float *p, int64_t n, hipStream_t s);
 int mfma_gateup(int dtype, const MfArgs &a, int tiles_max, hipStream_t s);
 int mfma_down(int dtype, const MfArgs &a, int tiles_max, hipStream_t s);

@@ -624,6 +624,7 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
     constexpr bool POW2 = MF::SCALE == 1, STEP = MF::SCALE == 2, MIN = MF::HAS_MIN;
     constexpr int NA = MIN ? NB : 1;  // accumulator sets of the minimum term
     extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int split_last;  // split-K: this block finished its work item's last split
     uint8_t *tab = smem;
     uint8_t *As = smem + ((MF::LDS + 15) & ~15);
     uint8_t *Ws = As + S::A_BYTES;  // window buffer(s): stage st uses Ws + (WDB ? st & 1 : 0) * W_BYTES
@@ -1044,6 +1045,7 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
                 }
             }
         } else {
+            const bool split = MODE == 2 && a.split_cnt;
 #pragma unroll
             for (int mb = 0; mb < MF_MB; mb++) {
                 if (mb >= mbs) break;
@@ -1056,7 +1058,45 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
                     for (int q = 0; q < NB; q++) {
                         const int n = nblk * S::RPB + wrow + 16 * q + l16;
                         if (n >= a.n) continue;
-                        a.dn[blockIdx.y * a.split_stride + (int64_t)pick * a.n + n] = value(q, mb, i, meta_sa[r]);
+                        float *p = a.dn + blockIdx.y * a.split_stride + (int64_t)pick * a.n + n;
+                        const float v = value(q, mb, i, meta_sa[r]);
+                        if (split)
+                            __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // at the coherence point
+                        else
+                            *p = v;
+                    }
+                }
+            }
+            if (split) {
+                // The last of the item's splits to get here adds the partial rows in split order (as a
+                // separate pass over all of them would): the partial stores are at the coherence
+                // point once this thread's stores have completed, before the block's arrival.
+                __builtin_amdgcn_s_waitcnt(0);
+                __syncthreads();
+                if (tid == 0)
+                    split_last = __hip_atomic_fetch_add(a.split_cnt + item, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                                 (int)gridDim.y - 1;
+                __syncthreads();
+                if (split_last) {
+                    // partial values read at the coherence point (buffer loads with the sc1 policy,
+                    // the form of an agent-scope load), 8 splits in flight at a time
+                    const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+                        (void *)a.dn, (short)0, (int)(gridDim.y * a.split_stride * 4), 0x00020000);
+                    const int cols = min(S::RPB, a.n - nblk * S::RPB), nsp = (int)gridDim.y;
+                    for (int e = tid; e < tile.m * cols; e += S::NT) {
+                        const int r = e / cols, n = nblk * S::RPB + (e - r * cols);
+                        const int o = (int)((int64_t)meta_pick[r] * a.n + n);
+                        float acc = 0.f;
+                        for (int s0 = 0; s0 < nsp; s0 += 8) {
+                            float v[8];
+#pragma unroll
+                            for (int u = 0; u < 8; u++)  // past the last split: 0 from the buffer's range, unused
+                                v[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, 4 * (o + (s0 + u) * (int)a.split_stride), 0, 16));
+#pragma unroll
+                            for (int u = 0; u < 8; u++)
+                                if (s0 + u < nsp) acc = (s0 + u == 0) ? v[u] : acc + v[u];
+                        }
+                        a.y[o] = acc;
                     }
                 }
             }
@@ -1175,7 +1215,14 @@ __global__ __launch_bounds__(1024) void k_piles(const uint32_t *slots, int TK, i
 // 2^(15 - e) with max|x| in [2^(e-1), 2^e) keeps the row's largest value in [2^14, 2^15) of
 // fp16; ascale receives 1/scale.
 template <int NV>
-__global__ __launch_bounds__(256) void k_pack_f16(const float *x, int rows, int k, int ldx, uint16_t *a16, float *ascale) {
+__global__ __launch_bounds__(256) void k_pack_f16(const float *x, int rows, int k, int ldx, uint16_t *a16, float *ascale,
+                                                  PackExtra e) {
+    if (e.tiles && blockIdx.x == 0) {  // tile i of a dense matmul: rows MF_MT*i .., "slot" 0
+        const int nt = (e.m + MF_MT - 1) / MF_MT;
+        for (int i = threadIdx.x; i < nt; i += blockDim.x) e.tiles[i] = MfTile{0, i * MF_MT, min(MF_MT, e.m - i * MF_MT), 0};
+        if (threadIdx.x == 0) *e.n_tiles = nt;
+    }
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < e.n_zero; i += gridDim.x * blockDim.x) e.zero[i] = 0;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= rows) return;
     const float *xr = x + (int64_t)row * ldx;
@@ -1246,13 +1293,15 @@ int mfma_piles(const uint32_t *slots, int TK, int K, int n_slots, int *pile_pick
     return check_launch("k_piles");
 }
 
-int pack_rows_f16(const float *x, int rows, int k, int ldx, uint16_t *a16, float *ascale, hipStream_t s) {
+int pack_rows_f16(const float *x, int rows, int k, int ldx, uint16_t *a16, float *ascale, hipStream_t s,
+                  const PackExtra *extra) {
     if (rows == 0) return CW_OK;
     if (k % 4 || ldx % 4) return set_error(CW_ENOTSUP, "pack: row of %d (stride %d) is not whole float4s", k, ldx);
     const dim3 grid((rows + 3) / 4);
     const int nv = (k + 255) / 256;
+    const PackExtra e = extra ? *extra : PackExtra{};
 #define CW_PACK(N) \
-    if (nv <= N) { hipLaunchKernelGGL(k_pack_f16<N>, grid, dim3(256), 0, s, x, rows, k, ldx, a16, ascale); return check_launch("k_pack_f16"); }
+    if (nv <= N) { hipLaunchKernelGGL(k_pack_f16<N>, grid, dim3(256), 0, s, x, rows, k, ldx, a16, ascale, e); return check_launch("k_pack_f16"); }
     CW_PACK(2) CW_PACK(4) CW_PACK(8) CW_PACK(12) CW_PACK(16) CW_PACK(32)
 #undef CW_PACK
     return set_error(CW_ENOTSUP, "pack: rows of %d above 8192", k);
@@ -1337,23 +1386,7 @@ static int by_fmt(int dtype, const MfArgs &a, int tiles_max, int splits, hipStre
     }
 }
 
-// tile i of a dense matmul: rows 64i .. 64i + 63 of x, "slot" 0
-__global__ void k_dense_tiles(MfTile *tiles, int *n_tiles, int m) {
-    const int nt = (m + MF_MT - 1) / MF_MT;
-    for (int i = threadIdx.x; i < nt; i += blockDim.x) tiles[i] = MfTile{0, i * MF_MT, min(MF_MT, m - i * MF_MT), 0};
-    if (threadIdx.x == 0) *n_tiles = nt;
-}
-
 static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
-
-// y[i] = sum over the S partial products, in split order
-__global__ void k_sum_splits(const float *part, int S, int64_t n, float *y) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-        float acc = part[i];
-        for (int s = 1; s < S; s++) acc += part[s * n + i];
-        y[i] = acc;
-    }
-}
 
 // the dense GEMM's N-block rows and stage size for a format (GmShape<MF, 2>)
 template <class MF>
@@ -1375,24 +1408,49 @@ static void dense_shape(int dtype, int &rpb, int &kst, int &per_cu) {
     default: return shape_of<MQ4_K>(rpb, kst, per_cu);
     }
 }
-// K splits: enough work items for every resident block, at least one stage each
+// The split count S minimises the stages on the critical path: the launch's blocks (work items,
+// padded as launch() pads them, times S) run in rounds of the resident blocks, and each block runs
+// its items' ceil(n_st / S) stages one after another. (Filling the resident blocks exactly, as a
+// first version did, left config 2's M = 512 at 768 blocks over 512 slots: 2 rounds of 6 stages
+// where 1 round of 8 does.) Ties go to fewer splits (less partial traffic).
 static int dense_splits(int dtype, int64_t m, int64_t n, int64_t k, int &split_st) {
     int rpb, kst, per_cu;
     dense_shape(dtype, rpb, kst, per_cu);
-    const int64_t blocks = (m + MF_MT - 1) / MF_MT * ((n + rpb - 1) / rpb);
+    const int64_t tiles = (m + MF_MT - 1) / MF_MT, n_nb = (n + rpb - 1) / rpb;
+    const int64_t R = tiles >= 8 ? 8 : tiles >= 4 ? 4 : tiles >= 2 ? 2 : 1;
+    const int64_t items = (tiles + R - 1) / R * R * n_nb, res = resident_blocks(per_cu);
+    const int64_t grid_x = items < res ? (items + 7) / 8 * 8 : res, per_block = (items + grid_x - 1) / grid_x;
     const int n_st = (int)((k / 32 + kst - 1) / kst);
-    int S = (int)((resident_blocks(per_cu) + blocks - 1) / blocks);
-    if (S > n_st) S = n_st;
-    if (S < 1) S = 1;
-    split_st = (n_st + S - 1) / S;
-    return (n_st + split_st - 1) / split_st;
+    int best_s = 1;
+    int64_t best = -1;
+    for (int S = 1; S <= n_st; S++) {
+        const int sst = (n_st + S - 1) / S;
+        if ((n_st + sst - 1) / sst != S) continue;  // the same split as a smaller S
+        if (S > 1 && (int64_t)S * m * n * 4 >= ((int64_t)1 << 31)) break;  // the partial rows stay under 2 GiB (32-bit offsets)
+        const int64_t cost = (grid_x * S + res - 1) / res * per_block * sst;
+        if (best < 0 || cost < best) {
+            best = cost;
+            best_s = S;
+        }
+    }
+    split_st = (n_st + best_s - 1) / best_s;
+    return best_s;
+}
+
+// work items of the dense GEMM's launch (M-tiles padded to the launch's run length, by N-blocks)
+static int64_t dense_items(int dtype, int64_t m, int64_t n) {
+    int rpb, kst, per_cu;
+    dense_shape(dtype, rpb, kst, per_cu);
+    const int64_t tiles = (m + MF_MT - 1) / MF_MT, n_nb = (n + rpb - 1) / rpb;
+    const int64_t R = tiles >= 8 ? 8 : tiles >= 4 ? 4 : tiles >= 2 ? 2 : 1;
+    return (tiles + R - 1) / R * R * n_nb;
 }
 
 size_t mfma_dense_workspace(int dtype, int64_t m, int64_t n, int64_t k) {
     int split_st;
     const int S = dense_splits(dtype, m, n, k, split_st);
     return al256(m * k * 2) + al256(m * 4) + al256((m + MF_MT - 1) / MF_MT * sizeof(MfTile)) + al256(4) +
-           (S > 1 ? al256((size_t)S * m * n * 4) : 0);
+           (S > 1 ? al256((size_t)S * m * n * 4) + al256((size_t)dense_items(dtype, m, n) * 4) : 0);
 }
 
 int mfma_dense(int dtype, const uint8_t *w, int64_t row_bytes, int n, int k, const float *x, int m, float *y, void *ws,
@@ -1406,11 +1464,17 @@ int mfma_dense(int dtype, const uint8_t *w, int64_t row_bytes, int n, int k, con
     float *xs = (float *)p; p += al256((size_t)m * 4);
     MfTile *tiles = (MfTile *)p; p += al256((size_t)(m + MF_MT - 1) / MF_MT * sizeof(MfTile));
     int *n_tiles = (int *)p; p += al256(4);
-    float *part = S > 1 ? (float *)p : nullptr;
-    hipLaunchKernelGGL(k_dense_tiles, dim3(1), dim3(256), 0, s, tiles, n_tiles, m);
-    int rc = check_launch("k_dense_tiles");
-    if (rc) return rc;
-    if ((rc = pack_rows_f16(x, m, k, k, x16, xs, s))) return rc;
+    float *part = nullptr;
+    int *cnt = nullptr;
+    if (S > 1) {
+        part = (float *)p;
+        p += al256((size_t)S * m * n * 4);
+        cnt = (int *)p;
+    }
+    // one launch packs x, writes the tile list and zeroes the split counters
+    const PackExtra extra = {tiles, n_tiles, m, cnt, S > 1 ? (int)dense_items(dtype, m, n) : 0};
+    int rc;
+    if ((rc = pack_rows_f16(x, m, k, k, x16, xs, s, &extra))) return rc;
     MfArgs a = {};
     a.w0 = w;
     a.s0 = 0;
@@ -1426,11 +1490,9 @@ int mfma_dense(int dtype, const uint8_t *w, int64_t row_bytes, int n, int k, con
     a.dn = S > 1 ? part : y;
     a.split_st = S > 1 ? split_st : 0;
     a.split_stride = (int64_t)m * n;
-    if ((rc = by_fmt<2>(dtype, a, (m + MF_MT - 1) / MF_MT, S, s))) return rc;
-    if (S == 1) return CW_OK;
-    const int64_t total = (int64_t)m * n, blocks = (total + 255) / 256;
-    hipLaunchKernelGGL(k_sum_splits, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s, part, S, total, y);
-    return check_launch("k_sum_splits");
+    a.split_cnt = cnt;
+    a.y = y;
+    return by_fmt<2>(dtype, a, (m + MF_MT - 1) / MF_MT, S, s);
 }
 
 int mfma_gateup(int dtype, const MfArgs &a, int tiles_max, hipStream_t s) { return by_fmt<0>(dtype, a, tiles_max, 1, s); }

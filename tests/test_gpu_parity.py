@@ -117,6 +117,24 @@ def test_qmatmul_matches_the_oracle(dtype, n, k, m, path, monkeypatch):
         assert err <= REL_L2_F32
 
 
+@pytest.mark.parametrize("m", [16, 512])
+def test_qmatmul_split_sum_is_deterministic(m, monkeypatch):
+    """Split over K, the dense GEMM's last split of each work item to finish adds the partial rows
+    in split order, whichever split that is: two calls give the same bits, and the result is the
+    oracle's at the fp16-activation bar."""
+    monkeypatch.setenv("CWMOE_MM_MIN_ROWS", "1")
+    say("qmatmul split sum", m)
+    rng = np.random.default_rng(70 + m)
+    n, k = 4096, 4096
+    raw = synth.random_blocks(F.Q4_K, n * k, rng)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    qm = ops.QMatMul(ops.QTensor.from_blocks(raw, F.Q4_K, (n, k)))
+    y1 = host(qm.forward(dev(x)))
+    y2 = host(qm.forward(dev(x)))
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+    assert O.rel_l2(y1, O.qmatmul_f64(F.Q4_K, raw, n, k, x)) <= REL_L2_GATE
+
+
 @pytest.mark.parametrize("path", sorted(MM_PATHS))
 def test_qmatmul_edge_scales(path, monkeypatch):
     # zero and subnormal f16 scales (and a zero dmin) take the kernels' zero-scale branches
