@@ -255,6 +255,51 @@ __device__ __forceinline__ void store_coherent(float *p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Gate/up rows staged through LDS. A row of 17-byte MXFP4 blocks read by each lane as its own
+// blocks (a byte and an unaligned 16-byte load per block) streams at ~2.9 TB/s on MI355X in a
+// microbenchmark of the config-4 gate/up pattern (4 picks x 2 matrices x 2,880 rows, 1 or 2 items
+// in flight per wave); the same rows as aligned 16-byte chunks copied into LDS by the load unit
+// (global_load_lds_dwordx4) and read back there stream at 4.1-4.4 TB/s. Each wave owns two item
+// buffers: the next item's rows (and its bias values) go out before the current item is read.
+template <class F> struct RowDma { static constexpr bool on = false; };
+template <> struct RowDma<FMXFP4> { static constexpr bool on = true; };
+
+// One 16-byte chunk per lane from global memory into LDS at lds_base + 16 * lane. Issued as inline
+// asm: the compiler's waits then do not cover these loads (the kernel waits for them itself with
+// vmcnt), and no LDS read of the kernel is taken to alias them. M0 is saved and restored.
+__device__ __forceinline__ void lds_dma16(const void *g, void *lds_base) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)lds_base);
+    uint32_t keep;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(keep) : "v"(g), "s"(m) : "memory");
+}
+// The same for one dword per lane, at lds_base + 4 * lane.
+__device__ __forceinline__ void lds_dma4(const void *g, void *lds_base) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)lds_base);
+    uint32_t keep;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(keep) : "v"(g), "s"(m) : "memory");
+}
+
+// An MXFP4 block at byte o of an LDS row window: the scale byte, then 16 code bytes read as five
+// aligned dwords and shifted into place.
+__device__ __forceinline__ FMXFP4::Raw mx_from_lds(const uint8_t *win, int o) {
+    FMXFP4::Raw r;
+    r.e = win[o];
+    const int a = o + 1;
+    const uint32_t *w = (const uint32_t *)(win + (a & ~3));
+    const uint32_t d0 = w[0], d1 = w[1], d2 = w[2], d3 = w[3], d4 = w[4], sh = a & 3;
+    r.q.x = __builtin_amdgcn_alignbyte(d1, d0, sh);
+    r.q.y = __builtin_amdgcn_alignbyte(d2, d1, sh);
+    r.q.z = __builtin_amdgcn_alignbyte(d3, d2, sh);
+    r.q.w = __builtin_amdgcn_alignbyte(d4, d3, sh);
+    return r;
+}
+
+// Bytes of a row's window in LDS: its 16-byte chunks from the one holding its first byte, plus the
+// 4 bytes that the last block's dword reads may touch past its end.
+__host__ __device__ __forceinline__ int row_window(int row_bytes) { return ((row_bytes + 15 + 15 + 4) >> 4) << 4; }
+
 // The whole decode layer (one token) in one launch of a grid that fits on the device at once.
 // Loads are issued as early as their addresses are known, since every wait on them counts in
 // issue order:
@@ -267,7 +312,8 @@ __device__ __forceinline__ void store_coherent(float *p, float v) {
 //      computes down row groups of 64/LD rows: per-pick dots, combined in pick order.
 // At least 3 waves per SIMD (at most 168 VGPRs): the grid is sized from occupancy, and the
 // gpt-oss shape's 182-VGPR build ran 2 blocks per CU (39.0 us per layer; 36.4 at 3, with a few
-// spilled registers); the other instances fit already.
+// spilled registers, none since its gate/up rows are staged through LDS: 155 VGPRs); the other
+// instances fit already.
 template <class FG, int LG, int XG, class FD, int LD, int XD, int PER, int PPW>
 __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
     constexpr int RI = 2;  // rows (of RPG) per gate/up item: 4 measured slower (config 4 spills, config 5 too)
@@ -364,7 +410,53 @@ __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
             }
         }
     };
-    if (gwave < n_items) load_item(gwave);
+    constexpr bool GDMA = RowDma<FG>::on;
+    static_assert(!GDMA || (LG == 64 && XG == 2), "the LDS-staged gate/up rows take one row per wave pass");
+    // GDMA: this wave's two item buffers in the (not yet used) hidden-row region: per buffer RI
+    // gate rows, RI up rows, then the 2*RI bias values
+    const int win = row_window(nsbg * FG::TS);
+    const int ibuf = 2 * RI * win + 16;
+    uint8_t *wbuf = (uint8_t *)hs + wave * 2 * ibuf;
+    auto issue_item = [&](int it, int b) {
+        const int j = it / row_items, r0 = (it - j * row_items) * RI;
+        // both shuffles with every lane active: a lane outside a branch gives 0 to a shuffle
+        const uint32_t slot = __shfl(my_slot, j), e = __shfl(rid, j);
+        const uint32_t sl = slot == 0xFFFFFFFFu ? 0 : slot;
+        uint8_t *ib = wbuf + b * ibuf;
+#pragma unroll
+        for (int q = 0; q < RI; q++) {
+            const int r = min(r0 + q, a.I - 1);
+#pragma unroll
+            for (int m = 0; m < 2; m++) {
+                const uint8_t *row = (m ? a.wu + (int64_t)sl * a.su : a.wg + (int64_t)sl * a.sg) + (int64_t)r * a.rbg;
+                const uint8_t *al = (const uint8_t *)((uintptr_t)row & ~(uintptr_t)15);
+                // chunks past the row's last one re-read that chunk: no load leaves the 16-byte
+                // granule of the row's last byte
+                const int nch = (int)(((uintptr_t)row & 15) + nsbg * FG::TS + 15) >> 4;
+                uint8_t *w = ib + (2 * q + m) * win;
+                lds_dma16(al + 16 * min(lane, nch - 1), w);
+                if (lane < (win >> 4) - 64) lds_dma16(al + 16 * min(64 + lane, nch - 1), w + 1024);
+            }
+        }
+        // bias values (gate rows, then up rows); a layer without biases re-reads x
+        if (lane < 2 * RI) {
+            const int q = lane % RI;
+            const float *bsrc = lane < RI ? a.bg : a.bu;
+            const float *src = bsrc ? bsrc + (int64_t)(e < (uint32_t)a.E ? e : 0) * a.I + min(r0 + q, a.I - 1) : a.x;
+            lds_dma4(src, ib + 2 * RI * win);
+        }
+    };
+    if constexpr (GDMA) {
+        // x is waited for here, where it has arrived during the top-k: a wait the compiler would
+        // otherwise place ahead of the item loop counts the first item's row loads as well
+#pragma unroll
+        for (int i = 0; i < XG; i++)
+#pragma unroll
+            for (int k = 0; k < 32; k++) asm volatile("" ::"v"(xr[i][k]));
+        if (gwave < n_items) issue_item(gwave, 0);
+    } else {
+        if (gwave < n_items) load_item(gwave);
+    }
 
     const int subd = lane % LD, rsd = lane / LD, nsbd = a.P / 32;
     typename FD::Raw draw[PPW][XD];
@@ -394,6 +486,69 @@ __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
     tg.store(ldsg, threadIdx.x);
     __syncthreads();
 
+    if constexpr (GDMA) {
+        // the previous item's hidden values, stored once the next wait is behind (a store counts
+        // in vmcnt, and a wait issued right after it would wait for its round trip)
+        float hv[RI];
+        int hj = -1, hr0 = 0;
+        bool hbad = false;
+        auto flush = [&]() {
+            if (hj >= 0 && lane == 0) {
+#pragma unroll
+                for (int q = 0; q < RI; q++)
+                    if (hr0 + q < a.I) store_coherent(a.h + (int64_t)hj * a.P + hr0 + q, hbad ? __int_as_float(0x7fc00000) : hv[q]);
+            }
+        };
+        for (int it = gwave, b = 0; it < n_items; it += total_waves, b ^= 1) {
+            // per item: 2*RI rows of two chunk loads each, and the bias load
+            if (it + total_waves < n_items) {
+                issue_item(it + total_waves, b ^ 1);
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * RI + 1) : "memory");
+            } else {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            }
+            flush();
+            const int j = it / row_items, r0 = (it - j * row_items) * RI;
+            const uint32_t slot = __shfl(my_slot, j);
+            const uint32_t sl = slot == 0xFFFFFFFFu ? 0 : slot;
+            const uint8_t *ib = wbuf + b * ibuf;
+#pragma unroll
+            for (int q = 0; q < RI; q++) {
+                const int r = min(r0 + q, a.I - 1);
+                const int og = (int)((uintptr_t)(a.wg + (int64_t)sl * a.sg + (int64_t)r * a.rbg) & 15);
+                const int ou = (int)((uintptr_t)(a.wu + (int64_t)sl * a.su + (int64_t)r * a.rbg) & 15);
+                float g = 0.f, u = 0.f;
+#pragma unroll
+                for (int i = 0; i < XG; i++) {
+                    const int sb = subg + i * LG, sbc = min(sb, nsbg - 1);
+                    const typename FG::Raw wg = mx_from_lds(ib + (2 * q) * win, og + FG::TS * sbc);
+                    const typename FG::Raw wu = mx_from_lds(ib + (2 * q + 1) * win, ou + FG::TS * sbc);
+                    if (sb < nsbg) {
+                        g += FG::dot(wg, ldsg, xr[i]);
+                        u += FG::dot(wu, ldsg, xr[i]);
+                    }
+                }
+                g = group_sum<LG>(g);
+                u = group_sum<LG>(u);
+                float o;
+                if (a.act == CW_ACT_SILU) {
+                    o = g / (1.0f + expf(-g)) * u;
+                } else {
+                    const float *bias = (const float *)(ib + 2 * RI * win);
+                    if (a.bg) g += bias[q];
+                    if (a.bu) u += bias[RI + q];
+                    g = fminf(g, a.limit);
+                    u = fminf(fmaxf(u, -a.limit), a.limit);
+                    o = (u + 1.0f) * (g * (1.0f / (1.0f + expf(-(g * a.alpha)))));
+                }
+                hv[q] = o;
+            }
+            hj = j;
+            hr0 = r0;
+            hbad = slot == 0xFFFFFFFFu;
+        }
+        flush();
+    } else
     for (int it = gwave; it < n_items; it += total_waves) {
         if (it != gwave) load_item(it);
         const int j = it / row_items, r0 = (it - j * row_items) * RI * RPG + rsg;
@@ -581,6 +736,17 @@ static int by_fmt(int dtype, const MoeArgs &a, int T, hipStream_t s) {
 
 // LDS for the staged hidden rows of one decode call: K rows of P floats, 36 per 32
 static size_t decode_hidden_lds(const MoeArgs &a) { return (size_t)a.K * (a.P / 32) * 36 * sizeof(float); }
+// the dynamic LDS of an instance: the hidden rows, or for LDS-staged gate/up rows (RI = 2) the
+// four waves' two item buffers if those are larger (they are used before the hidden rows)
+template <class FG>
+static size_t decode_lds(const MoeArgs &a) {
+    size_t n = decode_hidden_lds(a);
+    if (RowDma<FG>::on) {
+        const size_t items = 4 * 2 * (size_t)(2 * 2 * row_window(a.H / 32 * FG::TS) + 16);
+        if (items > n) n = items;
+    }
+    return n;
+}
 static constexpr size_t DECODE_MAX_HIDDEN_LDS = 64 * 1024;
 
 // Grid of the persistent decode kernel: every block must be resident at once for the barrier, so
@@ -621,7 +787,13 @@ static int decode_grid(Kern kern, int which, const MoeArgs &a, size_t lds, int w
 
 template <class FG, int LG, int XG, class FD, int LD, int XD, int PER, int PPW>
 static int decode_launch_per(const MoeArgs &a, int which, hipStream_t s) {
-    const size_t lds = decode_hidden_lds(a);
+    // LDS-staged gate/up rows: two chunk loads per row, so that every load instruction the
+    // kernel's waits count has active lanes
+    if (RowDma<FG>::on) {
+        const int w = row_window(a.H / 32 * FG::TS);
+        if (w <= 1024 || w > 2048) return CW_ENOTSUP;
+    }
+    const size_t lds = decode_lds<FG>(a);
     const int RPD = 64 / LD;
     auto kern = k_moe_decode<FG, LG, XG, FD, LD, XD, PER, PPW>;
     const int grid = decode_grid(kern, which, a, lds, (a.H + RPD - 1) / RPD);
