@@ -345,7 +345,16 @@ __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
     tg.load(threadIdx.x);
     const int subg = lane % LG, rsg = lane / LG, nsbg = a.H / 32;
     float xr[XG][32];
-    load_xs<XG>(xr, a.x, subg, LG, nsbg);
+    if constexpr (RowDma<FG>::on) {
+        // x once per block into the (not yet used) hidden-row region, read into registers below:
+        // every wave loading all of x (35 MB across config 4's grid) held up the logits and x
+        // loads of the blocks placed third on a CU by ~7 us
+        const int nxc = a.H / 4;
+        for (int c0 = 0; c0 < nxc; c0 += 256)
+            lds_dma16(a.x + 4 * min(c0 + (int)threadIdx.x, nxc - 1), (uint8_t *)hs + 16 * (c0 + wave * 64));
+    } else {
+        load_xs<XG>(xr, a.x, subg, LG, nsbg);
+    }
 
     uint32_t rid = 0xFFFFFFFFu;      // lane j < K: pick j's expert
     uint32_t my_slot = 0xFFFFFFFFu;  // ... and its slot
@@ -447,12 +456,25 @@ __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
         }
     };
     if constexpr (GDMA) {
-        // x is waited for here, where it has arrived during the top-k: a wait the compiler would
-        // otherwise place ahead of the item loop counts the first item's row loads as well
+        // x (copied during the top-k) from LDS into registers; the block then lets the item
+        // buffers overwrite it
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
 #pragma unroll
-        for (int i = 0; i < XG; i++)
+        for (int i = 0; i < XG; i++) {
+            const int sb = subg + i * LG;
+            const bool in = sb < nsbg;
+            const float4 *src = (const float4 *)(hs + 32 * (in ? sb : nsbg - 1));
 #pragma unroll
-            for (int k = 0; k < 32; k++) asm volatile("" ::"v"(xr[i][k]));
+            for (int v = 0; v < 8; v++) {
+                const float4 f = src[v];
+                xr[i][4 * v] = in ? f.x : 0.f;
+                xr[i][4 * v + 1] = in ? f.y : 0.f;
+                xr[i][4 * v + 2] = in ? f.z : 0.f;
+                xr[i][4 * v + 3] = in ? f.w : 0.f;
+            }
+        }
+        __syncthreads();
         if (gwave < n_items) issue_item(gwave, 0);
     } else {
         if (gwave < n_items) load_item(gwave);
@@ -743,7 +765,9 @@ static size_t decode_lds(const MoeArgs &a) {
     size_t n = decode_hidden_lds(a);
     if (RowDma<FG>::on) {
         const size_t items = 4 * 2 * (size_t)(2 * 2 * row_window(a.H / 32 * FG::TS) + 16);
+        const size_t xs = (size_t)(a.H / 4 + 255) / 256 * 256 * 16;  // x, copied in rounds of 256 chunks
         if (items > n) n = items;
+        if (xs > n) n = xs;
     }
     return n;
 }
@@ -792,6 +816,7 @@ static int decode_launch_per(const MoeArgs &a, int which, hipStream_t s) {
     if (RowDma<FG>::on) {
         const int w = row_window(a.H / 32 * FG::TS);
         if (w <= 1024 || w > 2048) return CW_ENOTSUP;
+        if ((uintptr_t)a.x & 15) return CW_ENOTSUP;  // x is copied in 16-byte chunks
     }
     const size_t lds = decode_lds<FG>(a);
     const int RPD = 64 / LD;

@@ -598,6 +598,28 @@ def test_moe_layer_marks_out_of_range_slots(path, T, monkeypatch):
         assert O.rel_l2(got[~hit], want[~hit]) <= REL_L2_GATE
 
 
+def test_moe_decode_with_x_off_16_byte_alignment():
+    """The MXFP4 one-token layer copies x in 16-byte chunks; an x that starts 4 bytes past such a
+    boundary takes the two-kernel path, with the same result."""
+    say("moe decode, x at a 4-byte offset")
+    rng = np.random.default_rng(77)
+    E, K = 16, 4
+    layer = synth.moe_weights(E, K, 2880, 2880, (F.MXFP4,) * 3, rng, act=1)
+    x = rng.standard_normal((1, 2880)).astype(np.float32)
+    logits = rng.standard_normal((1, E)).astype(np.float32)
+    want, wids, _, _ = O.moe_layer(layer, x, logits)
+    moe = upload_layer(layer)
+    xs = torch.zeros(2881, dtype=torch.float32, device="cuda")
+    xs[1:] = dev(x).reshape(-1)
+    xo = xs[1:].reshape(1, 2880)
+    assert xo.data_ptr() % 16 == 4
+    out, ids, _ = moe.forward(xo, dev(logits))
+    aligned, _, _ = moe.forward(dev(x), dev(logits))
+    assert np.array_equal(host(ids).view(np.uint32), wids)
+    assert O.rel_l2(host(out), want) <= REL_L2_F32
+    assert O.rel_l2(host(aligned), want) <= REL_L2_F32
+
+
 def test_moe_layer_output_is_deterministic():
     rng = np.random.default_rng(77)
     layer = synth.moe_weights(64, 8, 2048, 512, (F.IQ2_XXS, F.IQ2_XXS, F.IQ2_S), rng)
