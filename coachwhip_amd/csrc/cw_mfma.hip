@@ -517,11 +517,14 @@ struct MIQ4_XS {
 
 // A stage is KST K-steps (8: 256 weights of k; 4 for Q8_0). The window of a row for a stage
 // holds the stage's bytes (an IQ, Q2_K or Q4_K super-block, or KST MXFP4 / Q8_0 blocks) from the
-// 16-byte boundary at or below their start, in PCS pieces of 16 bytes.
+// 16-byte boundary at or below their start, in PCS pieces of 16 bytes. PCS is odd: the 16 rows of
+// a fragment read their windows at a stride of 4*PCS dwords, and an even PCS put rows 8 (or 4)
+// apart on the same LDS banks (config 4 prefill 1,302-1,310 -> 1,253-1,261 us, config 3 271-275 ->
+// 267-268, the last piece a re-load nothing reads).
 template <class MF>
 struct Win {
     static constexpr int SEG = MF::SBK == 32 ? MF::KST * MF::TS : MF::TS;
-    static constexpr int PCS = (SEG + (MF::TS % 2 ? 15 : 14) + 15) / 16;
+    static constexpr int PCS = ((SEG + (MF::TS % 2 ? 15 : 14) + 15) / 16) | 1;
     static constexpr int BYTES = 16 * PCS;
 };
 
