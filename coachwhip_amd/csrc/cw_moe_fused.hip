@@ -267,15 +267,16 @@ template <> struct RowDma<FMXFP4> { static constexpr bool on = true; };
 // One 16-byte chunk per lane from global memory into LDS at lds_base + 16 * lane. Issued as inline
 // asm: the compiler's waits then do not cover these loads (the kernel waits for them itself with
 // vmcnt), and no LDS read of the kernel is taken to alias them. M0 is saved and restored.
-__device__ __forceinline__ void lds_dma16(const void *g, void *lds_base) {
-    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)lds_base);
+// lds_base is an LDS byte address (lds_addr of the kernel's dynamic LDS plus an offset).
+__device__ __forceinline__ void lds_dma16(const void *g, uint32_t lds_base) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane(lds_base);
     uint32_t keep;
     asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
                  : "=&s"(keep) : "v"(g), "s"(m) : "memory");
 }
 // The same for one dword per lane, at lds_base + 4 * lane.
-__device__ __forceinline__ void lds_dma4(const void *g, void *lds_base) {
-    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)lds_base);
+__device__ __forceinline__ void lds_dma4(const void *g, uint32_t lds_base) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane(lds_base);
     uint32_t keep;
     asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
                  : "=&s"(keep) : "v"(g), "s"(m) : "memory");
@@ -308,22 +309,25 @@ __host__ __device__ __forceinline__ int row_window(int row_bytes) { return ((row
 //      first down rows (all its picks), stores the tables to LDS, then computes its gate/up
 //      items: dots, activation, hidden rows stored at the coherence point;
 //   3. device-wide barrier;
-//   4. each block copies all K hidden rows into LDS (one read per block, not per wave) and
-//      computes down row groups of 64/LD rows: per-pick dots, combined in pick order.
+//   4. each block copies all K hidden rows into LDS (one read per block, not per wave), and each
+//      of its G groups of 4 waves computes down row groups of 64/LD rows: per-pick dots,
+//      combined in pick order.
 // At least 3 waves per SIMD (at most 168 VGPRs): the grid is sized from occupancy, and the
 // gpt-oss shape's 182-VGPR build ran 2 blocks per CU (39.0 us per layer; 36.4 at 3, with a few
 // spilled registers, none since its gate/up rows are staged through LDS: 155 VGPRs); the other
 // instances fit already.
-template <class FG, int LG, int XG, class FD, int LD, int XD, int PER, int PPW>
-__global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
+template <class FG, int LG, int XG, class FD, int LD, int XD, int PER, int PPW, int G>
+__global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const MoeArgs a) {
     constexpr int RI = 2;  // rows (of RPG) per gate/up item: 4 measured slower (config 4 spills, config 5 too)
+    constexpr int NW = 4 * G, NT = 64 * NW;  // waves and threads of a block: G groups of 4 waves
     __shared__ __align__(16) uint8_t ldsg[FG::LDS_BYTES > 0 ? FG::LDS_BYTES : 16];
     __shared__ __align__(16) uint8_t ldsd[FD::LDS_BYTES > 0 ? FD::LDS_BYTES : 16];
     constexpr int RPG = 64 / LG, RPD = 64 / LD;
-    __shared__ float part[32 * RPD];
+    __shared__ float part[G][32 * RPD];
     __shared__ float pick_w[32];
     __shared__ uint32_t pick_e[32], pick_slot[32];
     extern __shared__ __align__(16) float hs[];  // hidden rows, sub-blocks of 32 floats 36 apart
+    const uint32_t hs_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float *)hs;  // its LDS address
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int K = a.K;
     // the logits alone first: every wave of the grid starts at once, and the table and x loads
@@ -342,7 +346,7 @@ __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
     }
     TableRegs<FG> tg;
     TableRegs<FD> td;
-    tg.load(threadIdx.x);
+    if (wave < 4) tg.load(threadIdx.x);  // the tables take 256 threads
     const int subg = lane % LG, rsg = lane / LG, nsbg = a.H / 32;
     float xr[XG][32];
     if constexpr (RowDma<FG>::on) {
@@ -350,8 +354,8 @@ __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
         // every wave loading all of x (35 MB across config 4's grid) held up the logits and x
         // loads of the blocks placed third on a CU by ~7 us
         const int nxc = a.H / 4;
-        for (int c0 = 0; c0 < nxc; c0 += 256)
-            lds_dma16(a.x + 4 * min(c0 + (int)threadIdx.x, nxc - 1), (uint8_t *)hs + 16 * (c0 + wave * 64));
+        for (int c0 = 0; c0 < nxc; c0 += NT)
+            lds_dma16(a.x + 4 * min(c0 + (int)threadIdx.x, nxc - 1), hs_lds + 16 * (c0 + wave * 64));
     } else {
         load_xs<XG>(xr, a.x, subg, LG, nsbg);
     }
@@ -392,7 +396,7 @@ __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
     // second sub-block, and the unconditional form measured 2.6-4 us slower for config 4.
     const int row_items = (a.I + RI * RPG - 1) / (RI * RPG);
     const int n_items = K * row_items;
-    const int gwave = blockIdx.x * 4 + wave, total_waves = gridDim.x * 4;
+    const int gwave = blockIdx.x * NW + wave, total_waves = gridDim.x * NW;
     typename FG::Raw rg[RI][XG], ru[RI][XG];
     auto load_item = [&](int it) {
         const int j = it / row_items, r0 = (it - j * row_items) * RI * RPG + rsg;
@@ -442,7 +446,7 @@ __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
                 // chunks past the row's last one re-read that chunk: no load leaves the 16-byte
                 // granule of the row's last byte
                 const int nch = (int)(((uintptr_t)row & 15) + nsbg * FG::TS + 15) >> 4;
-                uint8_t *w = ib + (2 * q + m) * win;
+                const uint32_t w = hs_lds + (uint32_t)(ib - (uint8_t *)hs) + (2 * q + m) * win;
                 lds_dma16(al + 16 * min(lane, nch - 1), w);
                 if (lane < (win >> 4) - 64) lds_dma16(al + 16 * min(64 + lane, nch - 1), w + 1024);
             }
@@ -452,7 +456,7 @@ __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
             const int q = lane % RI;
             const float *bsrc = lane < RI ? a.bg : a.bu;
             const float *src = bsrc ? bsrc + (int64_t)(e < (uint32_t)a.E ? e : 0) * a.I + min(r0 + q, a.I - 1) : a.x;
-            lds_dma4(src, ib + 2 * RI * win);
+            lds_dma4(src, hs_lds + (uint32_t)(ib - (uint8_t *)hs) + 2 * RI * win);
         }
     };
     if constexpr (GDMA) {
@@ -481,13 +485,14 @@ __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
     }
 
     const int subd = lane % LD, rsd = lane / LD, nsbd = a.P / 32;
+    const int grp = wave >> 2, wl = wave & 3;  // the down phase: wave group, and wave within it
     typename FD::Raw draw[PPW][XD];
     uint32_t dslot[PPW];
     {
-        const int r = blockIdx.x * RPD + rsd;
+        const int r = (blockIdx.x * G + grp) * RPD + rsd;
 #pragma unroll
         for (int q = 0; q < PPW; q++) {
-            const int j = wave + 4 * q;
+            const int j = wl + 4 * q;
             dslot[q] = __shfl(my_slot, j < K ? j : 0);
             if constexpr (XD == 1) {  // unconditional (unused past K)
                 const uint8_t *base = a.wd + (int64_t)(dslot[q] == 0xFFFFFFFFu ? 0 : dslot[q]) * a.sd + (int64_t)min(r, a.H - 1) * a.rbd;
@@ -504,8 +509,10 @@ __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
     }
     // down's table is needed only after the barrier: its loads go out behind the weights', and
     // it is stored to LDS once the gate/up items are done
-    td.load(threadIdx.x);
-    tg.store(ldsg, threadIdx.x);
+    if (wave < 4) {
+        td.load(threadIdx.x);
+        tg.store(ldsg, threadIdx.x);
+    }
     __syncthreads();
 
     if constexpr (GDMA) {
@@ -612,7 +619,7 @@ __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
         store_coherent(a.h + (int64_t)j * a.P + a.I + (c - j * (a.P - a.I)), 0.f);
     }
 
-    td.store(ldsd, threadIdx.x);
+    if (wave < 4) td.store(ldsd, threadIdx.x);
     const bool ok = grid_barrier((DecodeBarrier *)a.state, gridDim.x, a.polls);
 
     // every hidden row into LDS once per block, read at the coherence point (16-byte buffer
@@ -622,16 +629,16 @@ __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
     {
         const int nbytes = K * a.P * 4, hp = a.P / 4;
         const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc((void *)a.h, (short)0, nbytes, CW_BUFFER_DWORD3);
-        for (int v0 = 0; v0 < nbytes / 16; v0 += 256 * 8) {
+        for (int v0 = 0; v0 < nbytes / 16; v0 += NT * 8) {
             f32x4 t[8];
 #pragma unroll
             for (int u = 0; u < 8; u++) {
-                const int v = v0 + 256 * u + threadIdx.x;
+                const int v = v0 + NT * u + threadIdx.x;
                 t[u] = __builtin_amdgcn_raw_buffer_load_b128(hr, 16 * v, 0, CW_CPOL_SC1);  // past the end: 0, unused
             }
 #pragma unroll
             for (int u = 0; u < 8; u++) {
-                const int v = v0 + 256 * u + threadIdx.x;
+                const int v = v0 + NT * u + threadIdx.x;
                 if (v < nbytes / 16) {
                     const int j = v / hp, c = 4 * (v - j * hp);
                     *(f32x4 *)(hs + (j * nsbd + (c >> 5)) * 36 + (c & 31)) = t[u];
@@ -641,13 +648,15 @@ __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
     }
     __syncthreads();
 
-    // down + combine
-    for (int grp_i = blockIdx.x, first = 1; grp_i * RPD < a.H; grp_i += gridDim.x, first = 0) {
+    // down + combine: each wave group takes RPD rows per block pass (the loop's bound is the
+    // block's, so every thread meets the same barriers)
+    for (int bp = blockIdx.x, first = 1; bp * G * RPD < a.H; bp += gridDim.x, first = 0) {
+        const int grp_i = bp * G + grp;
         const int r = grp_i * RPD + rsd;
         if (!first) {
 #pragma unroll
             for (int q = 0; q < PPW; q++) {
-                const int j = wave + 4 * q;
+                const int j = wl + 4 * q;
                 if (j >= K) break;  // uniform across the wave
                 if (dslot[q] == 0xFFFFFFFFu || r >= a.H) continue;
 #pragma unroll
@@ -659,7 +668,7 @@ __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
         }
 #pragma unroll
         for (int q = 0; q < PPW; q++) {
-            const int j = wave + 4 * q;
+            const int j = wl + 4 * q;
             if (j >= K) break;
             const bool live = dslot[q] != 0xFFFFFFFFu && r < a.H;
             float d = 0.f;
@@ -675,15 +684,16 @@ __global__ __launch_bounds__(256, 3) void k_moe_decode(const MoeArgs a) {
                 }
             }
             d = group_sum<LD>(d);
-            if (subd == 0) part[j * RPD + rsd] = (dslot[q] == 0xFFFFFFFFu || !ok) ? __int_as_float(0x7fc00000) : d;
+            if (subd == 0) part[grp][j * RPD + rsd] = (dslot[q] == 0xFFFFFFFFu || !ok) ? __int_as_float(0x7fc00000) : d;
         }
         __syncthreads();
-        if (threadIdx.x < RPD) {
-            const int rr = grp_i * RPD + threadIdx.x;
+        const int tg4 = threadIdx.x & 255;
+        if (tg4 < RPD) {
+            const int rr = grp_i * RPD + tg4;
             if (rr < a.H) {
                 float acc = 0.f;
                 for (int j = 0; j < K; j++) {
-                    float d = part[j * RPD + threadIdx.x];
+                    float d = part[grp][j * RPD + tg4];
                     if (a.bd) d += a.bd[(int64_t)pick_e[j] * a.H + rr];
                     acc += pick_w[j] * d;
                 }
@@ -759,13 +769,13 @@ static int by_fmt(int dtype, const MoeArgs &a, int T, hipStream_t s) {
 // LDS for the staged hidden rows of one decode call: K rows of P floats, 36 per 32
 static size_t decode_hidden_lds(const MoeArgs &a) { return (size_t)a.K * (a.P / 32) * 36 * sizeof(float); }
 // the dynamic LDS of an instance: the hidden rows, or for LDS-staged gate/up rows (RI = 2) the
-// four waves' two item buffers if those are larger (they are used before the hidden rows)
-template <class FG>
+// waves' two item buffers or x if those are larger (they are used before the hidden rows)
+template <class FG, int G>
 static size_t decode_lds(const MoeArgs &a) {
     size_t n = decode_hidden_lds(a);
     if (RowDma<FG>::on) {
-        const size_t items = 4 * 2 * (size_t)(2 * 2 * row_window(a.H / 32 * FG::TS) + 16);
-        const size_t xs = (size_t)(a.H / 4 + 255) / 256 * 256 * 16;  // x, copied in rounds of 256 chunks
+        const size_t items = 4 * G * 2 * (size_t)(2 * 2 * row_window(a.H / 32 * FG::TS) + 16);
+        const size_t xs = (size_t)(a.H / 4 + 256 * G - 1) / (256 * G) * (256 * G) * 16;  // x, copied in rounds of one chunk per thread
         if (items > n) n = items;
         if (xs > n) n = xs;
     }
@@ -778,7 +788,7 @@ static constexpr size_t DECODE_MAX_HIDDEN_LDS = 64 * 1024;
 // device (a few entries remembered, under a lock, so concurrent callers never size a grid from
 // another call's entry). 0 on failure.
 template <class Kern>
-static int decode_grid(Kern kern, int which, const MoeArgs &a, size_t lds, int want) {
+static int decode_grid(Kern kern, int which, const MoeArgs &a, size_t lds, int threads, int want) {
     struct Occ {
         int dev = -1, which = -1;
         size_t lds = 0;
@@ -800,7 +810,7 @@ static int decode_grid(Kern kern, int which, const MoeArgs &a, size_t lds, int w
         o.which = which;
         o.lds = lds;
         if (hipDeviceGetAttribute(&o.cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&o.per_cu, kern, 256, lds) != hipSuccess || o.per_cu < 1)
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&o.per_cu, kern, threads, lds) != hipSuccess || o.per_cu < 1)
             return 0;
         std::lock_guard<std::mutex> lock(mu);
         cache[next++ & 7] = o;
@@ -809,7 +819,7 @@ static int decode_grid(Kern kern, int which, const MoeArgs &a, size_t lds, int w
     return grid < want ? grid : want;
 }
 
-template <class FG, int LG, int XG, class FD, int LD, int XD, int PER, int PPW>
+template <class FG, int LG, int XG, class FD, int LD, int XD, int PER, int PPW, int G>
 static int decode_launch_per(const MoeArgs &a, int which, hipStream_t s) {
     // LDS-staged gate/up rows: two chunk loads per row, so that every load instruction the
     // kernel's waits count has active lanes
@@ -818,29 +828,29 @@ static int decode_launch_per(const MoeArgs &a, int which, hipStream_t s) {
         if (w <= 1024 || w > 2048) return CW_ENOTSUP;
         if ((uintptr_t)a.x & 15) return CW_ENOTSUP;  // x is copied in 16-byte chunks
     }
-    const size_t lds = decode_lds<FG>(a);
+    const size_t lds = decode_lds<FG, G>(a);
     const int RPD = 64 / LD;
-    auto kern = k_moe_decode<FG, LG, XG, FD, LD, XD, PER, PPW>;
-    const int grid = decode_grid(kern, which, a, lds, (a.H + RPD - 1) / RPD);
+    auto kern = k_moe_decode<FG, LG, XG, FD, LD, XD, PER, PPW, G>;
+    const int grid = decode_grid(kern, 4 * which + G, a, lds, 256 * G, (a.H + RPD * G - 1) / (RPD * G));
     if (!grid) return set_error(CW_EHIP, "moe decode: occupancy query failed");
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, s, a);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(256 * G), lds, s, a);
     return check_launch("k_moe_decode");
 }
 
-template <class FG, int LG, int XG, class FD, int LD, int XD, int PPW>
+template <class FG, int LG, int XG, class FD, int LD, int XD, int PPW, int G>
 static int decode_launch(const MoeArgs &a, hipStream_t s) {
     // lanes hold 4, 8 or 16 router logits each (E up to 256, 512, 1024)
-    if (a.E <= 256) return decode_launch_per<FG, LG, XG, FD, LD, XD, 4, PPW>(a, 0, s);
-    if (a.E <= 512) return decode_launch_per<FG, LG, XG, FD, LD, XD, 8, PPW>(a, 1, s);
-    return decode_launch_per<FG, LG, XG, FD, LD, XD, 16, PPW>(a, 2, s);
+    if (a.E <= 256) return decode_launch_per<FG, LG, XG, FD, LD, XD, 4, PPW, G>(a, 0, s);
+    if (a.E <= 512) return decode_launch_per<FG, LG, XG, FD, LD, XD, 8, PPW, G>(a, 1, s);
+    return decode_launch_per<FG, LG, XG, FD, LD, XD, 16, PPW, G>(a, 2, s);
 }
 
-template <class FG, int LG, int XG, class FD, int LD, int XD>
+template <class FG, int LG, int XG, class FD, int LD, int XD, int G = 1>
 static int decode_ppw(const MoeArgs &a, hipStream_t s) {
     const int ppw = (a.K + 3) / 4;
-    if (ppw == 1) return decode_launch<FG, LG, XG, FD, LD, XD, 1>(a, s);
-    if (ppw == 2) return decode_launch<FG, LG, XG, FD, LD, XD, 2>(a, s);
-    if (ppw == 3) return decode_launch<FG, LG, XG, FD, LD, XD, 3>(a, s);
+    if (ppw == 1) return decode_launch<FG, LG, XG, FD, LD, XD, 1, G>(a, s);
+    if (ppw == 2) return decode_launch<FG, LG, XG, FD, LD, XD, 2, G>(a, s);
+    if (ppw == 3) return decode_launch<FG, LG, XG, FD, LD, XD, 3, G>(a, s);
     return CW_ENOTSUP;
 }
 
@@ -848,7 +858,10 @@ static int decode_ppw(const MoeArgs &a, hipStream_t s) {
 int moe_decode(int dtg, int dtd, const MoeArgs &a, hipStream_t s) {
     if (a.K > 12 || a.E > 1024 || decode_hidden_lds(a) > DECODE_MAX_HIDDEN_LDS) return CW_ENOTSUP;
     const int nsg = a.H / 32, nsd = a.P / 32;
-    if (dtg == CW_IQ2_XXS && dtd == CW_IQ2_S && nsg == 64 && nsd == 16) return decode_ppw<FIQ2_XXS, 64, 1, FIQ2_S, 16, 1>(a, s);
+    // config 3 in blocks of 8 waves, one per CU: each hidden row is staged once per CU, and half
+    // as many blocks meet at the barrier (12.58 -> 12.50 us per layer; config 5 measured slower
+    // so, 16.9 -> 18.9, and config 4 in blocks of 12 waves 30.1 -> 32.0)
+    if (dtg == CW_IQ2_XXS && dtd == CW_IQ2_S && nsg == 64 && nsd == 16) return decode_ppw<FIQ2_XXS, 64, 1, FIQ2_S, 16, 1, 2>(a, s);
     if (dtg == CW_IQ2_XXS && dtd == CW_IQ2_XXS && nsg == 64 && nsd == 16) return decode_ppw<FIQ2_XXS, 64, 1, FIQ2_XXS, 16, 1>(a, s);
     if (dtg == CW_IQ2_S && dtd == CW_IQ2_S && nsg == 64 && nsd == 16) return decode_ppw<FIQ2_S, 64, 1, FIQ2_S, 16, 1>(a, s);
     if (dtg == CW_IQ3_S && dtd == CW_Q4_K && nsg == 64 && nsd == 16) return decode_ppw<FIQ3_S, 64, 1, FQ4_K, 16, 1>(a, s);
