@@ -59,13 +59,16 @@ struct PackExtra {
 };
 
 bool mfma_supported(int dtype);
+// formats whose MFMA fragments take each 32-wide K step in a permuted order (MXFP4: a byte's two
+// nibbles side by side); their activations are packed with pack_rows_f16(..., perm = true)
+inline bool mfma_k_permuted(int dtype) { return dtype == CW_MXFP4; }
 // one block: expert piles of the (slot) picks, and the tile list
 int mfma_piles(const uint32_t *slots, int TK, int K, int n_slots, int *pile_pick, int *pile_tok, MfTile *tiles,
                int *n_tiles, hipStream_t s);
 int max_tiles(int TK, int n_slots);
 // rows x k f32 -> fp16 rows (ld = k) with per-row power-of-two scales
 int pack_rows_f16(const float *x, int rows, int k, int ldx, uint16_t *a16, float *ascale, hipStream_t s,
-                  const PackExtra *extra = nullptr);
+                  const PackExtra *extra = nullptr, bool perm = false);
 int fill_zero(float *p, int64_t n, hipStream_t s);
 int mfma_gateup(int dtype, const MfArgs &a, int tiles_max, hipStream_t s);
 int mfma_down(int dtype, const MfArgs &a, int tiles_max, hipStream_t s);

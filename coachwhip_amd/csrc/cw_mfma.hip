@@ -149,6 +149,12 @@ struct WinRef {
         const uint32_t *q = qa + off / 4;
         return __builtin_amdgcn_alignbyte(q[1], q[0], sh);
     }
+    // 4 bytes at p + ORG + off, any off
+    __device__ __forceinline__ uint32_t u32x(int off) const {
+        const uint32_t t = sh + (uint32_t)off;
+        const uint32_t *q = qa + (t >> 2);
+        return __builtin_amdgcn_alignbyte(q[1], q[0], t & 3);
+    }
     // 8 bytes at p + ORG + off, any off
     __device__ __forceinline__ uint2 u64x(int off) const {
         const uint32_t t = sh + (uint32_t)off, a = t & 3;
@@ -271,33 +277,37 @@ struct MMXFP4 {
         __device__ __forceinline__ void load(const WinRef &, int) {}
     };
     static __device__ __forceinline__ uint32_t expo(const uint8_t *win, int kk) { return lds_u8(win + TS * kk); }
-    // lane group grp takes the low (grp < 2) or high nibbles of bytes 8*(grp&1)..+8 (weights j and
-    // j+16 of a block are the low and high nibbles of byte j)
-    struct Raw { uint2 q; uint32_t e; };
+    // Lane group grp takes bytes 4grp..4grp+3 of the block, both nibbles of each: weights 4grp+i
+    // and 4grp+i+16 (the low and high nibbles of byte 4grp+i) at fragment positions 2i, 2i+1.
+    // The K order of a 32-weight step is thus permuted; the activations are packed in the same
+    // order (pack_rows_f16 with perm, mfma_k_permuted), so every product pairs the same weight
+    // and activation as in natural order.
+    struct Raw { uint32_t q; uint32_t e; };
     struct Look {};
     static __device__ __forceinline__ Raw raw(const WinRef &w, const Stage &, int kk, int grp) {
-        return Raw{w.u64x(TS * kk + 8 * (grp & 1)), expo(w.p, kk)};
+        return Raw{w.u32x(TS * kk + 4 * grp), expo(w.p, kk)};
     }
     static __device__ __forceinline__ Look look(const Raw &, const Stage &, int, int, const uint8_t *, bool) { return Look{}; }
     // The fragment by gfx950's scaled FP4 conversion (v_cvt_scalef32_pk_f16_fp4: the two E2M1
-    // values of one byte, low nibble first, times an f32 scale, to fp16): the lane's 8 nibbles are
-    // packed two to a byte (bytes 0 and 2 of each dword), and the scale 2^(de+1) gives the doubled
-    // E2M1 codes times 2^de, de = e - base <= 0 the block's exponent against the stage's largest.
-    // Every product is exact in fp16 down to 2^-24 of that largest block scale; below it, it rounds.
+    // values of one byte, low nibble first, times an f32 scale, to fp16), one conversion per byte
+    // of the lane's dword: the scale 2^(de+1) gives the doubled E2M1 codes times 2^de, de = e - base
+    // <= 0 the block's exponent against the stage's largest. Every product is exact in fp16 down
+    // to 2^-24 of that largest block scale; below it, it rounds.
     static __device__ __forceinline__ uint32_t cvt2(uint32_t v, float sc, int sel) {
         f16x2 h;
         if (sel == 0)
             h = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, sc, 0);
-        else
+        else if (sel == 1)
+            h = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, sc, 1);
+        else if (sel == 2)
             h = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, sc, 2);
+        else
+            h = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, sc, 3);
         return __builtin_bit_cast(uint32_t, h);
     }
-    static __device__ __forceinline__ uint4 make_mx(const Raw &r, int grp, int de) {
+    static __device__ __forceinline__ uint4 make_mx(const Raw &r, int, int de) {
         const float sc = de >= -127 ? __uint_as_float((uint32_t)(de + 128) << 23) : 0.f;
-        const int sh = 4 * (grp >> 1);
-        const uint32_t a = (r.q.x >> sh) & 0x0F0F0F0Fu, b = (r.q.y >> sh) & 0x0F0F0F0Fu;
-        const uint32_t pa = a | (a >> 4), pb = b | (b >> 4);
-        return make_uint4(cvt2(pa, sc, 0), cvt2(pa, sc, 2), cvt2(pb, sc, 0), cvt2(pb, sc, 2));
+        return make_uint4(cvt2(r.q, sc, 0), cvt2(r.q, sc, 1), cvt2(r.q, sc, 2), cvt2(r.q, sc, 3));
     }
 };
 
@@ -1217,7 +1227,7 @@ __global__ __launch_bounds__(1024) void k_piles(const uint32_t *slots, int TK, i
 // One wave per row, the row held in registers (NV float4 per lane, k <= 256*NV): scale =
 // 2^(15 - e) with max|x| in [2^(e-1), 2^e) keeps the row's largest value in [2^14, 2^15) of
 // fp16; ascale receives 1/scale.
-template <int NV>
+template <int NV, bool PERM>
 __global__ __launch_bounds__(256) void k_pack_f16(const float *x, int rows, int k, int ldx, uint16_t *a16, float *ascale,
                                                   PackExtra e) {
     if (e.tiles && blockIdx.x == 0) {  // tile i of a dense matmul: rows MF_MT*i .., "slot" 0
@@ -1231,10 +1241,25 @@ __global__ __launch_bounds__(256) void k_pack_f16(const float *x, int rows, int 
     const float *xr = x + (int64_t)row * ldx;
     float4 v[NV];
     float m = 0.f;
+    // loads from clamped addresses (all in flight at once), the values past the row zeroed after
+    if constexpr (PERM) {
+        // positions c..c+3 of a 32-wide step take its elements 2t, 2t+16, 2t+1, 2t+17 (t = (c % 32) / 4)
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int c = min(4 * lane + 256 * i, k - 4);
+            const float *b = xr + (c & ~31) + ((c & 31) >> 1);
+            const float2 lo = *(const float2 *)b, hi = *(const float2 *)(b + 16);
+            v[i] = make_float4(lo.x, hi.x, lo.y, hi.y);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NV; i++) v[i] = *(const float4 *)(xr + min(4 * lane + 256 * i, k - 4));
+    }
+#pragma unroll
+    for (int i = 0; i < NV; i++)
+        if (4 * lane + 256 * i >= k) v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int i = 0; i < NV; i++) {
-        const int c = 4 * lane + 256 * i;
-        v[i] = c < k ? *(const float4 *)(xr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
         m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
     }
     m = wave_max(m);
@@ -1297,14 +1322,19 @@ int mfma_piles(const uint32_t *slots, int TK, int K, int n_slots, int *pile_pick
 }
 
 int pack_rows_f16(const float *x, int rows, int k, int ldx, uint16_t *a16, float *ascale, hipStream_t s,
-                  const PackExtra *extra) {
+                  const PackExtra *extra, bool perm) {
     if (rows == 0) return CW_OK;
     if (k % 4 || ldx % 4) return set_error(CW_ENOTSUP, "pack: row of %d (stride %d) is not whole float4s", k, ldx);
+    if (perm && k % 32) return set_error(CW_ENOTSUP, "pack: a permuted row of %d is not whole 32-wide steps", k);
     const dim3 grid((rows + 3) / 4);
     const int nv = (k + 255) / 256;
     const PackExtra e = extra ? *extra : PackExtra{};
 #define CW_PACK(N) \
-    if (nv <= N) { hipLaunchKernelGGL(k_pack_f16<N>, grid, dim3(256), 0, s, x, rows, k, ldx, a16, ascale, e); return check_launch("k_pack_f16"); }
+    if (nv <= N) { \
+        if (perm) hipLaunchKernelGGL((k_pack_f16<N, true>), grid, dim3(256), 0, s, x, rows, k, ldx, a16, ascale, e); \
+        else hipLaunchKernelGGL((k_pack_f16<N, false>), grid, dim3(256), 0, s, x, rows, k, ldx, a16, ascale, e); \
+        return check_launch("k_pack_f16"); \
+    }
     CW_PACK(2) CW_PACK(4) CW_PACK(8) CW_PACK(12) CW_PACK(16) CW_PACK(32)
 #undef CW_PACK
     return set_error(CW_ENOTSUP, "pack: rows of %d above 8192", k);
@@ -1477,7 +1507,7 @@ int mfma_dense(int dtype, const uint8_t *w, int64_t row_bytes, int n, int k, con
     // one launch packs x, writes the tile list and zeroes the split counters
     const PackExtra extra = {tiles, n_tiles, m, cnt, S > 1 ? (int)dense_items(dtype, m, n) : 0};
     int rc;
-    if ((rc = pack_rows_f16(x, m, k, k, x16, xs, s, &extra))) return rc;
+    if ((rc = pack_rows_f16(x, m, k, k, x16, xs, s, &extra, mfma_k_permuted(dtype)))) return rc;
     MfArgs a = {};
     a.w0 = w;
     a.s0 = 0;

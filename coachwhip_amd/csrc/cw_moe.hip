@@ -211,7 +211,7 @@ static int moe_grouped(const cw_moe_desc *d, const MoeArgs &a, const MoeLayout &
     if ((rc = mfma_piles(slots, TK, K, a.n_slots, pile_pick, pile_tok, tiles, n_tiles, s))) return rc;
     uint16_t *x16 = (uint16_t *)(base + L.x16), *h16 = (uint16_t *)(base + L.h16);
     float *xscale = (float *)(base + L.xscale), *hscale = (float *)(base + L.hscale);
-    if ((rc = pack_rows_f16(a.x, T, a.H, a.H, x16, xscale, s))) return rc;
+    if ((rc = pack_rows_f16(a.x, T, a.H, a.H, x16, xscale, s, nullptr, mfma_k_permuted(d->dtype[0])))) return rc;
     if (P > a.I && (rc = fill_zero(a.h, (int64_t)TK * P, s))) return rc;
     const int tmax = max_tiles(TK, a.n_slots);
 
@@ -240,7 +240,7 @@ static int moe_grouped(const cw_moe_desc *d, const MoeArgs &a, const MoeLayout &
     g.h = a.h;
     g.ldh = P;
     if ((rc = mfma_gateup(d->dtype[0], g, tmax, s))) return rc;
-    if ((rc = pack_rows_f16(a.h, TK, P, P, h16, hscale, s))) return rc;
+    if ((rc = pack_rows_f16(a.h, TK, P, P, h16, hscale, s, nullptr, mfma_k_permuted(d->dtype[2])))) return rc;
 
     MfArgs dn = {};
     dn.w0 = a.wd;
@@ -518,7 +518,7 @@ int cw_matmul_id_grouped(int dtype, int64_t n, int64_t k, int64_t n_slots, int64
     uint16_t *x16 = (uint16_t *)(base + L.x16);
     float *xscale = (float *)(base + L.xscale);
     if ((rc = mfma_piles(ids, TK, K, (int)n_slots, pile_pick, pile_tok, tiles, n_tiles, s))) return rc;
-    if ((rc = pack_rows_f16(x, xpp ? TK : T, (int)k, (int)k, x16, xscale, s))) return rc;
+    if ((rc = pack_rows_f16(x, xpp ? TK : T, (int)k, (int)k, x16, xscale, s, nullptr, mfma_k_permuted(dtype)))) return rc;
     MfArgs a = {};
     a.w0 = (const uint8_t *)bank;
     a.s0 = slot_stride;
