@@ -619,6 +619,27 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
         store_coherent(a.h + (int64_t)j * a.P + a.I + (c - j * (a.P - a.I)), 0.f);
     }
 
+    // the second down pass's rows, requested before the barrier (x's registers are free by now),
+    // so they are in by the time the hidden rows are staged (config 4, whose rows take two passes:
+    // 29.7-30.0 -> 29.1-29.4 us per layer; the other instances keep their code: 12.50 against
+    // 12.59 us for config 3, which has one pass)
+    constexpr bool PF2 = RowDma<FG>::on;
+    typename FD::Raw draw2[PPW][XD];
+    const int bp2 = blockIdx.x + gridDim.x;
+    if (PF2 && bp2 * G * RPD < a.H) {
+        const int r2 = (bp2 * G + grp) * RPD + rsd;
+#pragma unroll
+        for (int q = 0; q < PPW; q++) {
+            const int j = wl + 4 * q;
+            if (j >= K) break;
+            if (dslot[q] == 0xFFFFFFFFu || r2 >= a.H) continue;
+#pragma unroll
+            for (int i = 0; i < XD; i++) {
+                const int sb = subd + i * LD;
+                if (sb < nsbd) draw2[q][i] = FD::load(a.wd + (int64_t)dslot[q] * a.sd + (int64_t)r2 * a.rbd, sb);
+            }
+        }
+    }
     if (wave < 4) td.store(ldsd, threadIdx.x);
     const bool ok = grid_barrier((DecodeBarrier *)a.state, gridDim.x, a.polls);
 
@@ -653,7 +674,12 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
     for (int bp = blockIdx.x, first = 1; bp * G * RPD < a.H; bp += gridDim.x, first = 0) {
         const int grp_i = bp * G + grp;
         const int r = grp_i * RPD + rsd;
-        if (!first) {
+        if (PF2 && !first && bp == bp2) {
+#pragma unroll
+            for (int q = 0; q < PPW; q++)
+#pragma unroll
+                for (int i = 0; i < XD; i++) draw[q][i] = draw2[q][i];
+        } else if (!first) {
 #pragma unroll
             for (int q = 0; q < PPW; q++) {
                 const int j = wl + 4 * q;
