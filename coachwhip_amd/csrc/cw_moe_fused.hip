@@ -349,13 +349,15 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
     if (wave < 4) tg.load(threadIdx.x);  // the tables take 256 threads
     const int subg = lane % LG, rsg = lane / LG, nsbg = a.H / 32;
     float xr[XG][32];
+    // GDMA: item buffer b of wave w at hs + (b * NW + w) * ibuf; x goes into the buffer-1 region
+    const int x_off = RowDma<FG>::on ? NW * (2 * RI * row_window(a.H / 32 * FG::TS) + 16) : 0;
     if constexpr (RowDma<FG>::on) {
         // x once per block into the (not yet used) hidden-row region, read into registers below:
         // every wave loading all of x (35 MB across config 4's grid) held up the logits and x
         // loads of the blocks placed third on a CU by ~7 us
         const int nxc = a.H / 4;
         for (int c0 = 0; c0 < nxc; c0 += NT)
-            lds_dma16(a.x + 4 * min(c0 + (int)threadIdx.x, nxc - 1), hs_lds + 16 * (c0 + wave * 64));
+            lds_dma16(a.x + 4 * min(c0 + (int)threadIdx.x, nxc - 1), hs_lds + x_off + 16 * (c0 + wave * 64));
     } else {
         load_xs<XG>(xr, a.x, subg, LG, nsbg);
     }
@@ -429,13 +431,13 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
     // gate rows, RI up rows, then the 2*RI bias values
     const int win = row_window(nsbg * FG::TS);
     const int ibuf = 2 * RI * win + 16;
-    uint8_t *wbuf = (uint8_t *)hs + wave * 2 * ibuf;
+    uint8_t *wbuf = (uint8_t *)hs + wave * ibuf;
     auto issue_item = [&](int it, int b) {
         const int j = it / row_items, r0 = (it - j * row_items) * RI;
         // both shuffles with every lane active: a lane outside a branch gives 0 to a shuffle
         const uint32_t slot = __shfl(my_slot, j), e = __shfl(rid, j);
         const uint32_t sl = slot == 0xFFFFFFFFu ? 0 : slot;
-        uint8_t *ib = wbuf + b * ibuf;
+        uint8_t *ib = wbuf + b * NW * ibuf;
 #pragma unroll
         for (int q = 0; q < RI; q++) {
             const int r = min(r0 + q, a.I - 1);
@@ -460,15 +462,20 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
         }
     };
     if constexpr (GDMA) {
-        // x (copied during the top-k) from LDS into registers; the block then lets the item
-        // buffers overwrite it
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // the first item's rows go out at once (into buffer 0); x (copied during the top-k into
+        // the buffer-1 region) is read into registers meanwhile, before any buffer 1 is filled
+        if (gwave < n_items) {
+            issue_item(gwave, 0);
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * RI + 1) : "memory");
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < XG; i++) {
             const int sb = subg + i * LG;
             const bool in = sb < nsbg;
-            const float4 *src = (const float4 *)(hs + 32 * (in ? sb : nsbg - 1));
+            const float4 *src = (const float4 *)((const float *)((const uint8_t *)hs + x_off) + 32 * (in ? sb : nsbg - 1));
 #pragma unroll
             for (int v = 0; v < 8; v++) {
                 const float4 f = src[v];
@@ -479,7 +486,6 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
             }
         }
         __syncthreads();
-        if (gwave < n_items) issue_item(gwave, 0);
     } else {
         if (gwave < n_items) load_item(gwave);
     }
@@ -540,7 +546,7 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
             const int j = it / row_items, r0 = (it - j * row_items) * RI;
             const uint32_t slot = __shfl(my_slot, j);
             const uint32_t sl = slot == 0xFFFFFFFFu ? 0 : slot;
-            const uint8_t *ib = wbuf + b * ibuf;
+            const uint8_t *ib = wbuf + b * NW * ibuf;
 #pragma unroll
             for (int q = 0; q < RI; q++) {
                 const int r = min(r0 + q, a.I - 1);
