@@ -316,9 +316,9 @@ __host__ __device__ __forceinline__ int row_window(int row_bytes) { return ((row
 // gpt-oss shape's 182-VGPR build ran 2 blocks per CU (39.0 us per layer; 36.4 at 3, with a few
 // spilled registers, none since its gate/up rows are staged through LDS: 155 VGPRs); the other
 // instances fit already.
-template <class FG, int LG, int XG, class FD, int LD, int XD, int PER, int PPW, int G>
+// RI: rows (of RPG) per gate/up item.
+template <class FG, int LG, int XG, class FD, int LD, int XD, int PER, int PPW, int G, int RI>
 __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const MoeArgs a) {
-    constexpr int RI = 2;  // rows (of RPG) per gate/up item: 4 measured slower (config 4 spills, config 5 too)
     constexpr int NW = 4 * G, NT = 64 * NW;  // waves and threads of a block: G groups of 4 waves
     __shared__ __align__(16) uint8_t ldsg[FG::LDS_BYTES > 0 ? FG::LDS_BYTES : 16];
     __shared__ __align__(16) uint8_t ldsd[FD::LDS_BYTES > 0 ? FD::LDS_BYTES : 16];
@@ -802,11 +802,11 @@ static int by_fmt(int dtype, const MoeArgs &a, int T, hipStream_t s) {
 static size_t decode_hidden_lds(const MoeArgs &a) { return (size_t)a.K * (a.P / 32) * 36 * sizeof(float); }
 // the dynamic LDS of an instance: the hidden rows, or for LDS-staged gate/up rows (RI = 2) the
 // waves' two item buffers or x if those are larger (they are used before the hidden rows)
-template <class FG, int G>
+template <class FG, int G, int RI>
 static size_t decode_lds(const MoeArgs &a) {
     size_t n = decode_hidden_lds(a);
     if (RowDma<FG>::on) {
-        const size_t items = 4 * G * 2 * (size_t)(2 * 2 * row_window(a.H / 32 * FG::TS) + 16);
+        const size_t items = 4 * G * 2 * (size_t)(2 * RI * row_window(a.H / 32 * FG::TS) + 16);
         const size_t xs = (size_t)(a.H / 4 + 256 * G - 1) / (256 * G) * (256 * G) * 16;  // x, copied in rounds of one chunk per thread
         if (items > n) n = items;
         if (xs > n) n = xs;
@@ -851,7 +851,7 @@ static int decode_grid(Kern kern, int which, const MoeArgs &a, size_t lds, int t
     return grid < want ? grid : want;
 }
 
-template <class FG, int LG, int XG, class FD, int LD, int XD, int PER, int PPW, int G>
+template <class FG, int LG, int XG, class FD, int LD, int XD, int PER, int PPW, int G, int RI>
 static int decode_launch_per(const MoeArgs &a, int which, hipStream_t s) {
     // LDS-staged gate/up rows: two chunk loads per row, so that every load instruction the
     // kernel's waits count has active lanes
@@ -860,29 +860,29 @@ static int decode_launch_per(const MoeArgs &a, int which, hipStream_t s) {
         if (w <= 1024 || w > 2048) return CW_ENOTSUP;
         if ((uintptr_t)a.x & 15) return CW_ENOTSUP;  // x is copied in 16-byte chunks
     }
-    const size_t lds = decode_lds<FG, G>(a);
+    const size_t lds = decode_lds<FG, G, RI>(a);
     const int RPD = 64 / LD;
-    auto kern = k_moe_decode<FG, LG, XG, FD, LD, XD, PER, PPW, G>;
+    auto kern = k_moe_decode<FG, LG, XG, FD, LD, XD, PER, PPW, G, RI>;
     const int grid = decode_grid(kern, 4 * which + G, a, lds, 256 * G, (a.H + RPD * G - 1) / (RPD * G));
     if (!grid) return set_error(CW_EHIP, "moe decode: occupancy query failed");
     hipLaunchKernelGGL(kern, dim3(grid), dim3(256 * G), lds, s, a);
     return check_launch("k_moe_decode");
 }
 
-template <class FG, int LG, int XG, class FD, int LD, int XD, int PPW, int G>
+template <class FG, int LG, int XG, class FD, int LD, int XD, int PPW, int G, int RI>
 static int decode_launch(const MoeArgs &a, hipStream_t s) {
     // lanes hold 4, 8 or 16 router logits each (E up to 256, 512, 1024)
-    if (a.E <= 256) return decode_launch_per<FG, LG, XG, FD, LD, XD, 4, PPW, G>(a, 0, s);
-    if (a.E <= 512) return decode_launch_per<FG, LG, XG, FD, LD, XD, 8, PPW, G>(a, 1, s);
-    return decode_launch_per<FG, LG, XG, FD, LD, XD, 16, PPW, G>(a, 2, s);
+    if (a.E <= 256) return decode_launch_per<FG, LG, XG, FD, LD, XD, 4, PPW, G, RI>(a, 0, s);
+    if (a.E <= 512) return decode_launch_per<FG, LG, XG, FD, LD, XD, 8, PPW, G, RI>(a, 1, s);
+    return decode_launch_per<FG, LG, XG, FD, LD, XD, 16, PPW, G, RI>(a, 2, s);
 }
 
-template <class FG, int LG, int XG, class FD, int LD, int XD, int G = 1>
+template <class FG, int LG, int XG, class FD, int LD, int XD, int G = 1, int RI = 2>
 static int decode_ppw(const MoeArgs &a, hipStream_t s) {
     const int ppw = (a.K + 3) / 4;
-    if (ppw == 1) return decode_launch<FG, LG, XG, FD, LD, XD, 1, G>(a, s);
-    if (ppw == 2) return decode_launch<FG, LG, XG, FD, LD, XD, 2, G>(a, s);
-    if (ppw == 3) return decode_launch<FG, LG, XG, FD, LD, XD, 3, G>(a, s);
+    if (ppw == 1) return decode_launch<FG, LG, XG, FD, LD, XD, 1, G, RI>(a, s);
+    if (ppw == 2) return decode_launch<FG, LG, XG, FD, LD, XD, 2, G, RI>(a, s);
+    if (ppw == 3) return decode_launch<FG, LG, XG, FD, LD, XD, 3, G, RI>(a, s);
     return CW_ENOTSUP;
 }
 
