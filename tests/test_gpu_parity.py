@@ -573,19 +573,24 @@ def test_moe_decode_barrier_gives_up_without_hanging(monkeypatch):
     assert cw.lib().cw_device_errors() == after
 
 
-@pytest.mark.parametrize("path,T", [("gemv", 1), ("gemv", 40), ("grouped", 40)])
-def test_moe_layer_marks_out_of_range_slots(path, T, monkeypatch):
+@pytest.mark.parametrize("path,T,shape", [("gemv", 1, "iq2"), ("gemv", 40, "iq2"), ("grouped", 40, "iq2"),
+                                          ("gemv", 1, "mxfp4"), ("grouped", 40, "mxfp4")])
+def test_moe_layer_marks_out_of_range_slots(path, T, shape, monkeypatch):
     """A slot table entry past the bank (a corrupt table) is rejected on the device on every path:
     the tokens that pick that expert get NaN outputs (the one-token decode, the two-kernel matvec
     path, and the grouped path, where such a pick is in no pile), the other tokens match the
-    oracle run on the intact table."""
+    oracle run on the intact table. The MXFP4 shape takes the decode instance whose gate/up rows
+    go through LDS."""
     monkeypatch.setenv("CWMOE_PREFILL_MIN_TOKENS", PATHS[path])
-    say("moe out-of-range slot", path, T)
+    say("moe out-of-range slot", path, T, shape)
     rng = np.random.default_rng(93 + T)
-    E, K = 64, 4
-    layer = synth.moe_weights(E, K, 2048, 512, (F.IQ2_XXS, F.IQ2_XXS, F.IQ2_S), rng)
+    if shape == "iq2":
+        E, K, h, I, dts, act = 64, 4, 2048, 512, (F.IQ2_XXS, F.IQ2_XXS, F.IQ2_S), 0
+    else:
+        E, K, h, I, dts, act = 16, 4, 2880, 2880, (F.MXFP4,) * 3, 1
+    layer = synth.moe_weights(E, K, h, I, dts, rng, act=act)
     table = np.arange(E, dtype=np.uint32)
-    x = rng.standard_normal((T, 2048)).astype(np.float32)
+    x = rng.standard_normal((T, h)).astype(np.float32)
     logits = rng.standard_normal((T, E)).astype(np.float32)
     want, wids, _, _ = O.moe_layer(layer, x, logits, slot_table=table, n_slots=E)
     table[wids[0, 1]] = E + 3
