@@ -768,7 +768,10 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
                 o += (uint32_t)(W::SEG * st_w);                                // the row's stage bytes
                 const uint32_t mis = ((uint32_t)(uintptr_t)mb + o) & 15;      // ... from a 16-byte boundary
                 const uint32_t pc = min(p, (mis + seg_w - 1) >> 4);
-                dma16<S::ADMA>(mb + (o - mis + 16 * pc), wbuf + (i - (tido & 63)) * 16);
+                // from the 16-byte boundary at or below the row's stage bytes, taken on the full
+                // address (a slot whose base is not 16-byte aligned has mis > o for its row 0)
+                const uint8_t *al = (const uint8_t *)(((uintptr_t)mb + o) & ~(uintptr_t)15);
+                dma16<S::ADMA>(al + 16 * pc, wbuf + (i - (tido & 63)) * 16);
             }
         };
         // Activations of half-stage h (K-steps h*KA .. h*KA+KA-1, clamped to the row: a clamped load

@@ -429,6 +429,7 @@ MOE_CASES = [
     ("c3_mixed_gate_up", 64, 8, 2048, 512, (F.IQ2_XXS, F.IQ2_S, F.IQ2_S), 0, 0, 3),
     ("c4_decode_shape", 16, 4, 2880, 2880, (F.MXFP4, F.MXFP4, F.MXFP4), 1, 0, 1),
     ("c4_decode_top5", 32, 5, 2880, 2880, (F.MXFP4, F.MXFP4, F.MXFP4), 1, 0, 1),  # 3-4 gate/up items per wave
+    ("c4_decode_odd_rows", 16, 4, 2880, 2877, (F.MXFP4, F.MXFP4, F.MXFP4), 1, 2880, 1),  # a last item of one row, padded hidden
     ("c4_prefill_shape", 16, 4, 2880, 2880, (F.MXFP4, F.MXFP4, F.MXFP4), 1, 0, 40),
     ("c4_padded", 16, 4, 1024, 720, (F.MXFP4, F.MXFP4, F.Q4_K), 1, 768, 5),
     ("iq3_s_grouped", 32, 6, 1024, 512, (F.IQ3_S, F.IQ3_S, F.IQ3_S), 0, 0, 48),
