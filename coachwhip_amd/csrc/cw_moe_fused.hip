@@ -193,9 +193,11 @@ __global__ __launch_bounds__(256) void k_moe_down(const MoeArgs a) {
 // calls with distinct workspaces are independent. Blocks first arrive on one of 32 counters
 // (blockIdx % 32: blocks go to the 8 XCDs round-robin, so each counter's blocks share an XCD); the
 // last of each clears it and arrives on a top counter, and the last of those clears it and bumps
-// the generation every block waits on. Splitting the arrivals over 33 counters, 128 bytes apart,
-// keeps them from serializing on one address (a microbenchmark of 512 blocks: one counter 6.1 us
-// above an empty launch, 8 counters 1.4 us, 32 counters 1.0 us). Everything the blocks
+// the generation, held in 32 copies 128 bytes apart: block b polls copy b % 32, and the last block
+// stores all 32 with one instruction. Splitting the arrivals over 33 counters keeps them from
+// serializing on one address (a microbenchmark of 512 blocks: one counter 6.1 us above an empty
+// launch, 8 counters 1.4 us, 32 counters 1.0 us); with one generation word, the polls of 768
+// blocks on it spread the blocks' release over ~1.3 us. Everything the blocks
 // exchange through memory inside the kernel is written and read with agent-scope atomics, which go
 // to the coherence point, so the counters need no fences: an agent-scope release / acquire pair
 // here (L2 write-back and invalidate in every block) measured 3x slower, and so did polling all 8
@@ -203,9 +205,8 @@ __global__ __launch_bounds__(256) void k_moe_down(const MoeArgs a) {
 // (g_decode_errors) instead of hanging; every block still arrives exactly once, so the state is
 // back at zero (and the generation one further) when the kernel ends, timed out or not.
 struct DecodeBarrier {
-    uint32_t sub[32][32];
-    uint32_t top[32];
-    uint32_t gen[32];
+    uint32_t sub[32][32];  // arrival counter x at sub[x][0]; the top counter at sub[0][16]
+    uint32_t gen[32][32];  // generation copy x at gen[x][0]
 };
 static_assert(sizeof(DecodeBarrier) <= DECODE_STATE_BYTES, "the decode state does not fit its workspace region");
 static __device__ uint32_t g_decode_errors;
@@ -216,27 +217,33 @@ static __device__ uint32_t g_decode_errors;
 #define CW_BUFFER_DWORD3 0x00020000
 #define CW_CPOL_SC1 16
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-__device__ bool grid_barrier(DecodeBarrier *b, uint32_t nblocks, uint32_t polls) {
+// `gen` is generation copy blockIdx % 32 as read by wave 0 at any point of this launch before it
+// arrives (the copies move only when every block has arrived, and they are equal between calls),
+// so that read is off the barrier's critical path.
+__device__ bool grid_barrier(DecodeBarrier *b, uint32_t nblocks, uint32_t polls, uint32_t gen) {
     __builtin_amdgcn_s_waitcnt(0);  // this thread's coherent stores have landed
     __syncthreads();
     __shared__ int ok;
-    if (threadIdx.x == 0) {
-        const uint32_t gen = __hip_atomic_load(&b->gen[0], __ATOMIC_RELAXED, CW_AGENT);
+    if (threadIdx.x < 64) {
         const uint32_t x = blockIdx.x & 31;
-        const uint32_t nsub = (nblocks - x + 31) / 32, nx = nblocks < 32 ? nblocks : 32;
-        bool last = false;
-        if (__hip_atomic_fetch_add(&b->sub[x][0], 1u, __ATOMIC_RELAXED, CW_AGENT) == nsub - 1) {
-            // the reset only has to land before the next call, which the kernel's end ensures
-            __hip_atomic_store(&b->sub[x][0], 0u, __ATOMIC_RELAXED, CW_AGENT);
-            last = __hip_atomic_fetch_add(&b->top[0], 1u, __ATOMIC_RELAXED, CW_AGENT) == nx - 1;
-            if (last) __hip_atomic_store(&b->top[0], 0u, __ATOMIC_RELAXED, CW_AGENT);
+        int last = 0;
+        if (threadIdx.x == 0) {
+            const uint32_t nsub = (nblocks - x + 31) / 32, nx = nblocks < 32 ? nblocks : 32;
+            if (__hip_atomic_fetch_add(&b->sub[x][0], 1u, __ATOMIC_RELAXED, CW_AGENT) == nsub - 1) {
+                // the reset only has to land before the next call, which the kernel's end ensures
+                __hip_atomic_store(&b->sub[x][0], 0u, __ATOMIC_RELAXED, CW_AGENT);
+                last = __hip_atomic_fetch_add(&b->sub[0][16], 1u, __ATOMIC_RELAXED, CW_AGENT) == nx - 1;
+                if (last) __hip_atomic_store(&b->sub[0][16], 0u, __ATOMIC_RELAXED, CW_AGENT);
+            }
         }
-        int good = 1;
+        last = __builtin_amdgcn_readfirstlane(last);
         if (last) {
-            __hip_atomic_fetch_add(&b->gen[0], 1u, __ATOMIC_RELAXED, CW_AGENT);
-        } else {
+            if (threadIdx.x < 32) __hip_atomic_store(&b->gen[threadIdx.x][0], gen + 1, __ATOMIC_RELAXED, CW_AGENT);
+            if (threadIdx.x == 0) ok = 1;
+        } else if (threadIdx.x == 0) {
+            int good = 1;
             uint32_t n = 0;
-            while (__hip_atomic_load(&b->gen[0], __ATOMIC_RELAXED, CW_AGENT) == gen) {
+            while (__hip_atomic_load(&b->gen[x][0], __ATOMIC_RELAXED, CW_AGENT) == gen) {
                 if (n++ >= polls) {
                     good = 0;
                     __hip_atomic_fetch_add(&g_decode_errors, 1u, __ATOMIC_RELAXED, CW_AGENT);
@@ -244,8 +251,8 @@ __device__ bool grid_barrier(DecodeBarrier *b, uint32_t nblocks, uint32_t polls)
                 }
                 __builtin_amdgcn_s_sleep(1);
             }
+            ok = good;
         }
-        ok = good;
     }
     __syncthreads();
     return ok != 0;
@@ -340,6 +347,8 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
     const bool routes = !ONE_ROUTER || wave == 0;
     float lv[PER];
     RouteState<PER> rst;
+    uint32_t gen = 0;  // the barrier's generation, read by wave 0 ahead of the logits
+    if (wave == 0) gen = __hip_atomic_load(&((DecodeBarrier *)a.state)->gen[blockIdx.x & 31][0], __ATOMIC_RELAXED, CW_AGENT);
     if (routes) {
         route_load<PER>(a.logits, a.E, lv);
         route_keys<PER>(lv, a.E, rst);
@@ -646,8 +655,22 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
             }
         }
     }
+    // the combine's down-bias values of this thread's row in both passes, also before the barrier
+    // (a load in the combine is a memory round trip after each pass's dots)
+    constexpr bool PFB = PF2 && PPW == 1;  // (more picks per wave would spill)
+    float bq[2][4 * PPW];
+    if constexpr (PFB) {
+        const int tg4 = threadIdx.x & 255;
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            const int rr = ((blockIdx.x + p * gridDim.x) * G + grp) * RPD + tg4;
+#pragma unroll
+            for (int j = 0; j < 4 * PPW; j++)
+                bq[p][j] = a.bd && tg4 < RPD && rr < a.H && j < K ? a.bd[(int64_t)pick_e[j] * a.H + rr] : 0.f;
+        }
+    }
     if (wave < 4) td.store(ldsd, threadIdx.x);
-    const bool ok = grid_barrier((DecodeBarrier *)a.state, gridDim.x, a.polls);
+    const bool ok = grid_barrier((DecodeBarrier *)a.state, gridDim.x, a.polls, gen);
 
     // every hidden row into LDS once per block, read at the coherence point (16-byte buffer
     // loads with the sc1 policy, the form of an agent-scope atomic load, 8 in flight per thread),
@@ -724,10 +747,16 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
             const int rr = grp_i * RPD + tg4;
             if (rr < a.H) {
                 float acc = 0.f;
-                for (int j = 0; j < K; j++) {
-                    float d = part[grp][j * RPD + tg4];
-                    if (a.bd) d += a.bd[(int64_t)pick_e[j] * a.H + rr];
-                    acc += pick_w[j] * d;
+                if (PFB && (first || bp == bp2)) {
+#pragma unroll
+                    for (int j = 0; j < 4 * PPW; j++)
+                        if (j < K) acc += pick_w[j] * (part[grp][j * RPD + tg4] + bq[first ? 0 : 1][j]);
+                } else {
+                    for (int j = 0; j < K; j++) {
+                        float d = part[grp][j * RPD + tg4];
+                        if (a.bd) d += a.bd[(int64_t)pick_e[j] * a.H + rr];
+                        acc += pick_w[j] * d;
+                    }
                 }
                 a.out[rr] = acc;
             }
