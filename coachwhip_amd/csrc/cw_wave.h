@@ -80,6 +80,23 @@ __device__ __forceinline__ uint32_t wave_max_key(uint32_t k) {
 template <int PER>
 __device__ __forceinline__ void route_load(const float *logits, int E, float (&v)[PER]) {
     const int lane = threadIdx.x & 63;
+    if constexpr (PER >= 8 && PER % 4 == 0) {
+        // every lane full and the logits 16-byte aligned: PER / 4 16-byte loads per lane (a
+        // dword load per logit makes each instruction touch every cache line of the logits;
+        // config 5's decode layer 16.5 -> 16.2 us, while 4 logits per lane measured 0.1 us
+        // slower as one 16-byte load)
+        if (E == 64 * PER && ((uintptr_t)logits & 15) == 0) {
+#pragma unroll
+            for (int c = 0; c < PER / 4; c++) {
+                const float4 t = ((const float4 *)logits)[lane * (PER / 4) + c];
+                v[4 * c] = t.x;
+                v[4 * c + 1] = t.y;
+                v[4 * c + 2] = t.z;
+                v[4 * c + 3] = t.w;
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int i = 0; i < PER; i++) {
         // clamped, not branched: loads in branches make the compiler wait for every later load
