@@ -848,7 +848,10 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
 #pragma unroll
                     for (int q = 0; q < NB; q++) {
                         zero[m][q] = false;
-                        int base = 0;
+                        // the base is the largest block exponent of the item's stages so far: the
+                        // accumulators only ever move down onto a larger base (moving them up onto a
+                        // smaller one overflowed f32 for rows whose block scales span more than 2^127)
+                        int base = st > st_lo ? rb[m][q] : 0;
 #pragma unroll
                         for (int kk = 0; kk < KST; kk++)
                             if (kk < nk) base = max(base, (int)MF::expo(win[m][q], kk));
@@ -1448,7 +1451,9 @@ static void dense_shape(int dtype, int &rpb, int &kst, int &per_cu) {
 // padded as launch() pads them, times S) run in rounds of the resident blocks, and each block runs
 // its items' ceil(n_st / S) stages one after another. (Filling the resident blocks exactly, as a
 // first version did, left config 2's M = 512 at 768 blocks over 512 slots: 2 rounds of 6 stages
-// where 1 round of 8 does.) Ties go to fewer splits (less partial traffic).
+// where 1 round of 8 does.) Each 8 splits add a stage to the cost: the last split of a work item
+// reads the partial rows 8 splits at a time (config 2 at M = 16: 16 splits of one stage measured
+// 19.4 us, 8 splits of two 17.8). Ties go to fewer splits (less partial traffic).
 static int dense_splits(int dtype, int64_t m, int64_t n, int64_t k, int &split_st) {
     int rpb, kst, per_cu;
     dense_shape(dtype, rpb, kst, per_cu);
@@ -1463,7 +1468,7 @@ static int dense_splits(int dtype, int64_t m, int64_t n, int64_t k, int &split_s
         const int sst = (n_st + S - 1) / S;
         if ((n_st + sst - 1) / sst != S) continue;  // the same split as a smaller S
         if (S > 1 && (int64_t)S * m * n * 4 >= ((int64_t)1 << 31)) break;  // the partial rows stay under 2 GiB (32-bit offsets)
-        const int64_t cost = (grid_x * S + res - 1) / res * per_block * sst;
+        const int64_t cost = (grid_x * S + res - 1) / res * per_block * sst + (S > 1 ? (S + 7) / 8 : 0);
         if (best < 0 || cost < best) {
             best = cost;
             best_s = S;

@@ -181,6 +181,27 @@ def test_qmatmul_mxfp4_exponents(path, monkeypatch):
             assert err <= REL_L2_F32
 
 
+def test_grouped_gemm_mxfp4_exponents_across_stages():
+    """The grouped MFMA GEMM runs a whole row of 90 MXFP4 blocks (12 stages) in one work item: its
+    accumulators follow the largest block exponent seen so far, and rows whose e8m0 scales swing
+    from 2^23 down to 2^-128 between stages stay finite (moving the accumulators up onto a smaller
+    stage base overflowed f32). One expert, 40 picks, against the f64 oracle at the fp16 bar."""
+    rng = np.random.default_rng(79)
+    n, k, T = 64, 2880, 40
+    raw = synth.random_blocks(F.MXFP4, n * k, rng).reshape(n, k // 32, F.type_size(F.MXFP4)).copy()
+    raw[:, :, 0] = np.array([0, 1, 90, 150], np.uint8)[rng.integers(0, 4, raw.shape[:2])]
+    raw[:, :8, 0] = 150                               # the first stage holds the row's largest scale
+    raw = raw.reshape(-1)
+    bank = ops.ExpertBank.from_blocks(raw, F.MXFP4, n, k, 1)
+    mv = ops.MoeMatvec(bank, 1, False)
+    assert T > mv.grouped_above
+    x = rng.standard_normal((T, k)).astype(np.float32)
+    out = host(mv.forward(dev(x), dev(np.zeros((T, 1), np.uint32))))[:, 0]
+    want = O.qmatmul_f64(F.MXFP4, raw, n, k, x)
+    assert np.all(np.isfinite(out))
+    assert O.rel_l2(out, want) <= REL_L2_GATE
+
+
 def test_qmatmul_rejects_bad_shapes():
     qt = ops.QTensor.from_blocks(np.zeros(34 * 2, np.uint8), F.Q8_0, (1, 64))
     with pytest.raises(cw.CwError):
