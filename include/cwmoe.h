@@ -204,9 +204,11 @@ typedef struct cw_moe_desc {
  * set, picks whose expert has no slot read slot 0 and are counted in *missing (device u32,
  * may be NULL). ids_out / w_out (T x K, device, may be NULL) receive the routing.
  * The workspace (256-byte aligned) must be zero-filled once before its first use, for example
- * when it is allocated: its first CW_MOE_STATE_BYTES bytes hold the one-token layer's sync state,
- * which every call leaves at zero again, at the same offset for every T (so one workspace serves
- * calls of any size). Calls that overlap in time need distinct workspaces. */
+ * when it is allocated: its first CW_MOE_STATE_BYTES bytes hold the one-token layer's sync state
+ * (arrival counters, which every call leaves at zero again, and generation words, which every
+ * call moves on together), at the same offset for every T (so one workspace serves calls of any
+ * size); the caller never writes that region again. Calls that overlap in time need distinct
+ * workspaces. */
 #define CW_MOE_STATE_BYTES 8192
 size_t cw_moe_workspace_size(const cw_moe_desc *desc, int T);
 int cw_moe_layer(const cw_moe_desc *desc, const float *x, const float *logits, int T, float *out,
