@@ -207,8 +207,8 @@ typedef struct cw_moe_desc {
  * when it is allocated: its first CW_MOE_STATE_BYTES bytes hold the one-token layer's sync state
  * (arrival counters, which every call leaves at zero again, and generation words, which every
  * call moves on together), at the same offset for every T (so one workspace serves calls of any
- * size); the caller never writes that region again. Calls that overlap in time need distinct
- * workspaces. */
+ * size); zero-filling it again between calls is harmless, any other write there breaks the
+ * barrier. Calls that overlap in time need distinct workspaces. */
 #define CW_MOE_STATE_BYTES 8192
 size_t cw_moe_workspace_size(const cw_moe_desc *desc, int T);
 int cw_moe_layer(const cw_moe_desc *desc, const float *x, const float *logits, int T, float *out,
