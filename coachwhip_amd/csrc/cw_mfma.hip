@@ -1494,6 +1494,102 @@ size_t mfma_dense_workspace(int dtype, int64_t m, int64_t n, int64_t k) {
            (S > 1 ? al256((size_t)S * m * n * 4) + al256((size_t)dense_items(dtype, m, n) * 4) : 0);
 }
 
+// Dense Q4_K QMatMul for 2..16 rows of x, one launch after the pack: block b takes weight rows
+// 16b .. 16b+15 over the whole of k, its W waves a share of at most 2 super-blocks each (4 each
+// measured 13.3 against 12.9 us for config 2 at M = 16: half the waves in flight), with all
+// of a wave's loads (the rows' super-block headers and code bytes, and its activation fragments)
+// issued at once: the persistent GEMM's per-stage window round trips and split-K partial rows
+// cost ~12 us here for ~0.3 us of MFMA work. MFMA operands as in k_gmm: A = a token's 8 fp16
+// activations (lane = token l16, K-group grp), B = a row's 8 codes sc*q (lane = row l16, K-group
+// grp), and the minimum term as a second accumulator with codes -m; each super-block's sums are
+// folded in f32 with the lane's row's d and dmin (a lane's 4 outputs share its row), the waves'
+// partial tiles summed in LDS in wave order, then scaled by the token's activation scale.
+constexpr int SKINNY_SB = 2;  // super-blocks per wave
+template <int W>
+__global__ __launch_bounds__(64 * W) void k_skinny_q4k(const uint8_t *w, int64_t row_bytes, int n, int k, const uint16_t *x16,
+                                                       const float *xs, int m, float *y) {
+    __shared__ float part[W][16 * 16];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, grp = lane >> 4;
+    const int nsb = k / 256, s0 = wave * nsb / W, s1 = (wave + 1) * nsb / W;  // this wave's super-blocks
+    const uint8_t *wr = w + (int64_t)min(blockIdx.x * 16 + l16, n - 1) * row_bytes;
+    const uint16_t *xr = x16 + (int64_t)min(l16, m - 1) * k + 8 * grp;
+    // every load at once, from clamped super-blocks (those past s1 are not used)
+    uint4 head[SKINNY_SB];
+    uint2 qs[SKINNY_SB][4];
+    uint4 xf[SKINNY_SB][8];
+#pragma unroll
+    for (int j = 0; j < SKINNY_SB; j++) {
+        const int sb = min(s0 + j, nsb - 1);
+        const uint8_t *blk = wr + 144 * sb;
+        head[j] = *(const uint4 *)blk;  // d, dmin, the 12 scale bytes
+#pragma unroll
+        for (int c = 0; c < 4; c++) qs[j][c] = *(const uint2 *)(blk + 16 + 32 * c + 8 * grp);
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++) xf[j][kk] = *(const uint4 *)(xr + 256 * sb + 32 * kk);
+    }
+    // nothing moves across this point: the scheduler would otherwise sink later super-blocks'
+    // loads behind earlier MFMAs (to save registers), one memory round trip per super-block
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 fin = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < SKINNY_SB; j++) {
+        // no branch on the wave's super-block count: a branch here kept the compiler from issuing
+        // the later super-blocks' loads before the first one's MFMAs
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f}, accm = {0.f, 0.f, 0.f, 0.f};
+        const uint32_t sb12[3] = {head[j].y, head[j].z, head[j].w};
+        auto sbyte = [&](int i) { return (sb12[i >> 2] >> (8 * (i & 3))) & 0xFFu; };
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++) {
+            uint32_t sc, mn;  // the 6-bit scale and min of sub-block kk (get_scale_min_k4)
+            if (kk < 4) {
+                sc = sbyte(kk) & 63;
+                mn = sbyte(kk + 4) & 63;
+            } else {
+                sc = (sbyte(kk + 4) & 0xF) | ((sbyte(kk - 4) >> 6) << 4);
+                mn = (sbyte(kk + 4) >> 4) | ((sbyte(kk) >> 6) << 4);
+            }
+            const int sh = 4 * (kk & 1);
+            const uint2 q = qs[j][kk >> 1];
+            const uint4 codes = fma4(bytes_plus_1024((q.x >> sh) & 0x0F0F0F0Fu, (q.y >> sh) & 0x0F0F0F0Fu), splat_f16f((float)sc),
+                                     splat_f16f(-1024.0f * (float)sc));
+            const uint32_t mv = splat_f16f(-(float)mn);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(xf[j][kk]), as_f16x8(codes), acc, 0, 0, 0);
+            accm = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(xf[j][kk]), as_f16x8(make_uint4(mv, mv, mv, mv)), accm, 0, 0, 0);
+        }
+        const bool live = s0 + j < s1;
+        const float d = live ? h2f(head[j].x & 0xFFFF) : 0.f, dmin = live ? h2f(head[j].x >> 16) : 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) fin[i] += d * acc[i] + dmin * accm[i];
+    }
+    // lane: tokens 4*grp + i of weight row l16
+#pragma unroll
+    for (int i = 0; i < 4; i++) part[wave][(4 * grp + i) * 16 + l16] = fin[i];
+    __syncthreads();
+    for (int e = threadIdx.x; e < 256; e += 64 * W) {
+        const int t = e >> 4, r = blockIdx.x * 16 + (e & 15);
+        float v = 0.f;
+#pragma unroll
+        for (int q = 0; q < W; q++) v += part[q][e];
+        if (t < m && r < n) y[(int64_t)t * n + r] = v * xs[t];
+    }
+}
+
+// 2..16 rows of Q4_K x: the pack (fp16 activations and their scales), then k_skinny_q4k
+static int dense_skinny_q4k(const uint8_t *w, int64_t row_bytes, int n, int k, const float *x, int m, float *y, uint16_t *x16,
+                            float *xs, hipStream_t s) {
+    int rc;
+    if ((rc = pack_rows_f16(x, m, k, k, x16, xs, s, nullptr, false))) return rc;
+    const int nsb = k / 256, waves = (nsb + SKINNY_SB - 1) / SKINNY_SB;
+    const dim3 grid((unsigned)((n + 15) / 16));
+    if (waves <= 1) hipLaunchKernelGGL(k_skinny_q4k<1>, grid, dim3(64), 0, s, w, row_bytes, n, k, x16, xs, m, y);
+    else if (waves <= 2) hipLaunchKernelGGL(k_skinny_q4k<2>, grid, dim3(128), 0, s, w, row_bytes, n, k, x16, xs, m, y);
+    else if (waves <= 4) hipLaunchKernelGGL(k_skinny_q4k<4>, grid, dim3(256), 0, s, w, row_bytes, n, k, x16, xs, m, y);
+    else if (waves <= 8) hipLaunchKernelGGL(k_skinny_q4k<8>, grid, dim3(512), 0, s, w, row_bytes, n, k, x16, xs, m, y);
+    else if (waves <= 16) hipLaunchKernelGGL(k_skinny_q4k<16>, grid, dim3(1024), 0, s, w, row_bytes, n, k, x16, xs, m, y);
+    else return set_error(CW_ENOTSUP, "qmatmul: k %d above %d for the skinny Q4_K path", k, 16 * SKINNY_SB * 256);
+    return check_launch("k_skinny_q4k");
+}
+
 int mfma_dense(int dtype, const uint8_t *w, int64_t row_bytes, int n, int k, const float *x, int m, float *y, void *ws,
                size_t ws_bytes, hipStream_t s) {
     const size_t need = mfma_dense_workspace(dtype, m, n, k);
@@ -1503,6 +1599,7 @@ int mfma_dense(int dtype, const uint8_t *w, int64_t row_bytes, int n, int k, con
     uint8_t *p = (uint8_t *)ws;
     uint16_t *x16 = (uint16_t *)p; p += al256((size_t)m * k * 2);
     float *xs = (float *)p; p += al256((size_t)m * 4);
+    if (dtype == CW_Q4_K && m <= 16) return dense_skinny_q4k(w, row_bytes, n, k, x, m, y, x16, xs, s);
     MfTile *tiles = (MfTile *)p; p += al256((size_t)(m + MF_MT - 1) / MF_MT * sizeof(MfTile));
     int *n_tiles = (int *)p; p += al256(4);
     float *part = nullptr;
