@@ -1508,24 +1508,38 @@ constexpr int SKINNY_SB = 2;  // super-blocks per wave
 template <int W>
 __global__ __launch_bounds__(64 * W) void k_skinny_q4k(const uint8_t *w, int64_t row_bytes, int n, int k, const uint16_t *x16,
                                                        const float *xs, int m, float *y) {
+    // a wave's 16 rows x SKINNY_SB super-blocks, copied as 16-byte chunks (row r's bytes at r * RB)
+    constexpr int RB = SKINNY_SB * 144, NCH = 16 * RB / 16, NI = (NCH + 63) / 64;
+    __shared__ __align__(16) uint8_t wl[W][NI * 1024];
     __shared__ float part[W][16 * 16];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, grp = lane >> 4;
     const int nsb = k / 256, s0 = wave * nsb / W, s1 = (wave + 1) * nsb / W;  // this wave's super-blocks
-    const uint8_t *wr = w + (int64_t)min(blockIdx.x * 16 + l16, n - 1) * row_bytes;
     const uint16_t *xr = x16 + (int64_t)min(l16, m - 1) * k + 8 * grp;
-    // every load at once, from clamped super-blocks (those past s1 are not used)
+    // every load at once, from clamped rows and super-blocks (those past s1 are not used): the
+    // weight bytes as whole 16-byte chunks of each row's run of super-blocks straight into LDS
+    // (per-lane 8-byte pieces of 16 rows measured slower), then the activation fragments
+#pragma unroll
+    for (int t = 0; t < NI; t++) {
+        const int c = min(64 * t + lane, NCH - 1), r = c / (RB / 16), piece = c - r * (RB / 16), j = piece / 9;
+        dma16<true>(w + (int64_t)min(blockIdx.x * 16 + r, n - 1) * row_bytes + 144 * min(s0 + j, nsb - 1) + 16 * (piece - 9 * j),
+                    &wl[wave][1024 * t]);
+    }
     uint4 head[SKINNY_SB];
     uint2 qs[SKINNY_SB][4];
     uint4 xf[SKINNY_SB][8];
 #pragma unroll
     for (int j = 0; j < SKINNY_SB; j++) {
         const int sb = min(s0 + j, nsb - 1);
-        const uint8_t *blk = wr + 144 * sb;
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++) xf[j][kk] = *(const uint4 *)(xr + 256 * sb + 32 * kk);
+    }
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(8 * SKINNY_SB) : "memory");  // the chunks have landed
+#pragma unroll
+    for (int j = 0; j < SKINNY_SB; j++) {
+        const uint8_t *blk = &wl[wave][l16 * RB + 144 * j];
         head[j] = *(const uint4 *)blk;  // d, dmin, the 12 scale bytes
 #pragma unroll
         for (int c = 0; c < 4; c++) qs[j][c] = *(const uint2 *)(blk + 16 + 32 * c + 8 * grp);
-#pragma unroll
-        for (int kk = 0; kk < 8; kk++) xf[j][kk] = *(const uint4 *)(xr + 256 * sb + 32 * kk);
     }
     // nothing moves across this point: the scheduler would otherwise sink later super-blocks'
     // loads behind earlier MFMAs (to save registers), one memory round trip per super-block
