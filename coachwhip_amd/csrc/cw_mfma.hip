@@ -890,13 +890,9 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
             // while its MFMAs run). The first step of the second half-stage reads its activations
             // after the barrier that publishes them. A scheduling fence closes each step (without
             // it the compiler interleaves all eight steps and runs out of registers).
-            // FULL: the stage has all KST steps (always for the super-block formats), so that no
-            // step's work sits behind a runtime test of the stage length (whose branches made the
-            // compiler copy the pipelined fragment registers at every join)
-            auto ksteps = [&](auto mbs_c, auto full_c) __attribute__((always_inline)) {
+            auto ksteps = [&](auto mbs_c) __attribute__((always_inline)) {
                 constexpr int MBS = decltype(mbs_c)::value;
-                constexpr bool FULL = decltype(full_c)::value;
-                const int nke = FULL ? KST : nk;
+                const int nke = MF::SBK == 32 ? nk : KST;  // super-block formats: every stage is whole
                 typename MF::Raw rw[2][NM][NB];
                 typename MF::Look lk[2][NM][NB];
                 f16x8 av[2][MBS];
@@ -1001,17 +997,13 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
                     __builtin_amdgcn_sched_barrier(0);
                 }
             };
-            auto by_mbs = [&](auto full_c) __attribute__((always_inline)) {
-                switch (mbs) {
-                case 1: ksteps(Ic<1>{}, full_c); break;
-                case 2: ksteps(Ic<2>{}, full_c); break;
-                case 3: ksteps(Ic<3>{}, full_c); break;
-                case 4: ksteps(Ic<4>{}, full_c); break;
-                default: ksteps(Ic<5>{}, full_c); break;
-                }
-            };
-            if (MF::SBK != 32 || nk == KST) by_mbs(std::true_type{});
-            else if constexpr (MF::SBK == 32) by_mbs(std::false_type{});
+            switch (mbs) {
+            case 1: ksteps(Ic<1>{}); break;
+            case 2: ksteps(Ic<2>{}); break;
+            case 3: ksteps(Ic<3>{}); break;
+            case 4: ksteps(Ic<4>{}); break;
+            default: ksteps(Ic<5>{}); break;
+            }
         }
 
         // epilogue: lane holds picks 16*mb + 4*grp + i (i < 4) of weight row n (block q)
