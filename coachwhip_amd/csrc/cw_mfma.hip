@@ -1613,7 +1613,8 @@ int mfma_dense(int dtype, const uint8_t *w, int64_t row_bytes, int n, int k, con
     uint8_t *p = (uint8_t *)ws;
     uint16_t *x16 = (uint16_t *)p; p += al256((size_t)m * k * 2);
     float *xs = (float *)p; p += al256((size_t)m * 4);
-    if (dtype == CW_Q4_K && m <= 16) return dense_skinny_q4k(w, row_bytes, n, k, x, m, y, x16, xs, s);
+    // (its rows are copied as 16-byte chunks: a matrix off 16-byte alignment takes the GEMM below)
+    if (dtype == CW_Q4_K && m <= 16 && ((uintptr_t)w & 15) == 0) return dense_skinny_q4k(w, row_bytes, n, k, x, m, y, x16, xs, s);
     MfTile *tiles = (MfTile *)p; p += al256((size_t)(m + MF_MT - 1) / MF_MT * sizeof(MfTile));
     int *n_tiles = (int *)p; p += al256(4);
     float *part = nullptr;

@@ -25,6 +25,10 @@ def dev(a):
     return ops.to_device(a)
 
 
+def dev_u8(a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint8)).to("cuda")
+
+
 def host(t):
     return t.detach().cpu().numpy()
 
@@ -203,6 +207,25 @@ def test_grouped_gemm_mxfp4_exponents_across_stages():
     want = O.qmatmul_f64(F.MXFP4, raw, n, k, x)
     assert np.all(np.isfinite(out))
     assert O.rel_l2(out, want) <= REL_L2_GATE
+
+
+@pytest.mark.parametrize("off", [0, 4])
+def test_qmatmul_q4k_few_rows_any_alignment(off, monkeypatch):
+    """Q4_K at 2..16 rows of x on the MFMA path: a 16-byte aligned matrix takes the one-launch
+    skinny GEMM (rows copied as 16-byte chunks), a matrix 4 bytes off alignment (a view into a
+    larger buffer) the persistent GEMM; both against the oracle at the fp16-activation bar."""
+    monkeypatch.setenv("CWMOE_MM_MIN_ROWS", "1")
+    rng = np.random.default_rng(90 + off)
+    n, k = 130, 1536
+    raw = synth.random_blocks(F.Q4_K, n * k, rng)
+    buf = torch.zeros(raw.size + 16, dtype=torch.uint8, device="cuda")
+    buf[off:off + raw.size] = dev_u8(raw)
+    w = buf[off:off + raw.size]
+    assert w.data_ptr() % 16 == off
+    for m in (2, 11, 16):
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        y = host(ops.QMatMul(ops.QTensor(w, F.Q4_K, (n, k))).forward(dev(x)))
+        assert O.rel_l2(y, O.qmatmul_f64(F.Q4_K, raw, n, k, x)) <= REL_L2_GATE
 
 
 def test_qmatmul_rejects_bad_shapes():
