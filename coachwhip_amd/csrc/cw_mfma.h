@@ -46,6 +46,9 @@ struct MfArgs {
     int64_t split_stride;
     int *split_cnt;
     float *y;
+    // MXFP4 on the scaled MFMA: activations packed by pack_rows_fp6 (ap_row bytes per row)
+    const uint8_t *ap;
+    int64_t ap_row;
 };
 
 // Work a pack launch also does for the dense matmul that follows it: the tile list of m rows, and
@@ -80,5 +83,15 @@ int mfma_dense(int dtype, const uint8_t *w, int64_t row_bytes, int n, int k, con
 // pick with slots[t*K+j] >= n_slots contributes NaN (it has no row)
 int combine_picks(const float *dn, const float *w, const float *bias, const uint32_t *ids, const uint32_t *slots, int n_slots,
                   int T, int K, int H, float *out, hipStream_t s);
+
+// MXFP4 grouped GEMMs on the block-scaled MFMA (cw_mxfp4.hip): the weights as stored (E2M1 codes
+// and E8M0 block scales), the activations as three FP6 terms with E8M0 scales per 32 values.
+bool mxfp4_scaled();
+// a matrix of k weights per row runs on the scaled MFMA (MXFP4, at least two 128-wide K steps)
+inline bool mxfp4_scaled_for(int dtype, int64_t k) { return dtype == CW_MXFP4 && k > 128 && k % 32 == 0 && mxfp4_scaled(); }
+size_t fp6_rows_bytes(int64_t rows, int64_t k);
+int pack_rows_fp6(const float *x, int rows, int k, int ldx, uint8_t *out, hipStream_t s);
+int mxfp4_gateup(const MfArgs &a, int tiles_max, hipStream_t s);
+int mxfp4_down(const MfArgs &a, int tiles_max, hipStream_t s);
 
 }  // namespace cw

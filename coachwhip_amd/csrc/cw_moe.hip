@@ -185,9 +185,11 @@ static MoeLayout layout(const cw_moe_desc *d, int T) {
         L.pile_tok = off; off = align256(off + TK * 4);
         L.tiles = off; off = align256(off + (size_t)max_tiles((int)TK, n_slots) * sizeof(MfTile));
         L.n_tiles = off; off = align256(off + 4);
-        L.x16 = off; off = align256(off + (size_t)T * d->hidden * 2);
+        // fp16 rows, or for MXFP4 on the scaled MFMA the rows packed as FP6 terms
+        const bool gx = mxfp4_scaled_for(d->dtype[0], d->hidden), dx = mxfp4_scaled_for(d->dtype[2], P);
+        L.x16 = off; off = align256(off + (gx ? fp6_rows_bytes(T, d->hidden) : (size_t)T * d->hidden * 2));
         L.xscale = off; off = align256(off + (size_t)T * 4);
-        L.h16 = off; off = align256(off + TK * (size_t)P * 2);
+        L.h16 = off; off = align256(off + (dx ? fp6_rows_bytes((int64_t)TK, P) : TK * (size_t)P * 2));
         L.hscale = off; off = align256(off + TK * 4);
         L.dn = off; off = align256(off + TK * (size_t)d->hidden * 4);
     }
@@ -211,7 +213,11 @@ static int moe_grouped(const cw_moe_desc *d, const MoeArgs &a, const MoeLayout &
     if ((rc = mfma_piles(slots, TK, K, a.n_slots, pile_pick, pile_tok, tiles, n_tiles, s))) return rc;
     uint16_t *x16 = (uint16_t *)(base + L.x16), *h16 = (uint16_t *)(base + L.h16);
     float *xscale = (float *)(base + L.xscale), *hscale = (float *)(base + L.hscale);
-    if ((rc = pack_rows_f16(a.x, T, a.H, a.H, x16, xscale, s, nullptr, mfma_k_permuted(d->dtype[0])))) return rc;
+    // MXFP4 matrices run on the block-scaled MFMA (activations as FP6 terms), the others on fp16 MFMA
+    const bool gx = mxfp4_scaled_for(d->dtype[0], a.H), dx = mxfp4_scaled_for(d->dtype[2], P);
+    if (gx) rc = pack_rows_fp6(a.x, T, a.H, a.H, (uint8_t *)x16, s);
+    else rc = pack_rows_f16(a.x, T, a.H, a.H, x16, xscale, s, nullptr, mfma_k_permuted(d->dtype[0]));
+    if (rc) return rc;
     if (P > a.I && (rc = fill_zero(a.h, (int64_t)TK * P, s))) return rc;
     const int tmax = max_tiles(TK, a.n_slots);
 
@@ -239,8 +245,17 @@ static int moe_grouped(const cw_moe_desc *d, const MoeArgs &a, const MoeLayout &
     g.ids = a.ids;
     g.h = a.h;
     g.ldh = P;
-    if ((rc = mfma_gateup(d->dtype[0], g, tmax, s))) return rc;
-    if ((rc = pack_rows_f16(a.h, TK, P, P, h16, hscale, s, nullptr, mfma_k_permuted(d->dtype[2])))) return rc;
+    if (gx) {
+        g.ap = (const uint8_t *)x16;
+        g.ap_row = (int64_t)fp6_rows_bytes(1, a.H);
+        rc = mxfp4_gateup(g, tmax, s);
+    } else {
+        rc = mfma_gateup(d->dtype[0], g, tmax, s);
+    }
+    if (rc) return rc;
+    if (dx) rc = pack_rows_fp6(a.h, TK, P, P, (uint8_t *)h16, s);
+    else rc = pack_rows_f16(a.h, TK, P, P, h16, hscale, s, nullptr, mfma_k_permuted(d->dtype[2]));
+    if (rc) return rc;
 
     MfArgs dn = {};
     dn.w0 = a.wd;
@@ -257,7 +272,14 @@ static int moe_grouped(const cw_moe_desc *d, const MoeArgs &a, const MoeLayout &
     dn.pile_pick = pile_pick;
     dn.K = K;
     dn.dn = (float *)(base + L.dn);
-    if ((rc = mfma_down(d->dtype[2], dn, tmax, s))) return rc;
+    if (dx) {
+        dn.ap = (const uint8_t *)h16;
+        dn.ap_row = (int64_t)fp6_rows_bytes(1, P);
+        rc = mxfp4_down(dn, tmax, s);
+    } else {
+        rc = mfma_down(d->dtype[2], dn, tmax, s);
+    }
+    if (rc) return rc;
     return combine_picks(dn.dn, a.w, a.bd, a.ids, slots, a.n_slots, T, K, a.H, a.out, s);
 }
 
@@ -363,7 +385,7 @@ __global__ void k_nan_rows(const uint32_t *ids, int n_picks, uint32_t n_slots, i
 struct GroupedLayout {
     size_t pile_pick, pile_tok, tiles, n_tiles, x16, xscale, total;
 };
-static GroupedLayout grouped_layout(int64_t k, int64_t n_slots, int x_per_pick, int K, int T) {
+static GroupedLayout grouped_layout(int dtype, int64_t k, int64_t n_slots, int x_per_pick, int K, int T) {
     const size_t TK = (size_t)T * K, rows = x_per_pick ? TK : (size_t)T;
     GroupedLayout L;
     size_t off = 0;
@@ -371,7 +393,8 @@ static GroupedLayout grouped_layout(int64_t k, int64_t n_slots, int x_per_pick, 
     L.pile_tok = off; off = align256(off + TK * 4);
     L.tiles = off; off = align256(off + (size_t)max_tiles((int)TK, (int)n_slots) * sizeof(MfTile));
     L.n_tiles = off; off = align256(off + 4);
-    L.x16 = off; off = align256(off + rows * (size_t)k * 2);
+    const bool gx = mxfp4_scaled_for(dtype, k);  // rows packed as FP6 terms for the scaled MFMA
+    L.x16 = off; off = align256(off + (gx ? fp6_rows_bytes((int64_t)rows, k) : rows * (size_t)k * 2));
     L.xscale = off; off = align256(off + rows * 4);
     L.total = off;
     return L;
@@ -496,7 +519,7 @@ int cw_shared_expert(const cw_shared_desc *d, const float *x, int T, float *out,
 size_t cw_matmul_id_grouped_workspace_size(int dtype, int64_t n, int64_t k, int64_t n_slots, int64_t slot_stride,
                                            int x_rows_per_expert, int K, int T) {
     if (grouped_check(dtype, n, k, n_slots, slot_stride, K, T) != CW_OK) return 0;
-    return grouped_layout(k, n_slots, x_rows_per_expert ? 1 : 0, K, T).total;
+    return grouped_layout(dtype, k, n_slots, x_rows_per_expert ? 1 : 0, K, T).total;
 }
 
 int cw_matmul_id_grouped(int dtype, int64_t n, int64_t k, int64_t n_slots, int64_t slot_stride, const void *bank,
@@ -506,9 +529,12 @@ int cw_matmul_id_grouped(int dtype, int64_t n, int64_t k, int64_t n_slots, int64
     if (rc) return rc;
     if (T == 0) return CW_OK;
     CW_REQUIRE(bank && x && ids && out, "matmul_id_grouped: null pointer");
-    CW_REQUIRE(((uintptr_t)x & 15u) == 0 && k % 4 == 0, "matmul_id_grouped: x must be 16-byte aligned rows of whole float4s");
+    // the activation pack reads whole float4s: an x off 16-byte alignment is a capability probe's
+    // "no" (the caller takes cw_matvec_id, which reads any x), not an argument error
+    if (((uintptr_t)x & 15u) != 0 || k % 4 != 0)
+        return set_error(CW_ENOTSUP, "matmul_id_grouped: x is not 16-byte aligned rows of whole float4s");
     const int xpp = x_rows_per_expert ? 1 : 0;
-    const GroupedLayout L = grouped_layout(k, n_slots, xpp, K, T);
+    const GroupedLayout L = grouped_layout(dtype, k, n_slots, xpp, K, T);
     CW_REQUIRE(ws && ws_bytes >= L.total, "matmul_id_grouped: workspace of %zu bytes, %zu needed", ws_bytes, L.total);
     hipStream_t s = (hipStream_t)stream;
     uint8_t *base = (uint8_t *)ws;
@@ -518,7 +544,10 @@ int cw_matmul_id_grouped(int dtype, int64_t n, int64_t k, int64_t n_slots, int64
     uint16_t *x16 = (uint16_t *)(base + L.x16);
     float *xscale = (float *)(base + L.xscale);
     if ((rc = mfma_piles(ids, TK, K, (int)n_slots, pile_pick, pile_tok, tiles, n_tiles, s))) return rc;
-    if ((rc = pack_rows_f16(x, xpp ? TK : T, (int)k, (int)k, x16, xscale, s, nullptr, mfma_k_permuted(dtype)))) return rc;
+    const bool gx = mxfp4_scaled_for(dtype, k);
+    if (gx) rc = pack_rows_fp6(x, xpp ? TK : T, (int)k, (int)k, (uint8_t *)x16, s);
+    else rc = pack_rows_f16(x, xpp ? TK : T, (int)k, (int)k, x16, xscale, s, nullptr, mfma_k_permuted(dtype));
+    if (rc) return rc;
     MfArgs a = {};
     a.w0 = (const uint8_t *)bank;
     a.s0 = slot_stride;
@@ -534,7 +563,14 @@ int cw_matmul_id_grouped(int dtype, int64_t n, int64_t k, int64_t n_slots, int64
     a.pile_pick = pile_pick;
     a.K = K;
     a.dn = out;
-    if ((rc = mfma_down(dtype, a, max_tiles(TK, (int)n_slots), s))) return rc;
+    if (gx) {
+        a.ap = (const uint8_t *)x16;
+        a.ap_row = (int64_t)fp6_rows_bytes(1, k);
+        rc = mxfp4_down(a, max_tiles(TK, (int)n_slots), s);
+    } else {
+        rc = mfma_down(dtype, a, max_tiles(TK, (int)n_slots), s);
+    }
+    if (rc) return rc;
     hipLaunchKernelGGL(k_nan_rows, flat_grid(TK), dim3(256), 0, s, ids, TK, (uint32_t)n_slots, (int)n, out);
     return check_launch("k_nan_rows");
 }

@@ -1,0 +1,477 @@
+// MXFP4 grouped GEMMs (the MoE layer's prefill, cw_matmul_id_grouped) on gfx950's block-scaled
+// MFMA (v_mfma_scale_f32_16x16x128_f8f6f4).
+//
+// The weights go to the matrix cores as GGUF stores them: a lane's A operand is one MXFP4 block,
+// its 16 code bytes unchanged (E2M1 codes, low nibble first) with the block's E8M0 byte as the
+// lane's scale. The MFMA's A operand takes K index 32g + e from nibble e of lane group g, and a
+// block's byte i holds weight i (low nibble) and weight i + 16 (high nibble): nibble e is weight
+// (e >> 1) + 16 (e & 1) of the block. The activations are arranged to meet that order.
+//
+// Activations are f32 rows packed once per call (k_pack_fp6x3) into three FP6 (E2M3) terms per
+// value: term t codes the residual the earlier terms left, each 32-value block with its own E8M0
+// scale per term. The B operand of a lane is 32 FP6 codes (6 bits each, code e at bits 6e..6e+5
+// of six dwords) with the lane's scale, and FP4 x FP6 issues at the FP4 rate, so the three terms
+// cost 48 cycles per 16x16x128 product where fp16 MFMA needs 64, and nothing is decoded on the
+// VALU. A term's scale puts the largest magnitude left in its block in (3.75, 7.5], where E2M3
+// steps are at most 0.5, so what it leaves is at most 1/15 of what it started from: after three
+// terms at most 1/3375 (2^-11.7) of the block's largest value (the fp16 path rounds each value to
+// 2^-11 of itself).
+//
+// Packed activations: per row, 304 bytes per 128-wide K step (4 blocks of 32 values, the last
+// step zero-filled past the row): term t of block g is 24 bytes of codes, dwords 0..3 at 96 t +
+// 16 g and dwords 4, 5 at 96 t + 64 + 8 g, and the block's three scale bytes (term t at bits 8t)
+// are the dword at 288 + 4 g. A lane's B operand is then one 16-byte and one 8-byte aligned load
+// that land in its six operand registers, and the four lanes of a token read consecutive bytes.
+#include <stdlib.h>
+
+#include <atomic>
+#include <type_traits>
+
+#include "cw_common.h"
+#include "cw_mfma.h"
+
+namespace cw {
+
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+// ------------------------------------------------------------------------------ the pack
+
+// FP6 E2M3 code of y, |y| <= 7.5, rounded to the nearest value (ties to even), and the value it
+// codes. E2M3: sign, 2 exponent bits (bias 1), 3 mantissa bits; steps of 1/8 below 2, 1/4 below
+// 4, 1/2 up to 7.5. Adding and subtracting 1.5 * 2^(s + 23) rounds to a multiple of 2^s in the
+// f32 addition's own round-to-nearest-even.
+__device__ __forceinline__ uint32_t e2m3_code(float y, float &q) {
+    const float a = fabsf(y);
+    const int e = (int)(__float_as_uint(a) >> 23) - 127;  // floor(log2 a) for normal a
+    const int s = max(e - 3, -3);
+    const float c = __uint_as_float(((uint32_t)(s + 150) << 23) | 0x400000u);
+    float r = a + c;
+    asm volatile("" : "+v"(r));  // keep (a + c) - c as two roundings
+    r = r - c;
+    const uint32_t rb = __float_as_uint(r);
+    const uint32_t code = r < 1.0f ? (uint32_t)(r * 8.0f) : ((((rb >> 23) - 126u) << 3) | ((rb >> 20) & 7u));
+    q = copysignf(r, y);
+    return code | ((__float_as_uint(y) >> 26) & 0x20u);
+}
+
+// One thread per (row, 32-value block): the block's values in registers, three terms, each
+// scaled by the power of two that puts the block's largest remaining magnitude in (3.75, 7.5].
+__global__ __launch_bounds__(256) void k_pack_fp6x3(const float *x, int rows, int k, int ldx, uint8_t *out) {
+    const int nb = k / 32, nbp = (nb + 3) & ~3;  // blocks, and block records per row (whole steps)
+    const int64_t n = (int64_t)rows * nbp;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        const int64_t row = i / nbp;
+        const int j = (int)(i - row * nbp);
+        uint8_t *dst = out + row * (int64_t)(nbp / 4) * 304 + (j >> 2) * 304;
+        const int g = j & 3;
+        if (j >= nb) {  // past the row: zero codes and scale bytes
+#pragma unroll
+            for (int t = 0; t < 3; t++) {
+                *(uint4 *)(dst + 96 * t + 16 * g) = make_uint4(0u, 0u, 0u, 0u);
+                *(uint2 *)(dst + 96 * t + 64 + 8 * g) = make_uint2(0u, 0u);
+            }
+            *(uint32_t *)(dst + 288 + 4 * g) = 0u;
+            continue;
+        }
+        const float4 *src = (const float4 *)(x + row * ldx + 32 * j);
+        float v[32];
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const float4 f = src[c];
+            v[4 * c] = f.x;
+            v[4 * c + 1] = f.y;
+            v[4 * c + 2] = f.z;
+            v[4 * c + 3] = f.w;
+        }
+        uint32_t w[3][6];
+        uint32_t sc = 0;
+#pragma unroll
+        for (int t = 0; t < 3; t++) {
+            float m = 0.f;
+#pragma unroll
+            for (int e = 0; e < 32; e++) m = fmaxf(m, fabsf(v[e]));
+            int ex = 0;
+            if (m > 0.f) frexpf(m, &ex);  // m = f * 2^ex, f in [0.5, 1)
+            int kk = m > 0.f ? ex - 3 : -127;
+            if (m > ldexpf(7.5f, kk)) kk++;
+            kk = min(max(kk, -127), 127);
+            sc |= (uint32_t)(kk + 127) << (8 * t);
+            const float inv = ldexpf(1.0f, -kk), scl = ldexpf(1.0f, kk);
+#pragma unroll
+            for (int d = 0; d < 6; d++) w[t][d] = 0;
+#pragma unroll
+            for (int e = 0; e < 32; e++) {
+                const int src_i = (e >> 1) + 16 * (e & 1);  // B element e meets nibble e of the block
+                float q;
+                const float y = v[src_i] * inv;
+                const uint32_t code = e2m3_code(y, q);
+                v[src_i] = (y - q) * scl;
+                const int bit = 6 * e;
+                w[t][bit >> 5] |= code << (bit & 31);
+                if ((bit & 31) > 26) w[t][(bit >> 5) + 1] |= code >> (32 - (bit & 31));
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 3; t++) {
+            *(uint4 *)(dst + 96 * t + 16 * g) = make_uint4(w[t][0], w[t][1], w[t][2], w[t][3]);
+            *(uint2 *)(dst + 96 * t + 64 + 8 * g) = make_uint2(w[t][4], w[t][5]);
+        }
+        *(uint32_t *)(dst + 288 + 4 * g) = sc;
+    }
+}
+
+// ------------------------------------------------------------------------------ the GEMM
+
+// 16 bytes from global memory to LDS, lane l writing lds_base + 16 l, and a stager's activation
+// operands of one step into registers (7 loads; p16/p8/p4 its K-group's bytes of term 0: term t's
+// codes, 16 bytes at 96 t and 8 bytes at 96 t + 64, the scale dword at 288). Issued as inline asm:
+// the kernel counts its vector memory operations itself (a running count, and the count after
+// each batch it will need) and waits for exactly the ones it needs, which the compiler, not seeing
+// loads it did not issue, could not do. lds_base is an LDS address, the same for the whole wave.
+__device__ __forceinline__ void gx_dma16(const void *g, uint32_t lds_base) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane(lds_base);
+    uint32_t keep;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(keep) : "v"(g), "s"(m) : "memory");
+}
+__device__ __forceinline__ void gx_ldx(u32x4 (&lo)[3], u32x2 (&hi)[3], uint32_t &sc, const uint8_t *p16, const uint8_t *p8,
+                                       const uint8_t *p4) {
+    asm volatile(
+        "global_load_dwordx4 %0, %7, off\n\tglobal_load_dwordx4 %1, %7, off offset:96\n\tglobal_load_dwordx4 %2, %7, off offset:192\n\t"
+        "global_load_dwordx2 %3, %8, off offset:64\n\tglobal_load_dwordx2 %4, %8, off offset:160\n\tglobal_load_dwordx2 %5, %8, off offset:256\n\t"
+        "global_load_dword %6, %9, off offset:288"
+        : "=&v"(lo[0]), "=&v"(lo[1]), "=&v"(lo[2]), "=&v"(hi[0]), "=&v"(hi[1]), "=&v"(hi[2]), "=&v"(sc)
+        : "v"(p16), "v"(p8), "v"(p4)
+        : "memory");
+}
+// s_waitcnt vmcnt(n) for a run-time n (the instruction takes an immediate; above 63 it waits for
+// more than asked, never less)
+__device__ __forceinline__ void gx_wait_vm(int n) {
+#define CW_VM(N) case N: asm volatile("s_waitcnt vmcnt(" #N ")" ::: "memory"); break;
+#define CW_VM8(B) CW_VM(B) CW_VM(B + 1) CW_VM(B + 2) CW_VM(B + 3) CW_VM(B + 4) CW_VM(B + 5) CW_VM(B + 6) CW_VM(B + 7)
+    switch (n < 0 ? 0 : n > 63 ? 63 : n) {
+        CW_VM8(0) CW_VM8(8) CW_VM8(16) CW_VM8(24) CW_VM8(32) CW_VM8(40) CW_VM8(48) CW_VM8(56)
+    }
+#undef CW_VM8
+#undef CW_VM
+}
+
+// A block has 8 waves: 4 row groups of RW weight rows (of each matrix: gate and up for MODE 0) by
+// 2 halves of the tile's 16-token blocks. A stage is one 128-wide K step. The weight bytes of a
+// stage go to LDS by direct loads, two stages ahead (three buffers), per row a window of the 6
+// 16-byte pieces holding its 4 blocks (68 bytes at any offset); the activation operands of a stage
+// (token block t: per lane three 16 + 8 byte code runs and a scale dword) are loaded into
+// registers by the first waves, one stage ahead, and stored to LDS, so that the direct loads carry
+// the weights alone. A wave waits for exactly the loads it needs next, then one barrier per stage
+// publishes them.
+template <int MODE>
+struct GxShape {
+    static constexpr int NW = 8, NT = 64 * NW;
+    static constexpr int NM = MODE == 0 ? 2 : 1;      // matrices (gate, up) per block
+    static constexpr int RW = MODE == 0 ? 48 : 96;    // rows per row group per matrix
+    static constexpr int FR = RW / 16;                // fragments per wave per matrix
+    static constexpr int NF = NM * FR;                // fragments per wave
+    static constexpr int RPB = 4 * RW;                // rows per matrix per block
+    static constexpr int PCS = 6;                     // pieces per row window
+    static constexpr int WROWS = NM * RPB;
+    static constexpr int W_INST = WROWS * PCS / 64;   // window loads per stage (wave instructions)
+    static constexpr int NJW = (W_INST + NW - 1) / NW;
+    static constexpr int W_BYTES = WROWS * PCS * 16;
+    static constexpr int WDEPTH = 3;
+    static constexpr int TB_BYTES = 3 * 1536 + 256;   // a token block's operands: per term 1 KB + 512 B, scales
+    static constexpr int A_BYTES = MF_MB * TB_BYTES;
+    static constexpr size_t LDS = WDEPTH * (size_t)W_BYTES + 2 * (size_t)A_BYTES;
+    static_assert(RPB * PCS % 64 == 0, "a window load lies in one matrix");
+    static_assert(LDS <= 160 * 1024, "the scaled GEMM's LDS does not fit");
+};
+
+// One work item (M-tile x N-block) of one wave, NTB of the tile's token blocks from tb0.
+template <int MODE, int NTB>
+__device__ __forceinline__ void gx_item(const MfArgs &a, const MfTile &tile, int nb, int mbs, int tb0, int wave, int lane,
+                                        uint8_t *smem, uint32_t lds0) {
+    using S = GxShape<MODE>;
+    const int grp = lane >> 4, l16 = lane & 15, rg = wave & 3;
+    const int nblk = a.k / 32, n_st = (nblk + 3) / 4;
+    uint8_t *const Wb = smem;
+    uint8_t *const Ab = smem + S::WDEPTH * S::W_BYTES;
+
+    const uint8_t *wb0 = a.w0 + (int64_t)tile.slot * a.s0;
+    const uint8_t *wb1 = S::NM > 1 ? a.w1 + (int64_t)tile.slot * a.s1 : wb0;
+    // window loads: wave instruction wi = wave + 8 j covers pieces 64 wi .. 64 wi + 63
+    uint32_t wo[S::NJW], wp[S::NJW];
+#pragma unroll
+    for (int j = 0; j < S::NJW; j++) {
+        const int pi = 64 * min(wave + 8 * j, S::W_INST - 1) + lane, r = pi / S::PCS;
+        wp[j] = (uint32_t)(pi - r * S::PCS);
+        const int n = nb * S::RPB + r % S::RPB;
+        wo[j] = (uint32_t)(n < a.n ? n : 0) * (uint32_t)a.row_bytes;
+    }
+    // activation staging: wave w < mbs stages token block w (lane = its K-group and token)
+    const bool stager = wave < mbs;
+    const uint8_t *xrow = a.ap;
+    if (stager) {
+        const int r = min(16 * wave + l16, tile.m - 1), pos = tile.pos0 + r;
+        xrow = a.ap + (int64_t)(a.rows ? a.rows[pos] : pos) * a.ap_row;
+    }
+    // this lane's rows' offsets from 16-byte alignment
+    uint32_t lmis[S::NF];
+#pragma unroll
+    for (int f = 0; f < S::NF; f++) {
+        const int mm = f / S::FR, n = nb * S::RPB + rg * S::RW + 16 * (f % S::FR) + l16;
+        lmis[f] = ((uint32_t)(uintptr_t)(mm ? wb1 : wb0) + (uint32_t)(n < a.n ? n : 0) * (uint32_t)a.row_bytes) & 15u;
+    }
+
+    int issued = 0;                    // this wave's loads in the item (it starts drained)
+    int m_w0 = 0, m_w1 = 0, m_w2 = 0;  // the count after each window buffer's loads (named, not
+                                       // indexed: an indexed array would live in scratch memory)
+    int m_x = 0;                       // ... after the activation loads
+    auto issue_w = [&](int st) __attribute__((always_inline)) {
+        const int buf = st % S::WDEPTH;
+        const uint32_t Wd = lds0 + buf * S::W_BYTES;
+        const uint32_t seg = 17u * (uint32_t)min(4, nblk - 4 * st);  // bytes of a row in this stage
+#pragma unroll
+        for (int j = 0; j < S::NJW; j++) {
+            const int wi = wave + 8 * j;
+            if (wi < S::W_INST) {
+                const uint8_t *mb = S::NM > 1 && wi >= S::W_INST / 2 ? wb1 : wb0;
+                const uint32_t o = wo[j] + 68u * (uint32_t)st;
+                const uint32_t mis = ((uint32_t)(uintptr_t)mb + o) & 15u;
+                const uint32_t pc = min(wp[j], (mis + seg - 1) >> 4);
+                const uint8_t *al = (const uint8_t *)(((uintptr_t)mb + o) & ~(uintptr_t)15);
+                gx_dma16(al + 16 * pc, Wd + wi * 1024);
+                issued++;
+            }
+        }
+        m_w0 = buf == 0 ? issued : m_w0;
+        m_w1 = buf == 1 ? issued : m_w1;
+        m_w2 = buf == 2 ? issued : m_w2;
+    };
+    u32x4 xl[3];
+    u32x2 xh[3];
+    uint32_t xs = 0;
+    auto load_x = [&](int st) __attribute__((always_inline)) {
+        if (stager) {
+            const uint8_t *p = xrow + 304 * st;
+            gx_ldx(xl, xh, xs, p + 16 * grp, p + 8 * grp, p + 4 * grp);
+            issued += 7;
+            m_x = issued;
+        }
+    };
+    auto store_x = [&](int buf) __attribute__((always_inline)) {
+        if (stager) {
+            gx_wait_vm(issued - m_x);
+            asm volatile("" : "+v"(xl[0]), "+v"(xl[1]), "+v"(xl[2]), "+v"(xh[0]), "+v"(xh[1]), "+v"(xh[2]), "+v"(xs));
+            uint8_t *d = Ab + buf * S::A_BYTES + wave * S::TB_BYTES;
+#pragma unroll
+            for (int t = 0; t < 3; t++) {
+                *(u32x4 *)(d + 1536 * t + 16 * lane) = xl[t];
+                *(u32x2 *)(d + 1536 * t + 1024 + 8 * lane) = xh[t];
+            }
+            *(uint32_t *)(d + 3 * 1536 + 4 * lane) = xs;
+        }
+    };
+
+    f32x4v acc[S::NF][NTB > 0 ? NTB : 1];
+#pragma unroll
+    for (int f = 0; f < S::NF; f++)
+#pragma unroll
+        for (int t = 0; t < (NTB > 0 ? NTB : 1); t++) acc[f][t] = f32x4v{0.f, 0.f, 0.f, 0.f};
+
+    load_x(0);
+    issue_w(0);
+    if (n_st > 1) issue_w(1);
+    store_x(0);
+    for (int st = 0; st < n_st; st++) {
+        {
+            const int buf = st % S::WDEPTH;
+            gx_wait_vm(issued - (buf == 0 ? m_w0 : buf == 1 ? m_w1 : m_w2));  // this wave's windows of stage st
+        }
+        __syncthreads();  // everyone's, and the activations stored; stage st-1's buffers are free
+        const bool more = st + 1 < n_st;
+        if (more) load_x(st + 1);
+        if (st + 2 < n_st) issue_w(st + 2);
+        if constexpr (NTB > 0) {
+            const uint8_t *Wd = Wb + (st % S::WDEPTH) * S::W_BYTES;
+            const uint8_t *Ad = Ab + (st & 1) * S::A_BYTES;
+            const bool live = 4 * st + grp < nblk;  // past the row's last block: codes 0
+            i32x8 av[S::NF];
+            int sa[S::NF];
+#pragma unroll
+            for (int f = 0; f < S::NF; f++) {
+                // the block's E8M0 byte at `off`, its 16 code bytes after it
+                const int lrow = (f / S::FR) * S::RPB + rg * S::RW + 16 * (f % S::FR) + l16;
+                const uint32_t off = (uint32_t)lrow * (S::PCS * 16) + ((lmis[f] + 4u * (uint32_t)st) & 15u) + 17u * grp;
+                const uint32_t cb = off + 1, sh = cb & 3;
+                const uint32_t *q = (const uint32_t *)(Wd + (cb & ~3u));
+                const uint32_t d0 = q[0], d1 = q[1], d2 = q[2], d3 = q[3], d4 = q[4];
+                const uint32_t e = Wd[off];
+                const i32x4 w4 = {(int)(live ? __builtin_amdgcn_alignbyte(d1, d0, sh) : 0u), (int)(live ? __builtin_amdgcn_alignbyte(d2, d1, sh) : 0u),
+                                  (int)(live ? __builtin_amdgcn_alignbyte(d3, d2, sh) : 0u), (int)(live ? __builtin_amdgcn_alignbyte(d4, d3, sh) : 0u)};
+                // an FP4 operand is dwords 0..3; the instruction ignores 4..7
+                av[f] = __builtin_shufflevector(w4, w4, 0, 1, 2, 3, -1, -1, -1, -1);
+                sa[f] = (int)(live ? e : 127u);
+            }
+#pragma unroll
+            for (int t = 0; t < NTB; t++) {
+                const uint8_t *d = Ad + (tb0 + t) * S::TB_BYTES;
+                const int sb = (int)*(const uint32_t *)(d + 3 * 1536 + 4 * lane);
+#pragma unroll
+                for (int j = 0; j < 3; j++) {
+                    // an FP6 operand is dwords 0..5; the instruction ignores 6 and 7
+                    const i32x4 l4 = *(const i32x4 *)(d + 1536 * j + 16 * lane);
+                    const i32x2 h2 = *(const i32x2 *)(d + 1536 * j + 1024 + 8 * lane);
+                    const i32x8 bo = __builtin_shufflevector(l4, __builtin_shufflevector(h2, h2, 0, 1, -1, -1), 0, 1, 2, 3, 4, 5, -1, -1);
+#pragma unroll
+                    for (int f = 0; f < S::NF; f++) {
+                        if (j == 0) acc[f][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[f], bo, acc[f][t], 4, 2, 0, sa[f], 0, sb);
+                        if (j == 1) acc[f][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[f], bo, acc[f][t], 4, 2, 0, sa[f], 1, sb);
+                        if (j == 2) acc[f][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[f], bo, acc[f][t], 4, 2, 0, sa[f], 2, sb);
+                    }
+                }
+            }
+        }
+        if (more) store_x((st + 1) & 1);  // stage st+1's operands (stage st-1's buffer, free)
+    }
+
+    // epilogue: lane holds weight rows 16 f' + 4 grp + i (i < 4) of token 16 (tb0 + t) + l16
+    gx_wait_vm(0);
+    if constexpr (NTB > 0) {
+#pragma unroll
+        for (int t = 0; t < NTB; t++) {
+            const int r = 16 * (tb0 + t) + l16;
+            if (r >= tile.m) continue;
+            const int pos = tile.pos0 + r;
+            const int pick = a.pile_pick ? a.pile_pick[pos] : pos;
+#pragma unroll
+            for (int f = 0; f < S::FR; f++) {
+                const int n = nb * S::RPB + rg * S::RW + 16 * f + 4 * grp;
+                if constexpr (MODE == 0) {
+                    const uint32_t e = a.act == CW_ACT_SILU ? 0u : a.ids[pick];
+                    float *hrow = a.h + (int64_t)pos * a.ldh;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        if (n + i >= a.n) continue;
+                        float g = acc[f][t][i], u = acc[S::FR + f][t][i], o;
+                        if (a.act == CW_ACT_SILU) {
+                            o = g / (1.0f + expf(-g)) * u;
+                        } else {
+                            if (a.bias0) g += a.bias0[(int64_t)e * a.n + n + i];
+                            if (a.bias1) u += a.bias1[(int64_t)e * a.n + n + i];
+                            g = fminf(g, a.limit);
+                            u = fminf(fmaxf(u, -a.limit), a.limit);
+                            o = (u + 1.0f) * (g * (1.0f / (1.0f + expf(-(g * a.alpha)))));
+                        }
+                        hrow[n + i] = o;
+                    }
+                } else {
+                    float *dst = a.dn + (int64_t)pick * a.n + n;
+                    if (n + 4 <= a.n && (a.n & 3) == 0) {
+                        *(float4 *)dst = make_float4(acc[f][t][0], acc[f][t][1], acc[f][t][2], acc[f][t][3]);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            if (n + i < a.n) dst[i] = acc[f][t][i];
+                    }
+                }
+            }
+        }
+    }
+}
+
+// MODE 0: gate and up with the activation, hidden rows written in pile order (ldh floats).
+// MODE 1: one output row per pick (dn, pick order), combined per token afterwards.
+template <int MODE>
+__global__ __launch_bounds__(512, 1) void k_gmx(const MfArgs a) {
+    using S = GxShape<MODE>;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)smem;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n_nb = (a.n + S::RPB - 1) / S::RPB;
+    const int R = a.run_tiles, n_tiles = *a.n_tiles;
+    // blocks go to the 8 XCDs round-robin; item b of each run of R*n_nb (R = run_tiles) takes
+    // M-tile R*run + b%R and N-block b/R, so an M-tile's N-blocks share an XCD and its L2
+    for (int item = blockIdx.x; item < a.n_items; item += gridDim.x) {
+        const int run = item / (R * n_nb), b = item - run * R * n_nb;
+        const int mt = run * R + (b & (R - 1));
+        if (mt >= n_tiles) continue;  // uniform across the block
+        const int nb = b / R;
+        __syncthreads();  // every wave is done with the previous item's buffers
+        const MfTile tile = a.tiles[mt];
+        const int mbs = (tile.m + 15) >> 4, half = wave >> 2, n0 = (mbs + 1) >> 1;
+        const int tb0 = half ? n0 : 0, ntb = half ? mbs - n0 : n0;
+        switch (ntb) {
+        case 0: gx_item<MODE, 0>(a, tile, nb, mbs, tb0, wave, lane, smem, lds0); break;
+        case 1: gx_item<MODE, 1>(a, tile, nb, mbs, tb0, wave, lane, smem, lds0); break;
+        case 2: gx_item<MODE, 2>(a, tile, nb, mbs, tb0, wave, lane, smem, lds0); break;
+        default: gx_item<MODE, 3>(a, tile, nb, mbs, tb0, wave, lane, smem, lds0); break;
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------ launchers
+
+int pack_rows_fp6(const float *x, int rows, int k, int ldx, uint8_t *out, hipStream_t s) {
+    if (rows == 0) return CW_OK;
+    if (k % 32) return set_error(CW_ENOTSUP, "pack fp6: rows of %d are not whole 32-value blocks", k);
+    const int64_t n = (int64_t)rows * (((k / 32) + 3) & ~3), blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(k_pack_fp6x3, dim3((unsigned)(blocks < 16384 ? blocks : 16384)), dim3(256), 0, s, x, rows, k, ldx, out);
+    return check_launch("k_pack_fp6x3");
+}
+
+size_t fp6_rows_bytes(int64_t rows, int64_t k) { return (size_t)rows * (size_t)((k + 127) / 128) * 304; }
+
+static int gx_device() {
+    int dev = 0;
+    return hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 ? dev : 0;
+}
+
+template <int MODE>
+static int gx_launch(const MfArgs &a, int tiles_max, hipStream_t s) {
+    using S = GxShape<MODE>;
+    if (a.k % 32 || a.k <= 128) return set_error(CW_ENOTSUP, "mxfp4 gemm: k %d is not whole blocks over two steps", a.k);
+    if ((int64_t)a.n * a.row_bytes >= ((int64_t)1 << 32))
+        return set_error(CW_ENOTSUP, "mxfp4 gemm: a matrix of %d rows of %lld bytes is 4 GiB or more", a.n, (long long)a.row_bytes);
+    static std::atomic<int> cus_of[64];
+    static std::atomic<bool> lds_set[64];
+    const int dev = gx_device();
+    int cus = cus_of[dev].load(std::memory_order_relaxed);
+    if (!cus) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 8) n = 256;
+        cus = n / 8 * 8;
+        cus_of[dev].store(cus, std::memory_order_relaxed);
+    }
+    if (!lds_set[dev].load(std::memory_order_acquire)) {
+        if (hipFuncSetAttribute((const void *)k_gmx<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::LDS) != hipSuccess)
+            return set_error(CW_EHIP, "mxfp4 gemm: cannot reserve %zu bytes of LDS", S::LDS);
+        lds_set[dev].store(true, std::memory_order_release);
+    }
+    const int n_nb = (a.n + S::RPB - 1) / S::RPB;
+    const int R = tiles_max >= 8 ? 8 : tiles_max >= 4 ? 4 : tiles_max >= 2 ? 2 : 1;
+    const int64_t items = (int64_t)((tiles_max + R - 1) / R) * R * n_nb;
+    if (items >= ((int64_t)1 << 31)) return set_error(CW_ENOTSUP, "mxfp4 gemm: %lld work items", (long long)items);
+    const int64_t blocks = items < cus ? (items + 7) / 8 * 8 : cus;
+    MfArgs b = a;
+    b.run_tiles = R;
+    b.n_items = (int)items;
+    hipLaunchKernelGGL((k_gmx<MODE>), dim3((unsigned)blocks), dim3(S::NT), S::LDS, s, b);
+    return check_launch("k_gmx");
+}
+
+int mxfp4_gateup(const MfArgs &a, int tiles_max, hipStream_t s) { return gx_launch<0>(a, tiles_max, s); }
+int mxfp4_down(const MfArgs &a, int tiles_max, hipStream_t s) { return gx_launch<1>(a, tiles_max, s); }
+
+// The scaled path is the default for MXFP4; CWMOE_MXFP4_F16=1 selects the fp16 MFMA path instead
+// (for comparisons). Read at each call: a workspace size and the call it is for must agree, so the
+// variable must not change between them.
+bool mxfp4_scaled() {
+    const char *e = getenv("CWMOE_MXFP4_F16");
+    return !(e && atoi(e) == 1);
+}
+
+}  // namespace cw

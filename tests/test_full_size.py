@@ -20,7 +20,8 @@ pytestmark = pytest.mark.gpu
 CONFIGS = [
     # name, E, K, h, I, dtypes, act, T
     ("config3_prefill", 256, 8, 2048, 512, "iq2", 0, 1500),
-    ("config4_prefill", 128, 4, 2880, 2880, "mxfp4", 1, 2048),
+    ("config4_prefill", 128, 4, 2880, 2880, "mxfp4", 1, 2048),          # block-scaled MFMA (FP4 x FP6 terms)
+    ("config4_prefill_fp16", 128, 4, 2880, 2880, "mxfp4", 1, 2048),     # CWMOE_MXFP4_F16=1: the fp16 MFMA path
 ]
 
 
@@ -30,7 +31,7 @@ def _layer(name, E, K, h, I, kind, act):
     from coachwhip_amd import ops, synth
     dts = (F.IQ2_XXS, F.IQ2_XXS, F.IQ2_S) if kind == "iq2" else (F.MXFP4,) * 3
     gen = torch.Generator(device="cuda")
-    gen.manual_seed(zlib.crc32(name.encode()))
+    gen.manual_seed(zlib.crc32(name.replace("_fp16", "").encode()))
     shapes = [(I, h), (I, h), (h, I)]
     banks = []
     for m, (n, k) in enumerate(shapes):
@@ -54,9 +55,10 @@ def test_full_size_prefill(name, E, K, h, I, kind, act, T, monkeypatch):
     from coachwhip_amd import synth
     from oracle import oracle as O
     monkeypatch.delenv("CWMOE_PREFILL_MIN_TOKENS", raising=False)
+    monkeypatch.setenv("CWMOE_MXFP4_F16", "1" if name.endswith("_fp16") else "0")
     print("full size", name, T, "tokens", flush=True)
     moe, host = _layer(name, E, K, h, I, kind, act)
-    rng = np.random.default_rng(zlib.crc32(name.encode()) + 1)
+    rng = np.random.default_rng(zlib.crc32(name.replace("_fp16", "").encode()) + 1)
     x = rng.standard_normal((T, h)).astype(np.float32)
     logits = rng.standard_normal((T, E)).astype(np.float32)
     out, ids, _ = moe.forward(torch.from_numpy(x).cuda(), torch.from_numpy(logits).cuda())

@@ -209,6 +209,35 @@ def test_grouped_gemm_mxfp4_exponents_across_stages():
     assert O.rel_l2(out, want) <= REL_L2_GATE
 
 
+@pytest.mark.parametrize("k,T", [(2880, 40), (256, 24), (160, 17), (1056, 90)])
+def test_mxfp4_grouped_scaled_and_fp16_paths(k, T, monkeypatch):
+    """MXFP4 above 8 tokens runs on the block-scaled MFMA (FP4 weights as stored x three FP6
+    activation terms); CWMOE_MXFP4_F16=1 selects the fp16 MFMA path. Both against the f64 oracle
+    at the 1e-3 gate, on row lengths with a half step at the end (2880, 1056: K not a multiple of
+    128), exactly two steps (256) and one step and a quarter (160), 1-6 token blocks per tile, an
+    id past the bank giving a NaN row; the two paths' outputs differ (different arithmetic)."""
+    rng = np.random.default_rng(k + T)
+    n, slots, K = 96, 5, 4
+    raw = synth.random_blocks(F.MXFP4, slots * n * k, rng)
+    bank = ops.ExpertBank.from_blocks(raw, F.MXFP4, n, k, slots)
+    ids = rng.integers(0, slots, size=(T, K), dtype=np.uint32)
+    ids[1, 3] = slots + 2
+    x = rng.standard_normal((T, k)).astype(np.float32)
+    want = O.matvec_id(F.MXFP4, n, k, raw, bank.slot_stride, x, np.minimum(ids, slots - 1), False)
+    outs = {}
+    for path, env in (("scaled", "0"), ("fp16", "1")):
+        monkeypatch.setenv("CWMOE_MXFP4_F16", env)
+        out = host(ops.MoeMatvec(bank, K, False).forward(dev(x), dev(ids)))
+        assert np.all(np.isnan(out[1, 3]))
+        keep = np.ones((T, K), bool)
+        keep[1, 3] = False
+        err = O.rel_l2(out[keep], want[keep])
+        say("  k", k, "T", T, path, "rel_l2", err)
+        assert err <= REL_L2_GATE
+        outs[path] = out[keep]
+    assert not np.array_equal(outs["scaled"], outs["fp16"])
+
+
 @pytest.mark.parametrize("off", [0, 4])
 def test_qmatmul_q4k_few_rows_any_alignment(off, monkeypatch):
     """Q4_K at 2..16 rows of x on the MFMA path: a 16-byte aligned matrix takes the one-launch
