@@ -5,7 +5,7 @@ the reference engine's QMatMul / MoE-layer interfaces (``coachwhip_amd.ops``, wh
 and the host bank bookkeeping (``coachwhip_amd.slots``).
 """
 from . import formats
-from ._lib import NO_SLOT, CwError, CwNotSupported, lib
+from ._lib import CW_MOE_STATE_BYTES, CW_MOE_STATUS_OFFSET, NO_SLOT, CwError, CwNotSupported, lib
 from .slots import Plan, Slots
 
-__all__ = ["formats", "lib", "CwError", "CwNotSupported", "NO_SLOT", "Slots", "Plan"]
+__all__ = ["formats", "lib", "CwError", "CwNotSupported", "NO_SLOT", "CW_MOE_STATE_BYTES", "CW_MOE_STATUS_OFFSET", "Slots", "Plan"]

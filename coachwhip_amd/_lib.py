@@ -11,6 +11,8 @@ LIB_PATH = os.path.join(HERE, "libcwmoe.so")
 
 CW_OK, CW_ENOTSUP, CW_EINVAL, CW_EHIP, CW_EFULL = 0, 1, 2, 3, 4
 NO_SLOT = 0xFFFFFFFF
+# include/cwmoe.h: the MoE-layer workspace's sync-state bytes and the offset of its status word
+CW_MOE_STATE_BYTES, CW_MOE_STATUS_OFFSET = 8448, 8320
 
 
 class CwError(RuntimeError):

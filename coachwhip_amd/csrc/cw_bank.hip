@@ -129,6 +129,7 @@ struct cw_bank {
     std::vector<uint8_t> filling;     // per slot: that copy may still be running
     std::vector<uint8_t> kept;        // per slot: placed by the last ensure
     hipEvent_t fence = nullptr;       // the last ensure's stream, when a prefetch was last called
+    hipEvent_t handoff = nullptr;     // the last ensure's stream, when an ensure comes on another one
     hipStream_t last = nullptr;       // the stream of the last ensure
     bool fenced = false;              // an ensure has run (last is set)
     cw_bank_stats st{};
@@ -138,6 +139,7 @@ struct cw_bank {
         for (hipEvent_t e : slot_ev)
             if (e) (void)hipEventDestroy(e);
         if (fence) (void)hipEventDestroy(fence);
+        if (handoff) (void)hipEventDestroy(handoff);
         if (copy) (void)hipStreamDestroy(copy);
         cw_slots_free(slots);
     }
@@ -290,6 +292,7 @@ cw_bank *cw_bank_new(const cw_bank_source *src, int n_slots, void *device_mem, s
     if (r == hipSuccess) r = hipStreamCreateWithFlags(&b->copy, hipStreamNonBlocking);
     for (int s = 0; s < n_slots && r == hipSuccess; s++) r = hipEventCreateWithFlags(&b->slot_ev[(size_t)s], hipEventDisableTiming);
     if (r == hipSuccess) r = hipEventCreateWithFlags(&b->fence, hipEventDisableTiming);
+    if (r == hipSuccess) r = hipEventCreateWithFlags(&b->handoff, hipEventDisableTiming);
     // the fill kernel needs a device view of all three stores and 16-byte pieces
     b->by_kernel = r == hipSuccess;
     for (int m = 0; m < 3 && b->by_kernel; m++) {
@@ -346,6 +349,13 @@ int cw_bank_ensure(cw_bank *b, const uint32_t *needed, int n_needed, cw_stream_t
     b->st.hits += (uint64_t)nh;
     b->st.prefetch_hits += ph;
     hipStream_t s = (hipStream_t)stream;
+    if (b->fenced && s != b->last) {
+        // the table patches a prefetch queued on the previous ensure's stream (its victims taken
+        // out) must land before this ensure's own patches, which may list a victim again
+        hipError_t w = hipEventRecord(b->handoff, b->last);
+        if (w == hipSuccess) w = hipStreamWaitEvent(s, b->handoff, 0);
+        if (w != hipSuccess) return cw::set_error(CW_EHIP, "bank: stream wait: %s", hipGetErrorString(w));
+    }
     std::vector<uint8_t> waited((size_t)b->n_slots, 0);
     for (int i = 0; i < nh; i++) {
         const uint32_t slot = hits[2 * i + 1];

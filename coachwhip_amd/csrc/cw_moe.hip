@@ -529,10 +529,10 @@ int cw_matmul_id_grouped(int dtype, int64_t n, int64_t k, int64_t n_slots, int64
     if (rc) return rc;
     if (T == 0) return CW_OK;
     CW_REQUIRE(bank && x && ids && out, "matmul_id_grouped: null pointer");
-    // the activation pack reads whole float4s: an x off 16-byte alignment is a capability probe's
-    // "no" (the caller takes cw_matvec_id, which reads any x), not an argument error
-    if (((uintptr_t)x & 15u) != 0 || k % 4 != 0)
-        return set_error(CW_ENOTSUP, "matmul_id_grouped: x is not 16-byte aligned rows of whole float4s");
+    // the activation packs read 16 bytes at a time from any 4-byte aligned row start (gfx950 runs
+    // with unaligned memory access enabled), as the reference takes any offset of x
+    CW_REQUIRE(((uintptr_t)x & 3u) == 0, "matmul_id_grouped: x is not 4-byte aligned");
+    if (k % 4 != 0) return set_error(CW_ENOTSUP, "matmul_id_grouped: rows of %lld are not whole float4s", (long long)k);
     const int xpp = x_rows_per_expert ? 1 : 0;
     const GroupedLayout L = grouped_layout(dtype, k, n_slots, xpp, K, T);
     CW_REQUIRE(ws && ws_bytes >= L.total, "matmul_id_grouped: workspace of %zu bytes, %zu needed", ws_bytes, L.total);

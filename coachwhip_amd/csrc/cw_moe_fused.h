@@ -23,13 +23,15 @@ struct MoeArgs {
     uint32_t *slots;               // T x K slots
     float *h;                      // T*K x P hidden rows
     float *out;                    // T x H
-    void *state;                   // the one-launch decode's sync state (DECODE_STATE_BYTES, zero
-                                   // before and after each call)
+    void *state;                   // the one-launch decode's sync state (DECODE_STATE_BYTES, zero-
+                                   // filled before the first call; each call leaves it valid)
     uint32_t polls;                // its bounded waits give up after this many polls
 };
 
-// workspace bytes of the decode's sync state, at the start of every MoE-layer workspace
-constexpr size_t DECODE_STATE_BYTES = 8192;
+// workspace bytes of the decode's sync state, at the start of every MoE-layer workspace: the
+// barrier (8 KB), a word that tells a valid state from foreign bytes, and the status word
+// (CW_MOE_STATUS_OFFSET)
+constexpr size_t DECODE_STATE_BYTES = 8192 + 256;
 
 int moe_gateup(int dtype, const MoeArgs &a, int T, hipStream_t s);
 // the whole layer for one token in one launch (CW_ENOTSUP for shapes it does not cover)

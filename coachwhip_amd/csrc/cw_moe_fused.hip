@@ -10,6 +10,8 @@
 // Decode is bound by memory latency rather than bandwidth (a layer reads ~7 MB), so both kernels
 // issue all their weight loads before anything that waits: the IQ grid copy into LDS and the
 // barrier come after the loads are in flight.
+#include <stddef.h>
+
 #include <mutex>
 
 #include "cw_common.h"
@@ -202,13 +204,25 @@ __global__ __launch_bounds__(256) void k_moe_down(const MoeArgs a) {
 // to the coherence point, so the counters need no fences: an agent-scope release / acquire pair
 // here (L2 write-back and invalidate in every block) measured 3x slower, and so did polling all 8
 // XCD counters from every block. A wait gives up after `polls` polls and counts an error
-// (g_decode_errors) instead of hanging; every block still arrives exactly once, so the state is
-// back at zero (and the generation one further) when the kernel ends, timed out or not.
+// (g_decode_errors, and the workspace's status word) instead of hanging; every block still
+// arrives exactly once, so the counters are back at zero (and the generation one further) when
+// the kernel ends, timed out or not.
+// The state must start zero-filled and then belong to the layer's calls alone. The last block to
+// arrive stores a marker word; a launch that finds neither zero nor the marker there (other bytes
+// written over the region) uses no counter, counts an error and gives NaN outputs, and so does an
+// arrival whose counter was already past its block count. Both leave the state as they found it:
+// the caller zero-fills it again.
 struct DecodeBarrier {
     uint32_t sub[32][32];  // arrival counter x at sub[x][0]; the top counter at sub[0][16]
     uint32_t gen[32][32];  // generation copy x at gen[x][0]
+    uint32_t mark;         // 0 (never used) or STATE_MARK (left by a completed call)
+    uint32_t pad[31];
+    uint32_t status;       // blocks of one-token calls that gave up or found the state invalid
 };
-static_assert(sizeof(DecodeBarrier) <= DECODE_STATE_BYTES, "the decode state does not fit its workspace region");
+constexpr uint32_t STATE_MARK = 0x434d5753u;
+static_assert(sizeof(DecodeBarrier) <= DECODE_STATE_BYTES && DECODE_STATE_BYTES == CW_MOE_STATE_BYTES,
+              "the decode state does not fit its workspace region");
+static_assert(offsetof(DecodeBarrier, status) == CW_MOE_STATUS_OFFSET, "the status word is where cwmoe.h says");
 static __device__ uint32_t g_decode_errors;
 
 #define CW_AGENT __HIP_MEMORY_SCOPE_AGENT
@@ -220,33 +234,58 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // `gen` is generation copy blockIdx % 32 as read by wave 0 at any point of this launch before it
 // arrives (the copies move only when every block has arrived, and they are equal between calls),
 // so that read is off the barrier's critical path.
-__device__ bool grid_barrier(DecodeBarrier *b, uint32_t nblocks, uint32_t polls, uint32_t gen) {
+// a failed wait or an invalid state: counted on the device and in the workspace's status word
+__device__ __forceinline__ void barrier_fail(DecodeBarrier *b) {
+    __hip_atomic_fetch_add(&g_decode_errors, 1u, __ATOMIC_RELAXED, CW_AGENT);
+    __hip_atomic_fetch_add(&b->status, 1u, __ATOMIC_RELAXED, CW_AGENT);
+}
+// `mark` is the state's marker word as read by wave 0 at kernel start (before any block can have
+// arrived, so every block reads the same value).
+__device__ bool grid_barrier(DecodeBarrier *b, uint32_t nblocks, uint32_t polls, uint32_t gen, uint32_t mark) {
     __builtin_amdgcn_s_waitcnt(0);  // this thread's coherent stores have landed
     __syncthreads();
     __shared__ int ok;
+    if (mark != 0 && mark != STATE_MARK) {  // foreign bytes: no counter is touched
+        if (threadIdx.x == 0) {
+            ok = 0;
+            if (blockIdx.x == 0) barrier_fail(b);
+        }
+        __syncthreads();
+        return false;
+    }
     if (threadIdx.x < 64) {
         const uint32_t x = blockIdx.x & 31;
-        int last = 0;
+        int last = 0, sane = 1;
         if (threadIdx.x == 0) {
             const uint32_t nsub = (nblocks - x + 31) / 32, nx = nblocks < 32 ? nblocks : 32;
-            if (__hip_atomic_fetch_add(&b->sub[x][0], 1u, __ATOMIC_RELAXED, CW_AGENT) == nsub - 1) {
+            const uint32_t c = __hip_atomic_fetch_add(&b->sub[x][0], 1u, __ATOMIC_RELAXED, CW_AGENT);
+            if (c == nsub - 1) {
                 // the reset only has to land before the next call, which the kernel's end ensures
                 __hip_atomic_store(&b->sub[x][0], 0u, __ATOMIC_RELAXED, CW_AGENT);
-                last = __hip_atomic_fetch_add(&b->sub[0][16], 1u, __ATOMIC_RELAXED, CW_AGENT) == nx - 1;
+                const uint32_t t = __hip_atomic_fetch_add(&b->sub[0][16], 1u, __ATOMIC_RELAXED, CW_AGENT);
+                last = t == nx - 1;
                 if (last) __hip_atomic_store(&b->sub[0][16], 0u, __ATOMIC_RELAXED, CW_AGENT);
+                sane = t < nx;
+            } else {
+                sane = c < nsub;
             }
+            if (!sane) barrier_fail(b);  // a counter past its block count: the state was not zero
         }
         last = __builtin_amdgcn_readfirstlane(last);
+        sane = __builtin_amdgcn_readfirstlane(sane);
         if (last) {
             if (threadIdx.x < 32) __hip_atomic_store(&b->gen[threadIdx.x][0], gen + 1, __ATOMIC_RELAXED, CW_AGENT);
-            if (threadIdx.x == 0) ok = 1;
+            if (threadIdx.x == 0) {
+                __hip_atomic_store(&b->mark, STATE_MARK, __ATOMIC_RELAXED, CW_AGENT);
+                ok = sane;
+            }
         } else if (threadIdx.x == 0) {
-            int good = 1;
+            int good = sane;
             uint32_t n = 0;
-            while (__hip_atomic_load(&b->gen[x][0], __ATOMIC_RELAXED, CW_AGENT) == gen) {
+            while (good && __hip_atomic_load(&b->gen[x][0], __ATOMIC_RELAXED, CW_AGENT) == gen) {
                 if (n++ >= polls) {
                     good = 0;
-                    __hip_atomic_fetch_add(&g_decode_errors, 1u, __ATOMIC_RELAXED, CW_AGENT);
+                    barrier_fail(b);
                     break;
                 }
                 __builtin_amdgcn_s_sleep(1);
@@ -347,8 +386,11 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
     const bool routes = !ONE_ROUTER || wave == 0;
     float lv[PER];
     RouteState<PER> rst;
-    uint32_t gen = 0;  // the barrier's generation, read by wave 0 ahead of the logits
-    if (wave == 0) gen = __hip_atomic_load(&((DecodeBarrier *)a.state)->gen[blockIdx.x & 31][0], __ATOMIC_RELAXED, CW_AGENT);
+    uint32_t gen = 0, mark = 0;  // the barrier's generation and the state's marker, read by wave 0 ahead of the logits
+    if (wave == 0) {
+        gen = __hip_atomic_load(&((DecodeBarrier *)a.state)->gen[blockIdx.x & 31][0], __ATOMIC_RELAXED, CW_AGENT);
+        mark = __hip_atomic_load(&((DecodeBarrier *)a.state)->mark, __ATOMIC_RELAXED, CW_AGENT);
+    }
     if (routes) {
         route_load<PER>(a.logits, a.E, lv);
         route_keys<PER>(lv, a.E, rst);
@@ -670,7 +712,7 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
         }
     }
     if (wave < 4) td.store(ldsd, threadIdx.x);
-    const bool ok = grid_barrier((DecodeBarrier *)a.state, gridDim.x, a.polls, gen);
+    const bool ok = grid_barrier((DecodeBarrier *)a.state, gridDim.x, a.polls, gen, mark);
 
     // every hidden row into LDS once per block, read at the coherence point (16-byte buffer
     // loads with the sc1 policy, the form of an agent-scope atomic load, 8 in flight per thread),

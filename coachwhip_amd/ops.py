@@ -22,7 +22,7 @@ import numpy as np
 import torch
 
 from . import formats as F
-from ._lib import CwError, MoeDesc, SharedDesc, check, lib, CW_EINVAL, CW_ENOTSUP
+from ._lib import CwError, MoeDesc, SharedDesc, check, lib, CW_EINVAL, CW_ENOTSUP, CW_MOE_STATE_BYTES, CW_MOE_STATUS_OFFSET
 
 
 def _stream():
@@ -358,6 +358,15 @@ class MoeLayer:
             # zero-filled once: the one-token layer keeps its sync state there, at zero between calls
             self._ws = torch.zeros(need, dtype=torch.uint8, device=device)
         return self._ws, need
+
+    def status(self) -> int:
+        """The workspace's status word (CW_MOE_STATUS_OFFSET): blocks of one-token calls whose
+        barrier gave up or found an invalid sync state. Read on the current stream (the Python
+        int waits for it)."""
+        if self._ws is None:
+            return 0
+        word = self._ws[CW_MOE_STATUS_OFFSET:CW_MOE_STATUS_OFFSET + 4].cpu()
+        return int(word.view(torch.int32)[0]) & 0xFFFFFFFF
 
     def forward(self, xs: torch.Tensor, logits: torch.Tensor, missing: torch.Tensor = None):
         """xs (T, hidden) f32, logits (T, E) f32 -> (out (T, hidden), ids (T, K), w (T, K))."""

@@ -23,9 +23,12 @@
  *    caller may fall back, as mv_id.rs:156-179 does with Ok(false)), CW_EINVAL (shape, stride
  *    or argument error, as candle::bail! in crates/engine/src/experts.rs:2204-2217), CW_EHIP
  *    (the HIP runtime failed). cw_last_error() describes the last failure on this thread.
- *  - Calls on distinct streams may run concurrently when they use distinct workspaces: a call
- *    keeps all its scratch, including the one-token MoE layer's device-wide barrier, in the
- *    workspace it is given.
+ *  - Calls on distinct streams may run concurrently when they use distinct workspaces (a call
+ *    keeps all its scratch in the workspace it is given), with one exception: a one-token
+ *    cw_moe_layer call (T = 1) is one persistent launch sized to fill the device, whose blocks
+ *    meet at a device-wide barrier. It must not overlap other work on the device: blocks that
+ *    cannot be scheduled make the barrier give up (outputs NaN, counted in the workspace's status
+ *    word and by cw_device_errors) instead of hanging.
  */
 #ifndef CWMOE_H
 #define CWMOE_H
@@ -132,8 +135,10 @@ int cw_matvec_id(int dtype, int64_t n, int64_t k, int64_t n_slots, int64_t slot_
 /* The cw_matvec_id contract for a batch of tokens, as grouped GEMMs on the matrix cores: picks are
  * grouped by slot, and each slot's picks multiply its matrix as one small matrix product (the
  * activations rounded to fp16 with a power-of-two scale per row: rel-L2 about 3e-4 against f64,
- * where cw_matvec_id's f32 path is about 1e-7). Ids >= n_slots give NaN rows, as in
- * cw_matvec_id. x is 16-byte aligned, k a multiple of 4. The workspace is sized by
+ * where cw_matvec_id's f32 path is about 1e-7; MXFP4 matrices above 128 weights per row run on
+ * the block-scaled MFMA, FP4 weights as stored against three FP6 terms of each activation with
+ * a power-of-two scale per 32 values: rel-L2 about 2e-5). Ids >= n_slots give NaN rows, as in
+ * cw_matvec_id. x is 4-byte aligned (any f32 offset), k a multiple of 4. The workspace is sized by
  * cw_matmul_id_grouped_workspace_size (0 when the call is not supported).
  * CW_ENOTSUP (the caller falls back to cw_matvec_id) for a dtype without a grouped kernel, more
  * than 1024 slots, k above 8192, or rows that are not whole 256-weight super-blocks (Q8_0 and
@@ -204,12 +209,21 @@ typedef struct cw_moe_desc {
  * set, picks whose expert has no slot read slot 0 and are counted in *missing (device u32,
  * may be NULL). ids_out / w_out (T x K, device, may be NULL) receive the routing.
  * The workspace (256-byte aligned) must be zero-filled once before its first use, for example
- * when it is allocated: its first CW_MOE_STATE_BYTES bytes hold the one-token layer's sync state
- * (arrival counters, which every call leaves at zero again, and generation words, which every
- * call moves on together), at the same offset for every T (so one workspace serves calls of any
- * size); zero-filling it again between calls is harmless, any other write there breaks the
- * barrier. Calls that overlap in time need distinct workspaces. */
-#define CW_MOE_STATE_BYTES 8192
+ * when it is allocated, and then belong to this layer's calls alone (not to a pool that hands the
+ * bytes to other work between calls): its first CW_MOE_STATE_BYTES bytes hold the one-token
+ * layer's sync state (arrival counters, which every call leaves at zero again, generation words,
+ * which every call moves on together, and a marker word), at the same offset for every T (so one
+ * workspace serves calls of any size). Zero-filling it again between calls is harmless. A call
+ * that finds other bytes there (or a counter past its block count) uses no counter, gives NaN
+ * outputs and counts the failure; the region must then be zero-filled again. Calls that overlap
+ * in time need distinct workspaces (and one-token calls must not overlap any other work).
+ * The u32 at byte CW_MOE_STATUS_OFFSET of the workspace counts, over the workspace's life, the
+ * blocks of one-token calls whose barrier gave up or found the state invalid (their outputs are
+ * NaN): a caller reads it on its stream (an asynchronous copy after the call), with no device
+ * synchronize, and compares it with the value before the call. No counterpart in the reference
+ * (its layer is several dispatches). */
+#define CW_MOE_STATE_BYTES 8448
+#define CW_MOE_STATUS_OFFSET 8320
 size_t cw_moe_workspace_size(const cw_moe_desc *desc, int T);
 int cw_moe_layer(const cw_moe_desc *desc, const float *x, const float *logits, int T, float *out,
                  uint32_t *ids_out, float *w_out, uint32_t *missing, void *ws, size_t ws_bytes,
@@ -283,8 +297,10 @@ int cw_gguf_experts(const cw_gguf *g, int layer, int which, int *dtype, int64_t 
 /* Device-side failures on the current device since the library loaded: a one-token layer runs as
  * one persistent launch whose blocks meet at a device-wide barrier; a barrier wait that gives up
  * (a block could not be scheduled; CWMOE_BARRIER_POLLS in the environment sets the polls, 131072
- * by default) makes the call's outputs NaN and is counted here. No counterpart in the reference
- * (its layer is several dispatches). Synchronizes the device. */
+ * by default) or a sync state that is not the layer's makes the call's outputs NaN and is counted
+ * here (and in the workspace's status word, CW_MOE_STATUS_OFFSET, which needs no device
+ * synchronize). No counterpart in the reference (its layer is several dispatches). Synchronizes
+ * the device. */
 uint32_t cw_device_errors(void);
 
 /* ---- the shrink to Q2_K ----------------------------------------------------------------- */

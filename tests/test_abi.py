@@ -27,6 +27,16 @@ def test_every_declared_symbol_is_exported_and_bound():
     assert set(names) == set(_lib.SIGNATURES), set(names) ^ set(_lib.SIGNATURES)
 
 
+def test_header_constants_match_the_binding():
+    """The workspace constants the header publishes (the one-token layer's sync-state bytes and its
+    status word's offset) are the ones the Python binding uses."""
+    text = open(os.path.join(ROOT, "include", "cwmoe.h")).read()
+    consts = dict(re.findall(r"#define (CW_MOE_[A-Z_]+) (\d+)\b", text))
+    assert int(consts["CW_MOE_STATE_BYTES"]) == _lib.CW_MOE_STATE_BYTES
+    assert int(consts["CW_MOE_STATUS_OFFSET"]) == _lib.CW_MOE_STATUS_OFFSET
+    assert _lib.CW_MOE_STATUS_OFFSET + 4 <= _lib.CW_MOE_STATE_BYTES
+
+
 def test_format_sizes():
     L = cw.lib()
     for dt in cw.formats.WEIGHT_TYPES:

@@ -182,6 +182,44 @@ def test_bank_prefetch_unlists_its_victims():
 
 
 @pytest.mark.gpu
+def test_bank_ensure_on_another_stream_follows_the_prefetch_patches():
+    """A prefetch takes its victims out of the table on the previous ensure's stream. An ensure on
+    a different stream that places a victim again must list it after that removal, not before:
+    the previous stream is held back by a long kernel here, so without the ordering the victim's
+    new entry would be overwritten by the late removal and the expert counted missing."""
+    import torch
+    from coachwhip_amd.bank import Bank
+    from coachwhip_amd.slots import Slots
+    print("bank: ensure on another stream", flush=True)
+    rng = np.random.default_rng(8)
+    E, S = 32, 8
+    raw = _random_store(rng, E)
+    bank = Bank(raw, DTYPES, SHAPES, E, S)
+    mirror = Slots(S)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    with torch.cuda.stream(s1):
+        assert bank.ensure(list(range(S))) == S and mirror.assign(list(range(S))) is not None
+        assert bank.ensure([0, 1]) == 0 and mirror.assign([0, 1]) is not None
+        held = {e: bank.slot_of(e) for e in range(S)}
+        ready = [0 if s in (held[0], held[1]) else 1 for s in range(S)]
+        torch.cuda._sleep(50_000_000)                      # s1 busy: the removal patches wait behind it
+        want = mirror.reserve([20, 21, 22], ready=lambda s: ready[s])
+        assert bank.prefetch([20, 21, 22]) == 3
+    victims = [e for e in range(S) if held[e] in {s for _, s in want}]
+    assert len(victims) == 3
+    with torch.cuda.stream(s2):
+        back = victims[:2]
+        loaded = bank.ensure(back + [20])
+        plan = mirror.assign(back + [20])
+        assert plan is not None and loaded == len(plan.misses) == 2
+    torch.cuda.synchronize()
+    # 21 and 22 are prefetched but not asked for: listed once their copies have landed
+    table = bank.table.cpu().numpy().view(np.uint32)
+    assert all(table[e] in (NO_SLOT, mirror.slot_of[e]) for e in (21, 22))
+    _check_bank(bank, mirror, raw, back + [20], skip=(21, 22))
+
+
+@pytest.mark.gpu
 def test_bank_rejects_bad_calls():
     from coachwhip_amd.bank import Bank
     print("bank: errors", flush=True)

@@ -319,6 +319,28 @@ def test_matmul_id_grouped_matches_the_oracle(dtype, n, k, rows_per_expert):
     assert np.array_equal(out2[keep].view(np.uint32), out[keep].view(np.uint32))
 
 
+def test_moe_matvec_grouped_takes_an_x_off_16_byte_alignment():
+    """Above 8 tokens MoeMatvec takes the grouped GEMM, as the reference's matmul_id_piles takes
+    any offset of x: an x view 4 bytes off 16-byte alignment (its packs read 16 bytes at a time,
+    unaligned) against the oracle at the 1e-3 gate, equal to the same x at an aligned address."""
+    rng = np.random.default_rng(41)
+    n, k, slots, T, K = 64, 512, 6, 20, 4
+    raw = synth.random_blocks(F.Q4_K, slots * n * k, rng)
+    bank = ops.ExpertBank.from_blocks(raw, F.Q4_K, n, k, slots)
+    ids = rng.integers(0, slots, size=(T, K), dtype=np.uint32)
+    x = rng.standard_normal((T, k)).astype(np.float32)
+    buf = torch.zeros(T * k + 4, dtype=torch.float32, device="cuda")
+    buf[1:1 + T * k] = dev(x).reshape(-1)
+    xv = buf[1:1 + T * k].view(T, k)
+    assert xv.data_ptr() % 16 == 4
+    mv = ops.MoeMatvec(bank, K, False)
+    assert T > mv.grouped_above
+    out = host(mv.forward(xv, dev(ids)))
+    want = O.matvec_id(F.Q4_K, n, k, raw, bank.slot_stride, x, ids, False)
+    assert O.rel_l2(out, want) <= REL_L2_GATE
+    assert np.array_equal(out.view(np.uint32), host(mv.forward(dev(x), dev(ids))).view(np.uint32))
+
+
 def test_matvec_id_marks_out_of_range_slots():
     rng = np.random.default_rng(2)
     raw = synth.random_blocks(F.Q8_0, 2 * 8 * 64, rng)
@@ -638,15 +660,52 @@ def test_moe_decode_barrier_gives_up_without_hanging(monkeypatch):
     want, _, _, _ = O.moe_layer(layer, x, logits)
     out, _, _ = moe.forward(dev(x), dev(logits))
     assert O.rel_l2(host(out), want) <= REL_L2_F32
-    before = cw.lib().cw_device_errors()
+    before, st_before = cw.lib().cw_device_errors(), moe.status()
     monkeypatch.setenv("CWMOE_BARRIER_POLLS", "0")
     out, _, _ = moe.forward(dev(x), dev(logits))
     got = host(out)
+    st_after = moe.status()  # the workspace's status word, no device synchronize needed
     after = cw.lib().cw_device_errors()
     monkeypatch.delenv("CWMOE_BARRIER_POLLS")
-    say("  errors", before, "->", after, "NaN outputs", int(np.isnan(got).sum()))
+    say("  errors", before, "->", after, "status", st_before, "->", st_after, "NaN outputs", int(np.isnan(got).sum()))
     assert after > before
+    assert st_after - st_before == after - before
     assert np.isnan(got).any()
+    out, _, _ = moe.forward(dev(x), dev(logits))
+    assert O.rel_l2(host(out), want) <= REL_L2_F32
+    assert cw.lib().cw_device_errors() == after and moe.status() == st_after
+
+
+@pytest.mark.parametrize("how", ["foreign_bytes", "counter_past_its_blocks"])
+def test_moe_decode_refuses_a_sync_state_that_is_not_its_own(how):
+    """The one-token layer's sync state must start zero-filled and then belong to the layer's
+    calls. Foreign bytes over the state region (as a pooled buffer would leave) are refused at
+    launch: no counter is used, the outputs are NaN, and the status word and the device error
+    count grow. A counter already past its block count (state not zeroed) is caught at arrival,
+    with NaN outputs. Zero-filling the region again restores the layer."""
+    say("moe decode state", how)
+    rng = np.random.default_rng(93)
+    E, K = 256, 8
+    layer = synth.moe_weights(E, K, 2048, 512, (F.IQ2_XXS, F.IQ2_XXS, F.IQ2_S), rng)
+    moe = upload_layer(layer)
+    x = rng.standard_normal((1, 2048)).astype(np.float32)
+    logits = rng.standard_normal((1, E)).astype(np.float32)
+    want, _, _, _ = O.moe_layer(layer, x, logits)
+    out, _, _ = moe.forward(dev(x), dev(logits))
+    assert O.rel_l2(host(out), want) <= REL_L2_F32
+    state = moe._ws[:cw.CW_MOE_STATE_BYTES]
+    if how == "foreign_bytes":
+        state[:cw.CW_MOE_STATUS_OFFSET] = 0x5A       # the status word itself left as it is
+    else:
+        state[:4] = torch.tensor([1000], dtype=torch.int32).view(torch.uint8).cuda()  # arrival counter 0
+    torch.cuda.synchronize()
+    before, st_before = cw.lib().cw_device_errors(), moe.status()
+    out, _, _ = moe.forward(dev(x), dev(logits))
+    got = host(out)
+    after, st_after = cw.lib().cw_device_errors(), moe.status()
+    say("  errors", before, "->", after, "status", st_before, "->", st_after, "NaN", int(np.isnan(got).sum()))
+    assert np.isnan(got).any() and after > before and st_after > st_before
+    state[:cw.CW_MOE_STATUS_OFFSET] = 0
     out, _, _ = moe.forward(dev(x), dev(logits))
     assert O.rel_l2(host(out), want) <= REL_L2_F32
     assert cw.lib().cw_device_errors() == after
