@@ -46,9 +46,9 @@ struct MfArgs {
     int64_t split_stride;
     int *split_cnt;
     float *y;
-    // MXFP4 on the scaled MFMA: activations packed by pack_rows_fp6 (ap_row bytes per row)
+    // MXFP4 on the scaled MFMA: activations packed by pack_rows_fp6 (ap_rows rows of ap_row bytes)
     const uint8_t *ap;
-    int64_t ap_row;
+    int64_t ap_row, ap_rows;
 };
 
 // Work a pack launch also does for the dense matmul that follows it: the tile list of m rows, and

@@ -248,6 +248,7 @@ static int moe_grouped(const cw_moe_desc *d, const MoeArgs &a, const MoeLayout &
     if (gx) {
         g.ap = (const uint8_t *)x16;
         g.ap_row = (int64_t)fp6_rows_bytes(1, a.H);
+        g.ap_rows = T;
         rc = mxfp4_gateup(g, tmax, s);
     } else {
         rc = mfma_gateup(d->dtype[0], g, tmax, s);
@@ -275,6 +276,7 @@ static int moe_grouped(const cw_moe_desc *d, const MoeArgs &a, const MoeLayout &
     if (dx) {
         dn.ap = (const uint8_t *)h16;
         dn.ap_row = (int64_t)fp6_rows_bytes(1, P);
+        dn.ap_rows = TK;
         rc = mxfp4_down(dn, tmax, s);
     } else {
         rc = mfma_down(d->dtype[2], dn, tmax, s);
@@ -566,6 +568,7 @@ int cw_matmul_id_grouped(int dtype, int64_t n, int64_t k, int64_t n_slots, int64
     if (gx) {
         a.ap = (const uint8_t *)x16;
         a.ap_row = (int64_t)fp6_rows_bytes(1, k);
+        a.ap_rows = xpp ? TK : T;
         rc = mxfp4_down(a, max_tiles(TK, (int)n_slots), s);
     } else {
         rc = mfma_down(dtype, a, max_tiles(TK, (int)n_slots), s);

@@ -127,27 +127,27 @@ __global__ __launch_bounds__(256) void k_pack_fp6x3(const float *x, int rows, in
 
 // ------------------------------------------------------------------------------ the GEMM
 
-// 16 bytes from global memory to LDS, lane l writing lds_base + 16 l, and a stager's activation
-// operands of one step into registers (7 loads; p16/p8/p4 its K-group's bytes of term 0: term t's
-// codes, 16 bytes at 96 t and 8 bytes at 96 t + 64, the scale dword at 288). Issued as inline asm:
-// the kernel counts its vector memory operations itself (a running count, and the count after
-// each batch it will need) and waits for exactly the ones it needs, which the compiler, not seeing
-// loads it did not issue, could not do. lds_base is an LDS address, the same for the whole wave.
-__device__ __forceinline__ void gx_dma16(const void *g, uint32_t lds_base) {
-    const uint32_t m = __builtin_amdgcn_readfirstlane(lds_base);
-    uint32_t keep;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
-                 : "=&s"(keep) : "v"(g), "s"(m) : "memory");
+// 16 bytes from global memory (base + off, base a wave-uniform 16-byte aligned address) to LDS,
+// lane l writing lds_base + 16 l, and a lane's activation operands of one step into registers (7
+// loads from base + o16 / o8 / o4, its K-group's bytes of term 0: term t's codes, 16 bytes at
+// 96 t and 8 bytes at 96 t + 64, the scale dword at 288). Issued as inline asm: the kernel counts
+// its vector memory operations itself (a running count, and the count after each batch it will
+// need) and waits for exactly the ones it needs, which the compiler, not seeing loads it did not
+// issue, could not do. Both take a uniform 64-bit base and 32-bit lane offsets, so that no lane
+// holds a 64-bit address. lds_base is an LDS address, the same for the whole wave.
+__device__ __forceinline__ void gx_dma16(const uint8_t *base, uint32_t off, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base),
+                 "s"(__builtin_amdgcn_readfirstlane(lds_base)) : "memory", "m0");
 }
-__device__ __forceinline__ void gx_ldx(u32x4 (&lo)[3], u32x2 (&hi)[3], uint32_t &sc, const uint8_t *p16, const uint8_t *p8,
-                                       const uint8_t *p4) {
-    asm volatile(
-        "global_load_dwordx4 %0, %7, off\n\tglobal_load_dwordx4 %1, %7, off offset:96\n\tglobal_load_dwordx4 %2, %7, off offset:192\n\t"
-        "global_load_dwordx2 %3, %8, off offset:64\n\tglobal_load_dwordx2 %4, %8, off offset:160\n\tglobal_load_dwordx2 %5, %8, off offset:256\n\t"
-        "global_load_dword %6, %9, off offset:288"
-        : "=&v"(lo[0]), "=&v"(lo[1]), "=&v"(lo[2]), "=&v"(hi[0]), "=&v"(hi[1]), "=&v"(hi[2]), "=&v"(sc)
-        : "v"(p16), "v"(p8), "v"(p4)
-        : "memory");
+__device__ __forceinline__ void gx_dma4(const uint8_t *base, uint32_t off, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" : : "v"(off), "s"(base),
+                 "s"(__builtin_amdgcn_readfirstlane(lds_base)) : "memory", "m0");
+}
+// s_waitcnt vmcnt(n) for n in {0, 4, 5} (a stage's wait: the window loads of one stage in flight)
+__device__ __forceinline__ void gx_wait_stage(int n) {
+    if (n == 5) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+    else if (n == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 // s_waitcnt vmcnt(n) for a run-time n (the instruction takes an immediate; above 63 it waits for
 // more than asked, never less)
@@ -163,12 +163,14 @@ __device__ __forceinline__ void gx_wait_vm(int n) {
 
 // A block has 8 waves: 4 row groups of RW weight rows (of each matrix: gate and up for MODE 0) by
 // 2 halves of the tile's 16-token blocks. A stage is one 128-wide K step. The weight bytes of a
-// stage go to LDS by direct loads, two stages ahead (three buffers), per row a window of the 6
-// 16-byte pieces holding its 4 blocks (68 bytes at any offset); the activation operands of a stage
-// (token block t: per lane three 16 + 8 byte code runs and a scale dword) are loaded into
-// registers by the first waves, one stage ahead, and stored to LDS, so that the direct loads carry
-// the weights alone. A wave waits for exactly the loads it needs next, then one barrier per stage
-// publishes them.
+// stage go to LDS by direct loads, three stages ahead (three buffers), per row a window of the 6
+// 16-byte pieces holding its 4 blocks (68 bytes at any offset). The activation operands of a
+// stage (token block t: per lane three 16 + 8 byte code runs and a scale dword) go to LDS by direct
+// loads too, two stages ahead (two buffers), issued by the first waves. Each wave reads the operands of
+// the next stage from LDS while it computes the current one: a token block's activation operands
+// right after that block's MFMAs, the weight operands at the end of the stage, so that their
+// latency hides behind the matrix work. One barrier per stage publishes every wave's loads (each
+// wave first waits for exactly its own).
 template <int MODE>
 struct GxShape {
     static constexpr int NW = 8, NT = 64 * NW;
@@ -195,41 +197,50 @@ template <int MODE, int NTB>
 __device__ __forceinline__ void gx_item(const MfArgs &a, const MfTile &tile, int nb, int mbs, int tb0, int wave, int lane,
                                         uint8_t *smem, uint32_t lds0) {
     using S = GxShape<MODE>;
+    constexpr int NB = NTB > 0 ? NTB : 1;
     const int grp = lane >> 4, l16 = lane & 15, rg = wave & 3;
     const int nblk = a.k / 32, n_st = (nblk + 3) / 4;
     uint8_t *const Wb = smem;
     uint8_t *const Ab = smem + S::WDEPTH * S::W_BYTES;
+    const uint32_t Al = lds0 + S::WDEPTH * S::W_BYTES;
 
     const uint8_t *wb0 = a.w0 + (int64_t)tile.slot * a.s0;
     const uint8_t *wb1 = S::NM > 1 ? a.w1 + (int64_t)tile.slot * a.s1 : wb0;
+    const uint8_t *wa0 = (const uint8_t *)((uintptr_t)wb0 & ~(uintptr_t)15);  // rounded down to 16 bytes
+    const uint8_t *wa1 = (const uint8_t *)((uintptr_t)wb1 & ~(uintptr_t)15);
+    const uint32_t wm0 = (uint32_t)(uintptr_t)wb0 & 15u, wm1 = (uint32_t)(uintptr_t)wb1 & 15u;
     // window loads: wave instruction wi = wave + 8 j covers pieces 64 wi .. 64 wi + 63
     uint32_t wo[S::NJW], wp[S::NJW];
 #pragma unroll
     for (int j = 0; j < S::NJW; j++) {
-        const int pi = 64 * min(wave + 8 * j, S::W_INST - 1) + lane, r = pi / S::PCS;
-        wp[j] = (uint32_t)(pi - r * S::PCS);
-        const int n = nb * S::RPB + r % S::RPB;
+        const int pi = 64 * min(wave + 8 * j, S::W_INST - 1) + lane, row = pi / S::PCS;
+        wp[j] = (uint32_t)(pi - row * S::PCS);
+        const int n = nb * S::RPB + row % S::RPB;
         wo[j] = (uint32_t)(n < a.n ? n : 0) * (uint32_t)a.row_bytes;
-    }
-    // activation staging: wave w < mbs stages token block w (lane = its K-group and token)
-    const bool stager = wave < mbs;
-    const uint8_t *xrow = a.ap;
-    if (stager) {
-        const int r = min(16 * wave + l16, tile.m - 1), pos = tile.pos0 + r;
-        xrow = a.ap + (int64_t)(a.rows ? a.rows[pos] : pos) * a.ap_row;
     }
     // this lane's rows' offsets from 16-byte alignment
     uint32_t lmis[S::NF];
 #pragma unroll
     for (int f = 0; f < S::NF; f++) {
         const int mm = f / S::FR, n = nb * S::RPB + rg * S::RW + 16 * (f % S::FR) + l16;
-        lmis[f] = ((uint32_t)(uintptr_t)(mm ? wb1 : wb0) + (uint32_t)(n < a.n ? n : 0) * (uint32_t)a.row_bytes) & 15u;
+        lmis[f] = ((mm ? wm1 : wm0) + (uint32_t)(n < a.n ? n : 0) * (uint32_t)a.row_bytes) & 15u;
+    }
+    // activation staging: wave w < mbs stages token block w (lane = its K-group and token)
+    const bool stager = wave < mbs;
+    uint32_t xr = 0;
+    if (stager) {
+        const int row = min(16 * wave + l16, tile.m - 1), pos = tile.pos0 + row;
+        xr = (uint32_t)(a.rows ? a.rows[pos] : pos) * (uint32_t)a.ap_row;
     }
 
+    // Loads are counted per wave: in stage s a wave issues the activation loads of s + 2 (10 if it
+    // stages a token block), then nw window loads of s + 3 (nw is 4 or 5, by wave). Before the
+    // barrier of stage st, a wave needs its windows of st + 1 (requested in st - 2) and its
+    // activations of st + 1 (requested in st - 1): only the windows of st + 2 may stay in flight.
+    const int nw = (S::W_INST - wave + 7) / 8;
     int issued = 0;                    // this wave's loads in the item (it starts drained)
-    int m_w0 = 0, m_w1 = 0, m_w2 = 0;  // the count after each window buffer's loads (named, not
-                                       // indexed: an indexed array would live in scratch memory)
-    int m_x = 0;                       // ... after the activation loads
+    int m_w0 = 0, m_a0 = 0;            // the count after stage 0's window and activation loads
+    // window loads of stage st into buffer st % 3 (this wave's share)
     auto issue_w = [&](int st) __attribute__((always_inline)) {
         const int buf = st % S::WDEPTH;
         const uint32_t Wd = lds0 + buf * S::W_BYTES;
@@ -238,104 +249,140 @@ __device__ __forceinline__ void gx_item(const MfArgs &a, const MfTile &tile, int
         for (int j = 0; j < S::NJW; j++) {
             const int wi = wave + 8 * j;
             if (wi < S::W_INST) {
-                const uint8_t *mb = S::NM > 1 && wi >= S::W_INST / 2 ? wb1 : wb0;
-                const uint32_t o = wo[j] + 68u * (uint32_t)st;
-                const uint32_t mis = ((uint32_t)(uintptr_t)mb + o) & 15u;
-                const uint32_t pc = min(wp[j], (mis + seg - 1) >> 4);
-                const uint8_t *al = (const uint8_t *)(((uintptr_t)mb + o) & ~(uintptr_t)15);
-                gx_dma16(al + 16 * pc, Wd + wi * 1024);
+                const bool m1 = S::NM > 1 && wi >= S::W_INST / 2;
+                // the row's bytes of stage st start at o past the aligned base
+                const uint32_t o = wo[j] + 68u * (uint32_t)st + (m1 ? wm1 : wm0);
+                const uint32_t pc = min(wp[j], ((o & 15u) + seg - 1) >> 4);
+                gx_dma16(m1 ? wa1 : wa0, (o & ~15u) + 16 * pc, Wd + wi * 1024);
                 issued++;
             }
         }
-        m_w0 = buf == 0 ? issued : m_w0;
-        m_w1 = buf == 1 ? issued : m_w1;
-        m_w2 = buf == 2 ? issued : m_w2;
+        if (st == 0) m_w0 = issued;
     };
-    u32x4 xl[3];
-    u32x2 xh[3];
-    uint32_t xs = 0;
-    auto load_x = [&](int st) __attribute__((always_inline)) {
+    // a stager's activation operands of stage st into activation buffer st % 2: per term the
+    // 16-byte code runs of the 64 lanes (1 KB), then their dwords 4 and 5 (256 bytes each), then
+    // the lanes' scale dwords, each a direct load from the packed row
+    auto issue_x = [&](int st) __attribute__((always_inline)) {
         if (stager) {
-            const uint8_t *p = xrow + 304 * st;
-            gx_ldx(xl, xh, xs, p + 16 * grp, p + 8 * grp, p + 4 * grp);
-            issued += 7;
-            m_x = issued;
-        }
-    };
-    auto store_x = [&](int buf) __attribute__((always_inline)) {
-        if (stager) {
-            gx_wait_vm(issued - m_x);
-            asm volatile("" : "+v"(xl[0]), "+v"(xl[1]), "+v"(xl[2]), "+v"(xh[0]), "+v"(xh[1]), "+v"(xh[2]), "+v"(xs));
-            uint8_t *d = Ab + buf * S::A_BYTES + wave * S::TB_BYTES;
+            const uint32_t o = xr + 304u * (uint32_t)st;
+            const uint32_t d = Al + (st & 1) * S::A_BYTES + wave * S::TB_BYTES;
 #pragma unroll
             for (int t = 0; t < 3; t++) {
-                *(u32x4 *)(d + 1536 * t + 16 * lane) = xl[t];
-                *(u32x2 *)(d + 1536 * t + 1024 + 8 * lane) = xh[t];
+                gx_dma16(a.ap, o + 96u * t + 16u * grp, d + 1536 * t);
+                gx_dma4(a.ap, o + 96u * t + 64u + 8u * grp, d + 1536 * t + 1024);
+                gx_dma4(a.ap, o + 96u * t + 68u + 8u * grp, d + 1536 * t + 1280);
             }
-            *(uint32_t *)(d + 3 * 1536 + 4 * lane) = xs;
+            gx_dma4(a.ap, o + 288u + 4u * grp, d + 3 * 1536);
+            issued += 10;
+        }
+        if (st == 0) m_a0 = issued;
+    };
+
+    // operands in registers: each token block's activations of the stage being computed, the raw
+    // weight dwords (5 around the block, and its E8M0 byte) of the next stage
+    i32x8 bo[NB][3];  // an FP6 operand is dwords 0..5; the instruction ignores 6 and 7
+    int bsc[NB];
+    uint32_t ra[S::NF][5], re[S::NF];
+    auto read_b = [&](int t, int st) __attribute__((always_inline)) {
+        const uint8_t *d = Ab + (st & 1) * S::A_BYTES + (tb0 + t) * S::TB_BYTES;
+#pragma unroll
+        for (int j = 0; j < 3; j++) {
+            const i32x4 l = *(const i32x4 *)(d + 1536 * j + 16 * lane);
+            const i32x2 h = {*(const int *)(d + 1536 * j + 1024 + 4 * lane), *(const int *)(d + 1536 * j + 1280 + 4 * lane)};
+            bo[t][j] = __builtin_shufflevector(l, __builtin_shufflevector(h, h, 0, 1, -1, -1), 0, 1, 2, 3, 4, 5, -1, -1);
+        }
+        bsc[t] = *(const int *)(d + 3 * 1536 + 4 * lane);
+    };
+    // LDS offset of the E8M0 byte of this lane's block of fragment f in stage st's window
+    auto aoff = [&](int f, int st) __attribute__((always_inline)) -> uint32_t {
+        const int lrow = (f / S::FR) * S::RPB + rg * S::RW + 16 * (f % S::FR) + l16;
+        return (uint32_t)lrow * (S::PCS * 16) + ((lmis[f] + 4u * (uint32_t)st) & 15u) + 17u * grp;
+    };
+    auto read_a = [&](int st) __attribute__((always_inline)) {
+        const uint8_t *Wd = Wb + (st % S::WDEPTH) * S::W_BYTES;
+#pragma unroll
+        for (int f = 0; f < S::NF; f++) {
+            const uint32_t off = aoff(f, st), cb = off + 1;
+            const uint32_t *q = (const uint32_t *)(Wd + (cb & ~3u));
+#pragma unroll
+            for (int i = 0; i < 5; i++) ra[f][i] = q[i];
+            re[f] = Wd[off];
         }
     };
 
-    f32x4v acc[S::NF][NTB > 0 ? NTB : 1];
+    f32x4v acc[S::NF][NB];
 #pragma unroll
     for (int f = 0; f < S::NF; f++)
 #pragma unroll
-        for (int t = 0; t < (NTB > 0 ? NTB : 1); t++) acc[f][t] = f32x4v{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < NB; t++) acc[f][t] = f32x4v{0.f, 0.f, 0.f, 0.f};
 
-    load_x(0);
+    // activations of stages 0 and 1 and windows of 0, 1 and 2 requested, then the operands of
+    // stage 0 read
+    issue_x(0);
     issue_w(0);
+    if (n_st > 1) issue_x(1);
     if (n_st > 1) issue_w(1);
-    store_x(0);
+    if (n_st > 2) issue_w(2);
+    gx_wait_vm(issued - (m_w0 > m_a0 ? m_w0 : m_a0));  // this wave's loads of stage 0
+    __syncthreads();                                    // everyone's
+    if constexpr (NTB > 0) {
+#pragma unroll
+        for (int t = 0; t < NTB; t++) read_b(t, 0);
+        read_a(0);
+    }
+    // Per stage st (its operands in registers): the activation loads of st + 2 and the window loads
+    // of st + 3 go out, and the MFMAs of st run with the reads of st + 1's operands between them.
     for (int st = 0; st < n_st; st++) {
-        {
-            const int buf = st % S::WDEPTH;
-            gx_wait_vm(issued - (buf == 0 ? m_w0 : buf == 1 ? m_w1 : m_w2));  // this wave's windows of stage st
-        }
-        __syncthreads();  // everyone's, and the activations stored; stage st-1's buffers are free
         const bool more = st + 1 < n_st;
-        if (more) load_x(st + 1);
-        if (st + 2 < n_st) issue_w(st + 2);
+        // this wave's loads of st + 1: its windows (requested two stages ago), then its
+        // activations (one stage ago, before the windows of st + 2, which stay in flight)
+        if (more) gx_wait_stage(st + 2 < n_st ? nw : 0);
+        // everyone's loads of st + 1 are in; window buffer st % 3 and activation buffer st % 2
+        // (read during st - 1) are free
+        __syncthreads();
+        if (st + 2 < n_st) issue_x(st + 2);
+        if (st + 3 < n_st) issue_w(st + 3);
         if constexpr (NTB > 0) {
-            const uint8_t *Wd = Wb + (st % S::WDEPTH) * S::W_BYTES;
-            const uint8_t *Ad = Ab + (st & 1) * S::A_BYTES;
-            const bool live = 4 * st + grp < nblk;  // past the row's last block: codes 0
+            const bool live = 4 * st + grp < nblk;  // past the row's last block
+            // the stage read next (unconditionally, so that no register keeps two values: the last
+            // stage reads itself again, unused)
+            const int sn = more ? st + 1 : st;
             i32x8 av[S::NF];
             int sa[S::NF];
 #pragma unroll
             for (int f = 0; f < S::NF; f++) {
-                // the block's E8M0 byte at `off`, its 16 code bytes after it
-                const int lrow = (f / S::FR) * S::RPB + rg * S::RW + 16 * (f % S::FR) + l16;
-                const uint32_t off = (uint32_t)lrow * (S::PCS * 16) + ((lmis[f] + 4u * (uint32_t)st) & 15u) + 17u * grp;
-                const uint32_t cb = off + 1, sh = cb & 3;
-                const uint32_t *q = (const uint32_t *)(Wd + (cb & ~3u));
-                const uint32_t d0 = q[0], d1 = q[1], d2 = q[2], d3 = q[3], d4 = q[4];
-                const uint32_t e = Wd[off];
-                const i32x4 w4 = {(int)(live ? __builtin_amdgcn_alignbyte(d1, d0, sh) : 0u), (int)(live ? __builtin_amdgcn_alignbyte(d2, d1, sh) : 0u),
-                                  (int)(live ? __builtin_amdgcn_alignbyte(d3, d2, sh) : 0u), (int)(live ? __builtin_amdgcn_alignbyte(d4, d3, sh) : 0u)};
+                const uint32_t sh = (aoff(f, st) + 1u) & 3u;
+                // past the row the codes are whatever the window holds: the activations there are
+                // zero and the scale is 1, so the products are 0
+                const i32x4 w4 = {(int)__builtin_amdgcn_alignbyte(ra[f][1], ra[f][0], sh),
+                                  (int)__builtin_amdgcn_alignbyte(ra[f][2], ra[f][1], sh),
+                                  (int)__builtin_amdgcn_alignbyte(ra[f][3], ra[f][2], sh),
+                                  (int)__builtin_amdgcn_alignbyte(ra[f][4], ra[f][3], sh)};
                 // an FP4 operand is dwords 0..3; the instruction ignores 4..7
                 av[f] = __builtin_shufflevector(w4, w4, 0, 1, 2, 3, -1, -1, -1, -1);
-                sa[f] = (int)(live ? e : 127u);
+                sa[f] = (int)(live ? (re[f] & 0xFFu) : 127u);
             }
 #pragma unroll
             for (int t = 0; t < NTB; t++) {
-                const uint8_t *d = Ad + (tb0 + t) * S::TB_BYTES;
-                const int sb = (int)*(const uint32_t *)(d + 3 * 1536 + 4 * lane);
+                const int sb = bsc[t];
 #pragma unroll
                 for (int j = 0; j < 3; j++) {
-                    // an FP6 operand is dwords 0..5; the instruction ignores 6 and 7
-                    const i32x4 l4 = *(const i32x4 *)(d + 1536 * j + 16 * lane);
-                    const i32x2 h2 = *(const i32x2 *)(d + 1536 * j + 1024 + 8 * lane);
-                    const i32x8 bo = __builtin_shufflevector(l4, __builtin_shufflevector(h2, h2, 0, 1, -1, -1), 0, 1, 2, 3, 4, 5, -1, -1);
 #pragma unroll
                     for (int f = 0; f < S::NF; f++) {
-                        if (j == 0) acc[f][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[f], bo, acc[f][t], 4, 2, 0, sa[f], 0, sb);
-                        if (j == 1) acc[f][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[f], bo, acc[f][t], 4, 2, 0, sa[f], 1, sb);
-                        if (j == 2) acc[f][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[f], bo, acc[f][t], 4, 2, 0, sa[f], 2, sb);
+                        if (j == 0) acc[f][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[f], bo[t][0], acc[f][t], 4, 2, 0, sa[f], 0, sb);
+                        if (j == 1) acc[f][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[f], bo[t][1], acc[f][t], 4, 2, 0, sa[f], 1, sb);
+                        if (j == 2) acc[f][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av[f], bo[t][2], acc[f][t], 4, 2, 0, sa[f], 2, sb);
                     }
                 }
+                // the block's operands of st + 1 go into its registers once its MFMAs are issued
+                // (the scheduling barrier keeps the compiler from hoisting the reads, which would
+                // need a second register set)
+                __builtin_amdgcn_sched_barrier(0);
+                read_b(t, sn);
             }
+            __builtin_amdgcn_sched_barrier(0);
+            read_a(sn);
         }
-        if (more) store_x((st + 1) & 1);  // stage st+1's operands (stage st-1's buffer, free)
     }
 
     // epilogue: lane holds weight rows 16 f' + 4 grp + i (i < 4) of token 16 (tb0 + t) + l16
@@ -343,9 +390,9 @@ __device__ __forceinline__ void gx_item(const MfArgs &a, const MfTile &tile, int
     if constexpr (NTB > 0) {
 #pragma unroll
         for (int t = 0; t < NTB; t++) {
-            const int r = 16 * (tb0 + t) + l16;
-            if (r >= tile.m) continue;
-            const int pos = tile.pos0 + r;
+            const int rr = 16 * (tb0 + t) + l16;
+            if (rr >= tile.m) continue;
+            const int pos = tile.pos0 + rr;
             const int pick = a.pile_pick ? a.pile_pick[pos] : pos;
 #pragma unroll
             for (int f = 0; f < S::FR; f++) {
@@ -434,8 +481,11 @@ template <int MODE>
 static int gx_launch(const MfArgs &a, int tiles_max, hipStream_t s) {
     using S = GxShape<MODE>;
     if (a.k % 32 || a.k <= 128) return set_error(CW_ENOTSUP, "mxfp4 gemm: k %d is not whole blocks over two steps", a.k);
-    if ((int64_t)a.n * a.row_bytes >= ((int64_t)1 << 32))
+    // lane offsets are 32-bit: from a matrix's 16-byte aligned base, and into the packed rows
+    if ((int64_t)a.n * a.row_bytes + 256 >= ((int64_t)1 << 32))
         return set_error(CW_ENOTSUP, "mxfp4 gemm: a matrix of %d rows of %lld bytes is 4 GiB or more", a.n, (long long)a.row_bytes);
+    if (a.ap_rows * a.ap_row >= ((int64_t)1 << 32))
+        return set_error(CW_ENOTSUP, "mxfp4 gemm: %lld packed activation rows are 4 GiB or more", (long long)a.ap_rows);
     static std::atomic<int> cus_of[64];
     static std::atomic<bool> lds_set[64];
     const int dev = gx_device();

@@ -275,6 +275,46 @@ def candle_matmul(dtype, w, n, k, x, threads=0):
     return y
 
 
+def candle_moe_layer(layer, x, logits, threads=0):
+    """candle's own CPU path for one MoE layer (crates/engine/src/experts.rs:2500-2537): route,
+    then per picked expert in expert-id order (the BTreeMap of experts.rs:2503-2510) the gate and up
+    QMatMuls (candle_matmul: x quantized to the weight's vec-dot type, Q8_0 for MXFP4,
+    k_quants.rs:738-759, 2551-2670), the activation with its biases, the down QMatMul and its bias,
+    scaled by the routing weight and index-added into the output in expert order. f32 throughout,
+    as candle computes it. Returns (out f32, ids, w)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    t = x.shape[0]
+    ids, w = route(logits, layer.top_k, layer.norm)
+    H, I = layer.hidden, layer.inter
+    width = max(layer.pad, I)
+    per_expert = {}
+    for tok in range(t):
+        for j in range(layer.top_k):
+            per_expert.setdefault(int(ids[tok, j]), []).append((tok, float(w[tok, j])))
+    out = np.zeros((t, H), dtype=np.float32)
+    for e in sorted(per_expert):
+        toks = np.array([p[0] for p in per_expert[e]], dtype=np.int64)
+        we = np.array([p[1] for p in per_expert[e]], dtype=np.float32)
+        xe = x[toks]
+        mats = [layer.host[m][e * layer.slot_stride[m]:(e + 1) * layer.slot_stride[m]] for m in range(3)]
+        g = candle_matmul(layer.dtypes[0], mats[0], I, H, xe, threads)
+        u = candle_matmul(layer.dtypes[1], mats[1], I, H, xe, threads)
+        picked = np.full(len(toks), e, dtype=np.uint32)
+        if layer.act == 1:
+            b = layer.bias
+            h = clamped_swiglu(g, u, b[0] if b else None, b[1] if b else None, picked, layer.pad,
+                               layer.alpha, layer.limit)
+        else:
+            h = silu_mul(g, u)
+            if width > I:
+                h = np.pad(h, ((0, 0), (0, width - I)))
+        y = candle_matmul(layer.dtypes[2], mats[2], H, width, h, threads)
+        if layer.act == 1 and layer.bias is not None:
+            y = y + layer.bias[2][e][None, :]
+        np.add.at(out, toks, y * we[:, None])
+    return out, ids, w
+
+
 def x86_level():
     """candle's x86 tier on this host: 2 AVX-512 VNNI, 1 AVX-VNNI, 0 AVX2, -1 none."""
     return lib().or_x86_level()

@@ -528,6 +528,7 @@ MOE_CASES = [
     ("iq2_xxs_decode", 64, 8, 2048, 512, (F.IQ2_XXS, F.IQ2_XXS, F.IQ2_XXS), 0, 0, 1),  # its own decode instance
     ("iq2_s_decode_e512", 512, 8, 2048, 512, (F.IQ2_S, F.IQ2_S, F.IQ2_S), 0, 0, 1),  # 8 logits per lane, one router wave
     ("c4_decode_shape", 16, 4, 2880, 2880, (F.MXFP4, F.MXFP4, F.MXFP4), 1, 0, 1),
+    ("c4_decode_e128", 128, 4, 2880, 2880, (F.MXFP4, F.MXFP4, F.MXFP4), 1, 0, 1),  # config 4's routing width
     ("c4_decode_top5", 32, 5, 2880, 2880, (F.MXFP4, F.MXFP4, F.MXFP4), 1, 0, 1),  # 3-4 gate/up items per wave
     ("c4_decode_odd_rows", 16, 4, 2880, 2877, (F.MXFP4, F.MXFP4, F.MXFP4), 1, 2880, 1),  # a last item of one row, padded hidden
     ("c4_prefill_shape", 16, 4, 2880, 2880, (F.MXFP4, F.MXFP4, F.MXFP4), 1, 0, 40),

@@ -217,3 +217,18 @@ def test_candle_cpu_path_deviation_is_activation_quantization_sized(dtype):
     x = rng.standard_normal((2, k)).astype(np.float32)
     err = O.rel_l2(O.candle_matmul(dtype, w, n, k, x), O.qmatmul_f64(dtype, w, n, k, x))
     assert 1e-4 < err < 3e-2
+
+
+@pytest.mark.parametrize("act", [0, 1])
+def test_candle_moe_layer_routes_alike_and_deviates_by_activation_quantization(act):
+    # candle's CPU MoE composition (experts.rs:2500-2537) is the config-4 CPU baseline
+    rng = np.random.default_rng(31 + act)
+    dts = (F.Q4_K, F.Q4_K, F.Q4_K) if act == 0 else (F.MXFP4, F.MXFP4, F.MXFP4)
+    layer = synth.moe_weights(16, 4, 512, 256 if act == 0 else 96, dts, rng, act=act,
+                              pad=0 if act == 0 else 128)
+    x = rng.standard_normal((5, 512)).astype(np.float32)
+    logits = rng.standard_normal((5, 16)).astype(np.float32)
+    want, wids, ww, _ = O.moe_layer(layer, x, logits)
+    got, ids, w = O.candle_moe_layer(layer, x, logits)
+    assert np.array_equal(ids, wids) and np.array_equal(w, ww)
+    assert 1e-4 < O.rel_l2(got, want) < 5e-2
