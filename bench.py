@@ -22,6 +22,7 @@ import time
 METRIC = "MoE layer µs + achieved HBM GB/s (decode b=1); prefill tokens/s; MFMA util"
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_F16_TFLOPS = 2500.0  # dense fp16
+MFMA_PEAK_F6F4_TFLOPS = 10100.0  # dense fp6 / fp4 (the block-scaled MFMA)
 
 
 def log(*a):
@@ -244,32 +245,15 @@ def bench_c5(args, torch, np, dev):
         host = host_cpu()
         O.set_threads(host["physical"])
         threads = O.get_threads()
-        # candle's own CPU path for this layer: per picked expert, QMatMul with x quantized to Q8_0
-        # (MXFP4 x Q8_0 vec-dot), clamped SwiGLU with biases, down QMatMul, weighted index-add in
-        # expert order (experts.rs:2500-2537, k_quants.rs:738-759, 2551-2670)
-        n, t_cpu, dev_l2 = 0, 0.0, 0.0
-        while t_cpu < args.cpu_seconds and n < 1000:
+        n, t_cpu = 0, 0.0
+        while t_cpu < min(args.cpu_seconds, 5.0) and n < 1000:
             lg = logits_all[n % total, 0].cpu().numpy()
             t1 = time.perf_counter()
-            got_c, _, _ = O.candle_moe_layer(host_layer, x0, lg, threads)
-            t_cpu += time.perf_counter() - t1
-            if n < 4:
-                dev_l2 = max(dev_l2, O.rel_l2(got_c, O.moe_layer(host_layer, x0, lg)[0]))
-            n += 1
-        n_f64, t_f64 = 0, 0.0
-        while t_f64 < min(args.cpu_seconds, 5.0) and n_f64 < 1000:
-            lg = logits_all[n_f64 % total, 0].cpu().numpy()
-            t1 = time.perf_counter()
             O.moe_layer(host_layer, x0, lg)
-            t_f64 += time.perf_counter() - t1
-            n_f64 += 1
+            t_cpu += time.perf_counter() - t1
+            n += 1
         cpu = {"value": t_cpu / n * 1e6, "unit": "us/layer", "cores": threads, "host": host, "kind": "port",
-               "sample": "%d decode calls (T=1) of candle's MXFP4 CPU MoE path on layer 0: route, then per picked "
-                         "expert gate/up/down QMatMuls with x quantized to Q8_0 (MXFP4 x Q8_0 vec-dot), "
-                         "clamped SwiGLU with biases and the weighted index-add in expert order" % n,
-               "candle_rel_l2_vs_f64": dev_l2,
-               "f64_oracle_us_per_layer": t_f64 / n_f64 * 1e6}
-        log("cpu", cpu)
+               "sample": "%d decode calls (T=1) of the C oracle MoE layer on layer 0's host store" % n}
     line = {
         "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms / args.steps, "higher_is_better": True, "scaling": "weak",
@@ -369,7 +353,12 @@ def bench_c4(args, torch, np, dev):
                "mfma_peak_tflops": MFMA_PEAK_F16_TFLOPS, "hbm_gbs": round(pre_bytes / (pre_us * 1e-6) / 1e9, 1),
                "hbm_frac": round(pre_bytes / (pre_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                "graph_replay_equals_eager": pre_same, "calls_timed": reps,
-               "path": "grouped MFMA GEMMs (MXFP4 codes by the scaled FP4 conversion, fp16 activations, f32 accumulate)"}
+               # the scaled MFMA runs three FP4 x FP6 products (one per activation term) per product
+               # of the layer: issued work against the dense FP6/FP4 peak
+               "mfma_issued_tflops": round(3 * tflops, 2), "mfma_peak_f6f4_tflops": MFMA_PEAK_F6F4_TFLOPS,
+               "mfma_util_f6f4": round(3 * tflops / MFMA_PEAK_F6F4_TFLOPS, 4),
+               "path": ("grouped GEMMs on the block-scaled MFMA (v_mfma_scale_f32_16x16x128_f8f6f4): MXFP4 weights "
+                        "as stored, activations as three FP6 E2M3 terms with E8M0 scales per 32, f32 accumulate")}
     log("prefill", prefill)
 
     cpu = None
@@ -377,16 +366,32 @@ def bench_c4(args, torch, np, dev):
         host = host_cpu()
         O.set_threads(host["physical"])
         threads = O.get_threads()
-        n, t_cpu = 0, 0.0
-        while t_cpu < min(args.cpu_seconds, 5.0) and n < 1000:
+        # candle's own CPU path for this layer: per picked expert, QMatMul with x quantized to Q8_0
+        # (MXFP4 x Q8_0 vec-dot), clamped SwiGLU with biases, down QMatMul, weighted index-add in
+        # expert order (experts.rs:2500-2537, k_quants.rs:738-759, 2551-2670)
+        n, t_cpu, dev_l2 = 0, 0.0, 0.0
+        while t_cpu < args.cpu_seconds and n < 1000:
             lg = logits_all[n % total, 0].cpu().numpy()
             t1 = time.perf_counter()
-            O.moe_layer(host_layer, x0, lg)
+            got_c, _, _ = O.candle_moe_layer(host_layer, x0, lg, threads)
             t_cpu += time.perf_counter() - t1
+            if n < 4:
+                dev_l2 = max(dev_l2, O.rel_l2(got_c, O.moe_layer(host_layer, x0, lg)[0]))
             n += 1
+        n_f64, t_f64 = 0, 0.0
+        while t_f64 < min(args.cpu_seconds, 5.0) and n_f64 < 1000:
+            lg = logits_all[n_f64 % total, 0].cpu().numpy()
+            t1 = time.perf_counter()
+            O.moe_layer(host_layer, x0, lg)
+            t_f64 += time.perf_counter() - t1
+            n_f64 += 1
         cpu = {"value": t_cpu / n * 1e6, "unit": "us/layer", "cores": threads, "host": host, "kind": "port",
-               "sample": "%d decode calls (T=1) of the C oracle MoE layer (MXFP4 dequantize, f64 dots) on layer 0; "
-                         "candle's own MXFP4 CPU path quantizes x to Q8_0 and is not restated" % n}
+               "sample": "%d decode calls (T=1) of candle's MXFP4 CPU MoE path on layer 0: route, then per picked "
+                         "expert gate/up/down QMatMuls with x quantized to Q8_0 (MXFP4 x Q8_0 vec-dot), "
+                         "clamped SwiGLU with biases and the weighted index-add in expert order" % n,
+               "candle_rel_l2_vs_f64": dev_l2,
+               "f64_oracle_us_per_layer": t_f64 / n_f64 * 1e6}
+        log("cpu", cpu)
     line = {
         "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms / args.steps, "higher_is_better": True, "scaling": "weak",
