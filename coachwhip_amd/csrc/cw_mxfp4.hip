@@ -41,99 +41,76 @@ typedef int i32x2 __attribute__((ext_vector_type(2)));
 
 // ------------------------------------------------------------------------------ the pack
 
-// FP6 E2M3 code of y, |y| <= 7.5, rounded to the nearest value (ties to even), and the value it
-// codes. E2M3: sign, 2 exponent bits (bias 1), 3 mantissa bits; steps of 1/8 below 2, 1/4 below
-// 4, 1/2 up to 7.5. Adding and subtracting 1.5 * 2^(s + 23) rounds to a multiple of 2^s in the
-// f32 addition's own round-to-nearest-even.
-__device__ __forceinline__ uint32_t e2m3_code(float y, float &q) {
-    const float a = fabsf(y);
-    const int e = (int)(__float_as_uint(a) >> 23) - 127;  // floor(log2 a) for normal a
-    const int s = max(e - 3, -3);
-    const float c = __uint_as_float(((uint32_t)(s + 150) << 23) | 0x400000u);
-    float r = a + c;
-    asm("" : "+v"(r));  // keep (a + c) - c as two roundings (not volatile: free to schedule)
-    r = r - c;
-    const uint32_t rb = __float_as_uint(r);
-    const uint32_t code = r < 1.0f ? (uint32_t)(r * 8.0f) : ((((rb >> 23) - 126u) << 3) | ((rb >> 20) & 7u));
-    q = copysignf(r, y);
-    return code | ((__float_as_uint(y) >> 26) & 0x20u);
-}
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x32 __attribute__((ext_vector_type(32)));
+typedef uint32_t u32x6 __attribute__((ext_vector_type(6)));
 
-// Two lanes per (row, 32-value block): lane h of the pair holds values 16 h .. 16 h + 15, which
-// are the B elements e = 2 k + h (element e meets nibble e of the weight block: weight position
-// (e >> 1) + 16 (e & 1)). Three terms, each scaled by the power of two that puts the block's
-// largest remaining magnitude (the pair's maximum) in (3.75, 7.5]; each lane codes its 16
-// elements into its bits of the term's 192-bit record, and the pair ORs its halves together.
+// One lane per (row, 32-value block): three terms, each scaled by the power of two that puts the
+// block's largest remaining magnitude in (3.75, 7.5], where FP6 E2M3 (sign, 2 exponent bits with
+// bias 1, 3 mantissa bits: steps of 1/8 below 2, 1/4 below 4, 1/2 up to 7.5) is exact to half a
+// step. gfx950 converts a term in one instruction (`v_cvt_scalef32_2xpk16_fp6_f32`: code 2i of the
+// 192-bit record from the first 16 values, code 2i + 1 from the second 16, each value divided by
+// the scale and rounded to the nearest E2M3 value, ties to even), which is the record's element
+// order: element e meets nibble e of the weight block, weight position (e >> 1) + 16 (e & 1). The
+// residual subtracts the term's value as decoded by `v_cvt_scalef32_pk32_f32_fp6` (code times the
+// scale), exactly: a value minus its rounding to 3 mantissa bits is representable.
 __global__ __launch_bounds__(256) void k_pack_fp6x3(const float *x, int rows, int k, int ldx, uint8_t *out) {
     const int nb = k / 32, nbp = (nb + 3) & ~3;  // blocks, and block records per row (whole steps)
-    const int64_t n = (int64_t)rows * nbp * 2;
-    // a uniform trip count, so that both lanes of a pair always run the shuffles together
-    const int64_t stride = (int64_t)gridDim.x * 256;
-    for (int64_t i0 = (int64_t)blockIdx.x * 256; i0 < n; i0 += stride) {
-        const int64_t i = i0 + threadIdx.x;
-        const bool in = i < n;
-        const int64_t pair = (in ? i : n - 1) >> 1;
-        const int h = (int)(i & 1);
-        const int64_t row = pair / nbp;
-        const int j = (int)(pair - row * nbp);
+    const int64_t n = (int64_t)rows * nbp;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        const int64_t row = i / nbp;
+        const int j = (int)(i - row * nbp);
         uint8_t *dst = out + row * (int64_t)(nbp / 4) * 304 + (j >> 2) * 304;
         const int g = j & 3;
-        const bool live = j < nb;  // past the row: zero codes and scale bytes
-        float v[16];
-        if (live) {
-            const float4 *src = (const float4 *)(x + row * ldx + 32 * j + 16 * h);
+        if (j >= nb) {  // past the row: zero codes and scale bytes
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const float4 f = src[c];
-                v[4 * c] = f.x;
-                v[4 * c + 1] = f.y;
-                v[4 * c + 2] = f.z;
-                v[4 * c + 3] = f.w;
+            for (int t = 0; t < 3; t++) {
+                *(uint4 *)(dst + 96 * t + 16 * g) = make_uint4(0u, 0u, 0u, 0u);
+                *(uint2 *)(dst + 96 * t + 64 + 8 * g) = make_uint2(0u, 0u);
             }
-        } else {
+            *(uint32_t *)(dst + 288 + 4 * g) = 0u;
+            continue;
+        }
+        const float4 *src = (const float4 *)(x + row * ldx + 32 * j);
+        f32x16 lo, hi;
 #pragma unroll
-            for (int e = 0; e < 16; e++) v[e] = 0.f;
+        for (int c = 0; c < 4; c++) {
+            const float4 f = src[c], h = src[4 + c];
+            lo[4 * c] = f.x;
+            lo[4 * c + 1] = f.y;
+            lo[4 * c + 2] = f.z;
+            lo[4 * c + 3] = f.w;
+            hi[4 * c] = h.x;
+            hi[4 * c + 1] = h.y;
+            hi[4 * c + 2] = h.z;
+            hi[4 * c + 3] = h.w;
         }
         uint32_t sc = 0;
 #pragma unroll
         for (int t = 0; t < 3; t++) {
             float m = 0.f;
 #pragma unroll
-            for (int e = 0; e < 16; e++) m = fmaxf(m, fabsf(v[e]));
-            m = fmaxf(m, __shfl_xor(m, 1));
+            for (int e = 0; e < 16; e++) m = fmaxf(m, fmaxf(fabsf(lo[e]), fabsf(hi[e])));
             int ex = 0;
             if (m > 0.f) frexpf(m, &ex);  // m = f * 2^ex, f in [0.5, 1)
             int kk = m > 0.f ? ex - 3 : -127;
             if (m > ldexpf(7.5f, kk)) kk++;
             kk = min(max(kk, -127), 127);
             sc |= (uint32_t)(kk + 127) << (8 * t);
-            const float inv = ldexpf(1.0f, -kk), scl = ldexpf(1.0f, kk);
-            uint32_t w[6] = {0u, 0u, 0u, 0u, 0u, 0u};
+            const float scl = ldexpf(1.0f, kk);
+            const u32x6 w = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(lo, hi, scl);
+            *(uint4 *)(dst + 96 * t + 16 * g) = make_uint4(w[0], w[1], w[2], w[3]);
+            *(uint2 *)(dst + 96 * t + 64 + 8 * g) = make_uint2(w[4], w[5]);
+            if (t < 2) {
+                const f32x32 q = __builtin_amdgcn_cvt_scalef32_pk32_f32_fp6(w, scl);  // element 2i: lo[i], 2i + 1: hi[i]
 #pragma unroll
-            for (int kq = 0; kq < 16; kq++) {
-                float q;
-                const float y = v[kq] * inv;
-                const uint32_t code = e2m3_code(y, q);
-                v[kq] = (y - q) * scl;
-                // element e = 2 kq + h at bits 6 e: 12 kq + 6 h (a code never straddles a dword
-                // boundary at an even element; at an odd one it may)
-                const int bit = 12 * kq + 6 * h;
-                const uint64_t cw = (uint64_t)code << (bit & 31);
-                const int d = bit >> 5;
-#pragma unroll
-                for (int dd = 0; dd < 6; dd++) {
-                    if (dd == d) w[dd] |= (uint32_t)cw;
-                    if (dd == d + 1) w[dd] |= (uint32_t)(cw >> 32);
+                for (int e = 0; e < 16; e++) {
+                    lo[e] -= q[2 * e];
+                    hi[e] -= q[2 * e + 1];
                 }
             }
-#pragma unroll
-            for (int dd = 0; dd < 6; dd++) w[dd] |= __shfl_xor(w[dd], 1);
-            if (in) {
-                if (h == 0) *(uint4 *)(dst + 96 * t + 16 * g) = make_uint4(w[0], w[1], w[2], w[3]);
-                else *(uint2 *)(dst + 96 * t + 64 + 8 * g) = make_uint2(w[4], w[5]);
-            }
         }
-        if (in && h == 0) *(uint32_t *)(dst + 288 + 4 * g) = live ? sc : 0u;
+        *(uint32_t *)(dst + 288 + 4 * g) = sc;
     }
 }
 
@@ -477,7 +454,7 @@ __global__ __launch_bounds__(512, 1) void k_gmx(const MfArgs a) {
 int pack_rows_fp6(const float *x, int rows, int k, int ldx, uint8_t *out, hipStream_t s) {
     if (rows == 0) return CW_OK;
     if (k % 32) return set_error(CW_ENOTSUP, "pack fp6: rows of %d are not whole 32-value blocks", k);
-    const int64_t n = (int64_t)rows * (((k / 32) + 3) & ~3) * 2, blocks = (n + 255) / 256;
+    const int64_t n = (int64_t)rows * (((k / 32) + 3) & ~3), blocks = (n + 255) / 256;
     hipLaunchKernelGGL(k_pack_fp6x3, dim3((unsigned)(blocks < 16384 ? blocks : 16384)), dim3(256), 0, s, x, rows, k, ldx, out);
     return check_launch("k_pack_fp6x3");
 }
