@@ -26,6 +26,7 @@ struct MoeArgs {
     void *state;                   // the one-launch decode's sync state (DECODE_STATE_BYTES, zero-
                                    // filled before the first call; each call leaves it valid)
     uint32_t polls;                // its bounded waits give up after this many polls
+    int per_cu;                    // blocks per CU of the one-launch decode (set by its launch)
 };
 
 // workspace bytes of the decode's sync state, at the start of every MoE-layer workspace: the

@@ -241,9 +241,27 @@ __device__ __forceinline__ void barrier_fail(DecodeBarrier *b) {
 }
 // `mark` is the state's marker word as read by wave 0 at kernel start (before any block can have
 // arrived, so every block reads the same value).
+// Phase stamps of the one-launch decode (a separate build, libcwmoe_phases.so, compiled with
+// CWMOE_PHASES; the library proper has none): thread 0 of every block stores s_memrealtime (a
+// 100 MHz clock) at 8 points of the kernel into stamps[block][point], which cw_dbg_phases copies
+// out after the call. A store issued at a point does not wait for anything; a later wait on this
+// block's stores (the barrier's) includes it, one store per block.
+#ifdef CWMOE_PHASES
+__device__ unsigned long long g_phase_stamps[4096 * 8];
+#define CW_PHASE(i)                                                                                    \
+    do {                                                                                               \
+        if (threadIdx.x == 0 && blockIdx.x < 4096) g_phase_stamps[blockIdx.x * 8 + (i)] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#else
+#define CW_PHASE(i) \
+    do {            \
+    } while (0)
+#endif
+
 __device__ bool grid_barrier(DecodeBarrier *b, uint32_t nblocks, uint32_t polls, uint32_t gen, uint32_t mark) {
     __builtin_amdgcn_s_waitcnt(0);  // this thread's coherent stores have landed
     __syncthreads();
+    CW_PHASE(4);  // arrived: the block's stores have landed
     __shared__ int ok;
     if (mark != 0 && mark != STATE_MARK) {  // foreign bytes: no counter is touched
         if (threadIdx.x == 0) {
@@ -376,6 +394,7 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
     const uint32_t hs_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float *)hs;  // its LDS address
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int K = a.K;
+    CW_PHASE(0);  // start
     // the logits alone first: every wave of the grid starts at once, and the table and x loads
     // of 2048 waves queued in front of them in L2 (~2.5 us to the first logit). Those loads are
     // issued once the logits are in and complete during the top-k. With 8 logits per lane or
@@ -440,6 +459,7 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
         rid = lane < K ? pick_e[lane] : 0xFFFFFFFFu;
         my_slot = lane < K ? pick_slot[lane] : 0xFFFFFFFFu;
     }
+    CW_PHASE(1);  // routed
 
     // gate / up items (pick j, RI*RPG rows) spread over every wave of the grid; the first item's
     // weights and the block's first down rows are requested right after routing. With one sub-block
@@ -585,10 +605,16 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
                     if (hr0 + q < a.I) store_coherent(a.h + (int64_t)hj * a.P + hr0 + q, hbad ? __int_as_float(0x7fc00000) : hv[q]);
             }
         };
-        for (int it = gwave, b = 0; it < n_items; it += total_waves, b ^= 1) {
+        // Items go out in rounds: round r covers the next wr(r) items, one per wave from wave 0.
+        // With several blocks per CU, the blocks placed later on a CU start their first items a
+        // few microseconds later (their loads queue behind the others'), so each later round
+        // leaves out one more of the CU's placement groups (blocks are placed in index order).
+        auto wr = [&](int r) { return a.per_cu > 1 ? total_waves * max(a.per_cu - r, 1) / a.per_cu : total_waves; };
+        for (int it = gwave, b = 0, r = 0; it < n_items; it = gwave < wr(r + 1) ? it + wr(r) : n_items, r++, b ^= 1) {
             // per item: 2*RI rows of two chunk loads each, and the bias load
-            if (it + total_waves < n_items) {
-                issue_item(it + total_waves, b ^ 1);
+            const int nx = gwave < wr(r + 1) ? it + wr(r) : n_items;
+            if (nx < n_items) {
+                issue_item(nx, b ^ 1);
                 asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * RI + 1) : "memory");
             } else {
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -670,6 +696,7 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
             }
         }
     }
+    CW_PHASE(2);  // this wave 0's gate/up items done
     // zero padding of hidden rows up to the width down reads
     for (int c = gwave * 64 + lane; c < K * (a.P - a.I); c += total_waves * 64) {
         const int j = c / (a.P - a.I);
@@ -712,7 +739,9 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
         }
     }
     if (wave < 4) td.store(ldsd, threadIdx.x);
+    CW_PHASE(3);  // at the barrier
     const bool ok = grid_barrier((DecodeBarrier *)a.state, gridDim.x, a.polls, gen, mark);
+    CW_PHASE(5);  // barrier open
 
     // every hidden row into LDS once per block, read at the coherence point (16-byte buffer
     // loads with the sc1 policy, the form of an agent-scope atomic load, 8 in flight per thread),
@@ -739,6 +768,7 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
         }
     }
     __syncthreads();
+    CW_PHASE(6);  // hidden rows staged
 
     // down + combine: each wave group takes RPD rows per block pass (the loop's bound is the
     // block's, so every thread meets the same barriers)
@@ -805,6 +835,7 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
         }
         __syncthreads();
     }
+    CW_PHASE(7);  // end
 }
 
 // ------------------------------------------------------------------------------ dispatch
@@ -891,7 +922,7 @@ static constexpr size_t DECODE_MAX_HIDDEN_LDS = 64 * 1024;
 // device (a few entries remembered, under a lock, so concurrent callers never size a grid from
 // another call's entry). 0 on failure.
 template <class Kern>
-static int decode_grid(Kern kern, int which, const MoeArgs &a, size_t lds, int threads, int want) {
+static int decode_grid(Kern kern, int which, const MoeArgs &a, size_t lds, int threads, int want, int *per_cu) {
     struct Occ {
         int dev = -1, which = -1;
         size_t lds = 0;
@@ -918,8 +949,9 @@ static int decode_grid(Kern kern, int which, const MoeArgs &a, size_t lds, int t
         std::lock_guard<std::mutex> lock(mu);
         cache[next++ & 7] = o;
     }
-    const int grid = o.per_cu * o.cus;
-    return grid < want ? grid : want;
+    const int grid = o.per_cu * o.cus < want ? o.per_cu * o.cus : want;
+    *per_cu = (grid + o.cus - 1) / o.cus;
+    return grid;
 }
 
 template <class FG, int LG, int XG, class FD, int LD, int XD, int PER, int PPW, int G, int RI>
@@ -934,9 +966,10 @@ static int decode_launch_per(const MoeArgs &a, int which, hipStream_t s) {
     const size_t lds = decode_lds<FG, G, RI>(a);
     const int RPD = 64 / LD;
     auto kern = k_moe_decode<FG, LG, XG, FD, LD, XD, PER, PPW, G, RI>;
-    const int grid = decode_grid(kern, 4 * which + G, a, lds, 256 * G, (a.H + RPD * G - 1) / (RPD * G));
+    MoeArgs b = a;
+    const int grid = decode_grid(kern, 4 * which + G, a, lds, 256 * G, (a.H + RPD * G - 1) / (RPD * G), &b.per_cu);
     if (!grid) return set_error(CW_EHIP, "moe decode: occupancy query failed");
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(256 * G), lds, s, a);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(256 * G), lds, s, b);
     return check_launch("k_moe_decode");
 }
 
@@ -973,6 +1006,14 @@ int moe_decode(int dtg, int dtd, const MoeArgs &a, hipStream_t s) {
     if (dtg == CW_MXFP4 && dtd == CW_MXFP4 && nsg == 90 && nsd == 90) return decode_ppw<FMXFP4, 64, 2, FMXFP4, 32, 3>(a, s);
     return CW_ENOTSUP;
 }
+
+#ifdef CWMOE_PHASES
+extern "C" int cw_dbg_phases(unsigned long long *out, int blocks) {
+    if (blocks < 0 || blocks > 4096) return -1;
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_phase_stamps), (size_t)blocks * 8 * sizeof(unsigned long long), 0,
+                               hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
+}
+#endif
 
 uint32_t decode_barrier_errors() {
     uint32_t n = 0;
