@@ -49,6 +49,11 @@ struct MfArgs {
     // MXFP4 on the scaled MFMA: activations packed by pack_rows_fp6 (ap_rows rows of ap_row bytes)
     const uint8_t *ap;
     int64_t ap_row, ap_rows;
+    // gate/up on the scaled MFMA: the hidden rows packed as the down GEMM's FP6 activations (hp,
+    // hp_row bytes per pile position, hp_blocks 32-value block records per row) instead of f32 h
+    uint8_t *hp;
+    int64_t hp_row;
+    int hp_blocks;
 };
 
 // Work a pack launch also does for the dense matmul that follows it: the tile list of m rows, and

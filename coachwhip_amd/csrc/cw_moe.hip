@@ -218,7 +218,9 @@ static int moe_grouped(const cw_moe_desc *d, const MoeArgs &a, const MoeLayout &
     if (gx) rc = pack_rows_fp6(a.x, T, a.H, a.H, (uint8_t *)x16, s);
     else rc = pack_rows_f16(a.x, T, a.H, a.H, x16, xscale, s, nullptr, mfma_k_permuted(d->dtype[0]));
     if (rc) return rc;
-    if (P > a.I && (rc = fill_zero(a.h, (int64_t)TK * P, s))) return rc;
+    // gate/up and down both on the scaled MFMA: gate/up packs the hidden rows itself
+    const bool fuse_h = gx && dx;
+    if (!fuse_h && P > a.I && (rc = fill_zero(a.h, (int64_t)TK * P, s))) return rc;
     const int tmax = max_tiles(TK, a.n_slots);
 
     MfArgs g = {};
@@ -249,12 +251,18 @@ static int moe_grouped(const cw_moe_desc *d, const MoeArgs &a, const MoeLayout &
         g.ap = (const uint8_t *)x16;
         g.ap_row = (int64_t)fp6_rows_bytes(1, a.H);
         g.ap_rows = T;
+        if (fuse_h) {
+            g.hp = (uint8_t *)h16;
+            g.hp_row = (int64_t)fp6_rows_bytes(1, P);
+            g.hp_blocks = (int)(g.hp_row / 304 * 4);
+        }
         rc = mxfp4_gateup(g, tmax, s);
     } else {
         rc = mfma_gateup(d->dtype[0], g, tmax, s);
     }
     if (rc) return rc;
-    if (dx) rc = pack_rows_fp6(a.h, TK, P, P, (uint8_t *)h16, s);
+    if (fuse_h) rc = CW_OK;
+    else if (dx) rc = pack_rows_fp6(a.h, TK, P, P, (uint8_t *)h16, s);
     else rc = pack_rows_f16(a.h, TK, P, P, h16, hscale, s, nullptr, mfma_k_permuted(d->dtype[2]));
     if (rc) return rc;
 

@@ -45,15 +45,55 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x32 __attribute__((ext_vector_type(32)));
 typedef uint32_t u32x6 __attribute__((ext_vector_type(6)));
 
-// One lane per (row, 32-value block): three terms, each scaled by the power of two that puts the
-// block's largest remaining magnitude in (3.75, 7.5], where FP6 E2M3 (sign, 2 exponent bits with
-// bias 1, 3 mantissa bits: steps of 1/8 below 2, 1/4 below 4, 1/2 up to 7.5) is exact to half a
-// step. gfx950 converts a term in one instruction (`v_cvt_scalef32_2xpk16_fp6_f32`: code 2i of the
-// 192-bit record from the first 16 values, code 2i + 1 from the second 16, each value divided by
-// the scale and rounded to the nearest E2M3 value, ties to even), which is the record's element
-// order: element e meets nibble e of the weight block, weight position (e >> 1) + 16 (e & 1). The
-// residual subtracts the term's value as decoded by `v_cvt_scalef32_pk32_f32_fp6` (code times the
-// scale), exactly: a value minus its rounding to 3 mantissa bits is representable.
+// The three-term record of one 32-value block (lo[i] = value i, hi[i] = value 16 + i) into block
+// g of the step record at dst. Each term is scaled by the power of two that puts the block's
+// largest remaining magnitude in (3.75, 7.5], where FP6 E2M3 (sign, 2 exponent bits with bias 1,
+// 3 mantissa bits: steps of 1/8 below 2, 1/4 below 4, 1/2 up to 7.5) is exact to half a step.
+// gfx950 converts a term in one instruction (`v_cvt_scalef32_2xpk16_fp6_f32`: code 2i of the
+// 192-bit record from lo[i], code 2i + 1 from hi[i], each value divided by the scale and rounded
+// to the nearest E2M3 value, ties to even), which is the record's element order: element e meets
+// nibble e of the weight block, weight position (e >> 1) + 16 (e & 1). The residual subtracts the
+// term's value as decoded by `v_cvt_scalef32_pk32_f32_fp6` (code times the scale), exactly: a
+// value minus its rounding to 3 mantissa bits is representable.
+__device__ __forceinline__ void fp6x3_record(f32x16 lo, f32x16 hi, uint8_t *dst, int g) {
+    uint32_t sc = 0;
+#pragma unroll
+    for (int t = 0; t < 3; t++) {
+        float m = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; e++) m = fmaxf(m, fmaxf(fabsf(lo[e]), fabsf(hi[e])));
+        int ex = 0;
+        if (m > 0.f) frexpf(m, &ex);  // m = f * 2^ex, f in [0.5, 1)
+        int kk = m > 0.f ? ex - 3 : -127;
+        if (m > ldexpf(7.5f, kk)) kk++;
+        kk = min(max(kk, -127), 127);
+        sc |= (uint32_t)(kk + 127) << (8 * t);
+        const float scl = ldexpf(1.0f, kk);
+        const u32x6 w = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(lo, hi, scl);
+        *(uint4 *)(dst + 96 * t + 16 * g) = make_uint4(w[0], w[1], w[2], w[3]);
+        *(uint2 *)(dst + 96 * t + 64 + 8 * g) = make_uint2(w[4], w[5]);
+        if (t < 2) {
+            const f32x32 q = __builtin_amdgcn_cvt_scalef32_pk32_f32_fp6(w, scl);  // element 2i: lo[i], 2i + 1: hi[i]
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                lo[e] -= q[2 * e];
+                hi[e] -= q[2 * e + 1];
+            }
+        }
+    }
+    *(uint32_t *)(dst + 288 + 4 * g) = sc;
+}
+// a zero record (codes and scale bytes 0), for blocks past a row
+__device__ __forceinline__ void fp6x3_zero(uint8_t *dst, int g) {
+#pragma unroll
+    for (int t = 0; t < 3; t++) {
+        *(uint4 *)(dst + 96 * t + 16 * g) = make_uint4(0u, 0u, 0u, 0u);
+        *(uint2 *)(dst + 96 * t + 64 + 8 * g) = make_uint2(0u, 0u);
+    }
+    *(uint32_t *)(dst + 288 + 4 * g) = 0u;
+}
+
+// One lane per (row, 32-value block).
 __global__ __launch_bounds__(256) void k_pack_fp6x3(const float *x, int rows, int k, int ldx, uint8_t *out) {
     const int nb = k / 32, nbp = (nb + 3) & ~3;  // blocks, and block records per row (whole steps)
     const int64_t n = (int64_t)rows * nbp;
@@ -63,12 +103,7 @@ __global__ __launch_bounds__(256) void k_pack_fp6x3(const float *x, int rows, in
         uint8_t *dst = out + row * (int64_t)(nbp / 4) * 304 + (j >> 2) * 304;
         const int g = j & 3;
         if (j >= nb) {  // past the row: zero codes and scale bytes
-#pragma unroll
-            for (int t = 0; t < 3; t++) {
-                *(uint4 *)(dst + 96 * t + 16 * g) = make_uint4(0u, 0u, 0u, 0u);
-                *(uint2 *)(dst + 96 * t + 64 + 8 * g) = make_uint2(0u, 0u);
-            }
-            *(uint32_t *)(dst + 288 + 4 * g) = 0u;
+            fp6x3_zero(dst, g);
             continue;
         }
         const float4 *src = (const float4 *)(x + row * ldx + 32 * j);
@@ -85,32 +120,7 @@ __global__ __launch_bounds__(256) void k_pack_fp6x3(const float *x, int rows, in
             hi[4 * c + 2] = h.z;
             hi[4 * c + 3] = h.w;
         }
-        uint32_t sc = 0;
-#pragma unroll
-        for (int t = 0; t < 3; t++) {
-            float m = 0.f;
-#pragma unroll
-            for (int e = 0; e < 16; e++) m = fmaxf(m, fmaxf(fabsf(lo[e]), fabsf(hi[e])));
-            int ex = 0;
-            if (m > 0.f) frexpf(m, &ex);  // m = f * 2^ex, f in [0.5, 1)
-            int kk = m > 0.f ? ex - 3 : -127;
-            if (m > ldexpf(7.5f, kk)) kk++;
-            kk = min(max(kk, -127), 127);
-            sc |= (uint32_t)(kk + 127) << (8 * t);
-            const float scl = ldexpf(1.0f, kk);
-            const u32x6 w = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(lo, hi, scl);
-            *(uint4 *)(dst + 96 * t + 16 * g) = make_uint4(w[0], w[1], w[2], w[3]);
-            *(uint2 *)(dst + 96 * t + 64 + 8 * g) = make_uint2(w[4], w[5]);
-            if (t < 2) {
-                const f32x32 q = __builtin_amdgcn_cvt_scalef32_pk32_f32_fp6(w, scl);  // element 2i: lo[i], 2i + 1: hi[i]
-#pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    lo[e] -= q[2 * e];
-                    hi[e] -= q[2 * e + 1];
-                }
-            }
-        }
-        *(uint32_t *)(dst + 288 + 4 * g) = sc;
+        fp6x3_record(lo, hi, dst, g);
     }
 }
 
@@ -376,6 +386,10 @@ __device__ __forceinline__ void gx_item(const MfArgs &a, const MfTile &tile, int
 
     // epilogue: lane holds weight rows 16 f' + 4 grp + i (i < 4) of token 16 (tb0 + t) + l16
     gx_wait_vm(0);
+    // hidden rows packed in the block (k_gmx): staged in LDS as [tile row][RPB] f32, once every
+    // wave is done with the buffers
+    const bool stage_h = MODE == 0 && a.hp != nullptr;
+    if (stage_h) __syncthreads();
     if constexpr (NTB > 0) {
 #pragma unroll
         for (int t = 0; t < NTB; t++) {
@@ -388,10 +402,17 @@ __device__ __forceinline__ void gx_item(const MfArgs &a, const MfTile &tile, int
                 const int n = nb * S::RPB + rg * S::RW + 16 * f + 4 * grp;
                 if constexpr (MODE == 0) {
                     const uint32_t e = a.act == CW_ACT_SILU ? 0u : a.ids[pick];
-                    float *hrow = a.h + (int64_t)pos * a.ldh;
+                    // staged: row rr of the tile at column n - nb * RPB (an index from the LDS base,
+                    // never a pointer formed below it: a generic address below the shared aperture
+                    // is taken for a global one)
+                    float *const hst = (float *)smem + rr * S::RPB + (n - nb * S::RPB);
+                    float *const hrow = a.h + (int64_t)pos * a.ldh + n;
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
-                        if (n + i >= a.n) continue;
+                        if (n + i >= a.n) {
+                            if (stage_h) hst[i] = 0.f;  // past the row: its packed values are 0
+                            continue;
+                        }
                         float g = acc[f][t][i], u = acc[S::FR + f][t][i], o;
                         if (a.act == CW_ACT_SILU) {
                             o = g / (1.0f + expf(-g)) * u;
@@ -402,7 +423,8 @@ __device__ __forceinline__ void gx_item(const MfArgs &a, const MfTile &tile, int
                             u = fminf(fmaxf(u, -a.limit), a.limit);
                             o = (u + 1.0f) * (g * (1.0f / (1.0f + expf(-(g * a.alpha)))));
                         }
-                        hrow[n + i] = o;
+                        if (stage_h) hst[i] = o;
+                        else hrow[i] = o;
                     }
                 } else {
                     float *dst = a.dn + (int64_t)pick * a.n + n;
@@ -446,6 +468,42 @@ __global__ __launch_bounds__(512, 1) void k_gmx(const MfArgs a) {
         case 2: gx_item<MODE, 2>(a, tile, nb, mbs, tb0, wave, lane, smem, lds0); break;
         default: gx_item<MODE, 3>(a, tile, nb, mbs, tb0, wave, lane, smem, lds0); break;
         }
+        if constexpr (MODE == 0) {
+            if (a.hp) {
+                // the tile's hidden values of this N-block, one thread per (tile row, 32-value
+                // block), into the down GEMM's FP6 records; rows' records past the GEMM's blocks
+                // (zeros) come with the last N-block
+                __syncthreads();
+                constexpr int NBL = S::RPB / 32;
+                const float *hb = (const float *)smem;
+                for (int e = threadIdx.x; e < tile.m * NBL; e += S::NT) {
+                    const int r = e / NBL, bl = e - r * NBL, jb = nb * NBL + bl;
+                    if (jb >= a.hp_blocks) continue;
+                    const float4 *src = (const float4 *)(hb + r * S::RPB + 32 * bl);
+                    f32x16 lo, hi;
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        const float4 f = src[c], h = src[4 + c];
+                        lo[4 * c] = f.x;
+                        lo[4 * c + 1] = f.y;
+                        lo[4 * c + 2] = f.z;
+                        lo[4 * c + 3] = f.w;
+                        hi[4 * c] = h.x;
+                        hi[4 * c + 1] = h.y;
+                        hi[4 * c + 2] = h.z;
+                        hi[4 * c + 3] = h.w;
+                    }
+                    fp6x3_record(lo, hi, a.hp + (int64_t)(tile.pos0 + r) * a.hp_row + (jb >> 2) * 304, jb & 3);
+                }
+                const int from = n_nb * NBL, cnt = a.hp_blocks - from;
+                if (nb == n_nb - 1 && cnt > 0) {
+                    for (int e = threadIdx.x; e < tile.m * cnt; e += S::NT) {
+                        const int r = e / cnt, jb = from + (e - r * cnt);
+                        fp6x3_zero(a.hp + (int64_t)(tile.pos0 + r) * a.hp_row + (jb >> 2) * 304, jb & 3);
+                    }
+                }
+            }
+        }
     }
 }
 
@@ -473,6 +531,8 @@ static int gx_launch(const MfArgs &a, int tiles_max, hipStream_t s) {
     // lane offsets are 32-bit: from a matrix's 16-byte aligned base, and into the packed rows
     if ((int64_t)a.n * a.row_bytes + 256 >= ((int64_t)1 << 32))
         return set_error(CW_ENOTSUP, "mxfp4 gemm: a matrix of %d rows of %lld bytes is 4 GiB or more", a.n, (long long)a.row_bytes);
+    if (MODE == 0 && a.hp && (size_t)MF_MT * S::RPB * 4 > S::LDS)
+        return set_error(CW_ENOTSUP, "mxfp4 gemm: the hidden rows' staging does not fit");
     if (a.ap_rows * a.ap_row >= ((int64_t)1 << 32))
         return set_error(CW_ENOTSUP, "mxfp4 gemm: %lld packed activation rows are 4 GiB or more", (long long)a.ap_rows);
     static std::atomic<int> cus_of[64];
