@@ -127,19 +127,13 @@ __global__ __launch_bounds__(256) void k_pack_fp6x3(const float *x, int rows, in
 // ------------------------------------------------------------------------------ the GEMM
 
 // 16 bytes from global memory (base + off, base a wave-uniform 16-byte aligned address) to LDS,
-// lane l writing lds_base + 16 l, and a lane's activation operands of one step into registers (7
-// loads from base + o16 / o8 / o4, its K-group's bytes of term 0: term t's codes, 16 bytes at
-// 96 t and 8 bytes at 96 t + 64, the scale dword at 288). Issued as inline asm: the kernel counts
-// its vector memory operations itself (a running count, and the count after each batch it will
-// need) and waits for exactly the ones it needs, which the compiler, not seeing loads it did not
-// issue, could not do. Both take a uniform 64-bit base and 32-bit lane offsets, so that no lane
-// holds a 64-bit address. lds_base is an LDS address, the same for the whole wave.
+// lane l writing lds_base + 16 l. Issued as inline asm: the kernel counts its vector memory
+// operations itself (a running count, and the count after each batch it will need) and waits for
+// exactly the ones it needs, which the compiler, not seeing loads it did not issue, could not do.
+// It takes a uniform 64-bit base and 32-bit lane offsets, so that no lane holds a 64-bit address.
+// lds_base is an LDS address, the same for the whole wave.
 __device__ __forceinline__ void gx_dma16(const uint8_t *base, uint32_t off, uint32_t lds_base) {
     asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base),
-                 "s"(__builtin_amdgcn_readfirstlane(lds_base)) : "memory", "m0");
-}
-__device__ __forceinline__ void gx_dma4(const uint8_t *base, uint32_t off, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" : : "v"(off), "s"(base),
                  "s"(__builtin_amdgcn_readfirstlane(lds_base)) : "memory", "m0");
 }
 // s_waitcnt vmcnt(n) for n in {0, 4, 5} (a stage's wait: the window loads of one stage in flight)
@@ -164,8 +158,8 @@ __device__ __forceinline__ void gx_wait_vm(int n) {
 // 2 halves of the tile's 16-token blocks. A stage is one 128-wide K step. The weight bytes of a
 // stage go to LDS by direct loads, three stages ahead (three buffers), per row a window of the 6
 // 16-byte pieces holding its 4 blocks (68 bytes at any offset). The activation operands of a
-// stage (token block t: per lane three 16 + 8 byte code runs and a scale dword) go to LDS by direct
-// loads too, two stages ahead (two buffers), issued by the first waves. Each wave reads the operands of
+// stage (token block t: its 16 tokens' 304-byte step records, whole) go to LDS by direct loads
+// too, two stages ahead (two buffers), issued by the first waves. Each wave reads the operands of
 // the next stage from LDS while it computes the current one: a token block's activation operands
 // right after that block's MFMAs, the weight operands at the end of the stage, so that their
 // latency hides behind the matrix work. One barrier per stage publishes every wave's loads (each
@@ -184,7 +178,9 @@ struct GxShape {
     static constexpr int NJW = (W_INST + NW - 1) / NW;
     static constexpr int W_BYTES = WROWS * PCS * 16;
     static constexpr int WDEPTH = 3;
-    static constexpr int TB_BYTES = 3 * 1536 + 256;   // a token block's operands: per term 1 KB + 512 B, scales
+    // a token block's operands of a stage: its 16 tokens' 304-byte step records side by side
+    // (4,864 bytes), padded to the five 1 KB direct loads that bring them
+    static constexpr int TB_BYTES = 5 * 1024;
     static constexpr int A_BYTES = MF_MB * TB_BYTES;
     static constexpr size_t LDS = WDEPTH * (size_t)W_BYTES + 2 * (size_t)A_BYTES;
     static_assert(RPB * PCS % 64 == 0, "a window load lies in one matrix");
@@ -225,14 +221,21 @@ __device__ __forceinline__ void gx_item(const MfArgs &a, const MfTile &tile, int
         lmis[f] = ((mm ? wm1 : wm0) + (uint32_t)(n < a.n ? n : 0) * (uint32_t)a.row_bytes) & 15u;
     }
     // activation staging: wave w < mbs stages token block w (lane = its K-group and token)
+    // wave w < mbs stages token block w: a stage's 16 records of 304 bytes are 304 16-byte
+    // pieces, piece p (token p / 19, its piece p % 19) brought by lane p % 64 of load p / 64 (the
+    // last load's lanes past piece 303 bring that piece again, into the block's padding)
     const bool stager = wave < mbs;
-    uint32_t xr = 0;
+    uint32_t xo[5] = {0, 0, 0, 0, 0};
     if (stager) {
-        const int row = min(16 * wave + l16, tile.m - 1), pos = tile.pos0 + row;
-        xr = (uint32_t)(a.rows ? a.rows[pos] : pos) * (uint32_t)a.ap_row;
+#pragma unroll
+        for (int c = 0; c < 5; c++) {
+            const int p = min(64 * c + lane, 303), tk = p / 19;
+            const int pos = tile.pos0 + min(16 * wave + tk, tile.m - 1);
+            xo[c] = (uint32_t)(a.rows ? a.rows[pos] : pos) * (uint32_t)a.ap_row + 16u * (uint32_t)(p - 19 * tk);
+        }
     }
 
-    // Loads are counted per wave: in stage s a wave issues the activation loads of s + 2 (10 if it
+    // Loads are counted per wave: in stage s a wave issues the activation loads of s + 2 (5 if it
     // stages a token block), then nw window loads of s + 3 (nw is 4 or 5, by wave). Before the
     // barrier of stage st, a wave needs its windows of st + 1 (requested in st - 2) and its
     // activations of st + 1 (requested in st - 1): only the windows of st + 2 may stay in flight.
@@ -258,21 +261,13 @@ __device__ __forceinline__ void gx_item(const MfArgs &a, const MfTile &tile, int
         }
         if (st == 0) m_w0 = issued;
     };
-    // a stager's activation operands of stage st into activation buffer st % 2: per term the
-    // 16-byte code runs of the 64 lanes (1 KB), then their dwords 4 and 5 (256 bytes each), then
-    // the lanes' scale dwords, each a direct load from the packed row
+    // a stager's token block of stage st into activation buffer st % 2 (five 1 KB direct loads)
     auto issue_x = [&](int st) __attribute__((always_inline)) {
         if (stager) {
-            const uint32_t o = xr + 304u * (uint32_t)st;
             const uint32_t d = Al + (st & 1) * S::A_BYTES + wave * S::TB_BYTES;
 #pragma unroll
-            for (int t = 0; t < 3; t++) {
-                gx_dma16(a.ap, o + 96u * t + 16u * grp, d + 1536 * t);
-                gx_dma4(a.ap, o + 96u * t + 64u + 8u * grp, d + 1536 * t + 1024);
-                gx_dma4(a.ap, o + 96u * t + 68u + 8u * grp, d + 1536 * t + 1280);
-            }
-            gx_dma4(a.ap, o + 288u + 4u * grp, d + 3 * 1536);
-            issued += 10;
+            for (int c = 0; c < 5; c++) gx_dma16(a.ap, xo[c] + 304u * (uint32_t)st, d + 1024 * c);
+            issued += 5;
         }
         if (st == 0) m_a0 = issued;
     };
@@ -283,14 +278,17 @@ __device__ __forceinline__ void gx_item(const MfArgs &a, const MfTile &tile, int
     int bsc[NB];
     uint32_t ra[S::NF][5], re[S::NF];
     auto read_b = [&](int t, int st) __attribute__((always_inline)) {
-        const uint8_t *d = Ab + (st & 1) * S::A_BYTES + (tb0 + t) * S::TB_BYTES;
+        // this lane's token's record: per term 16 code bytes of its K-group at 96 j + 16 grp and 8
+        // at 96 j + 64 + 8 grp, its scale dword at 288 + 4 grp (bank-conflict free: records are 76
+        // dwords apart)
+        const uint8_t *r = Ab + (st & 1) * S::A_BYTES + (tb0 + t) * S::TB_BYTES + 304 * l16;
 #pragma unroll
         for (int j = 0; j < 3; j++) {
-            const i32x4 l = *(const i32x4 *)(d + 1536 * j + 16 * lane);
-            const i32x2 h = {*(const int *)(d + 1536 * j + 1024 + 4 * lane), *(const int *)(d + 1536 * j + 1280 + 4 * lane)};
+            const i32x4 l = *(const i32x4 *)(r + 96 * j + 16 * grp);
+            const i32x2 h = *(const i32x2 *)(r + 96 * j + 64 + 8 * grp);
             bo[t][j] = __builtin_shufflevector(l, __builtin_shufflevector(h, h, 0, 1, -1, -1), 0, 1, 2, 3, 4, 5, -1, -1);
         }
-        bsc[t] = *(const int *)(d + 3 * 1536 + 4 * lane);
+        bsc[t] = *(const int *)(r + 288 + 4 * grp);
     };
     // LDS offset of the E8M0 byte of this lane's block of fragment f in stage st's window
     auto aoff = [&](int f, int st) __attribute__((always_inline)) -> uint32_t {
