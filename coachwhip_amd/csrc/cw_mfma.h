@@ -9,8 +9,11 @@ constexpr int MF_MB = 5;            // MFMA blocks of 16 picks per tile
 constexpr int MF_MT = 16 * MF_MB;   // picks per tile: 80 keeps the piles of a 1,500-token batch over
                                     // 256 experts (about 47 picks each) at one tile per expert
 
+// A tile: m picks of one slot's pile from pile position pos0, and the expert they were routed to
+// (every pick of a pile reads one slot, so one expert; the slot itself when the piles were built
+// without the picks' expert ids).
 struct MfTile {
-    int slot, pos0, m, pad;
+    int slot, pos0, m, expert;
 };
 
 struct MfArgs {
@@ -71,7 +74,7 @@ bool mfma_supported(int dtype);
 // nibbles side by side); their activations are packed with pack_rows_f16(..., perm = true)
 inline bool mfma_k_permuted(int dtype) { return dtype == CW_MXFP4; }
 // one block: expert piles of the (slot) picks, and the tile list
-int mfma_piles(const uint32_t *slots, int TK, int K, int n_slots, int *pile_pick, int *pile_tok, MfTile *tiles,
+int mfma_piles(const uint32_t *slots, const uint32_t *ids, int TK, int K, int n_slots, int *pile_pick, int *pile_tok, MfTile *tiles,
                int *n_tiles, hipStream_t s);
 int max_tiles(int TK, int n_slots);
 // rows x k f32 -> fp16 rows (ld = k) with per-row power-of-two scales

@@ -1149,13 +1149,14 @@ __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
 // PILE_LDS picks, the scatter goes to LDS and the piles leave in coalesced stores (random 4-byte
 // stores from one CU cost a memory transaction each).
 constexpr int PILE_PER = 16, PILE_LDS = 12288;
-__global__ __launch_bounds__(1024) void k_piles(const uint32_t *slots, int TK, int K, int n_slots, int *pile_pick,
-                                                 int *pile_tok, MfTile *tiles, int *n_tiles) {
-    __shared__ int cnt[1024], off[1024], cur[1024], wtot[16], wttot[16];
+__global__ __launch_bounds__(1024) void k_piles(const uint32_t *slots, const uint32_t *ids, int TK, int K, int n_slots,
+                                                 int *pile_pick, int *pile_tok, MfTile *tiles, int *n_tiles) {
+    __shared__ int cnt[1024], off[1024], cur[1024], rep[1024], wtot[16], wttot[16];
     __shared__ int staged[PILE_LDS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     cnt[tid] = 0;
     cur[tid] = 0;
+    rep[tid] = 0;
     const bool one = TK <= 1024 * PILE_PER;  // the common case: every slot read once, kept in registers
     uint32_t v[PILE_PER];
 #pragma unroll
@@ -1174,7 +1175,10 @@ __global__ __launch_bounds__(1024) void k_piles(const uint32_t *slots, int TK, i
         }
 #pragma unroll
         for (int q = 0; q < PILE_PER; q++)
-            if (v[q] < (uint32_t)n_slots) atomicAdd(&cnt[v[q]], 1);
+            if (v[q] < (uint32_t)n_slots) {
+                atomicAdd(&cnt[v[q]], 1);
+                atomicMax(&rep[v[q]], c0 + q * 1024 + tid);  // a pick of the slot, for its expert id
+            }
     }
     __syncthreads();
     // exclusive scans of the counts and of the tile counts: per wave, then over the 16 wave totals
@@ -1194,8 +1198,10 @@ __global__ __launch_bounds__(1024) void k_piles(const uint32_t *slots, int TK, i
     const int my_off = wc + ic - c, my_toff = wtc + itc - tc;
     if (tid == 1023) *n_tiles = my_toff + tc;
     off[tid] = my_off;
-    if (tid < n_slots)
-        for (int q = 0; q < tc; q++) tiles[my_toff + q] = MfTile{tid, my_off + q * MF_MT, min(MF_MT, c - q * MF_MT), 0};
+    if (tid < n_slots) {
+        const int ex = ids && c > 0 ? (int)ids[rep[tid]] : tid;
+        for (int q = 0; q < tc; q++) tiles[my_toff + q] = MfTile{tid, my_off + q * MF_MT, min(MF_MT, c - q * MF_MT), ex};
+    }
     __syncthreads();
     for (int c0 = 0; c0 < TK; c0 += 1024 * PILE_PER) {
         if (!one) {
@@ -1320,10 +1326,10 @@ bool mfma_supported(int dtype) {
 
 int max_tiles(int TK, int n_slots) { return (TK + MF_MT - 1) / MF_MT + (n_slots < TK ? n_slots : TK); }
 
-int mfma_piles(const uint32_t *slots, int TK, int K, int n_slots, int *pile_pick, int *pile_tok, MfTile *tiles, int *n_tiles,
-               hipStream_t s) {
+int mfma_piles(const uint32_t *slots, const uint32_t *ids, int TK, int K, int n_slots, int *pile_pick, int *pile_tok, MfTile *tiles,
+               int *n_tiles, hipStream_t s) {
     if (n_slots > 1024) return set_error(CW_ENOTSUP, "mfma: %d slots (1024 max)", n_slots);
-    hipLaunchKernelGGL(k_piles, dim3(1), dim3(1024), 0, s, slots, TK, K, n_slots, pile_pick, pile_tok, tiles, n_tiles);
+    hipLaunchKernelGGL(k_piles, dim3(1), dim3(1024), 0, s, slots, ids, TK, K, n_slots, pile_pick, pile_tok, tiles, n_tiles);
     return check_launch("k_piles");
 }
 

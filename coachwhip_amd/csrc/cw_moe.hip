@@ -210,7 +210,7 @@ static int moe_grouped(const cw_moe_desc *d, const MoeArgs &a, const MoeLayout &
     }
     int *pile_pick = (int *)(base + L.pile_pick), *pile_tok = (int *)(base + L.pile_tok), *n_tiles = (int *)(base + L.n_tiles);
     MfTile *tiles = (MfTile *)(base + L.tiles);
-    if ((rc = mfma_piles(slots, TK, K, a.n_slots, pile_pick, pile_tok, tiles, n_tiles, s))) return rc;
+    if ((rc = mfma_piles(slots, a.ids, TK, K, a.n_slots, pile_pick, pile_tok, tiles, n_tiles, s))) return rc;
     uint16_t *x16 = (uint16_t *)(base + L.x16), *h16 = (uint16_t *)(base + L.h16);
     float *xscale = (float *)(base + L.xscale), *hscale = (float *)(base + L.hscale);
     // MXFP4 matrices run on the block-scaled MFMA (activations as FP6 terms), the others on fp16 MFMA
@@ -553,7 +553,7 @@ int cw_matmul_id_grouped(int dtype, int64_t n, int64_t k, int64_t n_slots, int64
     MfTile *tiles = (MfTile *)(base + L.tiles);
     uint16_t *x16 = (uint16_t *)(base + L.x16);
     float *xscale = (float *)(base + L.xscale);
-    if ((rc = mfma_piles(ids, TK, K, (int)n_slots, pile_pick, pile_tok, tiles, n_tiles, s))) return rc;
+    if ((rc = mfma_piles(ids, nullptr, TK, K, (int)n_slots, pile_pick, pile_tok, tiles, n_tiles, s))) return rc;
     const bool gx = mxfp4_scaled_for(dtype, k);
     if (gx) rc = pack_rows_fp6(x, xpp ? TK : T, (int)k, (int)k, (uint8_t *)x16, s);
     else rc = pack_rows_f16(x, xpp ? TK : T, (int)k, (int)k, x16, xscale, s, nullptr, mfma_k_permuted(dtype));

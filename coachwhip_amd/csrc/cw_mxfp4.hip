@@ -387,19 +387,48 @@ __device__ __forceinline__ void gx_item(const MfArgs &a, const MfTile &tile, int
     // hidden rows packed in the block (k_gmx): staged in LDS as [tile row][RPB] f32, once every
     // wave is done with the buffers
     const bool stage_h = MODE == 0 && a.hp != nullptr;
-    if (stage_h) __syncthreads();
     if constexpr (NTB > 0) {
-#pragma unroll
-        for (int t = 0; t < NTB; t++) {
-            const int rr = 16 * (tb0 + t) + l16;
-            if (rr >= tile.m) continue;
-            const int pos = tile.pos0 + rr;
-            const int pick = a.pile_pick ? a.pile_pick[pos] : pos;
+        if constexpr (MODE == 0) {
+            // the bias of this lane's rows (gate and up rows n .. n + 3 of fragment f, the tile's
+            // expert), every load issued before any is used: one round trip per item
+            const bool swiglu = a.act != CW_ACT_SILU;
+            const int64_t eb = (int64_t)tile.expert * a.n;
+            float bg[S::FR][4], bu[S::FR][4];
 #pragma unroll
             for (int f = 0; f < S::FR; f++) {
                 const int n = nb * S::RPB + rg * S::RW + 16 * f + 4 * grp;
-                if constexpr (MODE == 0) {
-                    const uint32_t e = a.act == CW_ACT_SILU ? 0u : a.ids[pick];
+#pragma unroll
+                for (int m = 0; m < 2; m++) {
+                    const float *b = m ? a.bias1 : a.bias0;
+                    float *v = m ? bu[f] : bg[f];
+                    v[0] = v[1] = v[2] = v[3] = 0.f;
+                    if (!swiglu || !b) continue;
+                    if ((a.n & 3) == 0) {
+                        if (n < a.n) {
+                            const float4 q = *(const float4 *)(b + eb + n);
+                            v[0] = q.x;
+                            v[1] = q.y;
+                            v[2] = q.z;
+                            v[3] = q.w;
+                        }
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            if (n + i < a.n) v[i] = b[eb + n + i];
+                    }
+                }
+            }
+            // hidden rows packed in the block (k_gmx): staged in LDS as [tile row][RPB] f32, once
+            // every wave is done with the buffers
+            if (stage_h) __syncthreads();
+#pragma unroll
+            for (int t = 0; t < NTB; t++) {
+                const int rr = 16 * (tb0 + t) + l16;
+                if (rr >= tile.m) continue;
+                const int pos = tile.pos0 + rr;
+#pragma unroll
+                for (int f = 0; f < S::FR; f++) {
+                    const int n = nb * S::RPB + rg * S::RW + 16 * f + 4 * grp;
                     // staged: row rr of the tile at column n - nb * RPB (an index from the LDS base,
                     // never a pointer formed below it: a generic address below the shared aperture
                     // is taken for a global one)
@@ -412,11 +441,11 @@ __device__ __forceinline__ void gx_item(const MfArgs &a, const MfTile &tile, int
                             continue;
                         }
                         float g = acc[f][t][i], u = acc[S::FR + f][t][i], o;
-                        if (a.act == CW_ACT_SILU) {
+                        if (!swiglu) {
                             o = g / (1.0f + expf(-g)) * u;
                         } else {
-                            if (a.bias0) g += a.bias0[(int64_t)e * a.n + n + i];
-                            if (a.bias1) u += a.bias1[(int64_t)e * a.n + n + i];
+                            g += bg[f][i];
+                            u += bu[f][i];
                             g = fminf(g, a.limit);
                             u = fminf(fmaxf(u, -a.limit), a.limit);
                             o = (u + 1.0f) * (g * (1.0f / (1.0f + expf(-(g * a.alpha)))));
@@ -424,8 +453,23 @@ __device__ __forceinline__ void gx_item(const MfArgs &a, const MfTile &tile, int
                         if (stage_h) hst[i] = o;
                         else hrow[i] = o;
                     }
-                } else {
-                    float *dst = a.dn + (int64_t)pick * a.n + n;
+                }
+            }
+        } else {
+            // each token's pick (its output row), every load issued before any is used
+            int pk[NB];
+#pragma unroll
+            for (int t = 0; t < NTB; t++) {
+                const int rr = min(16 * (tb0 + t) + l16, tile.m - 1), pos = tile.pos0 + rr;
+                pk[t] = a.pile_pick ? a.pile_pick[pos] : pos;
+            }
+#pragma unroll
+            for (int t = 0; t < NTB; t++) {
+                if (16 * (tb0 + t) + l16 >= tile.m) continue;
+#pragma unroll
+                for (int f = 0; f < S::FR; f++) {
+                    const int n = nb * S::RPB + rg * S::RW + 16 * f + 4 * grp;
+                    float *dst = a.dn + (int64_t)pk[t] * a.n + n;
                     if (n + 4 <= a.n && (a.n & 3) == 0) {
                         *(float4 *)dst = make_float4(acc[f][t][0], acc[f][t][1], acc[f][t][2], acc[f][t][3]);
                     } else {
@@ -436,6 +480,8 @@ __device__ __forceinline__ void gx_item(const MfArgs &a, const MfTile &tile, int
                 }
             }
         }
+    } else if (stage_h) {
+        __syncthreads();  // the block's barrier before the staging, with no rows of its own
     }
 }
 
