@@ -136,6 +136,11 @@ __device__ __forceinline__ void gx_dma16(const uint8_t *base, uint32_t off, uint
     asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base),
                  "s"(__builtin_amdgcn_readfirstlane(lds_base)) : "memory", "m0");
 }
+// the same for 4 bytes (base 4-byte aligned; lane l writes lds_base + 4 l)
+__device__ __forceinline__ void gx_dma4(const uint8_t *base, uint32_t off, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" : : "v"(off), "s"(base),
+                 "s"(__builtin_amdgcn_readfirstlane(lds_base)) : "memory", "m0");
+}
 // s_waitcnt vmcnt(n) for n in {0, 4, 5} (a stage's wait: the window loads of one stage in flight)
 __device__ __forceinline__ void gx_wait_stage(int n) {
     if (n == 5) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
@@ -182,7 +187,13 @@ struct GxShape {
     // (4,864 bytes), padded to the five 1 KB direct loads that bring them
     static constexpr int TB_BYTES = 5 * 1024;
     static constexpr int A_BYTES = MF_MB * TB_BYTES;
-    static constexpr size_t LDS = WDEPTH * (size_t)W_BYTES + 2 * (size_t)A_BYTES;
+    // gate/up: the item's bias rows (gate, then up: RPB floats each) for the epilogue
+    static constexpr int BIAS_OFF = WDEPTH * W_BYTES + 2 * A_BYTES;
+    static constexpr int BIAS_BYTES = MODE == 0 ? NM * RPB * 4 : 0;
+    static constexpr size_t LDS = (size_t)BIAS_OFF + BIAS_BYTES;
+    // gate/up's hidden-row staging: rows of RPB floats 4 apart in banks (a 16-byte write per lane
+    // of 16 tokens hits 64 distinct banks)
+    static constexpr int HST = RPB + 4;
     static_assert(RPB * PCS % 64 == 0, "a window load lies in one matrix");
     static_assert(LDS <= 160 * 1024, "the scaled GEMM's LDS does not fit");
 };
@@ -319,6 +330,20 @@ __device__ __forceinline__ void gx_item(const MfArgs &a, const MfTile &tile, int
     issue_w(0);
     if (n_st > 1) issue_x(1);
     if (n_st > 1) issue_w(1);
+    // gate/up: the bias rows of the tile's expert into LDS (waves 0..5, 64 rows each), with the
+    // windows of stage 1 (complete by the first stage's wait; rows past n bring row n - 1)
+    if constexpr (MODE == 0) {
+        if (a.act != CW_ACT_SILU && wave < 2 * S::RPB / 64) {
+            const int m = wave / (S::RPB / 64), r0 = 64 * (wave - m * (S::RPB / 64));
+            const float *b = m ? a.bias1 : a.bias0;
+            if (b) {
+                const int n = min(nb * S::RPB + r0 + lane, a.n - 1);
+                gx_dma4((const uint8_t *)(b + (int64_t)tile.expert * a.n), (uint32_t)n * 4u,
+                        lds0 + S::BIAS_OFF + (m * S::RPB + r0) * 4);
+                issued++;
+            }
+        }
+    }
     if (n_st > 2) issue_w(2);
     gx_wait_vm(issued - (m_w0 > m_a0 ? m_w0 : m_a0));  // this wave's loads of stage 0
     __syncthreads();                                    // everyone's
@@ -384,43 +409,37 @@ __device__ __forceinline__ void gx_item(const MfArgs &a, const MfTile &tile, int
 
     // epilogue: lane holds weight rows 16 f' + 4 grp + i (i < 4) of token 16 (tb0 + t) + l16
     gx_wait_vm(0);
-    // hidden rows packed in the block (k_gmx): staged in LDS as [tile row][RPB] f32, once every
+    // hidden rows packed in the block (k_gmx): staged in LDS as [tile row][HST] f32, once every
     // wave is done with the buffers
     const bool stage_h = MODE == 0 && a.hp != nullptr;
     if constexpr (NTB > 0) {
         if constexpr (MODE == 0) {
-            // the bias of this lane's rows (gate and up rows n .. n + 3 of fragment f, the tile's
-            // expert), every load issued before any is used: one round trip per item
+            // the bias of this lane's rows (gate and up rows n .. n + 3 of fragment f), staged in
+            // LDS by the prologue
             const bool swiglu = a.act != CW_ACT_SILU;
-            const int64_t eb = (int64_t)tile.expert * a.n;
             float bg[S::FR][4], bu[S::FR][4];
 #pragma unroll
             for (int f = 0; f < S::FR; f++) {
-                const int n = nb * S::RPB + rg * S::RW + 16 * f + 4 * grp;
+                const int c = rg * S::RW + 16 * f + 4 * grp;  // the row's column in the block
 #pragma unroll
                 for (int m = 0; m < 2; m++) {
                     const float *b = m ? a.bias1 : a.bias0;
                     float *v = m ? bu[f] : bg[f];
                     v[0] = v[1] = v[2] = v[3] = 0.f;
                     if (!swiglu || !b) continue;
-                    if ((a.n & 3) == 0) {
-                        if (n < a.n) {
-                            const float4 q = *(const float4 *)(b + eb + n);
-                            v[0] = q.x;
-                            v[1] = q.y;
-                            v[2] = q.z;
-                            v[3] = q.w;
-                        }
-                    } else {
-#pragma unroll
-                        for (int i = 0; i < 4; i++)
-                            if (n + i < a.n) v[i] = b[eb + n + i];
-                    }
+                    const float4 q = *(const float4 *)(smem + S::BIAS_OFF + (m * S::RPB + c) * 4);
+                    v[0] = q.x;
+                    v[1] = q.y;
+                    v[2] = q.z;
+                    v[3] = q.w;
                 }
             }
-            // hidden rows packed in the block (k_gmx): staged in LDS as [tile row][RPB] f32, once
+            // hidden rows packed in the block (k_gmx): staged in LDS as [tile row][HST] f32, once
             // every wave is done with the buffers
             if (stage_h) __syncthreads();
+            // sigmoid(z) = 1 / (1 + 2^(-z log2 e)) on the hardware's exp2 and reciprocal (each
+            // within 1 ulp)
+            constexpr float LOG2E = 1.4426950408889634f;
 #pragma unroll
             for (int t = 0; t < NTB; t++) {
                 const int rr = 16 * (tb0 + t) + l16;
@@ -429,29 +448,31 @@ __device__ __forceinline__ void gx_item(const MfArgs &a, const MfTile &tile, int
 #pragma unroll
                 for (int f = 0; f < S::FR; f++) {
                     const int n = nb * S::RPB + rg * S::RW + 16 * f + 4 * grp;
-                    // staged: row rr of the tile at column n - nb * RPB (an index from the LDS base,
-                    // never a pointer formed below it: a generic address below the shared aperture
-                    // is taken for a global one)
-                    float *const hst = (float *)smem + rr * S::RPB + (n - nb * S::RPB);
-                    float *const hrow = a.h + (int64_t)pos * a.ldh + n;
+                    float o[4];
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
-                        if (n + i >= a.n) {
-                            if (stage_h) hst[i] = 0.f;  // past the row: its packed values are 0
-                            continue;
-                        }
-                        float g = acc[f][t][i], u = acc[S::FR + f][t][i], o;
+                        float g = acc[f][t][i], u = acc[S::FR + f][t][i];
                         if (!swiglu) {
-                            o = g / (1.0f + expf(-g)) * u;
+                            o[i] = g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * LOG2E)) * u;
                         } else {
                             g += bg[f][i];
                             u += bu[f][i];
                             g = fminf(g, a.limit);
                             u = fminf(fmaxf(u, -a.limit), a.limit);
-                            o = (u + 1.0f) * (g * (1.0f / (1.0f + expf(-(g * a.alpha)))));
+                            o[i] = (u + 1.0f) * (g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-(g * a.alpha) * LOG2E)));
                         }
-                        if (stage_h) hst[i] = o;
-                        else hrow[i] = o;
+                        if (n + i >= a.n) o[i] = 0.f;  // past the row: its packed values are 0
+                    }
+                    if (stage_h) {
+                        // row rr of the tile at column n - nb * RPB (an index from the LDS base,
+                        // never a pointer formed below it: a generic address below the shared
+                        // aperture is taken for a global one)
+                        *(float4 *)((float *)smem + rr * S::HST + (n - nb * S::RPB)) = make_float4(o[0], o[1], o[2], o[3]);
+                    } else {
+                        float *const hrow = a.h + (int64_t)pos * a.ldh + n;
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            if (n + i < a.n) hrow[i] = o[i];
                     }
                 }
             }
@@ -523,7 +544,7 @@ __global__ __launch_bounds__(512, 1) void k_gmx(const MfArgs a) {
                 for (int e = threadIdx.x; e < tile.m * NBL; e += S::NT) {
                     const int r = e / NBL, bl = e - r * NBL, jb = nb * NBL + bl;
                     if (jb >= a.hp_blocks) continue;
-                    const float4 *src = (const float4 *)(hb + r * S::RPB + 32 * bl);
+                    const float4 *src = (const float4 *)(hb + r * S::HST + 32 * bl);
                     f32x16 lo, hi;
 #pragma unroll
                     for (int c = 0; c < 4; c++) {
@@ -575,7 +596,7 @@ static int gx_launch(const MfArgs &a, int tiles_max, hipStream_t s) {
     // lane offsets are 32-bit: from a matrix's 16-byte aligned base, and into the packed rows
     if ((int64_t)a.n * a.row_bytes + 256 >= ((int64_t)1 << 32))
         return set_error(CW_ENOTSUP, "mxfp4 gemm: a matrix of %d rows of %lld bytes is 4 GiB or more", a.n, (long long)a.row_bytes);
-    if (MODE == 0 && a.hp && (size_t)MF_MT * S::RPB * 4 > S::LDS)
+    if (MODE == 0 && a.hp && (size_t)MF_MT * S::HST * 4 > (size_t)S::BIAS_OFF)
         return set_error(CW_ENOTSUP, "mxfp4 gemm: the hidden rows' staging does not fit");
     if (a.ap_rows * a.ap_row >= ((int64_t)1 << 32))
         return set_error(CW_ENOTSUP, "mxfp4 gemm: %lld packed activation rows are 4 GiB or more", (long long)a.ap_rows);
