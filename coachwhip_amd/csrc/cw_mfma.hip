@@ -1042,21 +1042,23 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
                         const int r = 16 * mb + 4 * grp + i;
                         if (r >= tile.m) continue;
                         const int pos = tile.pos0 + r;
-                        const int pick = meta_pick[r];
 #pragma unroll
                         for (int q = 0; q < NB; q++) {
                             const int n = nblk * S::RPB + wrow + 16 * q + l16;
                             if (n >= a.n) continue;
+                            // sigmoid(z) = 1 / (1 + 2^(-z log2 e)) on the hardware's exp2 and
+                            // reciprocal (each within 1 ulp)
+                            constexpr float LOG2E = 1.4426950408889634f;
                             float g = value(q, mb, i, meta_sa[r]), u = xu[r * S::RPB + wrow + 16 * q + l16], o;
                             if (a.act == CW_ACT_SILU) {
-                                o = g / (1.0f + expf(-g)) * u;
+                                o = g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * LOG2E)) * u;
                             } else {
-                                const uint32_t e = a.ids[pick];
-                                if (a.bias0) g += a.bias0[(int64_t)e * a.n + n];
-                                if (a.bias1) u += a.bias1[(int64_t)e * a.n + n];
+                                const int64_t e = tile.expert;  // every pick of the tile's
+                                if (a.bias0) g += a.bias0[e * a.n + n];
+                                if (a.bias1) u += a.bias1[e * a.n + n];
                                 g = fminf(g, a.limit);
                                 u = fminf(fmaxf(u, -a.limit), a.limit);
-                                o = (u + 1.0f) * (g * (1.0f / (1.0f + expf(-(g * a.alpha)))));
+                                o = (u + 1.0f) * (g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-(g * a.alpha) * LOG2E)));
                             }
                             a.h[(int64_t)pos * a.ldh + n] = o;
                         }
