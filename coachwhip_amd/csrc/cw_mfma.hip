@@ -355,27 +355,34 @@ struct MQ8_0 {
 };
 
 // Q4_K: y = d*sc*q - dmin*m per sub-block of 32 (k_quants.rs:1821-1849, get_scale_min_k4 in
-// quantized/utils.rs:50-60). Codes sc*q (<= 945) are exact in fp16 with d as the running scale;
-// the minimum term is a second product of the same activations with codes -m (<= 63) and dmin as
-// its running scale.
+// quantized/utils.rs:50-60).
 struct MQ4_K {
     static constexpr int TS = 144, SBK = 256, LDS = 16;
     static constexpr int KST = 8, SCALE = 0, ORG = 16;
-    static constexpr bool HAS_MIN = true;
+    static constexpr bool HAS_MIN = false;
     static __device__ void fill(uint8_t *, int, int) {}
-    // the 12 scale bytes (4..15) of the super-block, read once per stage
+    // The minimum term is folded into the codes: y = s (a q - b) per weight, with the running
+    // scale s = max(|d|, |dmin|) of the super-block, a = (d / s) sc and b = (dmin / s) m of the
+    // sub-block (both within 63 in magnitude, so fp16 keeps them to 2^-11 of themselves, and the
+    // code a q - b takes one rounding). One accumulator and one MFMA per weight fragment.
+    static __device__ __forceinline__ float s_of(float d, float dm) { return fmaxf(fabsf(d), fabsf(dm)); }
+    // the 12 scale bytes (4..15) of the super-block, and d and dmin over s, read once per stage
     struct Stage {
         uint32_t b[3];
+        float fd, fm;
         __device__ __forceinline__ void load(const WinRef &w, int) {
             const uint2 lo = w.u64(-12);
             b[0] = lo.x;
             b[1] = lo.y;
             b[2] = w.u64(-4).x;
+            const uint32_t dd = w.u32x(-16);  // d, then dmin
+            const float d = h2f(dd & 0xFFFFu), dm = h2f(dd >> 16), s = s_of(d, dm);
+            fd = s > 0.f ? d / s : 0.f;
+            fm = s > 0.f ? dm / s : 0.f;
         }
         __device__ __forceinline__ uint32_t byte(int i) const { return (b[i >> 2] >> (8 * (i & 3))) & 0xFF; }
     };
-    static __device__ __forceinline__ float scale(const uint8_t *win) { return h2f(lds_u16(win)); }
-    static __device__ __forceinline__ float dmin(const uint8_t *win) { return h2f(lds_u16(win + 2)); }
+    static __device__ __forceinline__ float scale(const uint8_t *win) { return s_of(h2f(lds_u16(win)), h2f(lds_u16(win + 2))); }
     // 6-bit scale and min of sub-block j
     static __device__ __forceinline__ void sc_m(const Stage &st, int j, uint32_t &sc, uint32_t &m) {
         if (j < 4) {
@@ -387,7 +394,7 @@ struct MQ4_K {
             m = (a >> 4) | ((hi >> 6) << 4);
         }
     }
-    // codes sc*q of sub-block kk (sub-blocks 2c, 2c+1 are the low and high nibbles of qs[32c..32c+32))
+    // codes a q - b of sub-block kk (sub-blocks 2c, 2c+1 are the low and high nibbles of qs[32c..32c+32))
     struct Raw { uint2 q; };
     struct Look {};
     static __device__ __forceinline__ Raw raw(const WinRef &w, const Stage &, int kk, int grp) { return Raw{w.u64(32 * (kk >> 1) + 8 * grp)}; }
@@ -395,18 +402,13 @@ struct MQ4_K {
     static __device__ __forceinline__ uint4 make(const Raw &r, const Look &, const Stage &stg, int kk, int, bool zero) {
         uint32_t sc, m;
         sc_m(stg, kk, sc, m);
-        if (zero) sc = 0;
+        const float a = zero ? 0.f : stg.fd * (float)sc, b = zero ? 0.f : stg.fm * (float)m;
         const uint2 q = r.q;
         const int sh = 4 * (kk & 1);
-        const uint4 x = bytes_plus_1024((q.x >> sh) & 0x0F0F0F0Fu, (q.y >> sh) & 0x0F0F0F0Fu);
-        return fma4(x, splat_f16f((float)sc), splat_f16f(-1024.0f * (float)sc));
-    }
-    // codes -m for all 8 weights (the minimum term)
-    static __device__ __forceinline__ uint4 min_frag(const Stage &stg, int kk, int, bool zero) {
-        uint32_t sc, m;
-        sc_m(stg, kk, sc, m);
-        const uint32_t v = zero ? 0u : splat_f16f(-(float)m);
-        return make_uint4(v, v, v, v);
+        // q as fp16 (1024 + q less 1024: exact), then a q - b
+        const uint4 x = fma4(bytes_plus_1024((q.x >> sh) & 0x0F0F0F0Fu, (q.y >> sh) & 0x0F0F0F0Fu), splat_f16f(1.0f),
+                             splat_f16f(-1024.0f));
+        return fma4(x, splat_f16f(a), splat_f16f(-b));
     }
 };
 
