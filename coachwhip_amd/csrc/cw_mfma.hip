@@ -589,7 +589,9 @@ struct GmShape {
     // slower with either).
     static constexpr bool FAST = !MF::HAS_MIN && !std::is_same<MF, MMXFP4>::value;
     static constexpr bool PF = FAST, ADMA = FAST;
-    static constexpr int KA = 4, HPS = MF::KST / KA;                // K-steps per activation buffer, buffers per stage
+    // K-steps per activation buffer and buffers per stage. Q4_K's down and dense instances take 2:
+    // the halved buffers make room for a second window buffer beside two blocks per CU.
+    static constexpr int KA = std::is_same<MF, MQ4_K>::value && MODE != 0 ? 2 : 4, HPS = MF::KST / KA;
     static constexpr int A_HALF = KA * MF_MB * 64 * 16, A_BYTES = 2 * A_HALF;  // two activation buffers
     static constexpr int META_BYTES = MF_MT * 8;                     // scale and pick of each row of the tile
     static constexpr int FIXED = ((MF::LDS + 15) & ~15) + A_BYTES + META_BYTES;
@@ -814,8 +816,8 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
             }
             __builtin_amdgcn_s_waitcnt(0);  // this stage's windows and first activations
             __syncthreads();
-            if (S::HPS == 2)
-                issue_a(2 * st + 1);
+            if (S::HPS >= 2)
+                issue_a(S::HPS * st + 1);
             else if (st + 1 < st_hi)
                 issue_a(st + 1);
             if constexpr (S::WDB)
@@ -911,7 +913,7 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
                         for (int q = 0; q < NB; q++) lk[kk & 1][m][q] = MF::look(rw[kk & 1][m][q], stg[m][q], kk, grp, tab, zero[m][q]);
                 };
                 auto issue_av = [&](int kk) __attribute__((always_inline)) {
-                    const uint8_t *Ak = As + ((S::HPS == 2 ? kk / S::KA : st) & 1) * S::A_HALF + (kk % S::KA) * MF_MB * 64 * 16;
+                    const uint8_t *Ak = As + ((S::HPS >= 2 ? kk / S::KA : st) & 1) * S::A_HALF + (kk % S::KA) * MF_MB * 64 * 16;
 #pragma unroll
                     for (int mb = 0; mb < MBS; mb++) av[kk & 1][mb] = *(const f16x8 *)(Ak + (mb * 64 + lane) * 16);
                 };
@@ -937,14 +939,19 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
 #pragma unroll
                 for (int kk = 0; kk < KST; kk++) {
                     if (kk >= nke) break;
-                    if (S::HPS == 2 && kk == S::KA) {
-                        // second half-stage: its activations (loaded during the first) are in
-                        if (S::WDB && st + 1 < st_hi)
+                    if (S::HPS >= 2 && kk > 0 && kk % S::KA == 0) {
+                        // a later part of the stage: its activations (loaded during the previous
+                        // part) are in. Only the first part's wait can leave the next stage's
+                        // windows in flight: later parts' activations were requested after them.
+                        if (S::WDB && st + 1 < st_hi && kk == S::KA)
                             __builtin_amdgcn_s_waitcnt(WAIT_BUT_W);
                         else
                             __builtin_amdgcn_s_waitcnt(0);
                         __syncthreads();
-                        if (st + 1 < st_hi) issue_a(2 * (st + 1));
+                        if (kk / S::KA + 1 < S::HPS)
+                            issue_a(S::HPS * st + kk / S::KA + 1);
+                        else if (st + 1 < st_hi)
+                            issue_a(S::HPS * (st + 1));
                         if constexpr (S::PF) issue_av(kk);
                     }
                     if constexpr (!S::PF) {
@@ -985,7 +992,7 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
                     if (kk + 2 < KST && kk + 2 < nke) issue_raw(kk + 2);  // into the buffer step kk has just used
                     if (S::PF && kk + 1 < KST && kk + 1 < nke) {
                         issue_look(kk + 1);
-                        if (!(S::HPS == 2 && kk + 1 == S::KA)) issue_av(kk + 1);
+                        if (!(S::HPS >= 2 && (kk + 1) % S::KA == 0)) issue_av(kk + 1);
                     }
 #pragma unroll
                     for (int mb = 0; mb < MBS; mb++)
