@@ -166,11 +166,10 @@ struct WinRef {
 
 // Traits common to the formats: KST K-steps per stage; SCALE 0 = one f16 scale per super-block
 // (read by scale()), 1 = MXFP4's power-of-two block scales, 2 = one f16 scale per 32-weight block
-// (read by step_scale()); HAS_MIN = an f16 dmin per super-block and a 6-bit m per sub-block.
+// (read by step_scale()).
 struct MIQ2_XXS {
     static constexpr int TS = 66, SBK = 256, LDS = 256 * 16;
     static constexpr int KST = 8, SCALE = 0, ORG = 2;
-    static constexpr bool HAS_MIN = false;
     static __device__ void fill(uint8_t *lds, int tid, int nt) { copy_tab(lds, c_iq2xxs_f16, tid, nt); }
     struct Stage {
         __device__ __forceinline__ void load(const WinRef &, int) {}
@@ -197,7 +196,6 @@ struct MIQ2_XXS {
 struct MIQ2_S {
     static constexpr int TS = 82, SBK = 256, LDS = 1024 * 16;
     static constexpr int KST = 8, SCALE = 0, ORG = 66;
-    static constexpr bool HAS_MIN = false;
     static __device__ void fill(uint8_t *lds, int tid, int nt) { copy_tab(lds, c_iq2s_f16, tid, nt); }
     // The lane's bits of qh[8] and scales[8] (bytes 66..81), read once per stage: qh bits 2grp,
     // 2grp+1 of byte kk at bits 8(kk&3) + 2(kk>>2) of qh; the scale nibble of byte kk for this
@@ -231,7 +229,6 @@ struct MIQ2_S {
 struct MIQ3_S {
     static constexpr int TS = 110, SBK = 256, LDS = 512 * 8;
     static constexpr int KST = 8, SCALE = 0, ORG = 66;
-    static constexpr bool HAS_MIN = false;
     static __device__ void fill(uint8_t *lds, int tid, int nt) { copy_tab(lds, c_iq3s_f16, tid, nt); }  // entry i: 4 halves at byte 8*i
     // The lane's bits of qh[8] (bytes 66..73: bits 2grp, 2grp+1 of byte kk at bits 8(kk&3) +
     // 2(kk>>2)) and scales[4] (bytes 106..109), read once per stage (the read of the scales also
@@ -271,7 +268,6 @@ struct MIQ3_S {
 struct MMXFP4 {
     static constexpr int TS = 17, SBK = 32, LDS = 0;
     static constexpr int KST = 8, SCALE = 1, ORG = 1;
-    static constexpr bool HAS_MIN = false;
     static __device__ void fill(uint8_t *, int, int) {}
     struct Stage {
         __device__ __forceinline__ void load(const WinRef &, int) {}
@@ -334,7 +330,6 @@ __device__ __forceinline__ uint32_t splat_f16f(float v) {
 struct MQ8_0 {
     static constexpr int TS = 34, SBK = 32, LDS = 16;
     static constexpr int KST = 4, SCALE = 2, ORG = 2;
-    static constexpr bool HAS_MIN = false;
     static __device__ void fill(uint8_t *, int, int) {}
     struct Stage {
         __device__ __forceinline__ void load(const WinRef &, int) {}
@@ -359,7 +354,6 @@ struct MQ8_0 {
 struct MQ4_K {
     static constexpr int TS = 144, SBK = 256, LDS = 16;
     static constexpr int KST = 8, SCALE = 0, ORG = 16;
-    static constexpr bool HAS_MIN = false;
     static __device__ void fill(uint8_t *, int, int) {}
     // The minimum term is folded into the codes: y = s (a q - b) per weight, with the running
     // scale s = max(|d|, |dmin|) of the super-block, a = (d / s) sc and b = (dmin / s) m of the
@@ -415,43 +409,44 @@ struct MQ4_K {
 // Q2_K (what the shrink writes): y = d*(sc&15)*q - dmin*(sc>>4) per 16 weights (k_quants.rs:1152-1190).
 // K-step kk is sub-block kk of 32 weights: bits 2(kk&3) of qs[32(kk>>2) ..), so lane group grp
 // reads the 8 bytes qs[32(kk>>2) + 8grp ..) and its 8 weights share scale byte 2kk + (grp>>1).
-// Codes sc*q (<= 45) with d as the running scale; the minimum term as for Q4_K, codes -m (<= 15).
+// The minimum term folded into the codes as for Q4_K: y = s (a q - b), s = max(|d|, |dmin|),
+// a = (d / s) (sc & 15), b = (dmin / s) (sc >> 4), both within 15 in magnitude.
 struct MQ2_K {
     static constexpr int TS = 84, SBK = 256, LDS = 16;
     static constexpr int KST = 8, SCALE = 0, ORG = 16;
-    static constexpr bool HAS_MIN = true;
     static __device__ void fill(uint8_t *, int, int) {}
-    // the 16 scale bytes (0..15) of the super-block, read once per stage
+    // the 16 scale bytes (0..15) of the super-block, and d and dmin over s, read once per stage
     struct Stage {
         uint32_t b[4];
+        float fd, fm;
         __device__ __forceinline__ void load(const WinRef &w, int) {
             const uint2 lo = w.u64(-16), hi = w.u64(-8);
             b[0] = lo.x;
             b[1] = lo.y;
             b[2] = hi.x;
             b[3] = hi.y;
+            const uint32_t dd = w.u32x(64);  // d, then dmin
+            const float d = h2f(dd & 0xFFFFu), dm = h2f(dd >> 16), s = MQ4_K::s_of(d, dm);
+            fd = s > 0.f ? d / s : 0.f;
+            fm = s > 0.f ? dm / s : 0.f;
         }
         // scale byte 2kk + (grp >> 1)
         __device__ __forceinline__ uint32_t byte(int kk, int grp) const {
             return (b[kk >> 1] >> (16 * (kk & 1) + 8 * (grp >> 1))) & 0xFF;
         }
     };
-    static __device__ __forceinline__ float scale(const uint8_t *win) { return h2f(lds_u16(win + 80)); }
-    static __device__ __forceinline__ float dmin(const uint8_t *win) { return h2f(lds_u16(win + 82)); }
+    static __device__ __forceinline__ float scale(const uint8_t *win) { return MQ4_K::s_of(h2f(lds_u16(win + 80)), h2f(lds_u16(win + 82))); }
     struct Raw { uint2 q; };
     struct Look {};
     static __device__ __forceinline__ Raw raw(const WinRef &w, const Stage &, int kk, int grp) { return Raw{w.u64(32 * (kk >> 2) + 8 * grp)}; }
     static __device__ __forceinline__ Look look(const Raw &, const Stage &, int, int, const uint8_t *, bool) { return Look{}; }
     static __device__ __forceinline__ uint4 make(const Raw &r, const Look &, const Stage &stg, int kk, int grp, bool zero) {
-        const uint32_t sc = zero ? 0u : stg.byte(kk, grp) & 0xF;
+        const uint32_t sb = stg.byte(kk, grp);
+        const float a = zero ? 0.f : stg.fd * (float)(sb & 0xF), b = zero ? 0.f : stg.fm * (float)(sb >> 4);
         const int sh = 2 * (kk & 3);
-        const uint4 x = bytes_plus_1024((r.q.x >> sh) & 0x03030303u, (r.q.y >> sh) & 0x03030303u);
-        return fma4(x, splat_f16f((float)sc), splat_f16f(-1024.0f * (float)sc));
-    }
-    // codes -m for the lane's 8 weights (the minimum term)
-    static __device__ __forceinline__ uint4 min_frag(const Stage &stg, int kk, int grp, bool zero) {
-        const uint32_t v = zero ? 0u : splat_f16f(-(float)(stg.byte(kk, grp) >> 4));
-        return make_uint4(v, v, v, v);
+        const uint4 x = fma4(bytes_plus_1024((r.q.x >> sh) & 0x03030303u, (r.q.y >> sh) & 0x03030303u), splat_f16f(1.0f),
+                             splat_f16f(-1024.0f));
+        return fma4(x, splat_f16f(a), splat_f16f(-b));
     }
 };
 
@@ -463,7 +458,6 @@ struct MQ2_K {
 struct MIQ3_XXS {
     static constexpr int TS = 98, SBK = 256, LDS = 256 * 8;
     static constexpr int KST = 8, SCALE = 0, ORG = 66;
-    static constexpr bool HAS_MIN = false;
     static __device__ void fill(uint8_t *lds, int tid, int nt) { copy_tab(lds, c_iq3xxs_f16, tid, nt); }  // entry i: 4 halves at byte 8*i
     struct Stage {
         __device__ __forceinline__ void load(const WinRef &, int) {}
@@ -492,7 +486,6 @@ struct MIQ3_XXS {
 struct MIQ4_XS {
     static constexpr int TS = 136, SBK = 256, LDS = 16;
     static constexpr int KST = 8, SCALE = 2, ORG = 0;
-    static constexpr bool HAS_MIN = false;
     static __device__ void fill(uint8_t *, int, int) {}
     // d | scales_h << 16 and scales_l[4]: the super-block's first 8 bytes, read once per stage
     struct Stage {
@@ -583,11 +576,9 @@ struct GmShape {
     static constexpr int NM = MODE == 0 ? 2 : 1;
     static constexpr int NB = 1;
     // PF: K-step table lookups and activation fragments read one step ahead (two register sets).
-    // ADMA: the stage loads issued as inline asm (dma16). Both for the formats where they measured
-    // faster: not for the formats with a minimum term (Q4_K, Q2_K), whose second accumulator set
-    // leaves no registers for the second fragment set and which spill, nor for MXFP4 (equal or
+    // ADMA: the stage loads issued as inline asm (dma16). Both for every format but MXFP4 (equal or
     // slower with either).
-    static constexpr bool FAST = !MF::HAS_MIN && !std::is_same<MF, MMXFP4>::value;
+    static constexpr bool FAST = !std::is_same<MF, MMXFP4>::value;
     static constexpr bool PF = FAST, ADMA = FAST;
     // K-steps per activation buffer and buffers per stage. Q4_K's down and dense instances take 2:
     // the halved buffers make room for a second window buffer beside two blocks per CU.
@@ -638,8 +629,7 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
     using W = Win<MF>;
     constexpr int NB = S::NB, KST = MF::KST;
     constexpr int NM = 1;  // matrices per wave (a block has S::NM: gate/up waves are split)
-    constexpr bool POW2 = MF::SCALE == 1, STEP = MF::SCALE == 2, MIN = MF::HAS_MIN;
-    constexpr int NA = MIN ? NB : 1;  // accumulator sets of the minimum term
+    constexpr bool POW2 = MF::SCALE == 1, STEP = MF::SCALE == 2;
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int split_last;  // split-K: this block finished its work item's last split
     uint8_t *tab = smem;
@@ -699,10 +689,8 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
 
         const int n_ks = a.k / 32, n_st = (n_ks + KST - 1) / KST;
         f32x4 acc[NM][NB][MF_MB];
-        f32x4 accm[NM][NA][MF_MB];  // minimum term (Q4_K, Q2_K)
         float rs[NM][NB];     // running scale (f16 scales) ...
         int rb[NM][NB];       // ... or running base exponent (MXFP4)
-        float rsm[NM][NA];    // running dmin (Q4_K, Q2_K)
 #pragma unroll
         for (int m = 0; m < NM; m++)
 #pragma unroll
@@ -712,21 +700,10 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
 #pragma unroll
                 for (int mb = 0; mb < MF_MB; mb++) {
                     acc[m][q][mb] = f32x4{0, 0, 0, 0};
-                    asm volatile("" : "+v"(acc[m][q][mb]));  // see accm below
-                }
-            }
-#pragma unroll
-        for (int m = 0; m < NM; m++)
-#pragma unroll
-            for (int q = 0; q < NA; q++) {
-                rsm[m][q] = 1.f;
-#pragma unroll
-                for (int mb = 0; mb < MF_MB; mb++) {
-                    accm[m][q][mb] = f32x4{0, 0, 0, 0};
                     // the compiler must not treat the four elements as one value from here on: with
-                    // that assumption it fed later MFMAs three stale copies (wrong rows 1-3 of each
-                    // 4-row group); the empty asm emits nothing
-                    asm volatile("" : "+v"(accm[m][q][mb]));
+                    // that assumption it once fed later MFMAs three stale copies (wrong rows 1-3 of
+                    // each 4-row group); the empty asm emits nothing
+                    asm volatile("" : "+v"(acc[m][q][mb]));
                 }
             }
 
@@ -839,8 +816,8 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
                     stg[m][q].load(wr[m][q], grp);
                 }
 
-            bool zero[NM][NB], zerom[NM][NA];
-            float ratio[NM][NB], ratiom[NM][NA];  // running-scale moves of this stage (scale per super-block)
+            bool zero[NM][NB];
+            float ratio[NM][NB];  // running-scale moves of this stage (scale per super-block)
             if constexpr (STEP) {
 #pragma unroll
                 for (int m = 0; m < NM; m++)
@@ -878,12 +855,6 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
                         zero[m][q] = d == 0.f;
                         ratio[m][q] = d != 0.f ? rs[m][q] * __builtin_amdgcn_rcpf(d) : 1.f;
                         rs[m][q] = d != 0.f ? d : rs[m][q];
-                        if constexpr (MIN) {
-                            const float dm = MF::dmin(win[m][q]);
-                            zerom[m][q] = dm == 0.f;
-                            ratiom[m][q] = dm != 0.f ? rsm[m][q] * __builtin_amdgcn_rcpf(dm) : 1.f;
-                            rsm[m][q] = dm != 0.f ? dm : rsm[m][q];
-                        }
                     }
             }
 
@@ -924,10 +895,6 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
                         for (int q = 0; q < NB; q++) {
 #pragma unroll
                             for (int mb = 0; mb < MBS; mb++) acc[m][q][mb] *= ratio[m][q];
-                            if constexpr (MIN) {
-#pragma unroll
-                                for (int mb = 0; mb < MBS; mb++) accm[m][q][mb] *= ratiom[m][q];
-                            }
                         }
                 }
                 issue_raw(0);
@@ -974,12 +941,7 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
                                 }
                             }
                     }
-                    f16x8 bf[NM][NB], bm[NM][NA];
-#pragma unroll
-                    for (int m = 0; m < NM; m++)
-#pragma unroll
-                        for (int q = 0; q < NA; q++)
-                            if constexpr (MIN) bm[m][q] = as_f16x8(MF::min_frag(stg[m][q], kk, grp, zerom[m][q]));
+                    f16x8 bf[NM][NB];
 #pragma unroll
                     for (int m = 0; m < NM; m++)
 #pragma unroll
@@ -1001,7 +963,6 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
 #pragma unroll
                             for (int q = 0; q < NB; q++) {
                                 acc[m][q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[kk & 1][mb], bf[m][q], acc[m][q][mb], 0, 0, 0);
-                                if constexpr (MIN) accm[m][q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[kk & 1][mb], bm[m][q], accm[m][q][mb], 0, 0, 0);
                             }
                     __builtin_amdgcn_sched_barrier(0);
                 }
@@ -1020,9 +981,7 @@ __global__ __launch_bounds__(1024, 4) void k_gmm(const MfArgs a) {
 #pragma unroll
         for (int q = 0; q < NB; q++) fs[q] = POW2 ? ldexpf(1.0f, rb[0][q] - 128) : rs[0][q];
         auto value = [&](int q, int mb, int i, float sa) __attribute__((always_inline)) {
-            float v = acc[0][q][mb][i] * fs[q];
-            if constexpr (MIN) v += accm[0][q][mb][i] * rsm[0][q];
-            return v * sa;
+            return acc[0][q][mb][i] * fs[q] * sa;
         };
         if constexpr (MODE == 0) {
             // the up waves hand their values to the gate waves through LDS (the activation
