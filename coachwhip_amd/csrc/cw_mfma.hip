@@ -1121,7 +1121,7 @@ __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
 constexpr int PILE_PER = 16, PILE_LDS = 12288;
 __global__ __launch_bounds__(1024) void k_piles(const uint32_t *slots, const uint32_t *ids, int TK, int K, int n_slots,
                                                  int *pile_pick, int *pile_tok, MfTile *tiles, int *n_tiles) {
-    __shared__ int cnt[1024], off[1024], cur[1024], rep[1024], wtot[16], wttot[16];
+    __shared__ int cnt[1024], off[1024], cur[1024], rep[1024], wtot[16], wttot[16], wftot[16];
     __shared__ int staged[PILE_LDS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     cnt[tid] = 0;
@@ -1151,26 +1151,35 @@ __global__ __launch_bounds__(1024) void k_piles(const uint32_t *slots, const uin
             }
     }
     __syncthreads();
-    // exclusive scans of the counts and of the tile counts: per wave, then over the 16 wave totals
+    // exclusive scans of the counts, the tile counts and the first tiles: per wave, then over the
+    // 16 wave totals. The tile list holds every slot's first tile, then the later tiles of the
+    // slots with more than MF_MT picks: the GEMMs hand out work items in list order, so the last
+    // round of items, which only some blocks run, takes the (smaller) remainder tiles.
     const int c = tid < n_slots ? cnt[tid] : 0;
-    const int tc = (c + MF_MT - 1) / MF_MT;
-    const int ic = wave_incl_scan(c, lane), itc = wave_incl_scan(tc, lane);
+    const int tc = (c + MF_MT - 1) / MF_MT, fc = c > 0 ? 1 : 0;
+    const int ic = wave_incl_scan(c, lane), itc = wave_incl_scan(tc, lane), ifc = wave_incl_scan(fc, lane);
     if (lane == 63) {
         wtot[wave] = ic;
         wttot[wave] = itc;
+        wftot[wave] = ifc;
     }
     __syncthreads();
-    int wc = 0, wtc = 0;
-    for (int w = 0; w < wave; w++) {
-        wc += wtot[w];
-        wtc += wttot[w];
+    int wc = 0, wtc = 0, wfc = 0, nf = 0;
+    for (int w = 0; w < 16; w++) {
+        if (w < wave) {
+            wc += wtot[w];
+            wtc += wttot[w];
+            wfc += wftot[w];
+        }
+        nf += wftot[w];
     }
-    const int my_off = wc + ic - c, my_toff = wtc + itc - tc;
+    const int my_off = wc + ic - c, my_toff = wtc + itc - tc, my_f = wfc + ifc - fc;
     if (tid == 1023) *n_tiles = my_toff + tc;
     off[tid] = my_off;
     if (tid < n_slots) {
         const int ex = ids && c > 0 ? (int)ids[rep[tid]] : tid;
-        for (int q = 0; q < tc; q++) tiles[my_toff + q] = MfTile{tid, my_off + q * MF_MT, min(MF_MT, c - q * MF_MT), ex};
+        for (int q = 0; q < tc; q++)
+            tiles[q == 0 ? my_f : nf + (my_toff - my_f) + q - 1] = MfTile{tid, my_off + q * MF_MT, min(MF_MT, c - q * MF_MT), ex};
     }
     __syncthreads();
     for (int c0 = 0; c0 < TK; c0 += 1024 * PILE_PER) {
