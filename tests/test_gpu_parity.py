@@ -601,6 +601,48 @@ def test_moe_layer_through_a_slot_table():
     assert O.rel_l2(host(out2), want2) <= REL_L2_F32
 
 
+@pytest.mark.parametrize("path", sorted(PATHS))
+@pytest.mark.parametrize("dts,x_scale", [((F.MXFP4,) * 3, 1.0), ((F.Q4_K, F.Q4_K, F.IQ4_XS), 2.0 ** -8)],
+                         ids=["mxfp4", "q4_k"])
+def test_moe_biases_follow_the_expert_through_a_slot_table(dts, x_scale, path, monkeypatch):
+    # clamped SwiGLU's biases are per expert while the weights are per slot: a permuted table
+    # catches a bias read by slot (or by tile) instead of by the picked expert. The synthetic
+    # Q4_K rows are large; unscaled x puts the gate/up sums in the thousands, where rounding x to
+    # fp16 alone moves the clamped SwiGLU by ~1e-3, so x is scaled down (and kept fp16-exact)
+    monkeypatch.setenv("CWMOE_PREFILL_MIN_TOKENS", PATHS[path])
+    say("moe bias slots", dts[0], path)
+    rng = np.random.default_rng(91)
+    E, K, slots, h, I, T = 48, 4, 20, 1024, 512, 40
+    layer = synth.moe_weights(E, K, h, I, dts, rng, n_slots=slots, act=1)
+    layer.bias = [b * 50.0 for b in layer.bias]  # large enough that a wrong row moves the output
+    table = np.full(E, 0xFFFFFFFF, dtype=np.uint32)
+    resident = rng.choice(E, size=slots, replace=False)
+    table[resident] = rng.permutation(slots).astype(np.uint32)
+    mask = np.full(E, -1e30, dtype=np.float32)
+    mask[resident] = 0.0
+    x = (rng.standard_normal((T, h)) * x_scale).astype(np.float16).astype(np.float32)
+    logits = rng.standard_normal((T, E)).astype(np.float32) + mask
+    assert not synth.near_ties_within_top_k(logits, K)
+    moe = upload_layer(layer, slot_table=table)
+    out, ids, _ = moe.forward(dev(x), dev(logits))
+    want, wids, _, wmiss = O.moe_layer(layer, x, logits, slot_table=table, n_slots=slots)
+    assert wmiss == 0
+    assert np.array_equal(host(ids).view(np.uint32), wids)
+    err = O.rel_l2(host(out), want)
+    say("  rel_l2", err)
+    assert err <= REL_L2_GATE
+    # the same layer with the biases of two resident experts swapped must not match
+    swapped = list(layer.bias)
+    a, b = resident[:2]
+    for m in range(3):
+        s = swapped[m].copy()
+        s[[a, b]] = s[[b, a]]
+        swapped[m] = s
+    layer.bias = swapped
+    other, _, _, _ = O.moe_layer(layer, x, logits, slot_table=table, n_slots=slots)
+    assert O.rel_l2(host(out), other) > 10 * REL_L2_GATE
+
+
 @pytest.mark.parametrize("E", [512, 400])
 def test_moe_decode_through_a_slot_table(E):
     """Config 5's one-token layer: the persistent decode kernel with 8 router logits per lane, where
