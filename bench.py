@@ -375,6 +375,35 @@ def bench_c4(args, torch, np, dev):
                         "as stored, activations as three FP6 E2M3 terms with E8M0 scales per 32, f32 accumulate")}
     log("prefill", prefill)
 
+    # the same layers with their expert matrices repacked in row groups of 16 (MXFP4_R16, opt-in:
+    # ExpertBank.rows16): the same blocks, read by the same kernels' row-group variants; outputs
+    # equal to the GGUF rows' bit for bit
+    r16 = None
+    if not args.no_rows16:
+        log("row groups of 16: repacking the chain's experts")
+        lay16 = [ops.MoeLayer(*[b.rows16() for b in lay.banks], n_experts=E, top_k=K, norm_topk_prob=True, act=lay.act)
+                 for lay in layers]
+        same = all(bool(torch.equal(lay16[l].forward(xp, lp)[0], eager[l])) for l in range(len(eager)))
+        d16 = lay16[0].forward(x_all[0], logits_all[0, 0])[0]
+        same = same and bool(torch.equal(d16, out0))
+        g16 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g16):
+            for r in range(reps):
+                lay16[r % L].forward(xp, lp)
+        torch.cuda.synchronize()
+        pre16, pre16_all = time_replays(torch, g16, reps)
+        del g16
+        ms16 = time_graph(torch, lay16, x_all, logits_all, args.warmup, args.steps)
+        dec16 = ms16 * 1e3 / (args.steps * L)
+        r16 = {"prefill_us_per_layer": round(pre16, 2), "prefill_tokens_per_s": round(T / (pre16 * 1e-6)),
+               "prefill_us_per_layer_replays": [round(v, 1) for v in pre16_all],
+               "decode_us_per_layer": round(dec16, 3), "decode_gbs": round(layer_bytes / (dec16 * 1e-6) / 1e9, 2),
+               "outputs_equal_gguf_rows": same,
+               "note": "opt-in layout (ExpertBank.rows16 / cw_repack_rows16); the line's value and prefill are GGUF rows"}
+        log("rows16", r16)
+        del lay16
+        torch.cuda.empty_cache()
+
     cpu = None
     if not args.no_cpu_baseline:
         host = host_cpu()
@@ -419,7 +448,7 @@ def bench_c4(args, torch, np, dev):
                      "traffic": measured_traffic(os.path.dirname(os.path.abspath(__file__)), TRAFFIC_PROFILE_C4),
                      "traffic_source": TRAFFIC_PROFILE_C4,
                      "kernel": "MoE decode layer (MXFP4, clamped SwiGLU)", "bytes_per_launch": layer_bytes},
-        "prefill": prefill, "parity": parity, "cpu_baseline": cpu,
+        "prefill": prefill, "layout_rows16": r16, "parity": parity, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
 
@@ -635,6 +664,7 @@ def main():
     ap.add_argument("--prefill-tokens", type=int, default=1500)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-rows16", action="store_true", help="c4: skip the row-groups-of-16 layout's numbers")
     ap.add_argument("--seed", type=int, default=3)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of known size (for scaling HBM counters) and exit")

@@ -70,6 +70,8 @@ SIGNATURES = {
     "cw_matvec_id": ([_I, _L, _L, _L, _L, _P, _P, _I, _P, _I, _I, _P, _P], _I),
     "cw_matmul_id_grouped_workspace_size": ([_I, _L, _L, _L, _L, _I, _I, _I], ctypes.c_size_t),
     "cw_matmul_id_grouped": ([_I, _L, _L, _L, _L, _P, _P, _I, _P, _I, _I, _P, _P, ctypes.c_size_t, _P], _I),
+    "cw_rows16_bytes": ([_L, _L], _L),
+    "cw_repack_rows16": ([_P, _L, _P, _L, _L, _L, _L, _P], _I),
     "cw_swiglu": ([_P, _P, _P, _L, _P], _I),
     "cw_clamped_swiglu": ([_P, _P, _P, _P, _P, _L, _I, _I, ctypes.c_float, ctypes.c_float, _P, _P], _I),
     "cw_weighted_sum": ([_P, _P, _P, _P, _I, _I, _I, _P, _P], _I),

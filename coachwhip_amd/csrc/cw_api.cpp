@@ -42,7 +42,7 @@ const char *cw_last_error(void) { return g_err; }
 int cw_block_size(int dtype) {
     switch (dtype) {
     case CW_F32: case CW_F16: return 1;
-    case CW_Q8_0: case CW_MXFP4: return 32;
+    case CW_Q8_0: case CW_MXFP4: case CW_MXFP4_R16: return 32;
     case CW_Q2_K: case CW_Q3_K: case CW_Q4_K: case CW_Q5_K: case CW_Q6_K: case CW_IQ2_XXS: case CW_IQ2_S:
     case CW_IQ3_XXS: case CW_IQ3_S: case CW_IQ4_XS: return 256;
     default: return 0;
@@ -64,7 +64,7 @@ int cw_type_size(int dtype) {
     case CW_IQ2_XXS: return 66;
     case CW_IQ2_S: return 82;
     case CW_IQ3_S: return 110;
-    case CW_MXFP4: return 17;
+    case CW_MXFP4: case CW_MXFP4_R16: return 17;
     default: return 0;
     }
 }

@@ -57,6 +57,9 @@ struct MfArgs {
     uint8_t *hp;
     int64_t hp_row;
     int hp_blocks;
+    // the weights' layout on the scaled MFMA: 0 GGUF rows (CW_MXFP4), 1 rows in groups of 16
+    // (CW_MXFP4_R16)
+    int layout;
 };
 
 // Work a pack launch also does for the dense matmul that follows it: the tile list of m rows, and
@@ -96,10 +99,17 @@ int combine_picks(const float *dn, const float *w, const float *bias, const uint
 // and E8M0 block scales), the activations as three FP6 terms with E8M0 scales per 32 values.
 bool mxfp4_scaled();
 // a matrix of k weights per row runs on the scaled MFMA (MXFP4, at least two 128-wide K steps)
-inline bool mxfp4_scaled_for(int dtype, int64_t k) { return dtype == CW_MXFP4 && k > 128 && k % 32 == 0 && mxfp4_scaled(); }
+// (MXFP4 in row groups of 16 has no other path)
+inline bool mxfp4_scaled_for(int dtype, int64_t k) {
+    return k > 128 && k % 32 == 0 && ((dtype == CW_MXFP4 && mxfp4_scaled()) || dtype == CW_MXFP4_R16);
+}
 size_t fp6_rows_bytes(int64_t rows, int64_t k);
 int pack_rows_fp6(const float *x, int rows, int k, int ldx, uint8_t *out, hipStream_t s);
 int mxfp4_gateup(const MfArgs &a, int tiles_max, hipStream_t s);
 int mxfp4_down(const MfArgs &a, int tiles_max, hipStream_t s);
+// n_mats MXFP4 matrices of n GGUF rows of k weights (src_stride bytes apart) into the row-group
+// layout of CW_MXFP4_R16 (dst_stride bytes apart, each (n + 15) / 16 * 16 rows)
+int rows16_repack(const uint8_t *src, int64_t src_stride, uint8_t *dst, int64_t dst_stride, int64_t n_mats, int n, int k,
+                  hipStream_t s);
 
 }  // namespace cw

@@ -1300,7 +1300,7 @@ __global__ void k_fill_zero(float *p, int64_t n) {
 
 bool mfma_supported(int dtype) {
     return dtype == CW_IQ2_XXS || dtype == CW_IQ2_S || dtype == CW_IQ3_S || dtype == CW_MXFP4 || dtype == CW_Q4_K || dtype == CW_Q8_0 ||
-           dtype == CW_Q2_K || dtype == CW_IQ3_XXS || dtype == CW_IQ4_XS;
+           dtype == CW_Q2_K || dtype == CW_IQ3_XXS || dtype == CW_IQ4_XS || dtype == CW_MXFP4_R16;
 }
 
 int max_tiles(int TK, int n_slots) { return (TK + MF_MT - 1) / MF_MT + (n_slots < TK ? n_slots : TK); }

@@ -128,8 +128,14 @@ static uint32_t decode_polls() {
     return e ? (uint32_t)strtoul(e, nullptr, 10) : (1u << 17);
 }
 
+static bool has_rows16(const cw_moe_desc *d) {
+    return d->dtype[0] == CW_MXFP4_R16 || d->dtype[1] == CW_MXFP4_R16 || d->dtype[2] == CW_MXFP4_R16;
+}
+
+// Matrices in row groups of 16 are read by the grouped GEMMs at any token count (and by the
+// one-launch decode for one token, where it has an instance).
 static bool grouped_path(const cw_moe_desc *d, int T) {
-    return T >= prefill_min_tokens() && d->dtype[0] == d->dtype[1] && mfma_supported(d->dtype[0]) &&
+    return (T >= prefill_min_tokens() || has_rows16(d)) && d->dtype[0] == d->dtype[1] && mfma_supported(d->dtype[0]) &&
            mfma_supported(d->dtype[2]) && (d->slot_table ? d->n_slots : d->n_experts) <= 1024;
 }
 
@@ -149,17 +155,23 @@ static int check_desc(const cw_moe_desc *d, int T) {
     const int n_slots = d->slot_table ? d->n_slots : d->n_experts;
     CW_REQUIRE(n_slots > 0, "moe: %d slots", n_slots);
     for (int m = 0; m < 3; m++) {
-        if (!is_weight_type(d->dtype[m])) return set_error(CW_ENOTSUP, "moe: matrix %d has unsupported dtype %d", m, d->dtype[m]);
+        if (!is_expert_type(d->dtype[m])) return set_error(CW_ENOTSUP, "moe: matrix %d has unsupported dtype %d", m, d->dtype[m]);
         const int bs = cw_block_size(d->dtype[m]);
         CW_REQUIRE(ks[m] % bs == 0, "moe: matrix %d rows of %d weights are not whole %d-weight blocks", m, ks[m], bs);
         if (ks[m] > max_gemv_k()) return set_error(CW_ENOTSUP, "moe: rows of %d weights exceed %d", ks[m], max_gemv_k());
-        const int64_t need = (int64_t)ns[m] * (ks[m] / bs) * cw_type_size(d->dtype[m]);
+        const int64_t need = matrix_bytes(d->dtype[m], ns[m], (int64_t)(ks[m] / bs) * cw_type_size(d->dtype[m]));
         CW_REQUIRE(d->slot_stride[m] >= need, "moe: matrix %d slot stride %lld below its %lld bytes", m,
                    (long long)d->slot_stride[m], (long long)need);
         CW_REQUIRE(d->w[m] != nullptr, "moe: matrix %d is null", m);
     }
     CW_REQUIRE(d->act == CW_ACT_CLAMPED_SWIGLU || (!d->bias[0] && !d->bias[1] && !d->bias[2]),
                "moe: biases need the clamped SwiGLU activation");
+    if (has_rows16(d) && !grouped_path(d, 1 > T ? 1 : T))
+        return set_error(CW_ENOTSUP, "moe: matrices in row groups of 16 need gate and up of one type, grouped-GEMM "
+                                     "formats and at most 1024 slots");
+    for (int m = 0; m < 3; m++)
+        if (d->dtype[m] == CW_MXFP4_R16 && !mxfp4_scaled_for(CW_MXFP4_R16, ks[m]))
+            return set_error(CW_ENOTSUP, "moe: matrix %d in row groups of 16 has rows of %d weights (over 128 needed)", m, ks[m]);
     return CW_OK;
 }
 
@@ -247,6 +259,7 @@ static int moe_grouped(const cw_moe_desc *d, const MoeArgs &a, const MoeLayout &
     g.ids = a.ids;
     g.h = a.h;
     g.ldh = P;
+    g.layout = d->dtype[0] == CW_MXFP4_R16;
     if (gx) {
         g.ap = (const uint8_t *)x16;
         g.ap_row = (int64_t)fp6_rows_bytes(1, a.H);
@@ -281,6 +294,7 @@ static int moe_grouped(const cw_moe_desc *d, const MoeArgs &a, const MoeLayout &
     dn.pile_pick = pile_pick;
     dn.K = K;
     dn.dn = (float *)(base + L.dn);
+    dn.layout = d->dtype[2] == CW_MXFP4_R16;
     if (dx) {
         dn.ap = (const uint8_t *)h16;
         dn.ap_row = (int64_t)fp6_rows_bytes(1, P);
@@ -338,11 +352,13 @@ static int moe_layer(const cw_moe_desc *d, const float *x, const float *logits, 
     a.state = base + L.state;
     a.polls = decode_polls();
 
-    if (L.grouped) return moe_grouped(d, a, L, base, T, s);
-    if (T == 1 && d->dtype[0] == d->dtype[1] && decode_single_launch()) {
+    // one token: the one-launch decode where it has an instance (MXFP4_R16 matrices go to the
+    // grouped GEMMs otherwise)
+    if (T == 1 && d->dtype[0] == d->dtype[1] && decode_single_launch() && (!L.grouped || has_rows16(d))) {
         rc = moe_decode(d->dtype[0], d->dtype[2], a, s);
         if (rc != CW_ENOTSUP) return rc;
     }
+    if (L.grouped) return moe_grouped(d, a, L, base, T, s);
     if (d->dtype[0] == d->dtype[1]) {
         if ((rc = moe_gateup(d->dtype[0], a, T, s))) return rc;
     } else {
@@ -412,7 +428,7 @@ static GroupedLayout grouped_layout(int dtype, int64_t k, int64_t n_slots, int x
 
 // CW_OK when the grouped GEMM takes this call, else the status to return (CW_ENOTSUP: use cw_matvec_id)
 static int grouped_check(int dtype, int64_t n, int64_t k, int64_t n_slots, int64_t slot_stride, int K, int T) {
-    if (!is_weight_type(dtype)) return set_error(CW_ENOTSUP, "matmul_id_grouped: dtype %d is not supported", dtype);
+    if (!is_expert_type(dtype)) return set_error(CW_ENOTSUP, "matmul_id_grouped: dtype %d is not supported", dtype);
     if (!mfma_supported(dtype)) return set_error(CW_ENOTSUP, "matmul_id_grouped: dtype %d has no grouped kernel", dtype);
     const int bs = cw_block_size(dtype);
     CW_REQUIRE(n > 0 && k > 0 && n < (1ll << 31), "matmul_id_grouped: n %lld, k %lld", (long long)n, (long long)k);
@@ -421,10 +437,12 @@ static int grouped_check(int dtype, int64_t n, int64_t k, int64_t n_slots, int64
     CW_REQUIRE(n_slots > 0, "matmul_id_grouped: %lld slots", (long long)n_slots);
     CW_REQUIRE((int64_t)T * K < (1ll << 30), "matmul_id_grouped: %lld picks", (long long)T * K);
     const int64_t row_bytes = k / bs * cw_type_size(dtype);
-    CW_REQUIRE(slot_stride >= n * row_bytes, "matmul_id_grouped: slot stride %lld below the %lld-byte matrix",
-               (long long)slot_stride, (long long)(n * row_bytes));
+    CW_REQUIRE(slot_stride >= matrix_bytes(dtype, n, row_bytes), "matmul_id_grouped: slot stride %lld below the %lld-byte matrix",
+               (long long)slot_stride, (long long)matrix_bytes(dtype, n, row_bytes));
     if (n_slots > 1024) return set_error(CW_ENOTSUP, "matmul_id_grouped: %lld slots (1024 max)", (long long)n_slots);
-    if (k % 256 && dtype != CW_Q8_0 && dtype != CW_MXFP4)
+    if (dtype == CW_MXFP4_R16 && !mxfp4_scaled_for(dtype, k))
+        return set_error(CW_ENOTSUP, "matmul_id_grouped: rows in groups of 16 of %lld weights (over 128 needed)", (long long)k);
+    if (k % 256 && dtype != CW_Q8_0 && dtype != CW_MXFP4 && dtype != CW_MXFP4_R16)
         return set_error(CW_ENOTSUP, "matmul_id_grouped: k %lld is not whole super-blocks", (long long)k);
     if (k > 8192) return set_error(CW_ENOTSUP, "matmul_id_grouped: k %lld above 8192", (long long)k);
     return CW_OK;
@@ -573,6 +591,7 @@ int cw_matmul_id_grouped(int dtype, int64_t n, int64_t k, int64_t n_slots, int64
     a.pile_pick = pile_pick;
     a.K = K;
     a.dn = out;
+    a.layout = dtype == CW_MXFP4_R16;
     if (gx) {
         a.ap = (const uint8_t *)x16;
         a.ap_row = (int64_t)fp6_rows_bytes(1, k);
@@ -584,6 +603,26 @@ int cw_matmul_id_grouped(int dtype, int64_t n, int64_t k, int64_t n_slots, int64
     if (rc) return rc;
     hipLaunchKernelGGL(k_nan_rows, flat_grid(TK), dim3(256), 0, s, ids, TK, (uint32_t)n_slots, (int)n, out);
     return check_launch("k_nan_rows");
+}
+
+int64_t cw_rows16_bytes(int64_t n, int64_t k) {
+    return n > 0 && k > 0 && k % 32 == 0 ? matrix_bytes(CW_MXFP4_R16, n, k / 32 * 17) : 0;
+}
+
+int cw_repack_rows16(const void *src, int64_t src_stride, void *dst, int64_t dst_stride, int64_t n_mats, int64_t n,
+                     int64_t k, cw_stream_t stream) {
+    CW_REQUIRE(n > 0 && n < (1ll << 31) && n_mats >= 0, "repack_rows16: n %lld, %lld matrices", (long long)n, (long long)n_mats);
+    CW_REQUIRE(k > 128 && k % 32 == 0 && k <= 8192, "repack_rows16: k %lld (a multiple of 32, 160..8192)", (long long)k);
+    const int64_t rb = k / 32 * 17;
+    CW_REQUIRE(src_stride >= n * rb && dst_stride >= cw_rows16_bytes(n, k), "repack_rows16: strides %lld, %lld too small",
+               (long long)src_stride, (long long)dst_stride);
+    CW_REQUIRE(n_mats == 0 || (src && dst), "repack_rows16: null pointer");
+    CW_REQUIRE((((uintptr_t)dst | (uintptr_t)dst_stride) & 15) == 0, "repack_rows16: dst and its stride must be 16-byte aligned");
+    const uint8_t *s8 = (const uint8_t *)src;
+    uint8_t *d8 = (uint8_t *)dst;
+    CW_REQUIRE(n_mats == 0 || s8 + (n_mats - 1) * src_stride + n * rb <= d8 || d8 + (n_mats - 1) * dst_stride + cw_rows16_bytes(n, k) <= s8,
+               "repack_rows16: source and destination overlap");
+    return rows16_repack(s8, src_stride, d8, dst_stride, n_mats, (int)n, (int)k, (hipStream_t)stream);
 }
 
 int cw_route_topk(const float *logits, int T, int E, int K, int norm, uint32_t *ids, float *w, cw_stream_t stream) {

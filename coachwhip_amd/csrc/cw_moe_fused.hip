@@ -328,6 +328,34 @@ __device__ __forceinline__ void store_coherent(float *p, float v) {
 template <class F> struct RowDma { static constexpr bool on = false; };
 template <> struct RowDma<FMXFP4> { static constexpr bool on = true; };
 
+// MXFP4 matrices with their rows in groups of 16 (CW_MXFP4_R16): the same blocks, block sb of row r
+// at rows16_offset(r, sb). Their gate/up rows are LDS-staged as row pairs (below).
+struct FMXFP4R16 : FMXFP4 {};
+template <> struct RowDma<FMXFP4R16> { static constexpr bool on = true; };
+template <class F> struct Rows16 { static constexpr bool on = false; };
+template <> struct Rows16<FMXFP4R16> { static constexpr bool on = true; };
+
+// rows16_offset in 32 bits (the decode's matrices are below 2 GiB: its launch checks)
+__device__ __forceinline__ uint32_t rows16_off32(int r, int b, int nblk) {
+    const int c = b >> 2, cb = 4 * c + 4 <= nblk ? 4 : nblk - 4 * c;
+    return (uint32_t)(r >> 4) * (uint32_t)(272 * nblk) + (uint32_t)(c * 1088 + ((r & 15) * cb + (b & 3)) * 17);
+}
+// block sb of row r of the matrix at mat (rows of rb bytes), in format F's layout
+template <class F>
+__device__ __forceinline__ typename F::Raw load_rc(const uint8_t *mat, int64_t r, int64_t rb, int sb) {
+    if constexpr (Rows16<F>::on) return F::load(mat + rows16_off32((int)r, sb, (int)rb / 17), 0);
+    else return F::load(mat + r * rb, sb);
+}
+
+// A row pair (rows r0, r0 + 1, r0 even: one group) of an MXFP4_R16 matrix staged in LDS: the pair's
+// blocks of step c are one run of 34 cb bytes (cb = blocks of the step) at rows16_offset(r0, 4c),
+// 8-byte aligned for the full steps and 4-byte aligned for a last step of fewer blocks, brought
+// as the 16-byte pieces that hold it: 9 per full step, pr16_last for the last, in step order.
+// (Staging a whole group per block instead, one contiguous run of each matrix, measured slower:
+// its loads wait for x, and its rows for all of the group's loads.)
+__host__ __device__ __forceinline__ int pr16_last(int nblk) { return nblk % 4 ? (12 + 34 * (nblk % 4) + 15) / 16 : 0; }
+__host__ __device__ __forceinline__ int pr16_pieces(int nblk) { return 9 * (nblk / 4) + pr16_last(nblk); }
+
 // One 16-byte chunk per lane from global memory into LDS at lds_base + 16 * lane. Issued as inline
 // asm: the compiler's waits then do not cover these loads (the kernel waits for them itself with
 // vmcnt), and no LDS read of the kernel is taken to alias them. M0 is saved and restored.
@@ -364,6 +392,14 @@ __device__ __forceinline__ FMXFP4::Raw mx_from_lds(const uint8_t *win, int o) {
 // Bytes of a row's window in LDS: its 16-byte chunks from the one holding its first byte, plus the
 // 4 bytes that the last block's dword reads may touch past its end.
 __host__ __device__ __forceinline__ int row_window(int row_bytes) { return ((row_bytes + 15 + 15 + 4) >> 4) << 4; }
+// LDS-staged gate/up rows: a window per row (GGUF rows), or per row pair of each matrix (MXFP4_R16),
+// and a wave's item buffer (RI rows of gate and up, then 2 RI bias values in 16 bytes)
+template <class FG>
+__host__ __device__ __forceinline__ int gu_window(int nsbg) {
+    return Rows16<FG>::on ? 16 * pr16_pieces(nsbg) : row_window(nsbg * FG::TS);
+}
+template <class FG, int RI>
+__host__ __device__ __forceinline__ int gu_ibuf(int nsbg) { return (Rows16<FG>::on ? 2 : 2 * RI) * gu_window<FG>(nsbg) + 16; }
 
 // The whole decode layer (one token) in one launch of a grid that fits on the device at once.
 // Loads are issued as early as their addresses are known, since every wait on them counts in
@@ -420,7 +456,7 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
     const int subg = lane % LG, rsg = lane / LG, nsbg = a.H / 32;
     float xr[XG][32];
     // GDMA: item buffer b of wave w at hs + (b * NW + w) * ibuf; x goes into the buffer-1 region
-    const int x_off = RowDma<FG>::on ? NW * (2 * RI * row_window(a.H / 32 * FG::TS) + 16) : 0;
+    const int x_off = RowDma<FG>::on ? NW * gu_ibuf<FG, RI>(a.H / 32) : 0;
     if constexpr (RowDma<FG>::on) {
         // x once per block into the (not yet used) hidden-row region, read into registers below:
         // every wave loading all of x (35 MB across config 4's grid) held up the logits and x
@@ -500,8 +536,7 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
     static_assert(!GDMA || (LG == 64 && XG == 2), "the LDS-staged gate/up rows take one row per wave pass");
     // GDMA: this wave's two item buffers in the (not yet used) hidden-row region: per buffer RI
     // gate rows, RI up rows, then the 2*RI bias values
-    const int win = row_window(nsbg * FG::TS);
-    const int ibuf = 2 * RI * win + 16;
+    const int win = gu_window<FG>(nsbg), ibuf = gu_ibuf<FG, RI>(nsbg);
     uint8_t *wbuf = (uint8_t *)hs + wave * ibuf;
     auto issue_item = [&](int it, int b) {
         const int j = it / row_items, r0 = (it - j * row_items) * RI;
@@ -509,6 +544,23 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
         const uint32_t slot = __shfl(my_slot, j), e = __shfl(rid, j);
         const uint32_t sl = slot == 0xFFFFFFFFu ? 0 : slot;
         uint8_t *ib = wbuf + b * NW * ibuf;
+        if constexpr (Rows16<FG>::on) {
+            // the row pair of each matrix: 4 loads of up to 64 pieces, the last with the lanes of
+            // the pieces left; a pair past I reads the last pair
+            const int rp = min(r0, (a.I - 1) & ~1), npc = pr16_pieces(nsbg), nfull = nsbg / 4;
+#pragma unroll
+            for (int m = 0; m < 2; m++) {
+                const uint8_t *mat = m ? a.wu + (int64_t)sl * a.su : a.wg + (int64_t)sl * a.sg;
+                const uint32_t w = hs_lds + (uint32_t)(ib - (uint8_t *)hs) + m * win;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int p = min(64 * i + lane, npc - 1), c = p < 9 * nfull ? p / 9 : nfull;
+                    const uint8_t *run = mat + rows16_off32(rp, 4 * c, nsbg);
+                    if (i < 3 || 64 * i + lane < npc)  // the launch keeps 192 < npc <= 256
+                        lds_dma16((const uint8_t *)((uintptr_t)run & ~(uintptr_t)15) + 16 * (p - 9 * c), w + 1024 * i);
+                }
+            }
+        } else {
 #pragma unroll
         for (int q = 0; q < RI; q++) {
             const int r = min(r0 + q, a.I - 1);
@@ -524,12 +576,13 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
                 if (lane < (win >> 4) - 64) lds_dma16(al + 16 * min(64 + lane, nch - 1), w + 1024);
             }
         }
+        }
         // bias values (gate rows, then up rows); a layer without biases re-reads x
         if (lane < 2 * RI) {
             const int q = lane % RI;
             const float *bsrc = lane < RI ? a.bg : a.bu;
             const float *src = bsrc ? bsrc + (int64_t)(e < (uint32_t)a.E ? e : 0) * a.I + min(r0 + q, a.I - 1) : a.x;
-            lds_dma4(src, hs_lds + (uint32_t)(ib - (uint8_t *)hs) + 2 * RI * win);
+            lds_dma4(src, hs_lds + (uint32_t)(ib - (uint8_t *)hs) + (ibuf - 16));
         }
     };
     if constexpr (GDMA) {
@@ -572,14 +625,14 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
             const int j = wl + 4 * q;
             dslot[q] = __shfl(my_slot, j < K ? j : 0);
             if constexpr (XD == 1) {  // unconditional (unused past K)
-                const uint8_t *base = a.wd + (int64_t)(dslot[q] == 0xFFFFFFFFu ? 0 : dslot[q]) * a.sd + (int64_t)min(r, a.H - 1) * a.rbd;
-                draw[q][0] = FD::load(base, min(subd, nsbd - 1));
+                const uint8_t *mat = a.wd + (int64_t)(dslot[q] == 0xFFFFFFFFu ? 0 : dslot[q]) * a.sd;
+                draw[q][0] = load_rc<FD>(mat, min(r, a.H - 1), a.rbd, min(subd, nsbd - 1));
             } else if (j < K && dslot[q] != 0xFFFFFFFFu && r < a.H) {
-                const uint8_t *base = a.wd + (int64_t)dslot[q] * a.sd + (int64_t)r * a.rbd;
+                const uint8_t *mat = a.wd + (int64_t)dslot[q] * a.sd;
 #pragma unroll
                 for (int i = 0; i < XD; i++) {
                     const int sb = subd + i * LD;
-                    if (sb < nsbd) draw[q][i] = FD::load(base, sb);
+                    if (sb < nsbd) draw[q][i] = load_rc<FD>(mat, r, a.rbd, sb);
                 }
             }
         }
@@ -627,14 +680,24 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
 #pragma unroll
             for (int q = 0; q < RI; q++) {
                 const int r = min(r0 + q, a.I - 1);
-                const int og = (int)((uintptr_t)(a.wg + (int64_t)sl * a.sg + (int64_t)r * a.rbg) & 15);
-                const int ou = (int)((uintptr_t)(a.wu + (int64_t)sl * a.su + (int64_t)r * a.rbg) & 15);
                 float g = 0.f, u = 0.f;
 #pragma unroll
                 for (int i = 0; i < XG; i++) {
                     const int sb = subg + i * LG, sbc = min(sb, nsbg - 1);
-                    const typename FG::Raw wg = mx_from_lds(ib + (2 * q) * win, og + FG::TS * sbc);
-                    const typename FG::Raw wu = mx_from_lds(ib + (2 * q + 1) * win, ou + FG::TS * sbc);
+                    typename FG::Raw wg, wu;
+                    if constexpr (Rows16<FG>::on) {
+                        // row q's block sbc in its pair's run of step c (pieces from 9 c; the run at
+                        // its offset in its first piece: the group's steps start 16-byte aligned)
+                        const int rp = min(r0, (a.I - 1) & ~1), c = sbc >> 2, cb = 4 * c + 4 <= nsbg ? 4 : nsbg - 4 * c;
+                        const int o = 144 * c + (((rp & 15) * 17 * cb) & 15) + (r - rp) * 17 * cb + 17 * (sbc & 3);
+                        wg = mx_from_lds(ib, o);
+                        wu = mx_from_lds(ib + win, o);
+                    } else {
+                        const int og = (int)((uintptr_t)(a.wg + (int64_t)sl * a.sg + (int64_t)r * a.rbg) & 15);
+                        const int ou = (int)((uintptr_t)(a.wu + (int64_t)sl * a.su + (int64_t)r * a.rbg) & 15);
+                        wg = mx_from_lds(ib + (2 * q) * win, og + FG::TS * sbc);
+                        wu = mx_from_lds(ib + (2 * q + 1) * win, ou + FG::TS * sbc);
+                    }
                     if (sb < nsbg) {
                         g += FG::dot(wg, ldsg, xr[i]);
                         u += FG::dot(wu, ldsg, xr[i]);
@@ -646,7 +709,7 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
                 if (a.act == CW_ACT_SILU) {
                     o = g / (1.0f + expf(-g)) * u;
                 } else {
-                    const float *bias = (const float *)(ib + 2 * RI * win);
+                    const float *bias = (const float *)(ib + (ibuf - 16));
                     if (a.bg) g += bias[q];
                     if (a.bu) u += bias[RI + q];
                     g = fminf(g, a.limit);
@@ -720,7 +783,7 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
 #pragma unroll
             for (int i = 0; i < XD; i++) {
                 const int sb = subd + i * LD;
-                if (sb < nsbd) draw2[q][i] = FD::load(a.wd + (int64_t)dslot[q] * a.sd + (int64_t)r2 * a.rbd, sb);
+                if (sb < nsbd) draw2[q][i] = load_rc<FD>(a.wd + (int64_t)dslot[q] * a.sd, r2, a.rbd, sb);
             }
         }
     }
@@ -789,7 +852,7 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
 #pragma unroll
                 for (int i = 0; i < XD; i++) {
                     const int sb = subd + i * LD;
-                    if (sb < nsbd) draw[q][i] = FD::load(a.wd + (int64_t)dslot[q] * a.sd + (int64_t)r * a.rbd, sb);
+                    if (sb < nsbd) draw[q][i] = load_rc<FD>(a.wd + (int64_t)dslot[q] * a.sd, r, a.rbd, sb);
                 }
             }
         }
@@ -908,7 +971,7 @@ template <class FG, int G, int RI>
 static size_t decode_lds(const MoeArgs &a) {
     size_t n = decode_hidden_lds(a);
     if (RowDma<FG>::on) {
-        const size_t items = 4 * G * 2 * (size_t)(2 * RI * row_window(a.H / 32 * FG::TS) + 16);
+        const size_t items = 4 * G * 2 * (size_t)gu_ibuf<FG, RI>(a.H / 32);
         const size_t xs = (size_t)(a.H / 4 + 256 * G - 1) / (256 * G) * (256 * G) * 16;  // x, copied in rounds of one chunk per thread
         if (items > n) n = items;
         if (xs > n) n = xs;
@@ -963,6 +1026,13 @@ static int decode_launch_per(const MoeArgs &a, int which, hipStream_t s) {
         if (w <= 1024 || w > 2048) return CW_ENOTSUP;
         if ((uintptr_t)a.x & 15) return CW_ENOTSUP;  // x is copied in 16-byte chunks
     }
+    if (Rows16<FG>::on) {  // a row pair's four loads per matrix (192 < pieces <= 256), matrices 16-byte aligned
+        const int np = pr16_pieces(a.H / 32);
+        if (np <= 192 || np > 256 || a.I < 2) return CW_ENOTSUP;
+        if (((uintptr_t)a.wg | (uintptr_t)a.wu | (uintptr_t)a.sg | (uintptr_t)a.su) & 15) return CW_ENOTSUP;
+        if ((int64_t)(a.I + 15) * a.rbg >= ((int64_t)1 << 31)) return CW_ENOTSUP;  // 32-bit offsets
+    }
+    if (Rows16<FD>::on && (int64_t)(a.H + 15) * a.rbd >= ((int64_t)1 << 31)) return CW_ENOTSUP;  // 32-bit offsets in down
     const size_t lds = decode_lds<FG, G, RI>(a);
     const int RPD = 64 / LD;
     auto kern = k_moe_decode<FG, LG, XG, FD, LD, XD, PER, PPW, G, RI>;
@@ -1004,6 +1074,8 @@ int moe_decode(int dtg, int dtd, const MoeArgs &a, hipStream_t s) {
     // gpt-oss rows (2,880 weights): down at 32 lanes per row, two rows per block pass (half the
     // passes, reductions and block barriers of 64 lanes per row: 44.9 -> 39.2 us per layer)
     if (dtg == CW_MXFP4 && dtd == CW_MXFP4 && nsg == 90 && nsd == 90) return decode_ppw<FMXFP4, 64, 2, FMXFP4, 32, 3>(a, s);
+    if (dtg == CW_MXFP4_R16 && dtd == CW_MXFP4_R16 && nsg == 90 && nsd == 90)
+        return decode_ppw<FMXFP4R16, 64, 2, FMXFP4R16, 32, 3>(a, s);
     return CW_ENOTSUP;
 }
 

@@ -141,10 +141,11 @@ __device__ __forceinline__ void gx_dma4(const uint8_t *base, uint32_t off, uint3
     asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" : : "v"(off), "s"(base),
                  "s"(__builtin_amdgcn_readfirstlane(lds_base)) : "memory", "m0");
 }
-// s_waitcnt vmcnt(n) for n in {0, 4, 5} (a stage's wait: the window loads of one stage in flight)
+// s_waitcnt vmcnt(n) for n in {0, 3, 4, 5} (a stage's wait: the window loads of one stage in flight)
 __device__ __forceinline__ void gx_wait_stage(int n) {
     if (n == 5) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
     else if (n == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else if (n == 3) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 // s_waitcnt vmcnt(n) for a run-time n (the instruction takes an immediate; above 63 it waits for
@@ -161,15 +162,21 @@ __device__ __forceinline__ void gx_wait_vm(int n) {
 
 // A block has 8 waves: 4 row groups of RW weight rows (of each matrix: gate and up for MODE 0) by
 // 2 halves of the tile's 16-token blocks. A stage is one 128-wide K step. The weight bytes of a
-// stage go to LDS by direct loads, three stages ahead (three buffers), per row a window of the 6
-// 16-byte pieces holding its 4 blocks (68 bytes at any offset). The activation operands of a
+// stage go to LDS by direct loads, three stages ahead (three buffers). From GGUF rows (L = 0) a
+// row's window is the 6 16-byte pieces holding its 4 blocks (68 bytes at any offset): for the
+// gpt-oss shape 384 short runs 1,530 bytes apart per stage. From rows in groups of 16 (L = 1,
+// CW_MXFP4_R16: a group's blocks of one stage side by side) a stage is 24 runs of 1,088 bytes,
+// 16-byte aligned, which HBM serves faster (a loads-only microbenchmark of config 4's gate/up
+// windows on MI355X: 190 against 273 us; with the MFMAs and activation loads: 278 against 352),
+// and lands in LDS as rows of 68 bytes (17 cb for a last stage of cb < 4 blocks), each matrix's
+// groups from whole 1 KB loads of their own. The activation operands of a
 // stage (token block t: its 16 tokens' 304-byte step records, whole) go to LDS by direct loads
 // too, two stages ahead (two buffers), issued by the first waves. Each wave reads the operands of
 // the next stage from LDS while it computes the current one: a token block's activation operands
 // right after that block's MFMAs, the weight operands at the end of the stage, so that their
 // latency hides behind the matrix work. One barrier per stage publishes every wave's loads (each
 // wave first waits for exactly its own).
-template <int MODE>
+template <int MODE, int L = 0>
 struct GxShape {
     static constexpr int NW = 8, NT = 64 * NW;
     static constexpr int NM = MODE == 0 ? 2 : 1;      // matrices (gate, up) per block
@@ -177,11 +184,15 @@ struct GxShape {
     static constexpr int FR = RW / 16;                // fragments per wave per matrix
     static constexpr int NF = NM * FR;                // fragments per wave
     static constexpr int RPB = 4 * RW;                // rows per matrix per block
-    static constexpr int PCS = 6;                     // pieces per row window
+    static constexpr int PCS = 6;                     // pieces per row window (L = 0)
     static constexpr int WROWS = NM * RPB;
-    static constexpr int W_INST = WROWS * PCS / 64;   // window loads per stage (wave instructions)
+    // L = 1: GPM row groups of 16 per matrix, 68 pieces each per full stage, a matrix's MI window
+    // loads in an LDS region of its own
+    static constexpr int GPM = RPB / 16;
+    static constexpr int MI = (GPM * 68 + 63) / 64;
+    static constexpr int W_INST = L ? NM * MI : WROWS * PCS / 64;  // window loads per stage (wave instructions)
     static constexpr int NJW = (W_INST + NW - 1) / NW;
-    static constexpr int W_BYTES = WROWS * PCS * 16;
+    static constexpr int W_BYTES = W_INST * 1024;
     static constexpr int WDEPTH = 3;
     // a token block's operands of a stage: its 16 tokens' 304-byte step records side by side
     // (4,864 bytes), padded to the five 1 KB direct loads that bring them
@@ -195,14 +206,17 @@ struct GxShape {
     // of 16 tokens hits 64 distinct banks)
     static constexpr int HST = RPB + 4;
     static_assert(RPB * PCS % 64 == 0, "a window load lies in one matrix");
+    static_assert(RPB % 16 == 0, "an N-block is whole row groups");
     static_assert(LDS <= 160 * 1024, "the scaled GEMM's LDS does not fit");
 };
 
-// One work item (M-tile x N-block) of one wave, NTB of the tile's token blocks from tb0.
-template <int MODE, int NTB>
+
+// One work item (M-tile x N-block) of one wave, NTB of the tile's token blocks from tb0; L is the
+// weights' layout (0: GGUF rows, 1: rows in groups of 16).
+template <int MODE, int NTB, int L>
 __device__ __forceinline__ void gx_item(const MfArgs &a, const MfTile &tile, int nb, int mbs, int tb0, int wave, int lane,
                                         uint8_t *smem, uint32_t lds0) {
-    using S = GxShape<MODE>;
+    using S = GxShape<MODE, L>;
     constexpr int NB = NTB > 0 ? NTB : 1;
     const int grp = lane >> 4, l16 = lane & 15, rg = wave & 3;
     const int nblk = a.k / 32, n_st = (nblk + 3) / 4;
@@ -212,24 +226,42 @@ __device__ __forceinline__ void gx_item(const MfArgs &a, const MfTile &tile, int
 
     const uint8_t *wb0 = a.w0 + (int64_t)tile.slot * a.s0;
     const uint8_t *wb1 = S::NM > 1 ? a.w1 + (int64_t)tile.slot * a.s1 : wb0;
-    const uint8_t *wa0 = (const uint8_t *)((uintptr_t)wb0 & ~(uintptr_t)15);  // rounded down to 16 bytes
+    // L = 0: rounded down to 16 bytes; L = 1: the matrices are 16-byte aligned (the launch checks)
+    const uint8_t *wa0 = (const uint8_t *)((uintptr_t)wb0 & ~(uintptr_t)15);
     const uint8_t *wa1 = (const uint8_t *)((uintptr_t)wb1 & ~(uintptr_t)15);
     const uint32_t wm0 = (uint32_t)(uintptr_t)wb0 & 15u, wm1 = (uint32_t)(uintptr_t)wb1 & 15u;
-    // window loads: wave instruction wi = wave + 8 j covers pieces 64 wi .. 64 wi + 63
+    const int ngr = (a.n + 15) >> 4;  // L = 1: the matrix's row groups
+    // window loads: wave instruction wi = wave + 8 j covers pieces 64 wi .. 64 wi + 63 (L = 0), or
+    // of its matrix m = wi / MI pieces 64 (wi - m MI) .. + 63 (L = 1: in a stage of cb blocks piece
+    // p is piece p % 17 cb of group p / 17 cb; pieces past the N-block's last bring its last again,
+    // into the region's padding, and groups past the matrix bring its last group). L = 1 keeps the
+    // offsets of a full stage (wo, plus 1,088 bytes per stage) and of a last stage of fewer blocks
+    // (wp, whole).
     uint32_t wo[S::NJW], wp[S::NJW];
 #pragma unroll
     for (int j = 0; j < S::NJW; j++) {
-        const int pi = 64 * min(wave + 8 * j, S::W_INST - 1) + lane, row = pi / S::PCS;
-        wp[j] = (uint32_t)(pi - row * S::PCS);
-        const int n = nb * S::RPB + row % S::RPB;
-        wo[j] = (uint32_t)(n < a.n ? n : 0) * (uint32_t)a.row_bytes;
+        if constexpr (L == 0) {
+            const int pi = 64 * min(wave + 8 * j, S::W_INST - 1) + lane, row = pi / S::PCS;
+            wp[j] = (uint32_t)(pi - row * S::PCS);
+            const int n = nb * S::RPB + row % S::RPB;
+            wo[j] = (uint32_t)(n < a.n ? n : 0) * (uint32_t)a.row_bytes;
+        } else {
+            const int wi = min(wave + 8 * j, S::W_INST - 1), m = wi / S::MI;
+            const int lp = min(64 * (wi - m * S::MI) + lane, S::GPM * 68 - 1), gw = lp / 68;
+            const int g = min(nb * S::GPM + gw, ngr - 1);
+            wo[j] = (uint32_t)g * 16u * (uint32_t)a.row_bytes + 16u * (uint32_t)(lp - 68 * gw);
+            const int cbl = nblk - 4 * (n_st - 1), ppg = 17 * cbl;  // the last stage's blocks
+            const int lq = min(64 * (wi - m * S::MI) + lane, S::GPM * ppg - 1), gq = lq / ppg;
+            const int gl = min(nb * S::GPM + gq, ngr - 1);
+            wp[j] = (uint32_t)gl * 16u * (uint32_t)a.row_bytes + 1088u * (uint32_t)(n_st - 1) + 16u * (uint32_t)(lq - ppg * gq);
+        }
     }
-    // this lane's rows' offsets from 16-byte alignment
+    // L = 0: this lane's rows' offsets from 16-byte alignment
     uint32_t lmis[S::NF];
 #pragma unroll
     for (int f = 0; f < S::NF; f++) {
         const int mm = f / S::FR, n = nb * S::RPB + rg * S::RW + 16 * (f % S::FR) + l16;
-        lmis[f] = ((mm ? wm1 : wm0) + (uint32_t)(n < a.n ? n : 0) * (uint32_t)a.row_bytes) & 15u;
+        lmis[f] = L ? 0u : ((mm ? wm1 : wm0) + (uint32_t)(n < a.n ? n : 0) * (uint32_t)a.row_bytes) & 15u;
     }
     // activation staging: wave w < mbs stages token block w (lane = its K-group and token)
     // wave w < mbs stages token block w: a stage's 16 records of 304 bytes are 304 16-byte
@@ -257,6 +289,20 @@ __device__ __forceinline__ void gx_item(const MfArgs &a, const MfTile &tile, int
     auto issue_w = [&](int st) __attribute__((always_inline)) {
         const int buf = st % S::WDEPTH;
         const uint32_t Wd = lds0 + buf * S::W_BYTES;
+        if constexpr (L == 1) {
+            const int cb = min(4, nblk - 4 * st);  // blocks per row in this stage
+#pragma unroll
+            for (int j = 0; j < S::NJW; j++) {
+                const int wi = wave + 8 * j;
+                if (wi < S::W_INST) {
+                    const bool m1 = S::NM > 1 && wi >= S::MI;
+                    gx_dma16(m1 ? wa1 : wa0, cb == 4 ? wo[j] + 1088u * (uint32_t)st : wp[j], Wd + wi * 1024);
+                    issued++;
+                }
+            }
+            if (st == 0) m_w0 = issued;
+            return;
+        }
         const uint32_t seg = 17u * (uint32_t)min(4, nblk - 4 * st);  // bytes of a row in this stage
 #pragma unroll
         for (int j = 0; j < S::NJW; j++) {
@@ -303,6 +349,10 @@ __device__ __forceinline__ void gx_item(const MfArgs &a, const MfTile &tile, int
     };
     // LDS offset of the E8M0 byte of this lane's block of fragment f in stage st's window
     auto aoff = [&](int f, int st) __attribute__((always_inline)) -> uint32_t {
+        if constexpr (L == 1) {
+            const int lr = rg * S::RW + 16 * (f % S::FR) + l16, cb = min(4, nblk - 4 * st);
+            return (uint32_t)((f / S::FR) * S::MI * 1024) + (uint32_t)lr * (17u * (uint32_t)cb) + 17u * grp;
+        }
         const int lrow = (f / S::FR) * S::RPB + rg * S::RW + 16 * (f % S::FR) + l16;
         return (uint32_t)lrow * (S::PCS * 16) + ((lmis[f] + 4u * (uint32_t)st) & 15u) + 17u * grp;
     };
@@ -508,9 +558,9 @@ __device__ __forceinline__ void gx_item(const MfArgs &a, const MfTile &tile, int
 
 // MODE 0: gate and up with the activation, hidden rows written in pile order (ldh floats).
 // MODE 1: one output row per pick (dn, pick order), combined per token afterwards.
-template <int MODE>
+template <int MODE, int L>
 __global__ __launch_bounds__(512, 1) void k_gmx(const MfArgs a) {
-    using S = GxShape<MODE>;
+    using S = GxShape<MODE, L>;
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)smem;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -528,10 +578,10 @@ __global__ __launch_bounds__(512, 1) void k_gmx(const MfArgs a) {
         const int mbs = (tile.m + 15) >> 4, half = wave >> 2, n0 = (mbs + 1) >> 1;
         const int tb0 = half ? n0 : 0, ntb = half ? mbs - n0 : n0;
         switch (ntb) {
-        case 0: gx_item<MODE, 0>(a, tile, nb, mbs, tb0, wave, lane, smem, lds0); break;
-        case 1: gx_item<MODE, 1>(a, tile, nb, mbs, tb0, wave, lane, smem, lds0); break;
-        case 2: gx_item<MODE, 2>(a, tile, nb, mbs, tb0, wave, lane, smem, lds0); break;
-        default: gx_item<MODE, 3>(a, tile, nb, mbs, tb0, wave, lane, smem, lds0); break;
+        case 0: gx_item<MODE, 0, L>(a, tile, nb, mbs, tb0, wave, lane, smem, lds0); break;
+        case 1: gx_item<MODE, 1, L>(a, tile, nb, mbs, tb0, wave, lane, smem, lds0); break;
+        case 2: gx_item<MODE, 2, L>(a, tile, nb, mbs, tb0, wave, lane, smem, lds0); break;
+        default: gx_item<MODE, 3, L>(a, tile, nb, mbs, tb0, wave, lane, smem, lds0); break;
         }
         if constexpr (MODE == 0) {
             if (a.hp) {
@@ -589,13 +639,15 @@ static int gx_device() {
     return hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 ? dev : 0;
 }
 
-template <int MODE>
+template <int MODE, int L>
 static int gx_launch(const MfArgs &a, int tiles_max, hipStream_t s) {
-    using S = GxShape<MODE>;
+    using S = GxShape<MODE, L>;
     if (a.k % 32 || a.k <= 128) return set_error(CW_ENOTSUP, "mxfp4 gemm: k %d is not whole blocks over two steps", a.k);
     // lane offsets are 32-bit: from a matrix's 16-byte aligned base, and into the packed rows
-    if ((int64_t)a.n * a.row_bytes + 256 >= ((int64_t)1 << 32))
+    if ((int64_t)(a.n + 15) / 16 * 16 * a.row_bytes + 256 >= ((int64_t)1 << 32))
         return set_error(CW_ENOTSUP, "mxfp4 gemm: a matrix of %d rows of %lld bytes is 4 GiB or more", a.n, (long long)a.row_bytes);
+    if (L == 1 && (((uintptr_t)a.w0 | (uintptr_t)a.s0) & 15 || (MODE == 0 && ((uintptr_t)a.w1 | (uintptr_t)a.s1) & 15)))
+        return set_error(CW_EINVAL, "mxfp4 gemm: matrices in row groups of 16 must start on 16-byte boundaries");
     if (MODE == 0 && a.hp && (size_t)MF_MT * S::HST * 4 > (size_t)S::BIAS_OFF)
         return set_error(CW_ENOTSUP, "mxfp4 gemm: the hidden rows' staging does not fit");
     if (a.ap_rows * a.ap_row >= ((int64_t)1 << 32))
@@ -611,7 +663,7 @@ static int gx_launch(const MfArgs &a, int tiles_max, hipStream_t s) {
         cus_of[dev].store(cus, std::memory_order_relaxed);
     }
     if (!lds_set[dev].load(std::memory_order_acquire)) {
-        if (hipFuncSetAttribute((const void *)k_gmx<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::LDS) != hipSuccess)
+        if (hipFuncSetAttribute((const void *)k_gmx<MODE, L>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::LDS) != hipSuccess)
             return set_error(CW_EHIP, "mxfp4 gemm: cannot reserve %zu bytes of LDS", S::LDS);
         lds_set[dev].store(true, std::memory_order_release);
     }
@@ -623,12 +675,50 @@ static int gx_launch(const MfArgs &a, int tiles_max, hipStream_t s) {
     MfArgs b = a;
     b.run_tiles = R;
     b.n_items = (int)items;
-    hipLaunchKernelGGL((k_gmx<MODE>), dim3((unsigned)blocks), dim3(S::NT), S::LDS, s, b);
+    hipLaunchKernelGGL((k_gmx<MODE, L>), dim3((unsigned)blocks), dim3(S::NT), S::LDS, s, b);
     return check_launch("k_gmx");
 }
 
-int mxfp4_gateup(const MfArgs &a, int tiles_max, hipStream_t s) { return gx_launch<0>(a, tiles_max, s); }
-int mxfp4_down(const MfArgs &a, int tiles_max, hipStream_t s) { return gx_launch<1>(a, tiles_max, s); }
+int mxfp4_gateup(const MfArgs &a, int tiles_max, hipStream_t s) {
+    return a.layout ? gx_launch<0, 1>(a, tiles_max, s) : gx_launch<0, 0>(a, tiles_max, s);
+}
+int mxfp4_down(const MfArgs &a, int tiles_max, hipStream_t s) {
+    return a.layout ? gx_launch<1, 1>(a, tiles_max, s) : gx_launch<1, 0>(a, tiles_max, s);
+}
+
+// ------------------------------------------------------------------------------ the row-group layout
+
+// One thread per (row, block) of each matrix: block b of GGUF row r to rows16_offset(r, b); rows
+// past n up to the group's end get zero blocks (scale 2^-127, codes 0: products 0).
+__global__ __launch_bounds__(256) void k_rows16(const uint8_t *src, int64_t src_stride, uint8_t *dst, int64_t dst_stride,
+                                                int64_t n_mats, int n, int nblk) {
+    const int rows = (n + 15) / 16 * 16;
+    const int64_t per = (int64_t)rows * nblk, total = n_mats * per;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        const int64_t mat = i / per, e = i - mat * per;
+        const int r = (int)(e / nblk), b = (int)(e - (int64_t)r * nblk);
+        uint8_t *d = dst + mat * dst_stride + rows16_offset(r, b, nblk);
+        if (r < n) {
+            const uint8_t *q = src + mat * src_stride + ((int64_t)r * nblk + b) * 17;
+#pragma unroll
+            for (int k = 0; k < 17; k++) d[k] = q[k];
+        } else {
+#pragma unroll
+            for (int k = 0; k < 17; k++) d[k] = 0;
+        }
+    }
+}
+
+int rows16_repack(const uint8_t *src, int64_t src_stride, uint8_t *dst, int64_t dst_stride, int64_t n_mats, int n, int k,
+                  hipStream_t s) {
+    const int nblk = k / 32;
+    const int64_t total = n_mats * (int64_t)((n + 15) / 16 * 16) * nblk;
+    if (total == 0) return CW_OK;
+    const int64_t blocks = (total + 255) / 256;
+    hipLaunchKernelGGL(k_rows16, dim3((unsigned)(blocks < 65536 ? blocks : 65536)), dim3(256), 0, s, src, src_stride, dst,
+                       dst_stride, n_mats, n, nblk);
+    return check_launch("k_rows16");
+}
 
 // The scaled path is the default for MXFP4; CWMOE_MXFP4_F16=1 selects the fp16 MFMA path instead
 // (for comparisons). Read at each call: a workspace size and the call it is for must agree, so the

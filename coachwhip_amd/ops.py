@@ -253,6 +253,17 @@ class ExpertBank:
             raise CwError(CW_EINVAL, "bank: %d bytes for %d slots of %d" % (raw.size, n_slots, stride))
         return cls(to_device(raw, device), dtype, n, k, n_slots, stride)
 
+    def rows16(self):
+        """This MXFP4 bank with each matrix's rows in groups of 16 (MXFP4_R16), repacked on the device
+        into a new bank: the same blocks, whose steps the kernels load as one run per group."""
+        if self.dtype != F.MXFP4:
+            raise CwError(CW_EINVAL, "rows16: a %s bank (MXFP4 only)" % F.NAMES[self.dtype])
+        stride = lib().cw_rows16_bytes(self.n, self.k)
+        data = torch.empty(stride * self.n_slots, dtype=torch.uint8, device=self.data.device)
+        check(lib().cw_repack_rows16(_p(self.data), self.slot_stride, _p(data), stride, self.n_slots, self.n, self.k,
+                                     _stream()))
+        return ExpertBank(data, F.MXFP4_R16, self.n, self.k, self.n_slots, stride)
+
 
 class MoeMatvec:
     """out[t][j] = W[ids[t][j]] . x_row, x_row = x[t] or x[t*nei0 + j] (rows_per_expert).
@@ -295,6 +306,10 @@ class MoeMatvec:
             raise CwError(CW_EINVAL, "x is %dx%d, expected k=%d for %d tokens" % (rows, k, self.bank.k, tokens))
         b = self.bank
         out = torch.empty((tokens, nei0, b.n), dtype=torch.float32, device=x.device)
+        if b.dtype == F.MXFP4_R16:  # rows in groups of 16 have the grouped GEMM only
+            if tokens and not self._grouped(x, ids, out, tokens):
+                raise CwError(CW_ENOTSUP, "a %dx%d MXFP4_R16 bank has no grouped kernel" % (b.n, b.k))
+            return out
         if self.grouped_above is not None and tokens > self.grouped_above and self._grouped(x, ids, out, tokens):
             return out
         check(lib().cw_matvec_id(b.dtype, b.n, b.k, b.n_slots, b.slot_stride, _p(b.data), _p(x), int(self.rows_per_expert),

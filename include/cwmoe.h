@@ -61,7 +61,13 @@ enum cw_dtype {
     CW_IQ3_S = 21,   /* {f16 d; u8 qs[64], qh[8], signs[32], scales[4]}: 110 B per 256 */
     CW_IQ2_S = 22,   /* {f16 d; u8 qs[64], qh[8], scales[8]}: 82 B per 256 */
     CW_IQ4_XS = 23,  /* {f16 d; u16 scales_h; u8 scales_l[4]; u8 qs[128]}: 136 B per 256 */
-    CW_MXFP4 = 39    /* {u8 e8m0; u8 qs[16]}: 17 B per 32 */
+    CW_MXFP4 = 39,   /* {u8 e8m0; u8 qs[16]}: 17 B per 32 */
+    /* Not a GGUF type: CW_MXFP4 blocks with each matrix's rows in groups of 16, the group's blocks
+     * of each 4-block step side by side (16 runs of 17 cb bytes, cb = blocks of the step), a group
+     * in the bytes its 16 GGUF rows take, the last group padded with zero rows. Made by
+     * cw_repack_rows16; read by the expert paths (cw_moe_layer, cw_matmul_id_grouped), whose
+     * GEMMs and decode load a step of each group as one run instead of one short run per row. */
+    CW_MXFP4_R16 = 295
 };
 
 enum cw_act { CW_ACT_SILU = 0, CW_ACT_CLAMPED_SWIGLU = 1 };
@@ -152,6 +158,15 @@ int cw_matmul_id_grouped(int dtype, int64_t n, int64_t k, int64_t n_slots, int64
                          const void *bank, const float *x, int x_rows_per_expert,
                          const uint32_t *ids, int K, int T, float *out, void *ws, size_t ws_bytes,
                          cw_stream_t stream);
+
+/* CW_MXFP4 matrices into CW_MXFP4_R16, on the device: n_mats matrices of n rows of k weights
+ * (src_stride bytes apart) to dst (dst_stride bytes apart, at least cw_rows16_bytes(n, k) each; dst
+ * and dst_stride 16-byte aligned; not in place). k above 128, a multiple of 32.
+ * No counterpart in the reference, which reads GGUF rows as stored: a device layout of the same
+ * blocks, for callers that load expert matrices once and run the MoE layer on them. */
+int64_t cw_rows16_bytes(int64_t n, int64_t k);
+int cw_repack_rows16(const void *src, int64_t src_stride, void *dst, int64_t dst_stride, int64_t n_mats, int64_t n,
+                     int64_t k, cw_stream_t stream);
 
 /* ---- activations and combine ------------------------------------------------------------ */
 

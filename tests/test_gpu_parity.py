@@ -643,6 +643,90 @@ def test_moe_biases_follow_the_expert_through_a_slot_table(dts, x_scale, path, m
     assert O.rel_l2(host(out), other) > 10 * REL_L2_GATE
 
 
+# ------------------------------------------------------------------------------ MXFP4 in row groups of 16
+
+@pytest.mark.parametrize("n,k", [(41, 2880), (96, 1056), (15, 160)])
+def test_rows16_repack_is_the_block_permutation(n, k):
+    # cw_repack_rows16 against the permutation on the host: block b of row r at rows16_offset(r, b),
+    # rows past n to the group's end zero blocks; three slots with a source stride above the matrix
+    say("rows16 repack", n, k)
+    rng = np.random.default_rng(n + k)
+    nb, slots = k // 32, 3
+    src_stride = F.matrix_bytes(F.MXFP4, n, k) + 48
+    raw = np.full((slots, src_stride), 0xA5, np.uint8)
+    raw[:, :n * nb * 17] = synth.random_blocks(F.MXFP4, slots * n * k, rng).reshape(slots, -1)
+    raw = raw.reshape(-1)
+    bank = ops.ExpertBank(dev(raw), F.MXFP4, n, k, slots, src_stride)
+    got = host(bank.rows16().data)
+    stride = F.matrix_bytes(F.MXFP4_R16, n, k)
+    assert got.size == slots * stride
+    want = np.zeros(slots * stride, np.uint8)
+    for s in range(slots):
+        blocks = raw[s * src_stride:s * src_stride + n * nb * 17].reshape(n, nb, 17)
+        for r in range(n):
+            for b in range(nb):
+                o = s * stride + F.rows16_offset(r, b, nb)
+                want[o:o + 17] = blocks[r, b]
+    assert np.array_equal(got, want)
+
+
+R16_CASES = [
+    # name, E, K, h, I, pad, T: one token takes the one-launch decode (the gpt-oss row length), more the grouped GEMMs
+    ("c4_decode", 16, 4, 2880, 2880, 0, 1),
+    ("c4_decode_e128", 128, 4, 2880, 2880, 0, 1),
+    ("c4_decode_odd_rows", 16, 4, 2880, 2877, 2880, 1),
+    ("c4_tokens", 16, 4, 2880, 2880, 0, 40),
+    ("c4_odd_rows_tokens", 16, 4, 2880, 2877, 2880, 24),
+    ("short_rows_one_token", 16, 4, 1024, 512, 0, 1),   # no decode instance: the grouped GEMMs
+    ("short_rows", 32, 6, 1024, 720, 768, 33),
+]
+
+
+@pytest.mark.parametrize("name,E,K,h,I,pad,T", R16_CASES, ids=[c[0] for c in R16_CASES])
+def test_moe_layer_rows16_matches_gguf_rows(name, E, K, h, I, pad, T):
+    # the same layer from GGUF rows and from rows in groups of 16: the kernels take the same
+    # blocks in the same order, so the outputs are the same bits; both against the oracle at the gate
+    say("moe rows16", name)
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    layer = synth.moe_weights(E, K, h, I, (F.MXFP4,) * 3, rng, act=1, pad=pad)
+    x = rng.standard_normal((T, h)).astype(np.float32)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    assert not synth.near_ties_within_top_k(logits, K)
+    rows = upload_layer(layer)
+    rp = ops.MoeLayer(*[b.rows16() for b in rows.banks], n_experts=E, top_k=K,
+                       norm_topk_prob=layer.norm, act=rows.act)
+    want, wids, _, _ = O.moe_layer(layer, x, logits)
+    op, idsp, _ = rp.forward(dev(x), dev(logits))
+    assert np.array_equal(host(idsp).view(np.uint32), wids)
+    err = O.rel_l2(host(op), want)
+    say("  rel_l2", err)
+    assert err <= REL_L2_GATE
+    if T == 1 and h == 2880:
+        o, _, _ = rows.forward(dev(x), dev(logits))
+        assert np.array_equal(host(o).view(np.uint32), host(op).view(np.uint32))
+
+
+@pytest.mark.parametrize("T", [40, 5])
+def test_matmul_id_grouped_rows16_matches_gguf_rows(T):
+    # cw_matmul_id_grouped on an MXFP4_R16 bank (every token count: it has no matvec): the same bits
+    # as the GGUF bank on the grouped path, an id past the bank giving a NaN row
+    rng = np.random.default_rng(400 + T)
+    n, k, slots, K = 200, 2880, 6, 4
+    raw = synth.random_blocks(F.MXFP4, slots * n * k, rng)
+    bank = ops.ExpertBank.from_blocks(raw, F.MXFP4, n, k, slots)
+    ids = rng.integers(0, slots, size=(T, K), dtype=np.uint32)
+    ids[1, 2] = slots + 1
+    x = rng.standard_normal((T, k)).astype(np.float32)
+    outp = host(ops.MoeMatvec(bank.rows16(), K, False).forward(dev(x), dev(ids)))
+    out = host(ops.MoeMatvec(bank, K, False, grouped_above=0).forward(dev(x), dev(ids)))
+    assert np.all(np.isnan(outp[1, 2]))
+    assert np.array_equal(outp.view(np.uint32), out.view(np.uint32))
+    keep = np.ones((T, K), bool)
+    keep[1, 2] = False
+    want = O.matvec_id(F.MXFP4, n, k, raw, bank.slot_stride, x, np.minimum(ids, slots - 1), False)
+    assert O.rel_l2(outp[keep], want[keep]) <= REL_L2_GATE
+
+
 @pytest.mark.parametrize("E", [512, 400])
 def test_moe_decode_through_a_slot_table(E):
     """Config 5's one-token layer: the persistent decode kernel with 8 router logits per lane, where

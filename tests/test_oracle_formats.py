@@ -523,3 +523,22 @@ def test_tables_equal_the_reference_shader_text():
     assert list(y[:16]) == G.reference_kvalues_iq4nl()
     assert list(G.ksigns_closed_form()) == G.reference_table("ksigns_iq2xs")
     assert G.reference_table("kmask_iq2xs") == [1 << i for i in range(8)]
+
+
+@pytest.mark.parametrize("n,nblk", [(40, 90), (16, 5), (33, 8), (17, 7)])
+def test_rows16_offsets_are_a_block_permutation_with_contiguous_steps(n, nblk):
+    """MXFP4_R16 (rows in groups of 16): every block of the padded matrix lands on its own 17-byte
+    slot of the same bytes, each group keeps the bytes its 16 GGUF rows take, and a group's blocks
+    of one 4-block step are one run, row after row (what the kernels load per step)."""
+    rows = (n + 15) // 16 * 16
+    offs = {(r, b): F.rows16_offset(r, b, nblk) for r in range(rows) for b in range(nblk)}
+    assert sorted(offs.values()) == list(range(0, rows * nblk * 17, 17))
+    rb = nblk * 17
+    for (r, b), o in offs.items():
+        assert (r // 16) * 16 * rb <= o < (r // 16 + 1) * 16 * rb
+    for g in range(rows // 16):
+        for c in range((nblk + 3) // 4):
+            cb = min(4, nblk - 4 * c)
+            run = [offs[(16 * g + i, 4 * c + k)] for i in range(16) for k in range(cb)]
+            assert run == list(range(run[0], run[0] + 17 * 16 * cb, 17))
+    assert F.matrix_bytes(F.MXFP4_R16, n, 32 * nblk) == rows * rb
