@@ -375,34 +375,37 @@ def bench_c4(args, torch, np, dev):
                         "as stored, activations as three FP6 E2M3 terms with E8M0 scales per 32, f32 accumulate")}
     log("prefill", prefill)
 
-    # the same layers with their expert matrices repacked in row groups of 16 (MXFP4_R16, opt-in:
-    # ExpertBank.rows16): the same blocks, read by the same kernels' row-group variants; outputs
-    # equal to the GGUF rows' bit for bit
+    # the same layers with expert matrices repacked in row groups of 16 (MXFP4_R16, opt-in:
+    # ExpertBank.rows16): all three, or down alone; the same blocks, read by the same kernels'
+    # row-group variants, outputs equal to the GGUF rows' bit for bit
     r16 = None
     if not args.no_rows16:
-        log("row groups of 16: repacking the chain's experts")
-        lay16 = [ops.MoeLayer(*[b.rows16() for b in lay.banks], n_experts=E, top_k=K, norm_topk_prob=True, act=lay.act)
-                 for lay in layers]
-        same = all(bool(torch.equal(lay16[l].forward(xp, lp)[0], eager[l])) for l in range(len(eager)))
-        d16 = lay16[0].forward(x_all[0], logits_all[0, 0])[0]
-        same = same and bool(torch.equal(d16, out0))
-        g16 = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g16):
-            for r in range(reps):
-                lay16[r % L].forward(xp, lp)
-        torch.cuda.synchronize()
-        pre16, pre16_all = time_replays(torch, g16, reps)
-        del g16
-        ms16 = time_graph(torch, lay16, x_all, logits_all, args.warmup, args.steps)
-        dec16 = ms16 * 1e3 / (args.steps * L)
-        r16 = {"prefill_us_per_layer": round(pre16, 2), "prefill_tokens_per_s": round(T / (pre16 * 1e-6)),
-               "prefill_us_per_layer_replays": [round(v, 1) for v in pre16_all],
-               "decode_us_per_layer": round(dec16, 3), "decode_gbs": round(layer_bytes / (dec16 * 1e-6) / 1e9, 2),
-               "outputs_equal_gguf_rows": same,
-               "note": "opt-in layout (ExpertBank.rows16 / cw_repack_rows16); the line's value and prefill are GGUF rows"}
-        log("rows16", r16)
-        del lay16
-        torch.cuda.empty_cache()
+        r16 = {"note": "opt-in layouts (ExpertBank.rows16 / cw_repack_rows16, at load); the line's value and "
+                       "prefill are GGUF rows"}
+        for which in ("all", "down"):
+            log("row groups of 16 (%s): repacking the chain's experts" % which)
+            lay16 = [ops.MoeLayer(*[b.rows16() if which == "all" or m == 2 else b for m, b in enumerate(lay.banks)],
+                                  n_experts=E, top_k=K, norm_topk_prob=True, act=lay.act) for lay in layers]
+            same = all(bool(torch.equal(lay16[l].forward(xp, lp)[0], eager[l])) for l in range(len(eager)))
+            d16 = lay16[0].forward(x_all[0], logits_all[0, 0])[0]
+            same = same and bool(torch.equal(d16, out0))
+            g16 = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g16):
+                for r in range(reps):
+                    lay16[r % L].forward(xp, lp)
+            torch.cuda.synchronize()
+            pre16, pre16_all = time_replays(torch, g16, reps)
+            del g16
+            ms16 = time_graph(torch, lay16, x_all, logits_all, args.warmup, args.steps)
+            dec16 = ms16 * 1e3 / (args.steps * L)
+            r16["gate_up_down" if which == "all" else "down_only"] = {
+                "prefill_us_per_layer": round(pre16, 2), "prefill_tokens_per_s": round(T / (pre16 * 1e-6)),
+                "prefill_us_per_layer_replays": [round(v, 1) for v in pre16_all],
+                "decode_us_per_layer": round(dec16, 3), "decode_gbs": round(layer_bytes / (dec16 * 1e-6) / 1e9, 2),
+                "outputs_equal_gguf_rows": same}
+            log("rows16", which, r16)
+            del lay16
+            torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu_baseline:

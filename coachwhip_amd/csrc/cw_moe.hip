@@ -128,14 +128,8 @@ static uint32_t decode_polls() {
     return e ? (uint32_t)strtoul(e, nullptr, 10) : (1u << 17);
 }
 
-static bool has_rows16(const cw_moe_desc *d) {
-    return d->dtype[0] == CW_MXFP4_R16 || d->dtype[1] == CW_MXFP4_R16 || d->dtype[2] == CW_MXFP4_R16;
-}
-
-// Matrices in row groups of 16 are read by the grouped GEMMs at any token count (and by the
-// one-launch decode for one token, where it has an instance).
 static bool grouped_path(const cw_moe_desc *d, int T) {
-    return (T >= prefill_min_tokens() || has_rows16(d)) && d->dtype[0] == d->dtype[1] && mfma_supported(d->dtype[0]) &&
+    return T >= prefill_min_tokens() && d->dtype[0] == d->dtype[1] && mfma_supported(d->dtype[0]) &&
            mfma_supported(d->dtype[2]) && (d->slot_table ? d->n_slots : d->n_experts) <= 1024;
 }
 
@@ -166,9 +160,8 @@ static int check_desc(const cw_moe_desc *d, int T) {
     }
     CW_REQUIRE(d->act == CW_ACT_CLAMPED_SWIGLU || (!d->bias[0] && !d->bias[1] && !d->bias[2]),
                "moe: biases need the clamped SwiGLU activation");
-    if (has_rows16(d) && !grouped_path(d, 1 > T ? 1 : T))
-        return set_error(CW_ENOTSUP, "moe: matrices in row groups of 16 need gate and up of one type, grouped-GEMM "
-                                     "formats and at most 1024 slots");
+    if ((d->dtype[0] == CW_MXFP4_R16 || d->dtype[1] == CW_MXFP4_R16) && d->dtype[0] != d->dtype[1])
+        return set_error(CW_ENOTSUP, "moe: gate and up in row groups of 16 need the same format");
     for (int m = 0; m < 3; m++)
         if (d->dtype[m] == CW_MXFP4_R16 && !mxfp4_scaled_for(CW_MXFP4_R16, ks[m]))
             return set_error(CW_ENOTSUP, "moe: matrix %d in row groups of 16 has rows of %d weights (over 128 needed)", m, ks[m]);
@@ -352,13 +345,11 @@ static int moe_layer(const cw_moe_desc *d, const float *x, const float *logits, 
     a.state = base + L.state;
     a.polls = decode_polls();
 
-    // one token: the one-launch decode where it has an instance (MXFP4_R16 matrices go to the
-    // grouped GEMMs otherwise)
-    if (T == 1 && d->dtype[0] == d->dtype[1] && decode_single_launch() && (!L.grouped || has_rows16(d))) {
+    if (L.grouped) return moe_grouped(d, a, L, base, T, s);
+    if (T == 1 && d->dtype[0] == d->dtype[1] && decode_single_launch()) {
         rc = moe_decode(d->dtype[0], d->dtype[2], a, s);
         if (rc != CW_ENOTSUP) return rc;
     }
-    if (L.grouped) return moe_grouped(d, a, L, base, T, s);
     if (d->dtype[0] == d->dtype[1]) {
         if ((rc = moe_gateup(d->dtype[0], a, T, s))) return rc;
     } else {

@@ -42,6 +42,24 @@ __device__ __forceinline__ void load_xs(float (&xr)[NX][32], const float *xrow, 
 
 // ------------------------------------------------------------------------------ gate / up
 
+// MXFP4 matrices with their rows in groups of 16 (CW_MXFP4_R16): the same blocks, block sb of row r
+// at rows16_offset(r, sb). The one-launch decode stages their gate/up rows in LDS as row pairs.
+struct FMXFP4R16 : FMXFP4 {};
+template <class F> struct Rows16 { static constexpr bool on = false; };
+template <> struct Rows16<FMXFP4R16> { static constexpr bool on = true; };
+
+// rows16_offset in 32 bits (the decode's matrices are below 2 GiB: its launch checks)
+__device__ __forceinline__ uint32_t rows16_off32(int r, int b, int nblk) {
+    const int c = b >> 2, cb = 4 * c + 4 <= nblk ? 4 : nblk - 4 * c;
+    return (uint32_t)(r >> 4) * (uint32_t)(272 * nblk) + (uint32_t)(c * 1088 + ((r & 15) * cb + (b & 3)) * 17);
+}
+// block sb of row r of the matrix at mat (rows of rb bytes), in format F's layout
+template <class F>
+__device__ __forceinline__ typename F::Raw load_rc(const uint8_t *mat, int64_t r, int64_t rb, int sb) {
+    if constexpr (Rows16<F>::on) return F::load(mat + rows16_off32((int)r, sb, (int)rb / 17), 0);
+    else return F::load(mat + r * rb, sb);
+}
+
 template <class Fmt, int LPR, int NX, int PER, int ROWS>
 __global__ __launch_bounds__(256) void k_moe_gateup(const MoeArgs a) {
     __shared__ __align__(16) uint8_t lds[Fmt::LDS_BYTES > 0 ? Fmt::LDS_BYTES : 16];
@@ -79,8 +97,8 @@ __global__ __launch_bounds__(256) void k_moe_gateup(const MoeArgs a) {
         for (int i = 0; i < NX; i++) {
             const int sb = sub + i * LPR;
             if (r < a.I && sb < nsb) {
-                rg[q][i] = Fmt::load(bg + (int64_t)r * a.rbg, sb);
-                ru[q][i] = Fmt::load(bu + (int64_t)r * a.rbg, sb);
+                rg[q][i] = load_rc<Fmt>(bg, r, a.rbg, sb);
+                ru[q][i] = load_rc<Fmt>(bu, r, a.rbg, sb);
             }
         }
     }
@@ -152,7 +170,7 @@ __global__ __launch_bounds__(256) void k_moe_down(const MoeArgs a) {
 #pragma unroll
             for (int i = 0; i < NX; i++) {
                 const int sb = sub + i * LPR;
-                if (r < a.H && sb < nsb) raw[q][i] = Fmt::load(base + (int64_t)r * a.rbd, sb);
+                if (r < a.H && sb < nsb) raw[q][i] = load_rc<Fmt>(base, r, a.rbd, sb);
             }
             load_xs<NX>(xr[q], a.h + (int64_t)(t * a.K + j) * a.P, sub, LPR, nsb);
         }
@@ -327,25 +345,7 @@ __device__ __forceinline__ void store_coherent(float *p, float v) {
 // buffers: the next item's rows (and its bias values) go out before the current item is read.
 template <class F> struct RowDma { static constexpr bool on = false; };
 template <> struct RowDma<FMXFP4> { static constexpr bool on = true; };
-
-// MXFP4 matrices with their rows in groups of 16 (CW_MXFP4_R16): the same blocks, block sb of row r
-// at rows16_offset(r, sb). Their gate/up rows are LDS-staged as row pairs (below).
-struct FMXFP4R16 : FMXFP4 {};
 template <> struct RowDma<FMXFP4R16> { static constexpr bool on = true; };
-template <class F> struct Rows16 { static constexpr bool on = false; };
-template <> struct Rows16<FMXFP4R16> { static constexpr bool on = true; };
-
-// rows16_offset in 32 bits (the decode's matrices are below 2 GiB: its launch checks)
-__device__ __forceinline__ uint32_t rows16_off32(int r, int b, int nblk) {
-    const int c = b >> 2, cb = 4 * c + 4 <= nblk ? 4 : nblk - 4 * c;
-    return (uint32_t)(r >> 4) * (uint32_t)(272 * nblk) + (uint32_t)(c * 1088 + ((r & 15) * cb + (b & 3)) * 17);
-}
-// block sb of row r of the matrix at mat (rows of rb bytes), in format F's layout
-template <class F>
-__device__ __forceinline__ typename F::Raw load_rc(const uint8_t *mat, int64_t r, int64_t rb, int sb) {
-    if constexpr (Rows16<F>::on) return F::load(mat + rows16_off32((int)r, sb, (int)rb / 17), 0);
-    else return F::load(mat + r * rb, sb);
-}
 
 // A row pair (rows r0, r0 + 1, r0 even: one group) of an MXFP4_R16 matrix staged in LDS: the pair's
 // blocks of step c are one run of 34 cb bytes (cb = blocks of the step) at rows16_offset(r0, 4c),
@@ -952,6 +952,7 @@ static int by_fmt(int dtype, const MoeArgs &a, int T, hipStream_t s) {
     case CW_Q2_K: return by_shape<FQ2_K, DOWN>(a, T, s);
     case CW_Q4_K: return by_shape<FQ4_K, DOWN>(a, T, s);
     case CW_MXFP4: return by_shape<FMXFP4, DOWN>(a, T, s);
+    case CW_MXFP4_R16: return by_shape<FMXFP4R16, DOWN>(a, T, s);
     case CW_IQ2_XXS: return by_shape<FIQ2_XXS, DOWN>(a, T, s);
     case CW_IQ2_S: return by_shape<FIQ2_S, DOWN>(a, T, s);
     case CW_IQ3_S: return by_shape<FIQ3_S, DOWN>(a, T, s);
@@ -1076,6 +1077,8 @@ int moe_decode(int dtg, int dtd, const MoeArgs &a, hipStream_t s) {
     if (dtg == CW_MXFP4 && dtd == CW_MXFP4 && nsg == 90 && nsd == 90) return decode_ppw<FMXFP4, 64, 2, FMXFP4, 32, 3>(a, s);
     if (dtg == CW_MXFP4_R16 && dtd == CW_MXFP4_R16 && nsg == 90 && nsd == 90)
         return decode_ppw<FMXFP4R16, 64, 2, FMXFP4R16, 32, 3>(a, s);
+    // gate/up as GGUF rows, down in row groups of 16: the decode's down phase reads both as fast
+    if (dtg == CW_MXFP4 && dtd == CW_MXFP4_R16 && nsg == 90 && nsd == 90) return decode_ppw<FMXFP4, 64, 2, FMXFP4R16, 32, 3>(a, s);
     return CW_ENOTSUP;
 }
 

@@ -671,39 +671,42 @@ def test_rows16_repack_is_the_block_permutation(n, k):
 
 
 R16_CASES = [
-    # name, E, K, h, I, pad, T: one token takes the one-launch decode (the gpt-oss row length), more the grouped GEMMs
+    # name, E, K, h, I, pad, T: one token takes the one-launch decode (the gpt-oss row length), a few
+    # the per-pick matvecs, more the grouped GEMMs
     ("c4_decode", 16, 4, 2880, 2880, 0, 1),
     ("c4_decode_e128", 128, 4, 2880, 2880, 0, 1),
     ("c4_decode_odd_rows", 16, 4, 2880, 2877, 2880, 1),
+    ("c4_few_tokens", 16, 4, 2880, 2880, 0, 5),
     ("c4_tokens", 16, 4, 2880, 2880, 0, 40),
     ("c4_odd_rows_tokens", 16, 4, 2880, 2877, 2880, 24),
-    ("short_rows_one_token", 16, 4, 1024, 512, 0, 1),   # no decode instance: the grouped GEMMs
+    ("short_rows_one_token", 16, 4, 1024, 512, 0, 1),   # no decode instance: the matvecs
     ("short_rows", 32, 6, 1024, 720, 768, 33),
 ]
 
 
+@pytest.mark.parametrize("which", ["all", "down"])
 @pytest.mark.parametrize("name,E,K,h,I,pad,T", R16_CASES, ids=[c[0] for c in R16_CASES])
-def test_moe_layer_rows16_matches_gguf_rows(name, E, K, h, I, pad, T):
-    # the same layer from GGUF rows and from rows in groups of 16: the kernels take the same
-    # blocks in the same order, so the outputs are the same bits; both against the oracle at the gate
-    say("moe rows16", name)
+def test_moe_layer_rows16_matches_gguf_rows(name, E, K, h, I, pad, T, which):
+    # the same layer from GGUF rows and with its matrices (all three, or down alone) in row groups
+    # of 16: every path takes the same blocks in the same order, so the outputs are the same bits;
+    # against the oracle at the gate
+    say("moe rows16", name, which)
     rng = np.random.default_rng(zlib.crc32(name.encode()))
     layer = synth.moe_weights(E, K, h, I, (F.MXFP4,) * 3, rng, act=1, pad=pad)
     x = rng.standard_normal((T, h)).astype(np.float32)
     logits = rng.standard_normal((T, E)).astype(np.float32)
     assert not synth.near_ties_within_top_k(logits, K)
     rows = upload_layer(layer)
-    rp = ops.MoeLayer(*[b.rows16() for b in rows.banks], n_experts=E, top_k=K,
-                       norm_topk_prob=layer.norm, act=rows.act)
+    banks = [b.rows16() if which == "all" or m == 2 else b for m, b in enumerate(rows.banks)]
+    rp = ops.MoeLayer(*banks, n_experts=E, top_k=K, norm_topk_prob=layer.norm, act=rows.act)
     want, wids, _, _ = O.moe_layer(layer, x, logits)
     op, idsp, _ = rp.forward(dev(x), dev(logits))
     assert np.array_equal(host(idsp).view(np.uint32), wids)
     err = O.rel_l2(host(op), want)
     say("  rel_l2", err)
     assert err <= REL_L2_GATE
-    if T == 1 and h == 2880:
-        o, _, _ = rows.forward(dev(x), dev(logits))
-        assert np.array_equal(host(o).view(np.uint32), host(op).view(np.uint32))
+    o, _, _ = rows.forward(dev(x), dev(logits))
+    assert np.array_equal(host(o).view(np.uint32), host(op).view(np.uint32))
 
 
 @pytest.mark.parametrize("T", [40, 5])
