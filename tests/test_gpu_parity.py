@@ -709,6 +709,33 @@ def test_moe_layer_rows16_matches_gguf_rows(name, E, K, h, I, pad, T, which):
     assert np.array_equal(host(o).view(np.uint32), host(op).view(np.uint32))
 
 
+@pytest.mark.parametrize("T", [1, 24])
+def test_moe_layer_rows16_through_a_slot_table(T):
+    # row groups of 16 in a bank of fewer slots than experts (slot-major, permuted table, biases
+    # per expert): the decode (T = 1) and the grouped GEMMs against the oracle and the GGUF rows
+    say("moe rows16 slots", T)
+    rng = np.random.default_rng(95 + T)
+    E, K, slots, h, I = 48, 4, 20, 2880, 2880
+    layer = synth.moe_weights(E, K, h, I, (F.MXFP4,) * 3, rng, n_slots=slots, act=1)
+    table = np.full(E, 0xFFFFFFFF, dtype=np.uint32)
+    resident = rng.choice(E, size=slots, replace=False)
+    table[resident] = rng.permutation(slots).astype(np.uint32)
+    mask = np.full(E, -1e30, dtype=np.float32)
+    mask[resident] = 0.0
+    x = rng.standard_normal((T, h)).astype(np.float32)
+    logits = rng.standard_normal((T, E)).astype(np.float32) + mask
+    assert not synth.near_ties_within_top_k(logits, K)
+    rows = upload_layer(layer, slot_table=table)
+    r16 = ops.MoeLayer(*[b.rows16() for b in rows.banks], n_experts=E, top_k=K, norm_topk_prob=layer.norm,
+                       act=rows.act, slot_table=dev(table))
+    want, wids, _, wmiss = O.moe_layer(layer, x, logits, slot_table=table, n_slots=slots)
+    out, ids, _ = r16.forward(dev(x), dev(logits))
+    assert wmiss == 0 and np.array_equal(host(ids).view(np.uint32), wids)
+    assert O.rel_l2(host(out), want) <= REL_L2_GATE
+    o, _, _ = rows.forward(dev(x), dev(logits))
+    assert np.array_equal(host(o).view(np.uint32), host(out).view(np.uint32))
+
+
 @pytest.mark.parametrize("T", [40, 5])
 def test_matmul_id_grouped_rows16_matches_gguf_rows(T):
     # cw_matmul_id_grouped on an MXFP4_R16 bank (every token count: it has no matvec): the same bits
