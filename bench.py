@@ -299,7 +299,10 @@ def bench_c4(args, torch, np, dev):
     --layers layers (12 by default: 20 GB of experts, so a step's 635 MB of picked experts cannot
     come from the 256 MB Infinity Cache), captured in a graph and timed like config 3; prefill:
     2,048 tokens, ten layer calls over the chain's layers captured in one graph (each call reads
-    another layer's 1.69 GB of experts from HBM)."""
+    another layer's 1.69 GB of experts from HBM). The experts are generated as GGUF rows and
+    repacked once, at load, into row groups of 16 (cw_repack_rows16), the library's layout for
+    MXFP4 experts; --gguf-rows times the GGUF rows instead. The other layout is timed after the
+    line's own (`layout_alternative`)."""
     from coachwhip_amd import formats as F
     from coachwhip_amd import ops, synth
     from oracle import oracle as O
@@ -321,6 +324,10 @@ def bench_c4(args, torch, np, dev):
         layers.append(ops.MoeLayer(*banks, n_experts=E, top_k=K, norm_topk_prob=True,
                                    act=ops.ExpertAct.clamped_swiglu(1.702, 7.0, *bias)))
         biases.append(bias)
+    rows16 = [ops.MoeLayer(*[b.rows16() for b in lay.banks], n_experts=E, top_k=K, norm_topk_prob=True, act=lay.act)
+              for lay in layers]
+    gguf = layers
+    layers, alt, alt_name = (gguf, rows16, "rows16") if args.gguf_rows else (rows16, gguf, "gguf rows")
     total = args.warmup + args.steps
     x_all = torch.randn((total, 1, H), generator=gen, device=dev).to(torch.bfloat16).float()
     logits_all = torch.randn((total, L, 1, E), generator=gen, device=dev)
@@ -328,8 +335,8 @@ def bench_c4(args, torch, np, dev):
 
     log("parity of layer 0 against the CPU oracle")
     out0, ids0, w0 = layers[0].forward(x_all[0], logits_all[0, 0])
-    host_layer = synth.MoeWeights(E, K, H, I, dts, [b.data.cpu().numpy() for b in layers[0].banks],
-                                  [b.slot_stride for b in layers[0].banks], E, act=1,
+    host_layer = synth.MoeWeights(E, K, H, I, dts, [b.data.cpu().numpy() for b in gguf[0].banks],
+                                  [b.slot_stride for b in gguf[0].banks], E, act=1,
                                   bias=[b.cpu().numpy() for b in biases[0]])
     x0, lg0 = x_all[0].cpu().numpy(), logits_all[0, 0].cpu().numpy()
     want, wids, ww, _ = O.moe_layer(host_layer, x0, lg0)
@@ -375,37 +382,31 @@ def bench_c4(args, torch, np, dev):
                         "as stored, activations as three FP6 E2M3 terms with E8M0 scales per 32, f32 accumulate")}
     log("prefill", prefill)
 
-    # the same layers with expert matrices repacked in row groups of 16 (MXFP4_R16, opt-in:
-    # ExpertBank.rows16): all three, or down alone; the same blocks, read by the same kernels'
-    # row-group variants, outputs equal to the GGUF rows' bit for bit
-    r16 = None
-    if not args.no_rows16:
-        r16 = {"note": "opt-in layouts (ExpertBank.rows16 / cw_repack_rows16, at load); the line's value and "
-                       "prefill are GGUF rows"}
-        for which in ("all", "down"):
-            log("row groups of 16 (%s): repacking the chain's experts" % which)
-            lay16 = [ops.MoeLayer(*[b.rows16() if which == "all" or m == 2 else b for m, b in enumerate(lay.banks)],
-                                  n_experts=E, top_k=K, norm_topk_prob=True, act=lay.act) for lay in layers]
-            same = all(bool(torch.equal(lay16[l].forward(xp, lp)[0], eager[l])) for l in range(len(eager)))
-            d16 = lay16[0].forward(x_all[0], logits_all[0, 0])[0]
-            same = same and bool(torch.equal(d16, out0))
-            g16 = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g16):
-                for r in range(reps):
-                    lay16[r % L].forward(xp, lp)
-            torch.cuda.synchronize()
-            pre16, pre16_all = time_replays(torch, g16, reps)
-            del g16
-            ms16 = time_graph(torch, lay16, x_all, logits_all, args.warmup, args.steps)
-            dec16 = ms16 * 1e3 / (args.steps * L)
-            r16["gate_up_down" if which == "all" else "down_only"] = {
-                "prefill_us_per_layer": round(pre16, 2), "prefill_tokens_per_s": round(T / (pre16 * 1e-6)),
-                "prefill_us_per_layer_replays": [round(v, 1) for v in pre16_all],
-                "decode_us_per_layer": round(dec16, 3), "decode_gbs": round(layer_bytes / (dec16 * 1e-6) / 1e9, 2),
-                "outputs_equal_gguf_rows": same}
-            log("rows16", which, r16)
-            del lay16
-            torch.cuda.empty_cache()
+    # the same experts in the other layout: prefill outputs bit-equal (the same blocks in the same
+    # order); the one-token layer with gate/up in row groups sums in its own order (K-split), so its
+    # distance from the oracle is given instead
+    other = None
+    if not args.no_alternative:
+        log("the other layout (%s)" % alt_name)
+        same = all(bool(torch.equal(alt[l].forward(xp, lp)[0], eager[l])) for l in range(len(eager)))
+        d_alt = alt[0].forward(x_all[0], logits_all[0, 0])[0]
+        g_alt = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_alt):
+            for r in range(reps):
+                alt[r % L].forward(xp, lp)
+        torch.cuda.synchronize()
+        pre_alt, pre_alt_all = time_replays(torch, g_alt, reps)
+        del g_alt
+        ms_alt = time_graph(torch, alt, x_all, logits_all, args.warmup, args.steps)
+        dec_alt = ms_alt * 1e3 / (args.steps * L)
+        other = {"layout": alt_name, "prefill_us_per_layer": round(pre_alt, 2),
+                 "prefill_tokens_per_s": round(T / (pre_alt * 1e-6)),
+                 "prefill_us_per_layer_replays": [round(v, 1) for v in pre_alt_all],
+                 "decode_us_per_layer": round(dec_alt, 3), "decode_gbs": round(layer_bytes / (dec_alt * 1e-6) / 1e9, 2),
+                 "prefill_outputs_equal": same, "decode_rel_l2": O.rel_l2(d_alt.cpu().numpy(), want)}
+        log("other layout", other)
+    del alt
+    torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -444,14 +445,16 @@ def bench_c4(args, torch, np, dev):
         "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (seeded MXFP4 blocks, biases and bf16-valued N(0,1) activations, generated on the device)",
         "config": {"workload": "config 4 decode: gpt-oss-style MoE layer chain, b=1", "experts": E, "top_k": K,
-                   "hidden": H, "expert_ffn": I, "weights": "mxfp4", "act": "clamped swiglu", "layers": L, "tokens": 1},
+                   "hidden": H, "expert_ffn": I, "weights": "mxfp4", "act": "clamped swiglu", "layers": L, "tokens": 1,
+                   "expert_layout": "gguf rows" if args.gguf_rows else "rows in groups of 16 (repacked at load)"},
         "us_per_layer": round(us_per_layer, 3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(os.path.dirname(os.path.abspath(__file__)), TRAFFIC_PROFILE_C4),
                      "traffic_source": TRAFFIC_PROFILE_C4,
-                     "kernel": "MoE decode layer (MXFP4, clamped SwiGLU)", "bytes_per_launch": layer_bytes},
-        "prefill": prefill, "layout_rows16": r16, "parity": parity, "cpu_baseline": cpu,
+                     "kernel": "MoE decode layer (MXFP4%s, clamped SwiGLU)" % ("" if args.gguf_rows else " in row groups of 16"),
+                     "bytes_per_launch": layer_bytes},
+        "prefill": prefill, "layout_alternative": other, "parity": parity, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
 
@@ -667,7 +670,8 @@ def main():
     ap.add_argument("--prefill-tokens", type=int, default=1500)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-rows16", action="store_true", help="c4: skip the row-groups-of-16 layout's numbers")
+    ap.add_argument("--gguf-rows", action="store_true", help="c4: time the experts as GGUF rows (default: row groups of 16)")
+    ap.add_argument("--no-alternative", action="store_true", help="c4: skip timing the other expert layout")
     ap.add_argument("--seed", type=int, default=3)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of known size (for scaling HBM counters) and exit")

@@ -347,14 +347,19 @@ template <class F> struct RowDma { static constexpr bool on = false; };
 template <> struct RowDma<FMXFP4> { static constexpr bool on = true; };
 template <> struct RowDma<FMXFP4R16> { static constexpr bool on = true; };
 
-// A row pair (rows r0, r0 + 1, r0 even: one group) of an MXFP4_R16 matrix staged in LDS: the pair's
-// blocks of step c are one run of 34 cb bytes (cb = blocks of the step) at rows16_offset(r0, 4c),
-// 8-byte aligned for the full steps and 4-byte aligned for a last step of fewer blocks, brought
-// as the 16-byte pieces that hold it: 9 per full step, pr16_last for the last, in step order.
-// (Staging a whole group per block instead, one contiguous run of each matrix, measured slower:
-// its loads wait for x, and its rows for all of the group's loads.)
-__host__ __device__ __forceinline__ int pr16_last(int nblk) { return nblk % 4 ? (12 + 34 * (nblk % 4) + 15) / 16 : 0; }
-__host__ __device__ __forceinline__ int pr16_pieces(int nblk) { return 9 * (nblk / 4) + pr16_last(nblk); }
+// K-split items of an MXFP4_R16 gate/up pair in the one-launch decode: an item is one pick's group
+// of 16 rows, its steps in parts of up to KS_STEPS (each part one contiguous run of each matrix:
+// 1,088 bytes per full step, 272 cb for a last step of cb blocks), two parts in flight in two LDS
+// buffers; each wave takes 2 steps of each part for all 16 rows (lane: row l / 4, block l % 4 of
+// the step), and the waves' partial sums meet in LDS in wave order. (Staging a row pair per wave
+// instead, as GGUF rows are, made the pair 23 short runs: 80 MB fetched per layer against 55.)
+// LDS: two buffers of two matrices' parts (9 KB each), then x (whole 16-byte chunks, as copied),
+// the waves' partial sums (16 rows x gate, up x 4 waves) and the 32 bias values.
+constexpr int KS_STEPS = 8, KS_SPAN = 9 * 1024, KS_BUF = 2 * KS_SPAN, KS_X = 2 * KS_BUF;
+__host__ __device__ __forceinline__ int ks_x_bytes(int h) { return (h / 4 + 255) / 256 * 256 * 16; }
+__host__ __device__ __forceinline__ int ks_part_off(int h) { return KS_X + ks_x_bytes(h); }
+__host__ __device__ __forceinline__ int ks_bias_off(int h) { return ks_part_off(h) + 4 * 16 * 2 * 4; }
+__host__ __device__ __forceinline__ int ks_lds(int h) { return ks_bias_off(h) + 32 * 4; }
 
 // One 16-byte chunk per lane from global memory into LDS at lds_base + 16 * lane. Issued as inline
 // asm: the compiler's waits then do not cover these loads (the kernel waits for them itself with
@@ -372,6 +377,15 @@ __device__ __forceinline__ void lds_dma4(const void *g, uint32_t lds_base) {
     uint32_t keep;
     asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
                  : "=&s"(keep) : "v"(g), "s"(m) : "memory");
+}
+
+// s_waitcnt vmcnt(n) for a run-time n in 0..31 (the instruction takes an immediate)
+__device__ __forceinline__ void wait_vm(int n) {
+#define CW_VM(N) case N: asm volatile("s_waitcnt vmcnt(" #N ")" ::: "memory"); break;
+#define CW_VM8(B) CW_VM(B) CW_VM(B + 1) CW_VM(B + 2) CW_VM(B + 3) CW_VM(B + 4) CW_VM(B + 5) CW_VM(B + 6) CW_VM(B + 7)
+    switch (n < 0 ? 0 : n > 31 ? 31 : n) { CW_VM8(0) CW_VM8(8) CW_VM8(16) CW_VM8(24) }
+#undef CW_VM8
+#undef CW_VM
 }
 
 // An MXFP4 block at byte o of an LDS row window: the scale byte, then 16 code bytes read as five
@@ -392,14 +406,6 @@ __device__ __forceinline__ FMXFP4::Raw mx_from_lds(const uint8_t *win, int o) {
 // Bytes of a row's window in LDS: its 16-byte chunks from the one holding its first byte, plus the
 // 4 bytes that the last block's dword reads may touch past its end.
 __host__ __device__ __forceinline__ int row_window(int row_bytes) { return ((row_bytes + 15 + 15 + 4) >> 4) << 4; }
-// LDS-staged gate/up rows: a window per row (GGUF rows), or per row pair of each matrix (MXFP4_R16),
-// and a wave's item buffer (RI rows of gate and up, then 2 RI bias values in 16 bytes)
-template <class FG>
-__host__ __device__ __forceinline__ int gu_window(int nsbg) {
-    return Rows16<FG>::on ? 16 * pr16_pieces(nsbg) : row_window(nsbg * FG::TS);
-}
-template <class FG, int RI>
-__host__ __device__ __forceinline__ int gu_ibuf(int nsbg) { return (Rows16<FG>::on ? 2 : 2 * RI) * gu_window<FG>(nsbg) + 16; }
 
 // The whole decode layer (one token) in one launch of a grid that fits on the device at once.
 // Loads are issued as early as their addresses are known, since every wait on them counts in
@@ -456,7 +462,7 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
     const int subg = lane % LG, rsg = lane / LG, nsbg = a.H / 32;
     float xr[XG][32];
     // GDMA: item buffer b of wave w at hs + (b * NW + w) * ibuf; x goes into the buffer-1 region
-    const int x_off = RowDma<FG>::on ? NW * gu_ibuf<FG, RI>(a.H / 32) : 0;
+    const int x_off = Rows16<FG>::on ? KS_X : RowDma<FG>::on ? NW * (2 * RI * row_window(a.H / 32 * FG::TS) + 16) : 0;
     if constexpr (RowDma<FG>::on) {
         // x once per block into the (not yet used) hidden-row region, read into registers below:
         // every wave loading all of x (35 MB across config 4's grid) held up the logits and x
@@ -536,7 +542,8 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
     static_assert(!GDMA || (LG == 64 && XG == 2), "the LDS-staged gate/up rows take one row per wave pass");
     // GDMA: this wave's two item buffers in the (not yet used) hidden-row region: per buffer RI
     // gate rows, RI up rows, then the 2*RI bias values
-    const int win = gu_window<FG>(nsbg), ibuf = gu_ibuf<FG, RI>(nsbg);
+    const int win = row_window(nsbg * FG::TS);
+    const int ibuf = 2 * RI * win + 16;
     uint8_t *wbuf = (uint8_t *)hs + wave * ibuf;
     auto issue_item = [&](int it, int b) {
         const int j = it / row_items, r0 = (it - j * row_items) * RI;
@@ -544,23 +551,7 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
         const uint32_t slot = __shfl(my_slot, j), e = __shfl(rid, j);
         const uint32_t sl = slot == 0xFFFFFFFFu ? 0 : slot;
         uint8_t *ib = wbuf + b * NW * ibuf;
-        if constexpr (Rows16<FG>::on) {
-            // the row pair of each matrix: 4 loads of up to 64 pieces, the last with the lanes of
-            // the pieces left; a pair past I reads the last pair
-            const int rp = min(r0, (a.I - 1) & ~1), npc = pr16_pieces(nsbg), nfull = nsbg / 4;
-#pragma unroll
-            for (int m = 0; m < 2; m++) {
-                const uint8_t *mat = m ? a.wu + (int64_t)sl * a.su : a.wg + (int64_t)sl * a.sg;
-                const uint32_t w = hs_lds + (uint32_t)(ib - (uint8_t *)hs) + m * win;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int p = min(64 * i + lane, npc - 1), c = p < 9 * nfull ? p / 9 : nfull;
-                    const uint8_t *run = mat + rows16_off32(rp, 4 * c, nsbg);
-                    if (i < 3 || 64 * i + lane < npc)  // the launch keeps 192 < npc <= 256
-                        lds_dma16((const uint8_t *)((uintptr_t)run & ~(uintptr_t)15) + 16 * (p - 9 * c), w + 1024 * i);
-                }
-            }
-        } else {
+        {
 #pragma unroll
         for (int q = 0; q < RI; q++) {
             const int r = min(r0 + q, a.I - 1);
@@ -588,7 +579,7 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
     if constexpr (GDMA) {
         // the first item's rows go out at once (into buffer 0); x (copied during the top-k into
         // the buffer-1 region) is read into registers meanwhile, before any buffer 1 is filled
-        if (gwave < n_items) {
+        if (!Rows16<FG>::on && gwave < n_items) {
             issue_item(gwave, 0);
             asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * RI + 1) : "memory");
         } else {
@@ -596,7 +587,7 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
         }
         __syncthreads();
 #pragma unroll
-        for (int i = 0; i < XG; i++) {
+        for (int i = 0; i < (Rows16<FG>::on ? 0 : XG); i++) {
             const int sb = subg + i * LG;
             const bool in = sb < nsbg;
             const float4 *src = (const float4 *)((const float *)((const uint8_t *)hs + x_off) + 32 * (in ? sb : nsbg - 1));
@@ -663,6 +654,107 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
         // few microseconds later (their loads queue behind the others'), so each later round
         // leaves out one more of the CU's placement groups (blocks are placed in index order).
         auto wr = [&](int r) { return a.per_cu > 1 ? total_waves * max(a.per_cu - r, 1) / a.per_cu : total_waves; };
+        if constexpr (Rows16<FG>::on) {
+            const int nst = (nsbg + 3) >> 2, nfull = nsbg >> 2, cbl = nsbg & 3, nparts = (nst + KS_STEPS - 1) / KS_STEPS;
+            const int ngi = (a.I + 15) >> 4, n_gi = K * ngi;
+            const int row = lane >> 2, blk = lane & 3;
+            // part p's bytes per matrix (full steps, then a last step of cbl blocks) and this wave's
+            // share of its 2 x ceil(bytes / 1 KB) loads: loads w, w + 4, ...
+            auto part_bytes = [&](int p) {
+                const int s0 = p * KS_STEPS, s1 = min(s0 + KS_STEPS, nst), full = min(s1, nfull) - s0;
+                return full * 1088 + (s1 > nfull ? 272 * cbl : 0);
+            };
+            auto part_loads = [&](int p) { return (2 * ((part_bytes(p) + 1023) >> 10) - wave + 3) >> 2; };
+            const float *xl = (const float *)((const uint8_t *)hs + KS_X);
+            float *partial = (float *)((uint8_t *)hs + ks_part_off(a.H));
+            const float *bias = (const float *)((const uint8_t *)hs + ks_bias_off(a.H));
+            for (int it = blockIdx.x; it < n_gi; it += gridDim.x) {
+                const int j = it / ngi, g = it - j * ngi;
+                const uint32_t slot = __shfl(my_slot, j), e = __shfl(rid, j);
+                const uint32_t sl = slot == 0xFFFFFFFFu ? 0 : slot;
+                const uint8_t *mg = a.wg + (int64_t)sl * a.sg, *mu = a.wu + (int64_t)sl * a.su;
+                auto issue_part = [&](int p) {
+                    const int pieces = part_bytes(p) >> 4, nins = (pieces + 63) >> 6;
+                    const uint32_t base = (uint32_t)g * (uint32_t)(272 * nsbg) + (uint32_t)(p * KS_STEPS * 1088);
+                    for (int ii = wave; ii < 2 * nins; ii += 4) {
+                        const int m = ii >= nins ? 1 : 0, ci = ii - m * nins;
+                        lds_dma16((m ? mu : mg) + base + 16u * (uint32_t)min(64 * ci + lane, pieces - 1),
+                                  hs_lds + (uint32_t)((p & 1) * KS_BUF + m * KS_SPAN + 1024 * ci));
+                    }
+                };
+                __syncthreads();  // the previous item is done with the buffers and the partial sums
+                issue_part(0);
+                if (wave == 0) {  // the group's 16 gate and 16 up bias values (a layer without biases re-reads x)
+                    const float *bsrc = lane < 16 ? a.bg : a.bu;
+                    const float *src = bsrc ? bsrc + (int64_t)(e < (uint32_t)a.E ? e : 0) * a.I + min(16 * g + (lane & 15), a.I - 1) : a.x;
+                    if (lane < 32) lds_dma4(src, hs_lds + (uint32_t)ks_bias_off(a.H));
+                }
+                if (nparts > 1) issue_part(1);
+                float accg = 0.f, accu = 0.f;
+                for (int p = 0; p < nparts; p++) {
+                    wait_vm(p + 1 < nparts ? part_loads(p + 1) : 0);  // this wave's loads of part p are in
+                    __syncthreads();                                  // everyone's
+                    const uint8_t *bgl = (const uint8_t *)hs + (p & 1) * KS_BUF;
+#pragma unroll
+                    for (int t = 0; t < 2; t++) {
+                        const int s = p * KS_STEPS + 2 * wave + t;  // this wave's step
+                        if (s < min(p * KS_STEPS + KS_STEPS, nst)) {
+                            const int cb = s < nfull ? 4 : cbl;
+                            if (blk < cb) {
+                                const int o = (s - p * KS_STEPS) * 1088 + (row * cb + blk) * 17;
+                                const typename FG::Raw wg = mx_from_lds(bgl, o);
+                                const typename FG::Raw wu = mx_from_lds(bgl + KS_SPAN, o);
+                                float xv[32];
+                                const float4 *xs4 = (const float4 *)(xl + 32 * (4 * s + blk));
+#pragma unroll
+                                for (int v = 0; v < 8; v++) {
+                                    const float4 f = xs4[v];
+                                    xv[4 * v] = f.x;
+                                    xv[4 * v + 1] = f.y;
+                                    xv[4 * v + 2] = f.z;
+                                    xv[4 * v + 3] = f.w;
+                                }
+                                accg += FG::dot(wg, ldsg, xv);
+                                accu += FG::dot(wu, ldsg, xv);
+                            }
+                        }
+                    }
+                    if (p + 2 < nparts) {
+                        __syncthreads();  // everyone is done with buffer p & 1
+                        issue_part(p + 2);
+                    }
+                }
+                // the row's 4 lanes, then the 4 waves in order
+                accg += dpp_f<0xB1>(accg);
+                accg += dpp_f<0x4E>(accg);
+                accu += dpp_f<0xB1>(accu);
+                accu += dpp_f<0x4E>(accu);
+                if (blk == 0) {
+                    partial[(wave * 16 + row) * 2] = accg;
+                    partial[(wave * 16 + row) * 2 + 1] = accu;
+                }
+                __syncthreads();
+                if (wave == 0 && lane < 16 && 16 * g + lane < a.I) {
+                    float gs = partial[lane * 2], us = partial[lane * 2 + 1];
+#pragma unroll
+                    for (int w = 1; w < 4; w++) {
+                        gs += partial[(w * 16 + lane) * 2];
+                        us += partial[(w * 16 + lane) * 2 + 1];
+                    }
+                    float o;
+                    if (a.act == CW_ACT_SILU) {
+                        o = gs / (1.0f + expf(-gs)) * us;
+                    } else {
+                        if (a.bg) gs += bias[lane];
+                        if (a.bu) us += bias[16 + lane];
+                        gs = fminf(gs, a.limit);
+                        us = fminf(fmaxf(us, -a.limit), a.limit);
+                        o = (us + 1.0f) * (gs * (1.0f / (1.0f + expf(-(gs * a.alpha)))));
+                    }
+                    store_coherent(a.h + (int64_t)j * a.P + 16 * g + lane, slot == 0xFFFFFFFFu ? __int_as_float(0x7fc00000) : o);
+                }
+            }
+        } else
         for (int it = gwave, b = 0, r = 0; it < n_items; it = gwave < wr(r + 1) ? it + wr(r) : n_items, r++, b ^= 1) {
             // per item: 2*RI rows of two chunk loads each, and the bias load
             const int nx = gwave < wr(r + 1) ? it + wr(r) : n_items;
@@ -684,20 +776,10 @@ __global__ __launch_bounds__(256 * G, G == 1 ? 3 : 1) void k_moe_decode(const Mo
 #pragma unroll
                 for (int i = 0; i < XG; i++) {
                     const int sb = subg + i * LG, sbc = min(sb, nsbg - 1);
-                    typename FG::Raw wg, wu;
-                    if constexpr (Rows16<FG>::on) {
-                        // row q's block sbc in its pair's run of step c (pieces from 9 c; the run at
-                        // its offset in its first piece: the group's steps start 16-byte aligned)
-                        const int rp = min(r0, (a.I - 1) & ~1), c = sbc >> 2, cb = 4 * c + 4 <= nsbg ? 4 : nsbg - 4 * c;
-                        const int o = 144 * c + (((rp & 15) * 17 * cb) & 15) + (r - rp) * 17 * cb + 17 * (sbc & 3);
-                        wg = mx_from_lds(ib, o);
-                        wu = mx_from_lds(ib + win, o);
-                    } else {
-                        const int og = (int)((uintptr_t)(a.wg + (int64_t)sl * a.sg + (int64_t)r * a.rbg) & 15);
-                        const int ou = (int)((uintptr_t)(a.wu + (int64_t)sl * a.su + (int64_t)r * a.rbg) & 15);
-                        wg = mx_from_lds(ib + (2 * q) * win, og + FG::TS * sbc);
-                        wu = mx_from_lds(ib + (2 * q + 1) * win, ou + FG::TS * sbc);
-                    }
+                    const int og = (int)((uintptr_t)(a.wg + (int64_t)sl * a.sg + (int64_t)r * a.rbg) & 15);
+                    const int ou = (int)((uintptr_t)(a.wu + (int64_t)sl * a.su + (int64_t)r * a.rbg) & 15);
+                    const typename FG::Raw wg = mx_from_lds(ib + (2 * q) * win, og + FG::TS * sbc);
+                    const typename FG::Raw wu = mx_from_lds(ib + (2 * q + 1) * win, ou + FG::TS * sbc);
                     if (sb < nsbg) {
                         g += FG::dot(wg, ldsg, xr[i]);
                         u += FG::dot(wu, ldsg, xr[i]);
@@ -972,7 +1054,7 @@ template <class FG, int G, int RI>
 static size_t decode_lds(const MoeArgs &a) {
     size_t n = decode_hidden_lds(a);
     if (RowDma<FG>::on) {
-        const size_t items = 4 * G * 2 * (size_t)gu_ibuf<FG, RI>(a.H / 32);
+        const size_t items = Rows16<FG>::on ? (size_t)ks_lds(a.H) : 4 * G * 2 * (size_t)(2 * RI * row_window(a.H / 32 * FG::TS) + 16);
         const size_t xs = (size_t)(a.H / 4 + 256 * G - 1) / (256 * G) * (256 * G) * 16;  // x, copied in rounds of one chunk per thread
         if (items > n) n = items;
         if (xs > n) n = xs;
@@ -1027,9 +1109,7 @@ static int decode_launch_per(const MoeArgs &a, int which, hipStream_t s) {
         if (w <= 1024 || w > 2048) return CW_ENOTSUP;
         if ((uintptr_t)a.x & 15) return CW_ENOTSUP;  // x is copied in 16-byte chunks
     }
-    if (Rows16<FG>::on) {  // a row pair's four loads per matrix (192 < pieces <= 256), matrices 16-byte aligned
-        const int np = pr16_pieces(a.H / 32);
-        if (np <= 192 || np > 256 || a.I < 2) return CW_ENOTSUP;
+    if (Rows16<FG>::on) {  // K-split items: matrices 16-byte aligned, at most 16 loads per wave per part
         if (((uintptr_t)a.wg | (uintptr_t)a.wu | (uintptr_t)a.sg | (uintptr_t)a.su) & 15) return CW_ENOTSUP;
         if ((int64_t)(a.I + 15) * a.rbg >= ((int64_t)1 << 31)) return CW_ENOTSUP;  // 32-bit offsets
     }

@@ -688,8 +688,9 @@ R16_CASES = [
 @pytest.mark.parametrize("name,E,K,h,I,pad,T", R16_CASES, ids=[c[0] for c in R16_CASES])
 def test_moe_layer_rows16_matches_gguf_rows(name, E, K, h, I, pad, T, which):
     # the same layer from GGUF rows and with its matrices (all three, or down alone) in row groups
-    # of 16: every path takes the same blocks in the same order, so the outputs are the same bits;
-    # against the oracle at the gate
+    # of 16, against the oracle at the gate: the same blocks in the same order give the same bits,
+    # except in the one-launch decode with gate/up in row groups (K-split, its own f32 order: held
+    # to the f32 bar)
     say("moe rows16", name, which)
     rng = np.random.default_rng(zlib.crc32(name.encode()))
     layer = synth.moe_weights(E, K, h, I, (F.MXFP4,) * 3, rng, act=1, pad=pad)
@@ -706,7 +707,10 @@ def test_moe_layer_rows16_matches_gguf_rows(name, E, K, h, I, pad, T, which):
     say("  rel_l2", err)
     assert err <= REL_L2_GATE
     o, _, _ = rows.forward(dev(x), dev(logits))
-    assert np.array_equal(host(o).view(np.uint32), host(op).view(np.uint32))
+    if T == 1 and h == 2880 and which == "all":
+        assert err <= REL_L2_F32
+    else:
+        assert np.array_equal(host(o).view(np.uint32), host(op).view(np.uint32))
 
 
 @pytest.mark.parametrize("T", [1, 24])
@@ -731,9 +735,13 @@ def test_moe_layer_rows16_through_a_slot_table(T):
     want, wids, _, wmiss = O.moe_layer(layer, x, logits, slot_table=table, n_slots=slots)
     out, ids, _ = r16.forward(dev(x), dev(logits))
     assert wmiss == 0 and np.array_equal(host(ids).view(np.uint32), wids)
-    assert O.rel_l2(host(out), want) <= REL_L2_GATE
-    o, _, _ = rows.forward(dev(x), dev(logits))
-    assert np.array_equal(host(o).view(np.uint32), host(out).view(np.uint32))
+    err = O.rel_l2(host(out), want)
+    assert err <= REL_L2_GATE
+    if T == 1:  # the K-split decode: its own f32 order
+        assert err <= REL_L2_F32
+    else:
+        o, _, _ = rows.forward(dev(x), dev(logits))
+        assert np.array_equal(host(o).view(np.uint32), host(out).view(np.uint32))
 
 
 @pytest.mark.parametrize("T", [40, 5])
