@@ -8,7 +8,10 @@ the earliest block's start in the same launch (thread 0 of each block reads s_me
 100 MHz clock), over eager single-token calls synchronised between them, on a chain of 8 layers
 of random experts so that no call finds its weights in a cache. Usage:
 
-    python3 -m coachwhip_amd.phases [c3] [c4]
+    python3 -m coachwhip_amd.phases [c3] [c4] [c4r16]
+
+c4r16 is config 4 with its experts repacked in row groups of 16 (ExpertBank.rows16), whose
+one-launch decode stages each pick's groups as K-split block items.
 """
 import ctypes
 import os
@@ -25,6 +28,7 @@ CONFIGS = {
     # name: experts, top-k, hidden, expert FFN, formats, clamped SwiGLU with biases
     "c3": (256, 8, 2048, 512, ("IQ2_XXS", "IQ2_XXS", "IQ2_S"), False),
     "c4": (128, 4, 2880, 2880, ("MXFP4", "MXFP4", "MXFP4"), True),
+    "c4r16": (128, 4, 2880, 2880, ("MXFP4", "MXFP4", "MXFP4"), True),
 }
 MAX_BLOCKS = 4096
 
@@ -47,6 +51,8 @@ def run(name, reps=4, layers=8, seed=5):
         ea = ops.ExpertAct.silu()
         if act:
             ea = ops.ExpertAct.clamped_swiglu(1.702, 7.0, *[torch.randn((E, n), generator=gen, device=dev) * 0.02 for n in (I, I, H)])
+        if name.endswith("r16"):
+            banks = [b.rows16() for b in banks]
         chain.append(ops.MoeLayer(*banks, n_experts=E, top_k=K, norm_topk_prob=True, act=ea))
     x = torch.randn((1, H), generator=gen, device=dev)
     buf = (ctypes.c_ulonglong * (MAX_BLOCKS * 8))()
