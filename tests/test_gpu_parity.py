@@ -676,6 +676,8 @@ R16_CASES = [
     ("c4_decode", 16, 4, 2880, 2880, 0, 1),
     ("c4_decode_e128", 128, 4, 2880, 2880, 0, 1),
     ("c4_decode_odd_rows", 16, 4, 2880, 2877, 2880, 1),
+    ("c4_decode_top5", 32, 5, 2880, 2880, 0, 1),       # 900 block items: more than one round of the grid
+    ("c4_decode_silu", 16, 4, 2880, 2880, 0, 1),       # SiLU, no biases
     ("c4_few_tokens", 16, 4, 2880, 2880, 0, 5),
     ("c4_tokens", 16, 4, 2880, 2880, 0, 40),
     ("c4_odd_rows_tokens", 16, 4, 2880, 2877, 2880, 24),
@@ -693,7 +695,7 @@ def test_moe_layer_rows16_matches_gguf_rows(name, E, K, h, I, pad, T, which):
     # to the f32 bar)
     say("moe rows16", name, which)
     rng = np.random.default_rng(zlib.crc32(name.encode()))
-    layer = synth.moe_weights(E, K, h, I, (F.MXFP4,) * 3, rng, act=1, pad=pad)
+    layer = synth.moe_weights(E, K, h, I, (F.MXFP4,) * 3, rng, act=0 if "silu" in name else 1, pad=pad)
     x = rng.standard_normal((T, h)).astype(np.float32)
     logits = rng.standard_normal((T, E)).astype(np.float32)
     assert not synth.near_ties_within_top_k(logits, K)
