@@ -1270,24 +1270,46 @@ __global__ __launch_bounds__(256) void k_pack_f16(const float *x, int rows, int 
     if (lane == 0) ascale[row] = ldexpf(1.0f, -ex);
 }
 
-// one thread per 4 outputs of a token: the weighted sum of its K picks' rows, bias added per pick.
-// A pick whose slot is out of range is in no pile and has no row: it contributes NaN, as it does
-// on the matvec and decode paths.
+// one thread per 4 outputs of a token: the weighted sum of its K picks' rows, bias added per pick,
+// in pick order. A pick whose slot is out of range is in no pile and has no row: it contributes
+// NaN, as it does on the matvec and decode paths. The picks go in chunks of CH, each chunk's
+// slots, weights and expert ids loaded together, then its rows and bias rows (every pick has a
+// row of dn, written or not, so those loads need no branch; past K a chunk reads pick K - 1
+// again, unused).
+template <int CH>
 __global__ __launch_bounds__(256) void k_combine(const float *dn, const float *w, const float *bias, const uint32_t *ids,
                                                  const uint32_t *slots, uint32_t n_slots, int K, int H, float *out) {
     const int t = blockIdx.y, j = 4 * (blockIdx.x * 256 + threadIdx.x);
     if (j >= H) return;
+    const float nan = __int_as_float(0x7fc00000);
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int e = 0; e < K; e++) {
-        const int64_t pick = (int64_t)t * K + e;
-        const float nan = __int_as_float(0x7fc00000);
-        float4 d = slots[pick] < n_slots ? *(const float4 *)(dn + pick * H + j) : make_float4(nan, nan, nan, nan);
-        if (bias) {
-            const float4 b = *(const float4 *)(bias + (int64_t)ids[pick] * H + j);
-            d.x += b.x; d.y += b.y; d.z += b.z; d.w += b.w;
+    for (int e0 = 0; e0 < K; e0 += CH) {
+        uint32_t sl[CH], id[CH];
+        float we[CH];
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            const int64_t pick = (int64_t)t * K + min(e0 + c, K - 1);
+            sl[c] = slots[pick];
+            we[c] = w[pick];
+            id[c] = bias ? ids[pick] : 0u;
         }
-        const float we = w[pick];
-        acc.x += d.x * we; acc.y += d.y * we; acc.z += d.z * we; acc.w += d.w * we;
+        float4 d[CH], b[CH];
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            const int64_t pick = (int64_t)t * K + min(e0 + c, K - 1);
+            d[c] = *(const float4 *)(dn + pick * H + j);
+            b[c] = bias ? *(const float4 *)(bias + (int64_t)id[c] * H + j) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            if (e0 + c >= K) break;
+            float4 v = sl[c] < n_slots ? d[c] : make_float4(nan, nan, nan, nan);
+            if (bias) {
+                v.x += b[c].x; v.y += b[c].y; v.z += b[c].z; v.w += b[c].w;
+            }
+            const float wc = we[c];
+            acc.x += v.x * wc; acc.y += v.y * wc; acc.z += v.z * wc; acc.w += v.w * wc;
+        }
     }
     *(float4 *)(out + (int64_t)t * H + j) = acc;
 }
@@ -1335,8 +1357,8 @@ int combine_picks(const float *dn, const float *w, const float *bias, const uint
                   int T, int K, int H, float *out, hipStream_t s) {
     if (T == 0) return CW_OK;
     if (H % 4) return set_error(CW_ENOTSUP, "combine: width %d is not a multiple of 4", H);
-    hipLaunchKernelGGL(k_combine, dim3((H / 4 + 255) / 256, T), dim3(256), 0, s, dn, w, bias, ids, slots, (uint32_t)n_slots, K, H,
-                       out);
+    const dim3 grid((H / 4 + 255) / 256, T);
+    hipLaunchKernelGGL(k_combine<4>, grid, dim3(256), 0, s, dn, w, bias, ids, slots, (uint32_t)n_slots, K, H, out);
     return check_launch("k_combine");
 }
 
