@@ -538,6 +538,8 @@ MOE_CASES = [
     ("c5_shrunk_q2_k", 64, 10, 2048, 512, (F.Q2_K, F.Q2_K, F.Q2_K), 0, 0, 1),
     ("q2_k_gate_up_tokens", 32, 4, 1024, 512, (F.Q2_K, F.Q2_K, F.Q4_K), 0, 0, 24),
     ("q2_k_grouped", 32, 4, 1024, 512, (F.Q2_K, F.Q2_K, F.Q2_K), 0, 0, 56),
+    ("q2_k_top10_tokens", 64, 10, 1024, 512, (F.Q2_K, F.Q2_K, F.Q2_K), 0, 0, 24),  # the combine's picks in chunks 4, 4, 2
+    ("iq2_s_top6_biases", 32, 6, 1024, 512, (F.IQ2_S, F.IQ2_S, F.IQ2_S), 1, 0, 24),  # down biases over a partial chunk
     ("iq3_xxs_iq4_xs", 32, 6, 1024, 512, (F.IQ3_XXS, F.IQ3_XXS, F.IQ4_XS), 0, 0, 3),
     ("iq3_xxs_iq4_xs_tokens", 32, 6, 1024, 512, (F.IQ3_XXS, F.IQ3_XXS, F.IQ4_XS), 0, 0, 40),
     ("q5_k_q6_k", 16, 4, 1024, 512, (F.Q5_K, F.Q5_K, F.Q6_K), 0, 0, 2),
